@@ -1,0 +1,210 @@
+/*
+ * wisp_hip — C ABI of the MI355X (gfx950) paged fused-MoE layer.
+ *
+ * Every entry point takes plain pointers, sizes and a hipStream_t, returns an
+ * int status (WISP_OK = 0) and never allocates device memory: the caller
+ * owns all buffers.  On failure wisp_last_error() returns a message.
+ *
+ * Each function names the reference code it replaces; paths are relative to
+ * the reference checkout (nokia-applied-research/WiSP).
+ */
+#ifndef WISP_HIP_H_
+#define WISP_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* wisp_stream_t; /* == hipStream_t */
+
+/* status codes */
+#define WISP_OK 0
+#define WISP_ERR_INVALID 1     /* bad argument (shape, id out of range, ...) */
+#define WISP_ERR_SUBBATCH 2    /* a call's working set exceeds cap; the
+                                  reference raises RuntimeError("... sub-batch")
+                                  at fused_moe.py:315-327 */
+#define WISP_ERR_HIP 3         /* HIP runtime error */
+#define WISP_ERR_UNSUPPORTED 4 /* shape/dtype outside what the kernels cover */
+
+/* element types */
+#define WISP_F32 0
+#define WISP_BF16 1
+
+/* layer modes (WISP_MODE, fused_moe.py:76-79) */
+#define WISP_MODE_PAGED 0
+#define WISP_MODE_RESIDENT 1
+
+/* expert-stage algorithms */
+#define WISP_ALGO_AUTO 0
+#define WISP_ALGO_GEMV 1  /* wave-per-row GEMV, decode shapes */
+#define WISP_ALGO_MFMA 2  /* bf16 MFMA grouped GEMM, batched/prefill shapes */
+
+/* ---- library -------------------------------------------------------- */
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* wisp_last_error(void);
+/* ABI version of this library. */
+int wisp_abi_version(void);
+/* int32 words a decision record needs for a call of T tokens x K experts. */
+int wisp_record_words(int T, int K);
+
+/* ---- group 1: routing and the pager -------------------------------- */
+
+/* Router softmax -> top-k -> optional renormalisation, one wave per token.
+ * logits [T, E] (WISP_F32 or WISP_BF16) -> topk_w f32 [T, K], topk_ids i32
+ * [T, K] in routing order (logit descending, ties to the lower id).
+ * If forward_counter is non-null, it is incremented once (layer-call count).
+ * Replaces: layer.select_experts(..., renormalize, scoring_func="softmax")
+ *           at src/wisp/integrations/vllm/fused_moe.py:1054-1076. */
+int wisp_route_topk_softmax(const void* logits, int logits_dtype, int T, int E, int K,
+                            int renormalize, float* topk_w, int32_t* topk_ids,
+                            int64_t* forward_counter, wisp_stream_t stream);
+
+/* The expert pager on the GPU (one workgroup).  Plans the greedy token
+ * groups (or one group if single_group), then for each group in order makes
+ * the LRU hit / evict / load decisions, updates the device state
+ * (expert_map [E], slot_to_expert [cap], lru_tick [cap], counters [8] =
+ * {clock, forward, miss, evict, hits, ...}), writes the slot each
+ * (token, k) reads into slots [T, K] (may be NULL), and writes the decision
+ * record (layout: wisp_amd/csrc/pager_core.h) to `record`, which may be
+ * pinned host memory.  Decisions are bit-exact with the reference.
+ * Replaces: WispMoEState.ensure_resident (fused_moe.py:264-358), the greedy
+ *           sub-batch planner (fused_moe.py:1119-1140) and the
+ *           torch.unique(...).cpu() syncs at fused_moe.py:279,1102,1174. */
+int wisp_pager_decide(const int32_t* topk_ids, int T, int K, int E, int cap,
+                      int single_group, int32_t* expert_map, int32_t* slot_to_expert,
+                      int64_t* lru_tick, int64_t* counters, int32_t* slots,
+                      int32_t* record, int record_words, wisp_stream_t stream);
+
+/* Same decisions computed sequentially on the host (host pointers).  The
+ * specification the GPU pager is tested against. */
+int wisp_pager_decide_host(const int32_t* topk_ids, int T, int K, int E, int cap,
+                           int single_group, int32_t* expert_map, int32_t* slot_to_expert,
+                           int64_t* lru_tick, int64_t* counters, int32_t* slots,
+                           int32_t* record, int record_words);
+
+/* Iteration order of CPython's set built from ascending keys (the order of
+ * the reference's `missing` list, fused_moe.py:279-283).  Host only.
+ * Returns n, or -1 if n is outside [0, 512]. */
+int wisp_cpython_set_order(const int32_t* keys, int n, int32_t* order);
+
+/* Greedy first-fit token grouping (host): group_end[g] = one past the last
+ * token of group g.  Returns the number of groups.
+ * Replaces: fused_moe.py:1119-1140. */
+int wisp_subbatch_plan(const int32_t* topk_ids, int T, int K, int cap, int32_t* group_end);
+
+/* Issue the page-in copies of one group of a decision record on copy_stream
+ * (hipMemcpyAsync from pinned host masters into HBM scratch slots).  Strides
+ * are in bytes.  When fused_slab != 0 the w2 bytes of an expert directly
+ * follow its w13 bytes in both the master and the slot, and one copy of
+ * w13_bytes + w2_bytes moves both.
+ * Replaces: scratch_w13[slot].copy_(cpu_w13[e]); scratch_w2[slot].copy_(...)
+ *           at fused_moe.py:351-352. */
+int wisp_pagein_issue(const int32_t* record, int record_words, int T, int K, int group,
+                      const void* master_w13, size_t master_w13_stride,
+                      const void* master_w2, size_t master_w2_stride,
+                      void* scratch_w13, size_t scratch_w13_stride,
+                      void* scratch_w2, size_t scratch_w2_stride,
+                      size_t w13_bytes, size_t w2_bytes, int fused_slab,
+                      wisp_stream_t copy_stream);
+
+/* ---- group 2: expert compute --------------------------------------- */
+
+/* Slot-remapped SwiGLU experts with the routing-order combine:
+ *   act[t,k] = silu(W13[s] x[t])[:I] * (W13[s] x[t])[I:],  s = slots[t,k]
+ *   out[t]   = sum_{k=0..K-1} topk_w[t,k] * (W2[s] act[t,k])  (k ascending)
+ * A slot of -1 contributes zero.  W13 of slot s is at w13 + s*w13_stride
+ * ([2I, H] row-major), W2 at w2 + s*w2_stride ([H, I] row-major); strides in
+ * elements.  act: workspace of T*K*I elements.  dtype WISP_F32 or WISP_BF16
+ * (x, weights, act and out share it).
+ * Replaces: vLLM fused_experts(..., expert_map=...) at
+ *           fused_moe.py:1106-1118 and 1155-1167. */
+int wisp_moe_experts(const void* x, int dtype, int T, int H, int I, int K,
+                     const float* topk_w, const int32_t* slots,
+                     const void* w13, size_t w13_stride, const void* w2, size_t w2_stride,
+                     void* act, void* out, int algo, wisp_stream_t stream);
+
+/* ---- group 3: the layer call --------------------------------------- */
+
+typedef struct wisp_layer_desc {
+  int num_experts, cap, hidden, inter, dtype, mode;
+  void* scratch_w13;             /* device, slot s at +s*stride [2I, H]  */
+  size_t scratch_w13_stride;     /* elements                             */
+  void* scratch_w2;              /* device, slot s at +s*stride [H, I]   */
+  size_t scratch_w2_stride;      /* elements                             */
+  const void* master_w13;        /* pinned host, expert e at +e*stride   */
+  size_t master_w13_stride;      /* elements                             */
+  const void* master_w2;
+  size_t master_w2_stride;       /* elements                             */
+  int32_t* expert_map;           /* device [num_experts]                 */
+  int32_t* slot_to_expert;       /* device [cap]                         */
+  int64_t* lru_tick;             /* device [cap]                         */
+  int64_t* counters;             /* device [8]                           */
+} wisp_layer_desc;
+
+typedef struct wisp_workspace {
+  int max_pairs;                 /* T*K the buffers below are sized for  */
+  float* topk_w;                 /* device [max_pairs]                   */
+  int32_t* topk_ids;             /* device [max_pairs]                   */
+  int32_t* slots;                /* device [max_pairs]                   */
+  void* act;                     /* device [max_pairs*inter]             */
+  int32_t* record;               /* pinned host [record_words]           */
+  int record_words;
+} wisp_workspace;
+
+/* Create / destroy the per-layer context (copy stream, events). */
+int wisp_layer_create(const wisp_layer_desc* desc, void** handle);
+int wisp_layer_destroy(void* handle);
+/* Re-point the context at a new scratch / cap (after a resize). */
+int wisp_layer_set_scratch(void* handle, void* scratch_w13, void* scratch_w2, int cap,
+                           int32_t* slot_to_expert, int64_t* lru_tick);
+
+/* One MoE layer call on `stream` for T tokens routed to top_k experts each:
+ * route, page (paged mode) and compute.  Returns WISP_ERR_SUBBATCH when one
+ * token alone needs more than cap experts.
+ * Replaces: _patched_forward_cuda / _wisp_forward_cuda_paged
+ *           (fused_moe.py:930-987, 990-1237). */
+int wisp_layer_forward(void* handle, const void* x, const void* logits, int logits_dtype,
+                       int T, int top_k, int renormalize, void* out, const wisp_workspace* ws,
+                       int algo, wisp_stream_t stream);
+
+/* Make the experts in ids[n] resident as one call (no sub-batching).
+ * Replaces: WispMoEState.ensure_resident (fused_moe.py:264-358). */
+int wisp_layer_ensure_resident(void* handle, const int32_t* ids, int n,
+                               const wisp_workspace* ws, wisp_stream_t stream);
+
+/* Copy every expert into slot e and set the identity map (cap == E).
+ * Replaces: WispMoEState.prime_identity (fused_moe.py:242-258). */
+int wisp_layer_prime_identity(void* handle, wisp_stream_t stream);
+
+/* Milliseconds the last paged forward's copies took on the copy stream and
+ * the bytes they moved (for page-in bandwidth reporting). */
+int wisp_layer_last_pagein(void* handle, float* ms, double* bytes);
+
+/* Read and reset the accumulated HIP-event durations of the expert kernels
+ * (first token group of each call: w13+SiLU kernel, then w2+combine kernel)
+ * and the number of timed launches; then switch timing on (enable != 0) or
+ * off.  Timing adds three event records per call on the caller's stream. */
+int wisp_layer_profile(void* handle, int enable, double* w13_ms, double* w2_ms,
+                       int64_t* launches);
+
+/* ---- group 4: probes ----------------------------------------------- */
+
+/* Pinned host -> device hipMemcpyAsync bandwidth: `iters` copies of `bytes`
+ * on `streams` streams; writes the per-iteration milliseconds.
+ * Replaces: scripts/m3_11_anvil_bandwidth_probe.py:42-82. */
+int wisp_probe_h2d(void* dst, const void* src_host, size_t bytes, int iters, int streams,
+                   float* ms_per_iter);
+
+/* Streaming device copy kernel (dst <- src, bytes multiple of 16), for the
+ * HBM read+write calibration of the byte counters. */
+int wisp_probe_hbm_copy(void* dst, const void* src, size_t bytes, wisp_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WISP_HIP_H_ */

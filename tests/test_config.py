@@ -1,0 +1,89 @@
+"""WISP_MODE / WISP_CAP_EXPERTS resolution and the install surface
+(reference fused_moe.py:76-118, 1245-1315; plugin.py:47-97)."""
+import importlib
+import logging
+
+import pytest
+
+fm = importlib.import_module("wisp_amd.integrations.vllm.fused_moe")
+
+
+@pytest.mark.parametrize("raw,want", [(None, "paged"), ("paged", "paged"), ("resident", "resident"),
+                                      ("copy", "copy"), ("day1", "copy"), ("day2a", "resident"),
+                                      ("day2b", "paged"), (" PAGED ", "paged")])
+def test_resolve_mode(monkeypatch, raw, want):
+    if raw is None:
+        monkeypatch.delenv("WISP_MODE", raising=False)
+    else:
+        monkeypatch.setenv("WISP_MODE", raw)
+    assert fm._resolve_mode() == want
+
+
+def test_resolve_mode_unknown_warns(monkeypatch, caplog):
+    monkeypatch.setenv("WISP_MODE", "bogus")
+    with caplog.at_level(logging.WARNING):
+        assert fm._resolve_mode() == "paged"
+    assert "unrecognised" in caplog.text
+
+
+@pytest.mark.parametrize("raw,E,want", [(None, 128, 24), (None, 8, 8), ("8", 128, 8),
+                                        ("1", 128, 2), ("999", 128, 128), ("0", 8, 2),
+                                        ("abc", 128, 128), ("-5", 16, 2)])
+def test_resolve_cap(monkeypatch, raw, E, want):
+    if raw is None:
+        monkeypatch.delenv("WISP_CAP_EXPERTS", raising=False)
+    else:
+        monkeypatch.setenv("WISP_CAP_EXPERTS", raw)
+    assert fm._resolve_cap_experts(E) == want
+
+
+def test_install_is_idempotent_and_refreshes_config(monkeypatch):
+    from wisp_amd.integrations.vllm import layer
+    cls = layer.UnquantizedFusedMoEMethod
+    orig = (cls.create_weights, cls.process_weights_after_loading, cls.forward_cuda)
+    try:
+        first = fm.install_wisp_moe(mode="paged", cap_experts=8)
+        assert fm.is_installed()
+        assert fm.install_wisp_moe(mode="resident") is False
+        assert fm._WISP_RUNTIME_CONFIG == {"mode": "resident", "cap_experts_override": None}
+        assert cls.forward_cuda is fm._patched_forward_cuda
+        assert first in (True, False)
+    finally:
+        cls.create_weights, cls.process_weights_after_loading, cls.forward_cuda = orig
+        if hasattr(cls, "_wisp_patched"):
+            delattr(cls, "_wisp_patched")
+
+
+def test_plugin_register_honours_disable(monkeypatch):
+    from wisp_amd.integrations.vllm import plugin
+    monkeypatch.setenv("WISP_PLUGIN_DISABLE", "1")
+    plugin.register()
+    assert not fm.is_installed()
+
+
+def test_create_weights_rejects_bias():
+    import torch
+    from wisp_amd.integrations.vllm.layer import FusedMoEConfig, UnquantizedFusedMoEMethod
+    m = UnquantizedFusedMoEMethod(FusedMoEConfig(has_bias=True))
+    with pytest.raises(NotImplementedError):
+        fm._patched_create_weights(m, torch.nn.Module(), 4, 16, 8, torch.float32)
+
+
+def test_create_weights_allocates_host_slab():
+    import torch
+    from wisp_amd.integrations.vllm.layer import UnquantizedFusedMoEMethod
+    layer = torch.nn.Module()
+    fm._patched_create_weights(UnquantizedFusedMoEMethod(), layer, 4, 16, 8, torch.bfloat16)
+    assert layer.w13_weight.shape == (4, 16, 16) and layer.w2_weight.shape == (4, 16, 8)
+    assert layer.w13_weight.device.type == "cpu"
+    # w2 of expert e follows its w13 in one slab: one copy per miss
+    assert layer.w2_weight.data_ptr() - layer.w13_weight.data_ptr() == 16 * 16 * 2
+    assert layer.w13_weight.stride(0) == layer.w2_weight.stride(0) == 3 * 8 * 16
+
+
+def test_unsupported_call_arguments():
+    with pytest.raises(NotImplementedError):
+        fm._check_supported({"scoring_func": "sigmoid"})
+    with pytest.raises(NotImplementedError):
+        fm._check_supported({"use_grouped_topk": True})
+    fm._check_supported({"scoring_func": "softmax", "topk_group": None})

@@ -1,0 +1,43 @@
+// Shared definitions for the wisp_hip library (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "../../include/wisp_hip.h"
+
+#define WISP_HD __host__ __device__
+
+namespace wisp {
+
+// Upper bounds baked into the single-workgroup pager kernel's LDS layout.
+constexpr int kMaxExperts = 512;
+constexpr int kMaxTopK = 64;
+// A CPython set of n <= kMaxExperts small ints never needs a table larger
+// than the smallest power of two above 4n, which is <= 8n.
+constexpr int kMaxSetTable = 8 * kMaxExperts;
+
+// Per-layer counters kept on the device, in this order.
+enum Counter : int {
+  kClock = 0,     // LRU clock (one tick per ensure_resident call)
+  kForward = 1,   // layer calls
+  kMiss = 2,
+  kEvict = 3,
+  kHits = 4,
+  kNumCounters = 8,
+};
+
+}  // namespace wisp
+
+#define WISP_HIP_TRY(expr)                               \
+  do {                                                   \
+    hipError_t _e = (expr);                              \
+    if (_e != hipSuccess) {                              \
+      wisp_set_last_error(hipGetErrorString(_e), #expr); \
+      return WISP_ERR_HIP;                               \
+    }                                                    \
+  } while (0)
+
+// Records a message retrievable through wisp_last_error().
+void wisp_set_last_error(const char* what, const char* where);

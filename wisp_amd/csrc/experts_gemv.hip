@@ -1,0 +1,299 @@
+// Decode-shape expert kernels (GEMV): w13 with fused SiLU*mul, then w2 with
+// the routing-order combine.
+//
+// Replaces vLLM fused_experts as called by the reference with the slot
+// remap (src/wisp/integrations/vllm/fused_moe.py:1106-1118, 1155-1167):
+//   act[t,k] = silu(W13[s][:I] x[t]) * (W13[s][I:] x[t]),   s = slots[t,k]
+//   out[t]   = sum_{k=0..K-1} w[t,k] * (W2[s] act[t,k])     (k ascending)
+//
+// Both kernels stream weight rows with 16-byte loads, one wavefront (or half
+// of one) per row, and reduce in a fixed butterfly order, so the bytes of
+// out[t] depend only on x[t], the routing of token t and the weights read -
+// never on the slot numbers, on cap or on the other tokens of the launch.
+// That is what makes paged output byte-identical to resident output.
+#include "common.h"
+
+namespace wisp {
+namespace {
+
+template <typename T>
+struct Vec;
+template <>
+struct Vec<float> {
+  static constexpr int N = 4;
+  __device__ static inline void unpack(const uint4& u, float* f) {
+    f[0] = __uint_as_float(u.x); f[1] = __uint_as_float(u.y);
+    f[2] = __uint_as_float(u.z); f[3] = __uint_as_float(u.w);
+  }
+};
+template <>
+struct Vec<uint16_t> {  // bf16 bits
+  static constexpr int N = 8;
+  __device__ static inline void unpack(const uint4& u, float* f) {
+    f[0] = __uint_as_float(u.x << 16); f[1] = __uint_as_float(u.x & 0xffff0000u);
+    f[2] = __uint_as_float(u.y << 16); f[3] = __uint_as_float(u.y & 0xffff0000u);
+    f[4] = __uint_as_float(u.z << 16); f[5] = __uint_as_float(u.z & 0xffff0000u);
+    f[6] = __uint_as_float(u.w << 16); f[7] = __uint_as_float(u.w & 0xffff0000u);
+  }
+};
+
+__device__ inline uint16_t f32_to_bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+template <typename T>
+__device__ inline void store_elem(T* p, float v);
+template <>
+__device__ inline void store_elem<float>(float* p, float v) { *p = v; }
+template <>
+__device__ inline void store_elem<uint16_t>(uint16_t* p, float v) { *p = f32_to_bf16_rne(v); }
+
+__device__ inline uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+
+__device__ inline float silu(float g) { return g / (1.0f + expf(-g)); }
+
+// ---------------------------------------------------------------------------
+// Kernel A: act = silu(gate) * up.  Block = 4 waves, each wave owns RW
+// consecutive i (gate row i and up row I + i) of one (token, k) pair; each
+// lane covers CH chunks of 16 bytes of a row (chunk c*64 + lane).
+// grid = (ceil(I / (4 * RW)), T * K).
+// ---------------------------------------------------------------------------
+template <typename T, int CH, int RW>
+__global__ __launch_bounds__(256) void w13_silu_kernel(const T* __restrict__ x, int H, int I,
+                                                        int K, const int32_t* __restrict__ slots,
+                                                        const T* __restrict__ w13,
+                                                        size_t w13_stride, T* __restrict__ act) {
+  constexpr int V = Vec<T>::N;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int pair = blockIdx.y;
+  const int t = pair / K;
+  const int i0 = (blockIdx.x * 4 + wave) * RW;
+  if (i0 >= I) return;
+  const int s = slots[pair];
+  T* arow = act + (size_t)pair * I;
+  if (s < 0) {
+    if (lane < RW && i0 + lane < I) store_elem(arow + i0 + lane, 0.f);
+    return;
+  }
+  const int nch = H / V;
+  const T* W = w13 + (size_t)s * w13_stride;
+  const T* xr = x + (size_t)t * H;
+
+  uint4 wg[RW][CH], wu[RW][CH], xv[CH];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int ch = c * 64 + lane;
+    xv[c] = ch < nch ? ld16(xr + (size_t)ch * V) : make_uint4(0, 0, 0, 0);
+  }
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const int i = min(i0 + r, I - 1);
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int ch = c * 64 + lane;
+      if (ch < nch) {
+        wg[r][c] = ld16(W + (size_t)i * H + (size_t)ch * V);
+        wu[r][c] = ld16(W + (size_t)(I + i) * H + (size_t)ch * V);
+      } else {
+        wg[r][c] = make_uint4(0, 0, 0, 0);
+        wu[r][c] = make_uint4(0, 0, 0, 0);
+      }
+    }
+  }
+  float ag[RW], au[RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) { ag[r] = 0.f; au[r] = 0.f; }
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    float xf[V];
+    Vec<T>::unpack(xv[c], xf);
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      float gf[V], uf[V];
+      Vec<T>::unpack(wg[r][c], gf);
+      Vec<T>::unpack(wu[r][c], uf);
+#pragma unroll
+      for (int q = 0; q < V; ++q) {
+        ag[r] = fmaf(gf[q], xf[q], ag[r]);
+        au[r] = fmaf(uf[q], xf[q], au[r]);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    for (int off = 32; off > 0; off >>= 1) {
+      ag[r] += __shfl_xor(ag[r], off);
+      au[r] += __shfl_xor(au[r], off);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+    if (lane == r && i0 + r < I) store_elem(arow + i0 + r, silu(ag[r]) * au[r]);
+}
+
+// ---------------------------------------------------------------------------
+// Kernel B: out[t, h] = sum_k w[t,k] * dot(W2[s_k][h, :], act[t,k,:]).
+// Block = K waves, wave k computes the dot products of expert k for the
+// 64/LPR rows of this block (LPR lanes per row, CH chunks per lane, or a
+// runtime chunk loop when CH == 0); the partials meet in LDS and one lane
+// per row sums them in routing order.
+// grid = (ceil(H / (64 / LPR)), T).
+// ---------------------------------------------------------------------------
+constexpr int kMaxKw2 = 16;
+
+template <typename T, int LPR, int CH>
+__global__ __launch_bounds__(1024) void w2_combine_kernel(const T* __restrict__ act, int H, int I,
+                                                           int K, const float* __restrict__ topk_w,
+                                                           const int32_t* __restrict__ slots,
+                                                           const T* __restrict__ w2,
+                                                           size_t w2_stride,
+                                                           T* __restrict__ out) {
+  constexpr int V = Vec<T>::N;
+  constexpr int RPW = 64 / LPR;
+  __shared__ float part[kMaxKw2][RPW];
+  const int k = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int sub = lane / LPR, l = lane % LPR;
+  const int t = blockIdx.y;
+  const int h = blockIdx.x * RPW + sub;
+  const int s = slots[t * K + k];
+  const int nch = I / V;
+  float d = 0.f;
+  if (s >= 0 && h < H) {
+    const T* wrow = w2 + (size_t)s * w2_stride + (size_t)h * I;
+    const T* arow = act + ((size_t)t * K + k) * I;
+    if (CH > 0) {
+      uint4 wv[CH > 0 ? CH : 1], av[CH > 0 ? CH : 1];
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        const int ch = c * LPR + l;
+        if (ch < nch) {
+          wv[c] = ld16(wrow + (size_t)ch * V);
+          av[c] = ld16(arow + (size_t)ch * V);
+        } else {
+          wv[c] = make_uint4(0, 0, 0, 0);
+          av[c] = make_uint4(0, 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        float wf[V], af[V];
+        Vec<T>::unpack(wv[c], wf);
+        Vec<T>::unpack(av[c], af);
+#pragma unroll
+        for (int q = 0; q < V; ++q) d = fmaf(wf[q], af[q], d);
+      }
+    } else {
+#pragma unroll 4
+      for (int ch = l; ch < nch; ch += LPR) {
+        float wf[V], af[V];
+        Vec<T>::unpack(ld16(wrow + (size_t)ch * V), wf);
+        Vec<T>::unpack(ld16(arow + (size_t)ch * V), af);
+#pragma unroll
+        for (int q = 0; q < V; ++q) d = fmaf(wf[q], af[q], d);
+      }
+    }
+  }
+  for (int off = LPR / 2; off > 0; off >>= 1) d += __shfl_xor(d, off);
+  if (l == 0) part[k][sub] = d;
+  __syncthreads();
+  if (threadIdx.x < RPW) {
+    const int r = threadIdx.x;
+    const int hh = blockIdx.x * RPW + r;
+    if (hh < H) {
+      float acc = 0.f;
+      for (int kk = 0; kk < K; ++kk) {
+        if (slots[t * K + kk] < 0) continue;
+        acc = fmaf(topk_w[t * K + kk], part[kk][r], acc);
+      }
+      store_elem(out + (size_t)t * H + hh, acc);
+    }
+  }
+}
+
+template <typename T, int CH>
+void launch_w13(const T* x, int T_, int H, int I, int K, const int32_t* slots, const T* w13,
+                size_t w13_stride, T* act, hipStream_t st) {
+  constexpr int RW = 2;
+  dim3 grid((I + 4 * RW - 1) / (4 * RW), T_ * K);
+  hipLaunchKernelGGL((w13_silu_kernel<T, CH, RW>), grid, dim3(256), 0, st, x, H, I, K, slots,
+                     w13, w13_stride, act);
+}
+
+template <typename T>
+int dispatch_w13(const T* x, int T_, int H, int I, int K, const int32_t* slots, const T* w13,
+                 size_t w13_stride, T* act, hipStream_t st) {
+  const int nch = H / Vec<T>::N;
+  const int ch = (nch + 63) / 64;
+  switch (ch) {
+    case 1: launch_w13<T, 1>(x, T_, H, I, K, slots, w13, w13_stride, act, st); break;
+    case 2: launch_w13<T, 2>(x, T_, H, I, K, slots, w13, w13_stride, act, st); break;
+    case 3: launch_w13<T, 3>(x, T_, H, I, K, slots, w13, w13_stride, act, st); break;
+    case 4: launch_w13<T, 4>(x, T_, H, I, K, slots, w13, w13_stride, act, st); break;
+    case 5: case 6: launch_w13<T, 6>(x, T_, H, I, K, slots, w13, w13_stride, act, st); break;
+    case 7: case 8: launch_w13<T, 8>(x, T_, H, I, K, slots, w13, w13_stride, act, st); break;
+    default: return WISP_ERR_UNSUPPORTED;
+  }
+  return WISP_OK;
+}
+
+template <typename T, int LPR, int CH>
+void launch_w2(const T* act, int T_, int H, int I, int K, const float* w, const int32_t* slots,
+               const T* w2, size_t w2_stride, T* out, hipStream_t st) {
+  constexpr int RPW = 64 / LPR;
+  dim3 grid((H + RPW - 1) / RPW, T_);
+  hipLaunchKernelGGL((w2_combine_kernel<T, LPR, CH>), grid, dim3(64 * K), 0, st, act, H, I, K, w,
+                     slots, w2, w2_stride, out);
+}
+
+template <typename T>
+int dispatch_w2(const T* act, int T_, int H, int I, int K, const float* w, const int32_t* slots,
+                const T* w2, size_t w2_stride, T* out, hipStream_t st) {
+  if (K > kMaxKw2) return WISP_ERR_UNSUPPORTED;
+  const int nch = I / Vec<T>::N;
+  if (nch <= 32 * 4) {  // half a wave per row, up to 4 chunks per lane
+    switch ((nch + 31) / 32) {
+      case 1: launch_w2<T, 32, 1>(act, T_, H, I, K, w, slots, w2, w2_stride, out, st); break;
+      case 2: launch_w2<T, 32, 2>(act, T_, H, I, K, w, slots, w2, w2_stride, out, st); break;
+      case 3: launch_w2<T, 32, 3>(act, T_, H, I, K, w, slots, w2, w2_stride, out, st); break;
+      default: launch_w2<T, 32, 4>(act, T_, H, I, K, w, slots, w2, w2_stride, out, st); break;
+    }
+  } else {
+    launch_w2<T, 64, 0>(act, T_, H, I, K, w, slots, w2, w2_stride, out, st);
+  }
+  return WISP_OK;
+}
+
+}  // namespace
+
+int experts_gemv(const void* x, int dtype, int T_, int H, int I, int K, const float* topk_w,
+                 const int32_t* slots, const void* w13, size_t w13_stride, const void* w2,
+                 size_t w2_stride, void* act, void* out, hipStream_t st, hipEvent_t ev_mid) {
+  if (T_ == 0) return WISP_OK;
+  int rc;
+  if (dtype == WISP_F32) {
+    rc = dispatch_w13<float>((const float*)x, T_, H, I, K, slots, (const float*)w13, w13_stride,
+                             (float*)act, st);
+    if (rc == WISP_OK && ev_mid) WISP_HIP_TRY(hipEventRecord(ev_mid, st));
+    if (rc == WISP_OK)
+      rc = dispatch_w2<float>((const float*)act, T_, H, I, K, topk_w, slots, (const float*)w2,
+                              w2_stride, (float*)out, st);
+  } else {
+    rc = dispatch_w13<uint16_t>((const uint16_t*)x, T_, H, I, K, slots, (const uint16_t*)w13,
+                                w13_stride, (uint16_t*)act, st);
+    if (rc == WISP_OK && ev_mid) WISP_HIP_TRY(hipEventRecord(ev_mid, st));
+    if (rc == WISP_OK)
+      rc = dispatch_w2<uint16_t>((const uint16_t*)act, T_, H, I, K, topk_w, slots,
+                                 (const uint16_t*)w2, w2_stride, (uint16_t*)out, st);
+  }
+  if (rc != WISP_OK) {
+    wisp_set_last_error("shape outside the GEMV kernels' coverage", "wisp_moe_experts");
+    return rc;
+  }
+  WISP_HIP_TRY(hipGetLastError());
+  return WISP_OK;
+}
+
+}  // namespace wisp

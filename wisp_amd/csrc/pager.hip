@@ -1,0 +1,505 @@
+// Expert pager: host (sequential) and device (one wavefront) implementations.
+//
+// Semantics follow the reference pager, src/wisp/integrations/vllm/fused_moe.py:
+//   * grouping: greedy first-fit over tokens in index order, a token joins
+//     the open group iff the union of routed experts stays <= cap or the
+//     group is empty (1119-1140; when the whole batch fits this is the single
+//     fast-path call at 1102-1118);
+//   * per group (ensure_resident, 264-358): needed = sorted unique ids; the
+//     missing experts in CPython set order; hits += |needed| - |missing|;
+//     all-hit -> clock += 1 and touch; else free slots ascending, eviction
+//     candidates = occupied slots whose expert is not needed, stable-sorted by
+//     tick; evict the first (missing - free) of them, appending each freed
+//     slot; clock += 1; each missing expert takes free.pop() (from the end);
+//     finally every needed expert's slot gets tick = clock;
+//   * a group needing more slots than cap -> WISP_ERR_SUBBATCH (the
+//     reference's "sub-batch" RuntimeError, 315-327), after hits were counted;
+//   * forward counter += 1 per layer call (1017), not per group.
+#include <algorithm>
+#include <vector>
+
+#include "common.h"
+#include "pager_core.h"
+
+namespace wisp {
+
+// ---------------------------------------------------------------------------
+// Host implementation (the specification the device kernel is checked against)
+// ---------------------------------------------------------------------------
+
+namespace {
+
+struct HostRecord {
+  int32_t* w;
+  RecordLayout L;
+  int ev = 0, ld = 0;
+};
+
+// One ensure_resident call on `needed` (ascending unique ids).
+int ensure_group_host(PagerView& st, const std::vector<int32_t>& needed, HostRecord& R,
+                      int g, int t0, int t1) {
+  const int U = (int)needed.size();
+  std::vector<int32_t> order(U > 0 ? U : 1), table(kMaxSetTable);
+  if (cpython_set_order(needed.data(), U, order.data(), table.data(), kMaxSetTable) != U)
+    return WISP_ERR_INVALID;
+  std::vector<char> is_needed(st.E, 0);
+  for (int e : needed) is_needed[e] = 1;
+
+  std::vector<int32_t> missing;
+  for (int j = 0; j < U; ++j)
+    if (st.map[order[j]] < 0) missing.push_back(order[j]);
+  const int hits = U - (int)missing.size();
+  st.ctr[kHits] += hits;
+
+  int32_t* G = R.w + R.L.group_base(g);
+  G[0] = t0; G[1] = t1; G[2] = U; G[3] = hits;
+  G[4] = R.ev; G[5] = 0; G[6] = R.ld; G[7] = 0;
+
+  if (missing.empty()) {
+    st.ctr[kClock] += 1;
+    for (int e : needed) st.tick[st.map[e]] = st.ctr[kClock];
+    return WISP_OK;
+  }
+
+  std::vector<int32_t> free_slots;
+  std::vector<std::pair<int64_t, int32_t>> cand;
+  for (int s = 0; s < st.cap; ++s) {
+    if (st.s2e[s] < 0) free_slots.push_back(s);
+    else if (!is_needed[st.s2e[s]]) cand.emplace_back(st.tick[s], s);
+  }
+  std::stable_sort(cand.begin(), cand.end(),
+                   [](const std::pair<int64_t, int32_t>& a, const std::pair<int64_t, int32_t>& b) {
+                     return a.first < b.first;
+                   });
+  const int shortfall = (int)missing.size() - (int)free_slots.size();
+  if (shortfall > 0) {
+    if (shortfall > (int)cand.size()) {
+      R.w[kRecFailGroup] = g;
+      R.w[kRecFailUnique] = U;
+      return WISP_ERR_SUBBATCH;
+    }
+    for (int r = 0; r < shortfall; ++r) {
+      const int s = cand[r].second;
+      const int victim = st.s2e[s];
+      st.map[victim] = -1;
+      st.s2e[s] = -1;
+      free_slots.push_back(s);
+      st.ctr[kEvict] += 1;
+      R.w[R.L.evicted_base() + 2 * R.ev] = victim;
+      R.w[R.L.evicted_base() + 2 * R.ev + 1] = s;
+      ++R.ev;
+      ++G[5];
+    }
+  }
+  st.ctr[kClock] += 1;
+  const int64_t clock = st.ctr[kClock];
+  for (int e : missing) {
+    const int s = free_slots.back();
+    free_slots.pop_back();
+    st.s2e[s] = e;
+    st.map[e] = s;
+    st.tick[s] = clock;
+    st.ctr[kMiss] += 1;
+    R.w[R.L.loaded_base() + 2 * R.ld] = e;
+    R.w[R.L.loaded_base() + 2 * R.ld + 1] = s;
+    ++R.ld;
+    ++G[7];
+  }
+  for (int e : needed) st.tick[st.map[e]] = clock;
+  return WISP_OK;
+}
+
+}  // namespace
+
+int pager_decide_host(PagerView st, const int32_t* ids, int T, int K, int single_group,
+                      int32_t* slots, int32_t* rec, int rec_words) {
+  RecordLayout L(T, K);
+  if (T < 0 || K < 1 || st.E < 1 || st.E > kMaxExperts || st.cap < 1 || st.cap > st.E ||
+      rec_words < L.words())
+    return WISP_ERR_INVALID;
+  for (int w = 0; w < 8; ++w) rec[w] = 0;
+  rec[kRecFailGroup] = -1;
+  const int P = T * K;
+  for (int p = 0; p < P; ++p) {
+    if (ids[p] < 0 || ids[p] >= st.E) {
+      rec[kRecStatus] = WISP_ERR_INVALID;
+      return WISP_ERR_INVALID;
+    }
+  }
+  if (!single_group) st.ctr[kForward] += 1;
+
+  // Plan the groups (contiguous token ranges).
+  std::vector<int> ends;
+  if (single_group) {
+    ends.push_back(T);
+  } else {
+    std::vector<char> cur(st.E, 0);
+    int cnt = 0, start = 0;
+    for (int t = 0; t < T; ++t) {
+      int nnew = 0;
+      std::vector<int> fresh;
+      for (int j = 0; j < K; ++j) {
+        const int e = ids[t * K + j];
+        if (!cur[e] && std::find(fresh.begin(), fresh.end(), e) == fresh.end()) {
+          fresh.push_back(e);
+          ++nnew;
+        }
+      }
+      if (cnt + nnew <= st.cap || t == start) {
+        for (int e : fresh) cur[e] = 1;
+        cnt += nnew;
+      } else {
+        ends.push_back(t);
+        std::fill(cur.begin(), cur.end(), 0);
+        start = t;
+        cnt = 0;
+        for (int j = 0; j < K; ++j) {
+          const int e = ids[t * K + j];
+          if (!cur[e]) { cur[e] = 1; ++cnt; }
+        }
+      }
+    }
+    ends.push_back(T);
+  }
+  rec[kRecGroupsPlanned] = (int)ends.size();
+
+  HostRecord R{rec, L};
+  int t0 = 0, status = WISP_OK;
+  for (int g = 0; g < (int)ends.size(); ++g) {
+    const int t1 = ends[g];
+    std::vector<char> mark(st.E, 0);
+    for (int p = t0 * K; p < t1 * K; ++p) mark[ids[p]] = 1;
+    std::vector<int32_t> needed;
+    for (int e = 0; e < st.E; ++e)
+      if (mark[e]) needed.push_back(e);
+    status = ensure_group_host(st, needed, R, g, t0, t1);
+    if (status != WISP_OK) break;
+    if (slots)
+      for (int p = t0 * K; p < t1 * K; ++p) slots[p] = st.map[ids[p]];
+    rec[kRecGroupsDone] = g + 1;
+    t0 = t1;
+  }
+  rec[kRecEvicted] = R.ev;
+  rec[kRecLoaded] = R.ld;
+  rec[kRecStatus] = status;
+  return status;
+}
+
+// ---------------------------------------------------------------------------
+// Device implementation: one wavefront, state staged in LDS.
+// ---------------------------------------------------------------------------
+
+namespace {
+
+__device__ inline int popc_below(uint64_t mask) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                   __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
+__device__ inline uint64_t ballot(bool p) { return __ballot(p); }
+
+struct PagerSmem {
+  int32_t map[kMaxExperts];
+  int32_t s2e[kMaxExperts];
+  int64_t tick[kMaxExperts];
+  uint32_t need[kMaxExperts / 32];
+  int32_t keys[kMaxExperts];
+  int32_t order[kMaxExperts];
+  int32_t table[kMaxSetTable];
+  int32_t missing[kMaxExperts];
+  int32_t freel[kMaxExperts];
+  int32_t cand[kMaxExperts];
+  int32_t sorted[kMaxExperts];
+};
+
+__global__ __launch_bounds__(64) void pager_kernel(
+    const int32_t* __restrict__ ids, int T, int K, int E, int cap, int single_group,
+    int32_t* __restrict__ map_g, int32_t* __restrict__ s2e_g, int64_t* __restrict__ tick_g,
+    int64_t* __restrict__ ctr_g, int32_t* __restrict__ slots_g, int32_t* __restrict__ rec) {
+  __shared__ PagerSmem sm;
+  const int lane = threadIdx.x;
+  const int nwords = (E + 31) >> 5;
+  const RecordLayout L(T, K);
+  const int P = T * K;
+
+  for (int e = lane; e < E; e += 64) sm.map[e] = map_g[e];
+  for (int s = lane; s < cap; s += 64) {
+    sm.s2e[s] = s2e_g[s];
+    sm.tick[s] = tick_g[s];
+  }
+  int64_t clock = ctr_g[kClock];
+  int64_t n_forward = ctr_g[kForward], n_miss = ctr_g[kMiss], n_evict = ctr_g[kEvict],
+          n_hits = ctr_g[kHits];
+
+  // Validate ids.
+  bool bad = false;
+  for (int p = lane; p < P; p += 64) bad |= (ids[p] < 0 || ids[p] >= E);
+  const bool any_bad = ballot(bad) != 0;
+
+  int status = WISP_OK, groups_done = 0, groups_planned = 0, fail_group = -1, fail_u = 0;
+  int ev_total = 0, ld_total = 0;
+
+  if (any_bad) {
+    status = WISP_ERR_INVALID;
+  } else {
+    if (!single_group) n_forward += 1;
+    int start = 0;
+    bool first = true;
+    while (first || start < T) {
+      first = false;
+      // ---- plan one group: tokens [start, end) -----------------------
+      for (int w = lane; w < nwords; w += 64) sm.need[w] = 0u;
+      __syncthreads();
+      int end = start, cnt = 0;
+      if (single_group) {
+        for (int p = lane; p < P; p += 64) {
+          const int e = ids[p];
+          atomicOr(&sm.need[e >> 5], 1u << (e & 31));
+        }
+        end = T;
+      } else {
+        while (end < T) {
+          bool fresh = false;
+          int e = 0;
+          if (lane < K) {
+            e = ids[end * K + lane];
+            const uint32_t old = atomicOr(&sm.need[e >> 5], 1u << (e & 31));
+            fresh = !(old & (1u << (e & 31)));
+          }
+          const uint64_t fb = ballot(fresh);
+          const int nnew = __popcll(fb);
+          if (cnt + nnew <= cap || end == start) {
+            cnt += nnew;
+            ++end;
+          } else {
+            if (fresh) atomicAnd(&sm.need[e >> 5], ~(1u << (e & 31)));
+            break;
+          }
+        }
+      }
+      __syncthreads();
+      const int g = groups_planned++;
+      const int t0 = start, t1 = end;
+      start = end;
+
+      // ---- sorted unique ids of the group ----------------------------
+      if (lane == 0) {
+        int u = 0;
+        for (int w = 0; w < nwords; ++w) {
+          uint32_t bits = sm.need[w];
+          while (bits) {
+            const int b = __builtin_ctz(bits);
+            bits &= bits - 1;
+            sm.keys[u++] = (w << 5) + b;
+          }
+        }
+        // CPython set iteration order of the ascending keys.
+        cpython_set_order(sm.keys, u, sm.order, sm.table, kMaxSetTable);
+      }
+      int U = 0;
+      for (int w = lane; w < nwords; w += 64) U += __popc(sm.need[w]);
+      for (int off = 32; off > 0; off >>= 1) U += __shfl_xor(U, off);
+      __syncthreads();
+
+      // ---- missing experts, in set order -----------------------------
+      int nmiss = 0;
+      for (int base = 0; base < U; base += 64) {
+        const int j = base + lane;
+        int e = -1;
+        bool m = false;
+        if (j < U) {
+          e = sm.order[j];
+          m = sm.map[e] < 0;
+        }
+        const uint64_t mb = ballot(m);
+        if (m) sm.missing[nmiss + popc_below(mb)] = e;
+        nmiss += __popcll(mb);
+      }
+      const int hits = U - nmiss;
+      n_hits += hits;
+      const int gb = L.group_base(g);
+      if (lane == 0) {
+        rec[gb + 0] = t0; rec[gb + 1] = t1; rec[gb + 2] = U; rec[gb + 3] = hits;
+        rec[gb + 4] = ev_total; rec[gb + 5] = 0; rec[gb + 6] = ld_total; rec[gb + 7] = 0;
+      }
+      __syncthreads();
+
+      if (nmiss > 0) {
+        // ---- free slots and eviction candidates, ascending slot --------
+        int nfree = 0, ncand = 0;
+        for (int base = 0; base < cap; base += 64) {
+          const int s = base + lane;
+          bool f = false, c = false;
+          if (s < cap) {
+            const int cur = sm.s2e[s];
+            f = cur < 0;
+            c = cur >= 0 && !(sm.need[cur >> 5] & (1u << (cur & 31)));
+          }
+          const uint64_t fbits = ballot(f), cbits = ballot(c);
+          if (f) sm.freel[nfree + popc_below(fbits)] = s;
+          if (c) sm.cand[ncand + popc_below(cbits)] = s;
+          nfree += __popcll(fbits);
+          ncand += __popcll(cbits);
+        }
+        __syncthreads();
+        const int shortfall = nmiss - nfree;
+        if (shortfall > ncand) {
+          status = WISP_ERR_SUBBATCH;
+          fail_group = g;
+          fail_u = U;
+          break;
+        }
+        if (shortfall > 0) {
+          // Stable sort of the candidates by tick (ties keep slot order).
+          for (int i = lane; i < ncand; i += 64) {
+            const int64_t ti = sm.tick[sm.cand[i]];
+            int r = 0;
+            for (int j = 0; j < ncand; ++j) {
+              const int64_t tj = sm.tick[sm.cand[j]];
+              r += (tj < ti) || (tj == ti && j < i);
+            }
+            sm.sorted[r] = sm.cand[i];
+          }
+          __syncthreads();
+          for (int r = lane; r < shortfall; r += 64) {
+            const int s = sm.sorted[r];
+            const int victim = sm.s2e[s];
+            sm.map[victim] = -1;
+            sm.s2e[s] = -1;
+            sm.freel[nfree + r] = s;
+            const int o = L.evicted_base() + 2 * (ev_total + r);
+            rec[o] = victim;
+            rec[o + 1] = s;
+          }
+          n_evict += shortfall;
+          ev_total += shortfall;
+          nfree += shortfall;
+          if (lane == 0) rec[gb + 5] = shortfall;
+          __syncthreads();
+        }
+        clock += 1;
+        for (int j = lane; j < nmiss; j += 64) {
+          const int s = sm.freel[nfree - 1 - j];
+          const int e = sm.missing[j];
+          sm.s2e[s] = e;
+          sm.map[e] = s;
+          sm.tick[s] = clock;
+          const int o = L.loaded_base() + 2 * (ld_total + j);
+          rec[o] = e;
+          rec[o + 1] = s;
+        }
+        n_miss += nmiss;
+        ld_total += nmiss;
+        if (lane == 0) rec[gb + 7] = nmiss;
+        __syncthreads();
+      } else {
+        clock += 1;
+      }
+      for (int j = lane; j < U; j += 64) sm.tick[sm.map[sm.keys[j]]] = clock;
+      __syncthreads();
+      if (slots_g)
+        for (int p = t0 * K + lane; p < t1 * K; p += 64) slots_g[p] = sm.map[ids[p]];
+      groups_done = g + 1;
+      __syncthreads();
+    }
+  }
+
+  for (int e = lane; e < E; e += 64) map_g[e] = sm.map[e];
+  for (int s = lane; s < cap; s += 64) {
+    s2e_g[s] = sm.s2e[s];
+    tick_g[s] = sm.tick[s];
+  }
+  if (lane == 0) {
+    ctr_g[kClock] = clock;
+    ctr_g[kForward] = n_forward;
+    ctr_g[kMiss] = n_miss;
+    ctr_g[kEvict] = n_evict;
+    ctr_g[kHits] = n_hits;
+    rec[kRecGroupsDone] = groups_done;
+    rec[kRecGroupsPlanned] = groups_planned;
+    rec[kRecFailGroup] = fail_group;
+    rec[kRecFailUnique] = fail_u;
+    rec[kRecEvicted] = ev_total;
+    rec[kRecLoaded] = ld_total;
+    rec[7] = 0;
+    rec[kRecStatus] = status;
+  }
+}
+
+}  // namespace
+
+int launch_pager(const int32_t* ids, int T, int K, int E, int cap, int single_group,
+                 int32_t* map, int32_t* s2e, int64_t* tick, int64_t* ctr, int32_t* slots,
+                 int32_t* rec, int rec_words, hipStream_t stream) {
+  RecordLayout L(T, K);
+  if (T < 0 || K < 1 || K > kMaxTopK || E < 1 || E > kMaxExperts || cap < 1 || cap > E ||
+      rec_words < L.words() || !map || !s2e || !tick || !ctr || !rec || (T > 0 && !ids)) {
+    wisp_set_last_error("invalid pager arguments", "wisp_pager_decide");
+    return WISP_ERR_INVALID;
+  }
+  hipLaunchKernelGGL(pager_kernel, dim3(1), dim3(64), 0, stream, ids, T, K, E, cap,
+                     single_group, map, s2e, tick, ctr, slots, rec);
+  WISP_HIP_TRY(hipGetLastError());
+  return WISP_OK;
+}
+
+}  // namespace wisp
+
+extern "C" int wisp_pager_decide(const int32_t* topk_ids, int T, int K, int E, int cap,
+                                 int single_group, int32_t* expert_map,
+                                 int32_t* slot_to_expert, int64_t* lru_tick,
+                                 int64_t* counters, int32_t* slots, int32_t* record,
+                                 int record_words, wisp_stream_t stream) {
+  return wisp::launch_pager(topk_ids, T, K, E, cap, single_group, expert_map, slot_to_expert,
+                            lru_tick, counters, slots, record, record_words,
+                            (hipStream_t)stream);
+}
+
+extern "C" int wisp_pager_decide_host(const int32_t* topk_ids, int T, int K, int E, int cap,
+                                      int single_group, int32_t* expert_map,
+                                      int32_t* slot_to_expert, int64_t* lru_tick,
+                                      int64_t* counters, int32_t* slots, int32_t* record,
+                                      int record_words) {
+  wisp::PagerView st{E, cap, expert_map, slot_to_expert, lru_tick, counters};
+  return wisp::pager_decide_host(st, topk_ids, T, K, single_group, slots, record,
+                                 record_words);
+}
+
+extern "C" int wisp_cpython_set_order(const int32_t* keys, int n, int32_t* order) {
+  if (n < 0 || n > wisp::kMaxExperts) return -1;
+  std::vector<int32_t> table(wisp::kMaxSetTable);
+  return wisp::cpython_set_order(keys, n, order, table.data(), wisp::kMaxSetTable);
+}
+
+extern "C" int wisp_subbatch_plan(const int32_t* topk_ids, int T, int K, int cap,
+                                  int32_t* group_end) {
+  if (T < 0 || K < 1 || cap < 1) return -1;
+  int ng = 0, cnt = 0, start = 0;
+  std::vector<int32_t> cur;  // current group's distinct experts
+  for (int t = 0; t < T; ++t) {
+    std::vector<int32_t> fresh;
+    for (int j = 0; j < K; ++j) {
+      const int32_t e = topk_ids[t * K + j];
+      if (std::find(cur.begin(), cur.end(), e) == cur.end() &&
+          std::find(fresh.begin(), fresh.end(), e) == fresh.end())
+        fresh.push_back(e);
+    }
+    if (cnt + (int)fresh.size() <= cap || t == start) {
+      cur.insert(cur.end(), fresh.begin(), fresh.end());
+      cnt += (int)fresh.size();
+    } else {
+      group_end[ng++] = t;
+      start = t;
+      cur.clear();
+      for (int j = 0; j < K; ++j) {
+        const int32_t e = topk_ids[t * K + j];
+        if (std::find(cur.begin(), cur.end(), e) == cur.end()) cur.push_back(e);
+      }
+      cnt = (int)cur.size();
+    }
+  }
+  group_end[ng++] = T;
+  return ng;
+}
+
+extern "C" int wisp_record_words(int T, int K) { return wisp::RecordLayout(T, K).words(); }

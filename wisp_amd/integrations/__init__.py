@@ -1,0 +1,1 @@
+"""Framework integrations of the paged fused-MoE layer."""
