@@ -159,6 +159,15 @@ def main() -> int:
     a13 = w13_bytes / t13 / 1e9 if t13 > 0 else 0.0
     agemm = (w13_bytes + w2_bytes) / (t13 + t2) / 1e9 if t13 + t2 > 0 else 0.0
 
+    # A plain 256 MiB device copy: the calibration dispatch for the profiler's
+    # HBM byte counters (FETCH_SIZE / WRITE_SIZE of a copy of known size).
+    cal = torch.empty(2, 256 << 20, dtype=torch.uint8, device=dev)
+    from wisp_amd import _lib
+    _lib.check(_lib.lib().wisp_probe_hbm_copy(cal[1].data_ptr(), cal[0].data_ptr(), 256 << 20,
+                                              _lib.stream_handle()), "hbm copy")
+    torch.cuda.synchronize()
+    del cal
+
     link = h2d_link(sh.expert_bytes)
     link_big = h2d_link(256 << 20, iters=8)
     pin_gbps = pin_bytes / (pin_ms * 1e-3) / 1e9 if pin_ms > 0 else 0.0

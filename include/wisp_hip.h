@@ -130,7 +130,11 @@ int wisp_moe_experts(const void* x, int dtype, int T, int H, int I, int K,
 /* ---- group 3: the layer call --------------------------------------- */
 
 typedef struct wisp_layer_desc {
-  int num_experts, cap, hidden, inter, dtype, mode;
+  int num_experts, cap;
+  int hidden, inter;             /* expert MLP shape; 0 for a pager-only
+                                    state (the forward call then fails)  */
+  int dtype, mode;
+  size_t w13_elems, w2_elems;    /* elements of one expert's w13 / w2    */
   void* scratch_w13;             /* device, slot s at +s*stride [2I, H]  */
   size_t scratch_w13_stride;     /* elements                             */
   void* scratch_w2;              /* device, slot s at +s*stride [H, I]   */

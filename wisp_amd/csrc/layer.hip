@@ -113,8 +113,8 @@ __global__ void identity_kernel(int32_t* map, int32_t* s2e, int64_t* tick, int E
 // Copies of `n` loaded (expert, slot) pairs.
 int issue_copies(Layer& L, const int32_t* pairs, int n, hipStream_t cs, double* bytes) {
   const size_t es = L.es;
-  const size_t w13_bytes = (size_t)2 * L.d.inter * L.d.hidden * es;
-  const size_t w2_bytes = (size_t)L.d.hidden * L.d.inter * es;
+  const size_t w13_bytes = L.d.w13_elems * es;
+  const size_t w2_bytes = L.d.w2_elems * es;
   for (int j = 0; j < n; ++j) {
     const int e = pairs[2 * j], s = pairs[2 * j + 1];
     if (e < 0 || e >= L.d.num_experts || s < 0 || s >= L.d.cap) {
@@ -247,30 +247,24 @@ extern "C" int wisp_layer_create(const wisp_layer_desc* desc, void** handle) {
   if (!desc || !handle) return WISP_ERR_INVALID;
   const wisp_layer_desc& d = *desc;
   if (d.num_experts < 1 || d.num_experts > kMaxExperts || d.cap < 1 || d.cap > d.num_experts ||
-      d.hidden < 1 ||
-      d.inter < 1 || (d.dtype != WISP_F32 && d.dtype != WISP_BF16) ||
+      d.hidden < 0 || d.inter < 0 || d.w13_elems < 1 || d.w2_elems < 1 ||
+      (d.hidden > 0 && (d.w13_elems != (size_t)2 * d.inter * d.hidden ||
+                        d.w2_elems != (size_t)d.hidden * d.inter)) ||
+      (d.dtype != WISP_F32 && d.dtype != WISP_BF16) ||
       (d.mode != WISP_MODE_PAGED && d.mode != WISP_MODE_RESIDENT) || !d.scratch_w13 ||
       !d.scratch_w2 || !d.master_w13 || !d.master_w2 || !d.expert_map || !d.slot_to_expert ||
-      !d.lru_tick || !d.counters || d.scratch_w13_stride < (size_t)2 * d.inter * d.hidden ||
-      d.scratch_w2_stride < (size_t)d.hidden * d.inter ||
-      d.master_w13_stride < (size_t)2 * d.inter * d.hidden ||
-      d.master_w2_stride < (size_t)d.hidden * d.inter ||
+      !d.lru_tick || !d.counters || d.scratch_w13_stride < d.w13_elems ||
+      d.scratch_w2_stride < d.w2_elems || d.master_w13_stride < d.w13_elems ||
+      d.master_w2_stride < d.w2_elems ||
       (d.mode == WISP_MODE_RESIDENT && d.cap != d.num_experts)) {
     wisp_set_last_error("invalid layer descriptor", "wisp_layer_create");
     return WISP_ERR_INVALID;
   }
   const size_t es = elem_size(d.dtype);
-  if ((d.scratch_w13_stride * es) % 16 || (d.scratch_w2_stride * es) % 16 ||
-      ((uintptr_t)d.scratch_w13) % 16 || ((uintptr_t)d.scratch_w2) % 16 ||
-      (d.hidden * es) % 16 || (d.inter * es) % 16) {
-    wisp_set_last_error("weights must be 16-byte aligned (H, I multiples of 16 bytes)",
-                        "wisp_layer_create");
-    return WISP_ERR_UNSUPPORTED;
-  }
   Layer* L = new Layer();
   L->d = d;
   L->es = es;
-  const size_t w13_elems = (size_t)2 * d.inter * d.hidden;
+  const size_t w13_elems = d.w13_elems;
   L->fused_slab = d.master_w13_stride == d.master_w2_stride &&
                   d.scratch_w13_stride == d.scratch_w2_stride &&
                   (const char*)d.master_w2 == (const char*)d.master_w13 + w13_elems * es &&
@@ -319,7 +313,7 @@ extern "C" int wisp_layer_set_scratch(void* handle, void* scratch_w13, void* scr
     return WISP_ERR_INVALID;
   (void)hipStreamSynchronize(L->copy_stream);
   L->pin_pending = false;
-  const size_t es = L->es, w13_elems = (size_t)2 * L->d.inter * L->d.hidden;
+  const size_t es = L->es, w13_elems = L->d.w13_elems;
   L->d.scratch_w13 = scratch_w13;
   L->d.scratch_w2 = scratch_w2;
   L->fused_slab = L->d.master_w13_stride == L->d.master_w2_stride &&
@@ -346,6 +340,16 @@ extern "C" int wisp_layer_forward(void* handle, const void* x, const void* logit
   if (rc != WISP_OK) return rc;
   hipStream_t st = (hipStream_t)stream;
   const wisp_layer_desc& d = L->d;
+  const size_t es = L->es;
+  if (d.hidden < 1 || d.inter < 1 || (d.hidden * es) % 16 || (d.inter * es) % 16 ||
+      (d.scratch_w13_stride * es) % 16 || (d.scratch_w2_stride * es) % 16 ||
+      ((uintptr_t)d.scratch_w13) % 16 || ((uintptr_t)d.scratch_w2) % 16 ||
+      (T > 0 && (((uintptr_t)x) % 16 || ((uintptr_t)out) % 16))) {
+    wisp_set_last_error("expert shape/alignment outside the kernels' coverage (H and I must "
+                        "be multiples of 16 bytes, buffers 16-byte aligned)",
+                        "wisp_layer_forward");
+    return WISP_ERR_UNSUPPORTED;
+  }
   const int a = choose_algo(algo, d.dtype, T);
   if (a == WISP_ALGO_MFMA && d.dtype != WISP_BF16) return WISP_ERR_UNSUPPORTED;
 
@@ -510,8 +514,11 @@ extern "C" int wisp_moe_experts(const void* x, int dtype, int T, int H, int I, i
     return WISP_ERR_INVALID;
   const size_t es = elem_size(dtype);
   if ((H * es) % 16 || (I * es) % 16 || (w13_stride * es) % 16 || (w2_stride * es) % 16 ||
-      ((uintptr_t)w13) % 16 || ((uintptr_t)w2) % 16)
+      ((uintptr_t)w13) % 16 || ((uintptr_t)w2) % 16 ||
+      (T > 0 && (((uintptr_t)x) % 16 || ((uintptr_t)act) % 16 || ((uintptr_t)out) % 16))) {
+    wisp_set_last_error("H, I and buffers must be 16-byte aligned", "wisp_moe_experts");
     return WISP_ERR_UNSUPPORTED;
+  }
   const int a = choose_algo(algo, dtype, T);
   if (a == WISP_ALGO_MFMA) {
     if (dtype != WISP_BF16) return WISP_ERR_UNSUPPORTED;

@@ -82,12 +82,11 @@ def _resolve_cap_experts(num_experts: int) -> int:
 _DTYPES = {torch.float32: _lib.WISP_F32, torch.bfloat16: _lib.WISP_BF16}
 
 
-def _check_master(t: torch.Tensor, rows: int, cols: int, name: str) -> None:
+def _check_master(t: torch.Tensor, name: str) -> None:
     if t.device.type != "cpu":
         raise ValueError(f"{name} must live in host memory")
-    if t.dim() != 3 or t.shape[1] != rows or t.shape[2] != cols or t.stride(2) != 1 \
-            or t.stride(1) != cols:
-        raise ValueError(f"{name} must be [E, {rows}, {cols}] with contiguous rows")
+    if t.dim() != 3 or t.stride(2) != 1 or t.stride(1) != t.shape[2]:
+        raise ValueError(f"{name} must be [E, rows, cols] with each expert contiguous")
 
 
 class _Workspace:
@@ -137,31 +136,40 @@ class WispMoEState:
         if cpu_w13.dtype not in _DTYPES or cpu_w2.dtype != cpu_w13.dtype:
             raise NotImplementedError(f"wisp: expert dtype {cpu_w13.dtype} not supported "
                                       "(float32 and bfloat16 are)")
+        _check_master(cpu_w13, "cpu_w13")
+        _check_master(cpu_w2, "cpu_w2")
         E, two_i, H = cpu_w13.shape
-        I = two_i // 2
-        _check_master(cpu_w13, 2 * I, H, "cpu_w13")
-        _check_master(cpu_w2, H, I, "cpu_w2")
+        I = cpu_w2.shape[2]
         if cpu_w2.shape[0] != E:
             raise ValueError("cpu_w13 and cpu_w2 disagree on num_experts")
+        # A pager-only state (shapes that are not a gated MLP) can page and
+        # be inspected but not run forward.
+        is_mlp = two_i == 2 * I and cpu_w2.shape[1] == H
         if not (1 <= cap_experts <= E):
             raise ValueError(f"cap_experts={cap_experts} outside [1, {E}]")
         self.layer_idx = int(layer_idx)
         self.num_experts = int(E)
         self.cap_experts = int(cap_experts)
         self.mode = mode
-        self.hidden, self.inter = int(H), int(I)
+        self.hidden, self.inter = (int(H), int(I)) if is_mlp else (0, 0)
+        self._w13_shape = tuple(cpu_w13.shape[1:])
+        self._w2_shape = tuple(cpu_w2.shape[1:])
         self.dtype = cpu_w13.dtype
         self.cpu_w13 = cpu_w13 if cpu_w13.is_pinned() else cpu_w13.pin_memory()
         self.cpu_w2 = cpu_w2 if cpu_w2.is_pinned() else cpu_w2.pin_memory()
         self.device = torch.device(device)
-        self._slab_elems = 3 * I * H
+        self._w13_elems = two_i * H
+        self._w2_elems = cpu_w2.shape[1] * I
+        # slab rounded up to 16 bytes so every slot stays 16-byte aligned
+        per16 = 16 // cpu_w13.element_size()
+        self._slab_elems = -(-(self._w13_elems + self._w2_elems) // per16) * per16
         self._alloc_scratch(self.cap_experts)
         dev = self.device
         self.expert_map_device = torch.full((E,), -1, dtype=torch.int32, device=dev)
         self._counters = torch.zeros(8, dtype=torch.int64, device=dev)
         self.stats_pred_hits = 0
         self.stats_pred_total = 0
-        self._ws = _Workspace(dev, I, self.dtype)
+        self._ws = _Workspace(dev, max(1, I), self.dtype)
         self._last_pairs = 0
         self._handle = C.c_void_p()
         self._desc = self._make_desc()
@@ -170,12 +178,12 @@ class WispMoEState:
 
     # -- construction helpers ---------------------------------------------
     def _alloc_scratch(self, cap: int) -> None:
-        H, I = self.hidden, self.inter
+        (r13, c13), (r2, c2) = self._w13_shape, self._w2_shape
         self._scratch = torch.empty((cap, self._slab_elems), dtype=self.dtype, device=self.device)
-        self.scratch_w13 = torch.as_strided(self._scratch, (cap, 2 * I, H),
-                                            (self._slab_elems, H, 1), 0)
-        self.scratch_w2 = torch.as_strided(self._scratch, (cap, H, I),
-                                           (self._slab_elems, I, 1), 2 * I * H)
+        self.scratch_w13 = torch.as_strided(self._scratch, (cap, r13, c13),
+                                            (self._slab_elems, c13, 1), 0)
+        self.scratch_w2 = torch.as_strided(self._scratch, (cap, r2, c2),
+                                           (self._slab_elems, c2, 1), self._w13_elems)
         self._slot_to_expert = torch.full((cap,), -1, dtype=torch.int32, device=self.device)
         self._lru_tick = torch.zeros(cap, dtype=torch.int64, device=self.device)
 
@@ -184,6 +192,7 @@ class WispMoEState:
         d.num_experts, d.cap = self.num_experts, self.cap_experts
         d.hidden, d.inter = self.hidden, self.inter
         d.dtype = _DTYPES[self.dtype]
+        d.w13_elems, d.w2_elems = self._w13_elems, self._w2_elems
         d.mode = _lib.WISP_MODE_RESIDENT if self.mode == _Mode.RESIDENT else _lib.WISP_MODE_PAGED
         d.scratch_w13, d.scratch_w13_stride = self.scratch_w13.data_ptr(), self._slab_elems
         d.scratch_w2, d.scratch_w2_stride = self.scratch_w2.data_ptr(), self._slab_elems
@@ -270,6 +279,9 @@ class WispMoEState:
                 renormalize: bool = True, out: torch.Tensor | None = None,
                 algo: int = _lib.WISP_ALGO_AUTO) -> torch.Tensor:
         """One layer call: ``x [T, H]``, ``router_logits [T, E]`` -> ``[T, H]``."""
+        if self.hidden == 0:
+            raise ValueError("wisp: expert tensors are not a gated MLP (w13 [E, 2I, H], "
+                             "w2 [E, H, I]); this state can page but not run forward")
         if x.dtype != self.dtype or x.dim() != 2 or x.shape[1] != self.hidden:
             raise ValueError(f"x must be [T, {self.hidden}] {self.dtype}")
         if router_logits.shape != (x.shape[0], self.num_experts):
