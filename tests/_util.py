@@ -55,3 +55,23 @@ def oracle_trace_matches(ora_res: dict, rec: dict) -> None:
         assert g["hits"] == o["hits"]
         assert g["evicted"] == [tuple(p) for p in o["evicted"]]
         assert g["loaded"] == [tuple(p) for p in o["loaded"]]
+
+
+def load_golden(name: str) -> dict:
+    import gzip
+    import json
+    import os
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", name)
+    with gzip.open(path, "rt") as f:
+        return json.load(f)
+
+
+def fixture_matches(entry: dict, rec: dict, s2e, tick, clock) -> None:
+    """Assert a parsed decision record plus the pager state after the call
+    equal one fixture trace entry."""
+    assert [list(g["tokens"]) for g in rec["groups"]] == entry["groups"]
+    for g, r in zip(rec["groups"], entry["records"]):
+        assert g["n_needed"] == r["n"] and g["hits"] == r["hits"]
+        assert [list(p) for p in g["evicted"]] == r["evicted"]
+        assert [list(p) for p in g["loaded"]] == r["loaded"]
+    assert list(s2e) == entry["s2e"] and list(tick) == entry["tick"] and clock == entry["clock"]

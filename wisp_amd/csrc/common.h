@@ -1,6 +1,7 @@
 // Shared definitions for the wisp_hip library (gfx950 only).
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <stddef.h>
@@ -27,6 +28,23 @@ enum Counter : int {
   kHits = 4,
   kNumCounters = 8,
 };
+
+// Optional kernel timing: {w13 start, w13 stop, w2 start, w2 stop}, recorded
+// by the dispatch itself (hipExtLaunchKernelGGL), so the elapsed time is the
+// kernel's own execution time.
+struct StageEvents {
+  hipEvent_t ev[4];
+};
+
+// Launch with or without dispatch timestamps.
+template <typename Kern, typename... Args>
+inline void launch_timed(Kern kernel, dim3 grid, dim3 block, hipStream_t st, hipEvent_t start,
+                         hipEvent_t stop, Args... args) {
+  if (start)
+    hipExtLaunchKernelGGL(kernel, grid, block, 0, st, start, stop, 0, args...);
+  else
+    hipLaunchKernelGGL(kernel, grid, block, 0, st, args...);
+}
 
 }  // namespace wisp
 

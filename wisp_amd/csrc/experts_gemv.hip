@@ -215,25 +215,25 @@ __global__ __launch_bounds__(1024) void w2_combine_kernel(const T* __restrict__ 
 
 template <typename T, int CH>
 void launch_w13(const T* x, int T_, int H, int I, int K, const int32_t* slots, const T* w13,
-                size_t w13_stride, T* act, hipStream_t st) {
+                size_t w13_stride, T* act, hipStream_t st, const StageEvents* ev) {
   constexpr int RW = 2;
   dim3 grid((I + 4 * RW - 1) / (4 * RW), T_ * K);
-  hipLaunchKernelGGL((w13_silu_kernel<T, CH, RW>), grid, dim3(256), 0, st, x, H, I, K, slots,
-                     w13, w13_stride, act);
+  launch_timed(w13_silu_kernel<T, CH, RW>, grid, dim3(256), st, ev ? ev->ev[0] : nullptr,
+               ev ? ev->ev[1] : nullptr, x, H, I, K, slots, w13, w13_stride, act);
 }
 
 template <typename T>
 int dispatch_w13(const T* x, int T_, int H, int I, int K, const int32_t* slots, const T* w13,
-                 size_t w13_stride, T* act, hipStream_t st) {
+                 size_t w13_stride, T* act, hipStream_t st, const StageEvents* ev) {
   const int nch = H / Vec<T>::N;
   const int ch = (nch + 63) / 64;
   switch (ch) {
-    case 1: launch_w13<T, 1>(x, T_, H, I, K, slots, w13, w13_stride, act, st); break;
-    case 2: launch_w13<T, 2>(x, T_, H, I, K, slots, w13, w13_stride, act, st); break;
-    case 3: launch_w13<T, 3>(x, T_, H, I, K, slots, w13, w13_stride, act, st); break;
-    case 4: launch_w13<T, 4>(x, T_, H, I, K, slots, w13, w13_stride, act, st); break;
-    case 5: case 6: launch_w13<T, 6>(x, T_, H, I, K, slots, w13, w13_stride, act, st); break;
-    case 7: case 8: launch_w13<T, 8>(x, T_, H, I, K, slots, w13, w13_stride, act, st); break;
+    case 1: launch_w13<T, 1>(x, T_, H, I, K, slots, w13, w13_stride, act, st, ev); break;
+    case 2: launch_w13<T, 2>(x, T_, H, I, K, slots, w13, w13_stride, act, st, ev); break;
+    case 3: launch_w13<T, 3>(x, T_, H, I, K, slots, w13, w13_stride, act, st, ev); break;
+    case 4: launch_w13<T, 4>(x, T_, H, I, K, slots, w13, w13_stride, act, st, ev); break;
+    case 5: case 6: launch_w13<T, 6>(x, T_, H, I, K, slots, w13, w13_stride, act, st, ev); break;
+    case 7: case 8: launch_w13<T, 8>(x, T_, H, I, K, slots, w13, w13_stride, act, st, ev); break;
     default: return WISP_ERR_UNSUPPORTED;
   }
   return WISP_OK;
@@ -241,27 +241,27 @@ int dispatch_w13(const T* x, int T_, int H, int I, int K, const int32_t* slots, 
 
 template <typename T, int LPR, int CH>
 void launch_w2(const T* act, int T_, int H, int I, int K, const float* w, const int32_t* slots,
-               const T* w2, size_t w2_stride, T* out, hipStream_t st) {
+               const T* w2, size_t w2_stride, T* out, hipStream_t st, const StageEvents* ev) {
   constexpr int RPW = 64 / LPR;
   dim3 grid((H + RPW - 1) / RPW, T_);
-  hipLaunchKernelGGL((w2_combine_kernel<T, LPR, CH>), grid, dim3(64 * K), 0, st, act, H, I, K, w,
-                     slots, w2, w2_stride, out);
+  launch_timed(w2_combine_kernel<T, LPR, CH>, grid, dim3(64 * K), st, ev ? ev->ev[2] : nullptr,
+               ev ? ev->ev[3] : nullptr, act, H, I, K, w, slots, w2, w2_stride, out);
 }
 
 template <typename T>
 int dispatch_w2(const T* act, int T_, int H, int I, int K, const float* w, const int32_t* slots,
-                const T* w2, size_t w2_stride, T* out, hipStream_t st) {
+                const T* w2, size_t w2_stride, T* out, hipStream_t st, const StageEvents* ev) {
   if (K > kMaxKw2) return WISP_ERR_UNSUPPORTED;
   const int nch = I / Vec<T>::N;
   if (nch <= 32 * 4) {  // half a wave per row, up to 4 chunks per lane
     switch ((nch + 31) / 32) {
-      case 1: launch_w2<T, 32, 1>(act, T_, H, I, K, w, slots, w2, w2_stride, out, st); break;
-      case 2: launch_w2<T, 32, 2>(act, T_, H, I, K, w, slots, w2, w2_stride, out, st); break;
-      case 3: launch_w2<T, 32, 3>(act, T_, H, I, K, w, slots, w2, w2_stride, out, st); break;
-      default: launch_w2<T, 32, 4>(act, T_, H, I, K, w, slots, w2, w2_stride, out, st); break;
+      case 1: launch_w2<T, 32, 1>(act, T_, H, I, K, w, slots, w2, w2_stride, out, st, ev); break;
+      case 2: launch_w2<T, 32, 2>(act, T_, H, I, K, w, slots, w2, w2_stride, out, st, ev); break;
+      case 3: launch_w2<T, 32, 3>(act, T_, H, I, K, w, slots, w2, w2_stride, out, st, ev); break;
+      default: launch_w2<T, 32, 4>(act, T_, H, I, K, w, slots, w2, w2_stride, out, st, ev); break;
     }
   } else {
-    launch_w2<T, 64, 0>(act, T_, H, I, K, w, slots, w2, w2_stride, out, st);
+    launch_w2<T, 64, 0>(act, T_, H, I, K, w, slots, w2, w2_stride, out, st, ev);
   }
   return WISP_OK;
 }
@@ -270,23 +270,21 @@ int dispatch_w2(const T* act, int T_, int H, int I, int K, const float* w, const
 
 int experts_gemv(const void* x, int dtype, int T_, int H, int I, int K, const float* topk_w,
                  const int32_t* slots, const void* w13, size_t w13_stride, const void* w2,
-                 size_t w2_stride, void* act, void* out, hipStream_t st, hipEvent_t ev_mid) {
+                 size_t w2_stride, void* act, void* out, hipStream_t st, const StageEvents* ev) {
   if (T_ == 0) return WISP_OK;
   int rc;
   if (dtype == WISP_F32) {
     rc = dispatch_w13<float>((const float*)x, T_, H, I, K, slots, (const float*)w13, w13_stride,
-                             (float*)act, st);
-    if (rc == WISP_OK && ev_mid) WISP_HIP_TRY(hipEventRecord(ev_mid, st));
+                             (float*)act, st, ev);
     if (rc == WISP_OK)
       rc = dispatch_w2<float>((const float*)act, T_, H, I, K, topk_w, slots, (const float*)w2,
-                              w2_stride, (float*)out, st);
+                              w2_stride, (float*)out, st, ev);
   } else {
     rc = dispatch_w13<uint16_t>((const uint16_t*)x, T_, H, I, K, slots, (const uint16_t*)w13,
-                                w13_stride, (uint16_t*)act, st);
-    if (rc == WISP_OK && ev_mid) WISP_HIP_TRY(hipEventRecord(ev_mid, st));
+                                w13_stride, (uint16_t*)act, st, ev);
     if (rc == WISP_OK)
       rc = dispatch_w2<uint16_t>((const uint16_t*)act, T_, H, I, K, topk_w, slots,
-                                 (const uint16_t*)w2, w2_stride, (uint16_t*)out, st);
+                                 (const uint16_t*)w2, w2_stride, (uint16_t*)out, st, ev);
   }
   if (rc != WISP_OK) {
     wisp_set_last_error("shape outside the GEMV kernels' coverage", "wisp_moe_experts");

@@ -37,20 +37,20 @@ int launch_pager(const int32_t* ids, int T, int K, int E, int cap, int single_gr
                  int32_t* rec, int rec_words, hipStream_t stream);
 int experts_gemv(const void* x, int dtype, int T, int H, int I, int K, const float* topk_w,
                  const int32_t* slots, const void* w13, size_t w13_stride, const void* w2,
-                 size_t w2_stride, void* act, void* out, hipStream_t st, hipEvent_t ev_mid);
+                 size_t w2_stride, void* act, void* out, hipStream_t st, const StageEvents* ev);
 int experts_mfma(const void* x, int T, int H, int I, int K, const float* topk_w,
                  const int32_t* slots, const void* w13, size_t w13_stride, const void* w2,
-                 size_t w2_stride, void* act, void* out, hipStream_t st, hipEvent_t ev_mid);
+                 size_t w2_stride, void* act, void* out, hipStream_t st, const StageEvents* ev);
 
 namespace {
 
 constexpr int kEventRing = 4;
 constexpr int kProfRing = 256;
 
-// HIP-event timing of the two expert kernels of the first group of a call:
-// ev[0] before the w13 kernel, ev[1] between the kernels, ev[2] after w2.
+// Dispatch-timestamp timing of the two expert kernels of the first group of
+// a call (see StageEvents).
 struct ProfSlot {
-  hipEvent_t ev[3] = {};
+  StageEvents se = {};
   bool pending = false;
 };
 
@@ -79,9 +79,9 @@ struct Layer {
 void prof_harvest(Layer& L, ProfSlot& p) {
   if (!p.pending) return;
   float a = 0.f, b = 0.f;
-  if (hipEventSynchronize(p.ev[2]) == hipSuccess &&
-      hipEventElapsedTime(&a, p.ev[0], p.ev[1]) == hipSuccess &&
-      hipEventElapsedTime(&b, p.ev[1], p.ev[2]) == hipSuccess) {
+  if (hipEventSynchronize(p.se.ev[3]) == hipSuccess &&
+      hipEventElapsedTime(&a, p.se.ev[0], p.se.ev[1]) == hipSuccess &&
+      hipEventElapsedTime(&b, p.se.ev[2], p.se.ev[3]) == hipSuccess) {
     L.prof_ms[0] += a;
     L.prof_ms[1] += b;
     L.prof_n += 1;
@@ -95,9 +95,9 @@ ProfSlot* prof_begin(Layer& L) {
   ProfSlot& p = L.prof[L.prof_next];
   L.prof_next = (L.prof_next + 1) % kProfRing;
   prof_harvest(L, p);
-  if (!p.ev[0]) {
-    for (int i = 0; i < 3; ++i)
-      if (hipEventCreate(&p.ev[i]) != hipSuccess) return nullptr;
+  if (!p.se.ev[0]) {
+    for (int i = 0; i < 4; ++i)
+      if (hipEventCreate(&p.se.ev[i]) != hipSuccess) return nullptr;
   }
   return &p;
 }
@@ -152,20 +152,16 @@ int experts(Layer& L, const void* x, int T, int K, const float* w, const int32_t
             void* act, void* out, int algo, hipStream_t st, bool timed) {
   const wisp_layer_desc& d = L.d;
   ProfSlot* p = timed && T > 0 ? prof_begin(L) : nullptr;
-  if (p) WISP_HIP_TRY(hipEventRecord(p->ev[0], st));
+  const StageEvents* se = p ? &p->se : nullptr;
   int rc;
   if (algo == WISP_ALGO_MFMA)
     rc = experts_mfma(x, T, d.hidden, d.inter, K, w, slots, d.scratch_w13, d.scratch_w13_stride,
-                      d.scratch_w2, d.scratch_w2_stride, act, out, st, p ? p->ev[1] : nullptr);
+                      d.scratch_w2, d.scratch_w2_stride, act, out, st, se);
   else
     rc = experts_gemv(x, d.dtype, T, d.hidden, d.inter, K, w, slots, d.scratch_w13,
-                      d.scratch_w13_stride, d.scratch_w2, d.scratch_w2_stride, act, out, st,
-                      p ? p->ev[1] : nullptr);
+                      d.scratch_w13_stride, d.scratch_w2, d.scratch_w2_stride, act, out, st, se);
   if (rc != WISP_OK) return rc;
-  if (p) {
-    WISP_HIP_TRY(hipEventRecord(p->ev[2], st));
-    p->pending = true;
-  }
+  if (p) p->pending = true;
   return WISP_OK;
 }
 
@@ -298,8 +294,8 @@ extern "C" int wisp_layer_destroy(void* handle) {
   if (L->ev_pin_start) (void)hipEventDestroy(L->ev_pin_start);
   if (L->ev_pin_end) (void)hipEventDestroy(L->ev_pin_end);
   for (int i = 0; i < wisp::kProfRing; ++i)
-    for (int j = 0; j < 3; ++j)
-      if (L->prof[i].ev[j]) (void)hipEventDestroy(L->prof[i].ev[j]);
+    for (int j = 0; j < 4; ++j)
+      if (L->prof[i].se.ev[j]) (void)hipEventDestroy(L->prof[i].se.ev[j]);
   if (L->copy_stream) (void)hipStreamDestroy(L->copy_stream);
   delete L;
   return WISP_OK;

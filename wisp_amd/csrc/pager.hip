@@ -198,6 +198,71 @@ __device__ inline int popc_below(uint64_t mask) {
 
 __device__ inline uint64_t ballot(bool p) { return __ballot(p); }
 
+// Insert `key` into a CPython set table of mask+1 <= 128 slots whose
+// occupancy is the bitmask (lo, hi); returns the slot (same probe sequence as
+// set_insert_clean).  All operands are wave-uniform.
+__device__ inline int probe_insert(uint64_t& lo, uint64_t& hi, uint32_t mask, int key) {
+  uint32_t perturb = (uint32_t)key;
+  uint32_t i = (uint32_t)key & mask;
+  for (;;) {
+    const int n = (i + 9 <= mask) ? 10 : 1;
+    for (int d = 0; d < n; ++d) {
+      const uint32_t s = i + d;
+      const uint64_t bit = 1ull << (s & 63);
+      uint64_t& w = s < 64 ? lo : hi;
+      if (!(w & bit)) {
+        w |= bit;
+        return (int)s;
+      }
+    }
+    perturb >>= 5;
+    i = (i * 5 + 1 + perturb) & mask;
+  }
+}
+
+// CPython set iteration position of each of U <= 64 ascending keys, key j
+// held by lane j.  Tables stay <= 128 slots for U <= 64 (growth happens at 5
+// and 19 keys), so the occupancy fits two 64-bit masks in scalar registers;
+// a resize re-inserts the keys in old slot order.  Returns the position of
+// this lane's key (lanes >= U return -1).
+__device__ int set_positions_wave(int key, int U, int lane) {
+  uint64_t lo = 0, hi = 0;
+  uint32_t mask = 7;
+  int myslot = -1;
+  for (int j = 0; j < U; ++j) {
+    const int kj = __builtin_amdgcn_readlane(key, j);
+    const int s = probe_insert(lo, hi, mask, kj);
+    if (lane == j) myslot = s;
+    const int fill = j + 1;
+    if ((uint32_t)fill * 5 >= mask * 3) {
+      uint32_t newsize = 8;
+      while (newsize <= (uint32_t)fill * 4) newsize <<= 1;
+      uint64_t nlo = 0, nhi = 0;
+      int newslot = -1;
+      for (int half = 0; half < 2; ++half) {
+        uint64_t bits = half ? hi : lo;
+        while (bits) {
+          const int sl = half * 64 + __builtin_ctzll(bits);
+          bits &= bits - 1;
+          const uint64_t who = __ballot(myslot == sl);
+          const int l = __builtin_ctzll(who);
+          const int kl = __builtin_amdgcn_readlane(key, l);
+          const int ns = probe_insert(nlo, nhi, newsize - 1, kl);
+          if (lane == l) newslot = ns;
+        }
+      }
+      lo = nlo;
+      hi = nhi;
+      mask = newsize - 1;
+      if (lane <= j) myslot = newslot;
+    }
+  }
+  if (lane >= U) return -1;
+  const uint64_t below_lo = myslot >= 64 ? lo : (lo & ((1ull << myslot) - 1));
+  const uint64_t below_hi = myslot >= 64 ? (hi & ((1ull << (myslot - 64)) - 1)) : 0ull;
+  return __popcll(below_lo) + __popcll(below_hi);
+}
+
 struct PagerSmem {
   int32_t map[kMaxExperts];
   int32_t s2e[kMaxExperts];
@@ -283,22 +348,23 @@ __global__ __launch_bounds__(64) void pager_kernel(
       start = end;
 
       // ---- sorted unique ids of the group ----------------------------
-      if (lane == 0) {
-        int u = 0;
-        for (int w = 0; w < nwords; ++w) {
-          uint32_t bits = sm.need[w];
-          while (bits) {
-            const int b = __builtin_ctz(bits);
-            bits &= bits - 1;
-            sm.keys[u++] = (w << 5) + b;
-          }
-        }
-        // CPython set iteration order of the ascending keys.
-        cpython_set_order(sm.keys, u, sm.order, sm.table, kMaxSetTable);
-      }
       int U = 0;
-      for (int w = lane; w < nwords; w += 64) U += __popc(sm.need[w]);
-      for (int off = 32; off > 0; off >>= 1) U += __shfl_xor(U, off);
+      for (int base = 0; base < E; base += 64) {
+        const int e = base + lane;
+        const bool in = e < E && ((sm.need[e >> 5] >> (e & 31)) & 1u);
+        const uint64_t bb = ballot(in);
+        if (in) sm.keys[U + popc_below(bb)] = e;
+        U += __popcll(bb);
+      }
+      __syncthreads();
+      // ---- CPython set iteration order of the ascending keys ----------
+      if (U <= 64) {
+        const int key = lane < U ? sm.keys[lane] : -1;
+        const int pos = set_positions_wave(key, U, lane);
+        if (lane < U) sm.order[pos] = key;
+      } else if (lane == 0) {
+        cpython_set_order(sm.keys, U, sm.order, sm.table, kMaxSetTable);
+      }
       __syncthreads();
 
       // ---- missing experts, in set order -----------------------------

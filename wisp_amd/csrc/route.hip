@@ -4,6 +4,7 @@
 // layer.select_experts(..., scoring_func="softmax", renormalize=...)
 // (src/wisp/integrations/vllm/fused_moe.py:1054-1076).  One wavefront per
 // token; each lane holds logits j*64 + lane (coalesced), so E <= 512.
+// Top-k by rank counting: no k rounds of cross-lane argmax.
 // Experts are ranked by logit, descending, ties to the lower id; weights are
 // p = exp(l - max) / sum_e exp(l_e - max) and, with renormalisation,
 // w = p / sum_topk p.  All sums use a fixed butterfly order.
@@ -25,62 +26,63 @@ __device__ inline float load_logit<uint16_t>(const uint16_t* p) {
   return __uint_as_float((uint32_t)(*p) << 16);
 }
 
+// One wave per token (4 tokens per block).  Each logit's rank is the number
+// of logits ahead of it in (value desc, id asc) order, counted against an LDS
+// copy of the row; ranks 0..K-1 are the routed experts in routing order.
 template <typename TL>
 __global__ __launch_bounds__(256) void route_kernel(const TL* __restrict__ logits, int T, int E,
                                                      int K, int renorm, float* __restrict__ w_out,
                                                      int32_t* __restrict__ id_out,
                                                      int64_t* __restrict__ forward_counter) {
+  __shared__ __align__(16) float s_row[4][kMaxExperts];
+  __shared__ float s_val[4][64];
+  __shared__ int s_id[4][64];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   if (forward_counter && blockIdx.x == 0 && threadIdx.x == 0) forward_counter[0] += 1;
   const int t = blockIdx.x * 4 + wave;
-  if (t >= T) return;
-  const TL* row = logits + (size_t)t * E;
-
+  const bool active = t < T;
+  const int per = (E + 63) >> 6;
   float v[kVals];
 #pragma unroll
   for (int j = 0; j < kVals; ++j) {
     const int e = j * 64 + lane;
-    v[j] = e < E ? load_logit(row + e) : -INFINITY;
+    v[j] = (active && j < per && e < E) ? load_logit(logits + (size_t)t * E + e) : -INFINITY;
+    if (j < per && e < E) s_row[wave][e] = v[j];
   }
-  float m = -INFINITY;
-#pragma unroll
-  for (int j = 0; j < kVals; ++j) m = fmaxf(m, v[j]);
-  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-  float s = 0.f;
-#pragma unroll
-  for (int j = 0; j < kVals; ++j)
-    if (j * 64 + lane < E) s += expf(v[j] - m);
-  for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
-
-  uint32_t taken = 0;
-  int my_id = -1;
-  float my_val = -INFINITY;
-  for (int r = 0; r < K; ++r) {
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
+  __syncthreads();
+  if (active) {
+    const float* row = s_row[wave];
 #pragma unroll
     for (int j = 0; j < kVals; ++j) {
       const int e = j * 64 + lane;
-      if (e < E && !(taken & (1u << j)) && (v[j] > bv || bi == 0x7fffffff)) {
-        bv = v[j];
-        bi = e;
+      if (j < per && e < E) {
+        const float x = v[j];
+        int r = 0;
+        int q = 0;
+        for (; q + 4 <= E; q += 4) {
+          const float4 c = *reinterpret_cast<const float4*>(row + q);
+          r += (c.x > x) | ((c.x == x) & (q + 0 < e));
+          r += (c.y > x) | ((c.y == x) & (q + 1 < e));
+          r += (c.z > x) | ((c.z == x) & (q + 2 < e));
+          r += (c.w > x) | ((c.w == x) & (q + 3 < e));
+        }
+        for (; q < E; ++q) r += (row[q] > x) | ((row[q] == x) & (q < e));
+        if (r < K) {
+          s_val[wave][r] = x;
+          s_id[wave][r] = e;
+        }
       }
-    }
-    for (int off = 32; off > 0; off >>= 1) {
-      const float ov = __shfl_xor(bv, off);
-      const int oi = __shfl_xor(bi, off);
-      if (ov > bv || (ov == bv && oi < bi)) {
-        bv = ov;
-        bi = oi;
-      }
-    }
-    if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
-    if (lane == r) {
-      my_id = bi;
-      my_val = bv;
     }
   }
-  float p = lane < K ? expf(my_val - m) / s : 0.f;
+  __syncthreads();
+  if (!active) return;
+  const float m = s_val[wave][0];
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < kVals; ++j)
+    if (j < per && j * 64 + lane < E) s += expf(v[j] - m);
+  for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+  float p = lane < K ? expf(s_val[wave][lane] - m) / s : 0.f;
   if (renorm) {
     float tot = p;
     for (int off = 32; off > 0; off >>= 1) tot += __shfl_xor(tot, off);
@@ -88,7 +90,7 @@ __global__ __launch_bounds__(256) void route_kernel(const TL* __restrict__ logit
   }
   if (lane < K) {
     w_out[(size_t)t * K + lane] = p;
-    id_out[(size_t)t * K + lane] = my_id;
+    id_out[(size_t)t * K + lane] = s_id[wave][lane];
   }
 }
 
