@@ -141,21 +141,21 @@ def main() -> int:
     elapsed = time.perf_counter() - t0
     log(f"timed {args.steps} layer calls in {elapsed:.3f}s")
 
-    w13_ms = w2_ms = 0.0
-    launches = 0
+    prof = {"w13": 0.0, "w2": 0.0, "calls": 0}
     pin_ms = pin_bytes = 0.0
     miss = hits = 0
     for st in states:
-        a, b, n = st.profile(False)
-        w13_ms, w2_ms, launches = w13_ms + a, w2_ms + b, launches + n
+        for k, v in st.profile(False).items():
+            prof[k] += v
         ms, nb = st.pagein_stats()
         pin_ms, pin_bytes = pin_ms + ms, pin_bytes + nb
         miss, hits = miss + st.stats_miss, hits + st.stats_hits
     K = sh.top_k
     w13_bytes = K * 2 * sh.inter * sh.hidden * sh.elem_bytes
     w2_bytes = K * sh.hidden * sh.inter * sh.elem_bytes
-    t13 = w13_ms / max(1, launches) * 1e-3
-    t2 = w2_ms / max(1, launches) * 1e-3
+    calls = max(1, prof["calls"])
+    t13 = prof["w13"] / calls * 1e-3
+    t2 = prof["w2"] / calls * 1e-3
     a13 = w13_bytes / t13 / 1e9 if t13 > 0 else 0.0
     agemm = (w13_bytes + w2_bytes) / (t13 + t2) / 1e9 if t13 + t2 > 0 else 0.0
 
@@ -206,8 +206,8 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(a13 / HBM_PEAK_GBPS, 4),
             "traffic": None,
-            "bytes_per_launch": w13_bytes,
-            "avg_us": round(t13 * 1e6, 3),
+            "bytes_per_call": w13_bytes,
+            "avg_us_per_call": round(t13 * 1e6, 3),
         },
         "expert_gemm": {
             "kernels": "w13_silu_kernel + w2_combine_kernel",
@@ -216,7 +216,7 @@ def main() -> int:
             "achieved_GBps": round(agemm, 1),
             "frac_hbm_peak": round(agemm / HBM_PEAK_GBPS, 4),
             "w2_avg_us": round(t2 * 1e6, 3),
-            "timed_launches": launches,
+            "timed_calls": prof["calls"],
         },
         "pagein": {
             "bytes": pin_bytes,

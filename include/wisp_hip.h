@@ -134,6 +134,10 @@ typedef struct wisp_layer_desc {
   int hidden, inter;             /* expert MLP shape; 0 for a pager-only
                                     state (the forward call then fails)  */
   int dtype, mode;
+  int pagein_streams;            /* 0: page-in copies run on the caller's
+                                    stream (stream order fences them);
+                                    1 or 2: on that many side streams,
+                                    fenced with events                    */
   size_t w13_elems, w2_elems;    /* elements of one expert's w13 / w2    */
   void* scratch_w13;             /* device, slot s at +s*stride [2I, H]  */
   size_t scratch_w13_stride;     /* elements                             */
@@ -154,6 +158,9 @@ typedef struct wisp_workspace {
   float* topk_w;                 /* device [max_pairs]                   */
   int32_t* topk_ids;             /* device [max_pairs]                   */
   int32_t* slots;                /* device [max_pairs]                   */
+  int32_t* flags;                /* device [1 + max_pairs]: experts loaded
+                                    by the call, then per pair 1 if its
+                                    expert was loaded by this call        */
   void* act;                     /* device [max_pairs*inter]             */
   int32_t* record;               /* pinned host [record_words]           */
   int record_words;
@@ -188,12 +195,13 @@ int wisp_layer_prime_identity(void* handle, wisp_stream_t stream);
  * the bytes they moved (for page-in bandwidth reporting). */
 int wisp_layer_last_pagein(void* handle, float* ms, double* bytes);
 
-/* Read and reset the accumulated HIP-event durations of the expert kernels
- * (first token group of each call: w13+SiLU kernel, then w2+combine kernel)
- * and the number of timed launches; then switch timing on (enable != 0) or
- * off.  Timing adds three event records per call on the caller's stream. */
+/* Read and reset the accumulated execution time (dispatch timestamps) of the
+ * w13+SiLU kernels and of the w2+combine kernels of all layer calls since the
+ * last read, and the number of layer calls; then switch timing on
+ * (enable != 0) or off.  A speculative w2 launch that found experts to load
+ * and exited is not counted. */
 int wisp_layer_profile(void* handle, int enable, double* w13_ms, double* w2_ms,
-                       int64_t* launches);
+                       int64_t* calls);
 
 /* ---- group 4: probes ----------------------------------------------- */
 

@@ -35,7 +35,7 @@ def bits(t):
     return t.view(torch.int16) if t.dtype == torch.bfloat16 else t.view(torch.int32)
 
 
-def drive(wl, cap, steps, check_out_every=1, tol=None, act_round=None):
+def drive(wl, cap, steps, check_out_every=1, tol=None, act_round=None, algo=0):
     sts = states(wl, cap)
     ora = PagerOracle(wl.shape.experts, cap)
     w13, w2 = wl.views()
@@ -43,7 +43,7 @@ def drive(wl, cap, steps, check_out_every=1, tol=None, act_round=None):
     for t in range(steps):
         x = wl.x[t].to(DEV)
         lg = wl.logits[t].to(DEV)
-        outs = {m: st.forward(x, lg, K, True) for m, st in sts.items()}
+        outs = {m: st.forward(x, lg, K, True, algo=algo) for m, st in sts.items()}
         torch.cuda.synchronize()
         assert torch.equal(bits(outs["paged"]), bits(outs["resident"])), t
         w_ref, ids_ref = route(wl.logits[t], K)
@@ -70,14 +70,19 @@ def test_toy_fp32_layer_all_steps():
     drive(wl, 4, wl.steps, tol=1e-5)
 
 
-def test_qwen3_bf16_layer_decode():
+@pytest.mark.parametrize("streams", ["0", "1", "2"])
+def test_qwen3_bf16_layer_decode(monkeypatch, streams):
+    # page-in on the caller's stream (default) or on side streams with events
+    monkeypatch.setenv("WISP_PAGEIN_STREAMS", streams)
     wl = W.qwen3_decode(steps=48, pin=True)
     sts = drive(wl, 8, wl.steps, check_out_every=8, tol=1e-2)
     ms, nbytes = sts["paged"].pagein_stats()
     assert nbytes > 0 and ms > 0
 
 
-def test_batched_subbatching_matches_resident_bytes():
+@pytest.mark.parametrize("streams", ["0", "2"])
+def test_batched_subbatching_matches_resident_bytes(monkeypatch, streams):
+    monkeypatch.setenv("WISP_PAGEIN_STREAMS", streams)
     # 16 tokens, cap 32 of 128 experts: several greedy groups per call
     wl = W.gaussian_logits("batch", seed=3, steps=3, tokens=16, pin=True)
     drive(wl, 32, wl.steps, check_out_every=1, tol=1e-2)
@@ -95,3 +100,4 @@ def test_overflow_token_raises_subbatch():
     x = wl.x[0].to(DEV)
     with pytest.raises(RuntimeError, match="sub-batch"):
         st.forward(x, wl.logits[0].to(DEV), 3, True)
+

@@ -37,7 +37,8 @@ _vp, _i32, _i64, _sz, _f32p = C.c_void_p, C.c_int, C.c_int64, C.c_size_t, C.POIN
 class LayerDesc(C.Structure):
     _fields_ = [
         ("num_experts", C.c_int), ("cap", C.c_int), ("hidden", C.c_int), ("inter", C.c_int),
-        ("dtype", C.c_int), ("mode", C.c_int), ("w13_elems", _sz), ("w2_elems", _sz),
+        ("dtype", C.c_int), ("mode", C.c_int), ("pagein_streams", C.c_int),
+        ("w13_elems", _sz), ("w2_elems", _sz),
         ("scratch_w13", _vp), ("scratch_w13_stride", _sz),
         ("scratch_w2", _vp), ("scratch_w2_stride", _sz),
         ("master_w13", _vp), ("master_w13_stride", _sz),
@@ -49,7 +50,7 @@ class LayerDesc(C.Structure):
 class Workspace(C.Structure):
     _fields_ = [
         ("max_pairs", C.c_int), ("topk_w", _vp), ("topk_ids", _vp), ("slots", _vp),
-        ("act", _vp), ("record", _vp), ("record_words", C.c_int),
+        ("flags", _vp), ("act", _vp), ("record", _vp), ("record_words", C.c_int),
     ]
 
 

@@ -18,6 +18,8 @@ constexpr int kMaxTopK = 64;
 // A CPython set of n <= kMaxExperts small ints never needs a table larger
 // than the smallest power of two above 4n, which is <= 8n.
 constexpr int kMaxSetTable = 8 * kMaxExperts;
+// Calls of at most this many tokens are routed inside the pager kernel.
+constexpr int kFusedRouteTokens = 8;
 
 // Per-layer counters kept on the device, in this order.
 enum Counter : int {
@@ -28,6 +30,16 @@ enum Counter : int {
   kHits = 4,
   kNumCounters = 8,
 };
+
+// Orders this wavefront's LDS accesses across lanes without waiting for its
+// outstanding global or host-memory stores (a block barrier would: on CDNA
+// the barrier's wait counts stores too).  Only valid where every LDS
+// producer and consumer is in the same wavefront.
+__device__ inline void wave_lds_sync() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt/expcnt left at max
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
 
 // Optional kernel timing: {w13 start, w13 stop, w2 start, w2 stop}, recorded
 // by the dispatch itself (hipExtLaunchKernelGGL), so the elapsed time is the

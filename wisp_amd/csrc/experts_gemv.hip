@@ -65,10 +65,13 @@ template <typename T, int CH, int RW>
 __global__ __launch_bounds__(256) void w13_silu_kernel(const T* __restrict__ x, int H, int I,
                                                         int K, const int32_t* __restrict__ slots,
                                                         const T* __restrict__ w13,
-                                                        size_t w13_stride, T* __restrict__ act) {
+                                                        size_t w13_stride, T* __restrict__ act,
+                                                        const int32_t* __restrict__ pair_filter,
+                                                        int want) {
   constexpr int V = Vec<T>::N;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int pair = blockIdx.y;
+  if (pair_filter && pair_filter[pair] != want) return;
   const int t = pair / K;
   const int i0 = (blockIdx.x * 4 + wave) * RW;
   if (i0 >= I) return;
@@ -150,10 +153,12 @@ __global__ __launch_bounds__(1024) void w2_combine_kernel(const T* __restrict__ 
                                                            const int32_t* __restrict__ slots,
                                                            const T* __restrict__ w2,
                                                            size_t w2_stride,
-                                                           T* __restrict__ out) {
+                                                           T* __restrict__ out,
+                                                           const int32_t* __restrict__ skip_if) {
   constexpr int V = Vec<T>::N;
   constexpr int RPW = 64 / LPR;
   __shared__ float part[kMaxKw2][RPW];
+  if (skip_if && *skip_if != 0) return;
   const int k = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int sub = lane / LPR, l = lane % LPR;
   const int t = blockIdx.y;
@@ -213,27 +218,37 @@ __global__ __launch_bounds__(1024) void w2_combine_kernel(const T* __restrict__ 
   }
 }
 
+// Optional controls of a launch: kernel timing events, the pair filter of
+// the w13 kernel (run only pairs with pair_filter[p] == want) and the skip
+// word of the w2 kernel (exit when *skip_if != 0).
+struct LaunchCtl {
+  hipEvent_t start = nullptr, stop = nullptr;
+  const int32_t* pair_filter = nullptr;
+  int want = 0;
+  const int32_t* skip_if = nullptr;
+};
+
 template <typename T, int CH>
 void launch_w13(const T* x, int T_, int H, int I, int K, const int32_t* slots, const T* w13,
-                size_t w13_stride, T* act, hipStream_t st, const StageEvents* ev) {
+                size_t w13_stride, T* act, hipStream_t st, const LaunchCtl& c) {
   constexpr int RW = 2;
   dim3 grid((I + 4 * RW - 1) / (4 * RW), T_ * K);
-  launch_timed(w13_silu_kernel<T, CH, RW>, grid, dim3(256), st, ev ? ev->ev[0] : nullptr,
-               ev ? ev->ev[1] : nullptr, x, H, I, K, slots, w13, w13_stride, act);
+  launch_timed(w13_silu_kernel<T, CH, RW>, grid, dim3(256), st, c.start, c.stop, x, H, I, K,
+               slots, w13, w13_stride, act, c.pair_filter, c.want);
 }
 
 template <typename T>
 int dispatch_w13(const T* x, int T_, int H, int I, int K, const int32_t* slots, const T* w13,
-                 size_t w13_stride, T* act, hipStream_t st, const StageEvents* ev) {
+                 size_t w13_stride, T* act, hipStream_t st, const LaunchCtl& c) {
   const int nch = H / Vec<T>::N;
   const int ch = (nch + 63) / 64;
   switch (ch) {
-    case 1: launch_w13<T, 1>(x, T_, H, I, K, slots, w13, w13_stride, act, st, ev); break;
-    case 2: launch_w13<T, 2>(x, T_, H, I, K, slots, w13, w13_stride, act, st, ev); break;
-    case 3: launch_w13<T, 3>(x, T_, H, I, K, slots, w13, w13_stride, act, st, ev); break;
-    case 4: launch_w13<T, 4>(x, T_, H, I, K, slots, w13, w13_stride, act, st, ev); break;
-    case 5: case 6: launch_w13<T, 6>(x, T_, H, I, K, slots, w13, w13_stride, act, st, ev); break;
-    case 7: case 8: launch_w13<T, 8>(x, T_, H, I, K, slots, w13, w13_stride, act, st, ev); break;
+    case 1: launch_w13<T, 1>(x, T_, H, I, K, slots, w13, w13_stride, act, st, c); break;
+    case 2: launch_w13<T, 2>(x, T_, H, I, K, slots, w13, w13_stride, act, st, c); break;
+    case 3: launch_w13<T, 3>(x, T_, H, I, K, slots, w13, w13_stride, act, st, c); break;
+    case 4: launch_w13<T, 4>(x, T_, H, I, K, slots, w13, w13_stride, act, st, c); break;
+    case 5: case 6: launch_w13<T, 6>(x, T_, H, I, K, slots, w13, w13_stride, act, st, c); break;
+    case 7: case 8: launch_w13<T, 8>(x, T_, H, I, K, slots, w13, w13_stride, act, st, c); break;
     default: return WISP_ERR_UNSUPPORTED;
   }
   return WISP_OK;
@@ -241,57 +256,84 @@ int dispatch_w13(const T* x, int T_, int H, int I, int K, const int32_t* slots, 
 
 template <typename T, int LPR, int CH>
 void launch_w2(const T* act, int T_, int H, int I, int K, const float* w, const int32_t* slots,
-               const T* w2, size_t w2_stride, T* out, hipStream_t st, const StageEvents* ev) {
+               const T* w2, size_t w2_stride, T* out, hipStream_t st, const LaunchCtl& c) {
   constexpr int RPW = 64 / LPR;
   dim3 grid((H + RPW - 1) / RPW, T_);
-  launch_timed(w2_combine_kernel<T, LPR, CH>, grid, dim3(64 * K), st, ev ? ev->ev[2] : nullptr,
-               ev ? ev->ev[3] : nullptr, act, H, I, K, w, slots, w2, w2_stride, out);
+  launch_timed(w2_combine_kernel<T, LPR, CH>, grid, dim3(64 * K), st, c.start, c.stop, act, H,
+               I, K, w, slots, w2, w2_stride, out, c.skip_if);
 }
 
 template <typename T>
 int dispatch_w2(const T* act, int T_, int H, int I, int K, const float* w, const int32_t* slots,
-                const T* w2, size_t w2_stride, T* out, hipStream_t st, const StageEvents* ev) {
+                const T* w2, size_t w2_stride, T* out, hipStream_t st, const LaunchCtl& c) {
   if (K > kMaxKw2) return WISP_ERR_UNSUPPORTED;
   const int nch = I / Vec<T>::N;
   if (nch <= 32 * 4) {  // half a wave per row, up to 4 chunks per lane
     switch ((nch + 31) / 32) {
-      case 1: launch_w2<T, 32, 1>(act, T_, H, I, K, w, slots, w2, w2_stride, out, st, ev); break;
-      case 2: launch_w2<T, 32, 2>(act, T_, H, I, K, w, slots, w2, w2_stride, out, st, ev); break;
-      case 3: launch_w2<T, 32, 3>(act, T_, H, I, K, w, slots, w2, w2_stride, out, st, ev); break;
-      default: launch_w2<T, 32, 4>(act, T_, H, I, K, w, slots, w2, w2_stride, out, st, ev); break;
+      case 1: launch_w2<T, 32, 1>(act, T_, H, I, K, w, slots, w2, w2_stride, out, st, c); break;
+      case 2: launch_w2<T, 32, 2>(act, T_, H, I, K, w, slots, w2, w2_stride, out, st, c); break;
+      case 3: launch_w2<T, 32, 3>(act, T_, H, I, K, w, slots, w2, w2_stride, out, st, c); break;
+      default: launch_w2<T, 32, 4>(act, T_, H, I, K, w, slots, w2, w2_stride, out, st, c); break;
     }
   } else {
-    launch_w2<T, 64, 0>(act, T_, H, I, K, w, slots, w2, w2_stride, out, st, ev);
+    launch_w2<T, 64, 0>(act, T_, H, I, K, w, slots, w2, w2_stride, out, st, c);
   }
   return WISP_OK;
 }
 
 }  // namespace
 
-int experts_gemv(const void* x, int dtype, int T_, int H, int I, int K, const float* topk_w,
-                 const int32_t* slots, const void* w13, size_t w13_stride, const void* w2,
-                 size_t w2_stride, void* act, void* out, hipStream_t st, const StageEvents* ev) {
+int gemv_w13(const void* x, int dtype, int T_, int H, int I, int K, const int32_t* slots,
+             const void* w13, size_t w13_stride, void* act, hipStream_t st,
+             hipEvent_t ev_start, hipEvent_t ev_stop, const int32_t* pair_filter, int want) {
   if (T_ == 0) return WISP_OK;
-  int rc;
-  if (dtype == WISP_F32) {
-    rc = dispatch_w13<float>((const float*)x, T_, H, I, K, slots, (const float*)w13, w13_stride,
-                             (float*)act, st, ev);
-    if (rc == WISP_OK)
-      rc = dispatch_w2<float>((const float*)act, T_, H, I, K, topk_w, slots, (const float*)w2,
-                              w2_stride, (float*)out, st, ev);
-  } else {
-    rc = dispatch_w13<uint16_t>((const uint16_t*)x, T_, H, I, K, slots, (const uint16_t*)w13,
-                                w13_stride, (uint16_t*)act, st, ev);
-    if (rc == WISP_OK)
-      rc = dispatch_w2<uint16_t>((const uint16_t*)act, T_, H, I, K, topk_w, slots,
-                                 (const uint16_t*)w2, w2_stride, (uint16_t*)out, st, ev);
-  }
+  LaunchCtl c;
+  c.start = ev_start;
+  c.stop = ev_stop;
+  c.pair_filter = pair_filter;
+  c.want = want;
+  const int rc = dtype == WISP_F32
+      ? dispatch_w13<float>((const float*)x, T_, H, I, K, slots, (const float*)w13, w13_stride,
+                            (float*)act, st, c)
+      : dispatch_w13<uint16_t>((const uint16_t*)x, T_, H, I, K, slots, (const uint16_t*)w13,
+                               w13_stride, (uint16_t*)act, st, c);
   if (rc != WISP_OK) {
-    wisp_set_last_error("shape outside the GEMV kernels' coverage", "wisp_moe_experts");
+    wisp_set_last_error("hidden size outside the GEMV kernels' coverage", "w13 kernel");
     return rc;
   }
   WISP_HIP_TRY(hipGetLastError());
   return WISP_OK;
+}
+
+int gemv_w2(const void* act, int dtype, int T_, int H, int I, int K, const float* topk_w,
+            const int32_t* slots, const void* w2, size_t w2_stride, void* out, hipStream_t st,
+            hipEvent_t ev_start, hipEvent_t ev_stop, const int32_t* skip_if) {
+  if (T_ == 0) return WISP_OK;
+  LaunchCtl c;
+  c.start = ev_start;
+  c.stop = ev_stop;
+  c.skip_if = skip_if;
+  const int rc = dtype == WISP_F32
+      ? dispatch_w2<float>((const float*)act, T_, H, I, K, topk_w, slots, (const float*)w2,
+                           w2_stride, (float*)out, st, c)
+      : dispatch_w2<uint16_t>((const uint16_t*)act, T_, H, I, K, topk_w, slots,
+                              (const uint16_t*)w2, w2_stride, (uint16_t*)out, st, c);
+  if (rc != WISP_OK) {
+    wisp_set_last_error("top_k above 16 is outside the GEMV kernels' coverage", "w2 kernel");
+    return rc;
+  }
+  WISP_HIP_TRY(hipGetLastError());
+  return WISP_OK;
+}
+
+int experts_gemv(const void* x, int dtype, int T_, int H, int I, int K, const float* topk_w,
+                 const int32_t* slots, const void* w13, size_t w13_stride, const void* w2,
+                 size_t w2_stride, void* act, void* out, hipStream_t st, const StageEvents* ev) {
+  int rc = gemv_w13(x, dtype, T_, H, I, K, slots, w13, w13_stride, act, st,
+                    ev ? ev->ev[0] : nullptr, ev ? ev->ev[1] : nullptr, nullptr, 0);
+  if (rc != WISP_OK) return rc;
+  return gemv_w2(act, dtype, T_, H, I, K, topk_w, slots, w2, w2_stride, out, st,
+                 ev ? ev->ev[2] : nullptr, ev ? ev->ev[3] : nullptr, nullptr);
 }
 
 }  // namespace wisp

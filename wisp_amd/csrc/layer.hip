@@ -1,16 +1,33 @@
-// The paged MoE layer call: routing, the GPU pager, page-in on a side stream
+// The paged MoE layer call: routing, the GPU pager, page-in on side streams
 // and the expert kernels, orchestrated on the host in C++.
 //
 // Replaces the reference's patched forward (src/wisp/integrations/vllm/
 // fused_moe.py:930-987, 990-1237) and the copy half of ensure_resident
-// (fused_moe.py:338-354).  Per paged call:
-//   1. route (wisp_route_topk_softmax) and pager kernel on the caller's
-//      stream; the pager writes its decision record to pinned host memory;
-//   2. one event sync, then for each token group: the group's copies on the
-//      layer's copy stream (after the previous group's expert kernels have
-//      finished reading the scratch - write-after-read fence), an event, the
-//      caller's stream waits on it (read-after-write fence), then the
-//      group's expert kernels.
+// (fused_moe.py:338-354).
+//
+// Paged call, one token group guaranteed (T*K <= cap, e.g. bs=1 decode):
+//   caller's stream: [route+pager] [w13, pairs that hit] [w2 unless loads]
+//   host:            wait for the decision record; if experts were loaded:
+//                    the copies, then [w13, loaded pairs] [w2].
+// The expert kernels of an all-hit call are already queued behind the pager,
+// so the GPU never waits for the host; on a miss call the hit experts'
+// gate/up GEMV runs while the host reads the record.  Nothing on the GPU
+// waits on a flag: the guards are a per-pair filter and a skip word the
+// pager kernel wrote.
+//
+// Paged call, several groups possible: route (fused into the pager for
+// T <= 8), pager, one sync, then per group: copies, the group's expert
+// kernels.
+//
+// Page-in copies run by default on the caller's stream, where stream order
+// is both fences (a copy follows the kernels that read the slot before it;
+// the kernels that read the slot follow the copy).  With side streams
+// (pagein_streams 1 or 2) each copy stream first waits on an event recorded
+// after the last kernels that read the scratch (write-after-read) and the
+// caller's stream waits on an event after the copies (read-after-write).
+// Measured on MI355X, each cross-queue event hop adds ~20 us of latency, so
+// side streams only pay off when there is independent work to overlap.
+//
 // Resident mode (cap == E, identity map) skips the pager and the sync and
 // reads expert e from slot e.
 #include <string.h>
@@ -32,9 +49,17 @@ extern "C" int wisp_abi_version(void) { return 1; }
 
 namespace wisp {
 
-int launch_pager(const int32_t* ids, int T, int K, int E, int cap, int single_group,
-                 int32_t* map, int32_t* s2e, int64_t* tick, int64_t* ctr, int32_t* slots,
-                 int32_t* rec, int rec_words, hipStream_t stream);
+int launch_pager(const int32_t* ids, const void* logits, int logits_dtype, int renorm,
+                 float* topk_w, int32_t* topk_ids, int T, int K, int E, int cap,
+                 int single_group, int32_t* map, int32_t* s2e, int64_t* tick, int64_t* ctr,
+                 int32_t* slots, int32_t* flags, int32_t* rec, int rec_words,
+                 hipStream_t stream);
+int gemv_w13(const void* x, int dtype, int T, int H, int I, int K, const int32_t* slots,
+             const void* w13, size_t w13_stride, void* act, hipStream_t st,
+             hipEvent_t ev_start, hipEvent_t ev_stop, const int32_t* pair_filter, int want);
+int gemv_w2(const void* act, int dtype, int T, int H, int I, int K, const float* topk_w,
+            const int32_t* slots, const void* w2, size_t w2_stride, void* out, hipStream_t st,
+            hipEvent_t ev_start, hipEvent_t ev_stop, const int32_t* skip_if);
 int experts_gemv(const void* x, int dtype, int T, int H, int I, int K, const float* topk_w,
                  const int32_t* slots, const void* w13, size_t w13_stride, const void* w2,
                  size_t w2_stride, void* act, void* out, hipStream_t st, const StageEvents* ev);
@@ -45,64 +70,64 @@ int experts_mfma(const void* x, int T, int H, int I, int K, const float* topk_w,
 namespace {
 
 constexpr int kEventRing = 4;
-constexpr int kProfRing = 256;
-
-// Dispatch-timestamp timing of the two expert kernels of the first group of
-// a call (see StageEvents).
-struct ProfSlot {
-  StageEvents se = {};
-  bool pending = false;
-};
+constexpr int kCopyStreams = 2;
+constexpr int kProfRing = 512;
 
 size_t elem_size(int dtype) { return dtype == WISP_F32 ? 4 : 2; }
 
+// One timed kernel launch (dispatch timestamps).
+struct ProfLaunch {
+  hipEvent_t start = nullptr, stop = nullptr;
+  int kind = 0;          // 0: w13 kernel, 1: w2 kernel
+  bool pending = false;
+  bool counted = true;   // false for a speculative launch that found nothing to do
+};
+
 struct Layer {
   wisp_layer_desc d;
-  hipStream_t copy_stream = nullptr;
+  int nstreams = 0;  // side copy streams in use (0: the caller's stream)
+  hipStream_t copy[kCopyStreams] = {};
   hipEvent_t ev_decided = nullptr;
-  hipEvent_t ev_copy[kEventRing] = {};
+  hipEvent_t ev_copy[kCopyStreams][kEventRing] = {};
   hipEvent_t ev_gemm[kEventRing] = {};
   hipEvent_t ev_pin_start = nullptr, ev_pin_end = nullptr;
   bool pin_pending = false;
   double pin_bytes_pending = 0;
   double pin_ms_total = 0, pin_bytes_total = 0;
-  int64_t pin_calls = 0;
   bool fused_slab = false;
   size_t es = 2;
   bool profile = false;
   int prof_next = 0;
-  ProfSlot prof[kProfRing];
+  ProfLaunch prof[kProfRing];
   double prof_ms[2] = {0, 0};
-  int64_t prof_n = 0;
+  int64_t prof_calls = 0;
 };
 
-void prof_harvest(Layer& L, ProfSlot& p) {
+void prof_harvest(Layer& L, ProfLaunch& p) {
   if (!p.pending) return;
-  float a = 0.f, b = 0.f;
-  if (hipEventSynchronize(p.se.ev[3]) == hipSuccess &&
-      hipEventElapsedTime(&a, p.se.ev[0], p.se.ev[1]) == hipSuccess &&
-      hipEventElapsedTime(&b, p.se.ev[2], p.se.ev[3]) == hipSuccess) {
-    L.prof_ms[0] += a;
-    L.prof_ms[1] += b;
-    L.prof_n += 1;
-  }
+  float ms = 0.f;
+  if (p.counted && hipEventSynchronize(p.stop) == hipSuccess &&
+      hipEventElapsedTime(&ms, p.start, p.stop) == hipSuccess)
+    L.prof_ms[p.kind] += ms;
   p.pending = false;
 }
 
-// Next free profiling slot (harvesting whatever it held), or null when off.
-ProfSlot* prof_begin(Layer& L) {
+// Next timing slot for a launch of `kind` (harvesting what it held), or null
+// when timing is off.
+ProfLaunch* prof_begin(Layer& L, int kind) {
   if (!L.profile) return nullptr;
-  ProfSlot& p = L.prof[L.prof_next];
+  ProfLaunch& p = L.prof[L.prof_next];
   L.prof_next = (L.prof_next + 1) % kProfRing;
   prof_harvest(L, p);
-  if (!p.se.ev[0]) {
-    for (int i = 0; i < 4; ++i)
-      if (hipEventCreate(&p.se.ev[i]) != hipSuccess) return nullptr;
-  }
+  if (!p.start && (hipEventCreate(&p.start) != hipSuccess ||
+                   hipEventCreate(&p.stop) != hipSuccess))
+    return nullptr;
+  p.kind = kind;
+  p.counted = true;
   return &p;
 }
 
-__global__ void identity_kernel(int32_t* map, int32_t* s2e, int64_t* tick, int E) {
+__global__ void identity_kernel(int32_t* map, int32_t* s2e, int E) {
   const int e = blockIdx.x * blockDim.x + threadIdx.x;
   if (e < E) {
     map[e] = e;
@@ -110,8 +135,9 @@ __global__ void identity_kernel(int32_t* map, int32_t* s2e, int64_t* tick, int E
   }
 }
 
-// Copies of `n` loaded (expert, slot) pairs.
-int issue_copies(Layer& L, const int32_t* pairs, int n, hipStream_t cs, double* bytes) {
+// Copies of `n` loaded (expert, slot) pairs on `st`, or alternating over the
+// side streams so one engine's per-copy setup overlaps the other's transfer.
+int issue_copies(Layer& L, const int32_t* pairs, int n, double* bytes, hipStream_t st) {
   const size_t es = L.es;
   const size_t w13_bytes = L.d.w13_elems * es;
   const size_t w2_bytes = L.d.w2_elems * es;
@@ -121,6 +147,7 @@ int issue_copies(Layer& L, const int32_t* pairs, int n, hipStream_t cs, double* 
       wisp_set_last_error("decision record holds an out-of-range pair", "page-in");
       return WISP_ERR_INVALID;
     }
+    hipStream_t cs = L.nstreams ? L.copy[j % L.nstreams] : st;
     char* d13 = (char*)L.d.scratch_w13 + (size_t)s * L.d.scratch_w13_stride * es;
     const char* m13 = (const char*)L.d.master_w13 + (size_t)e * L.d.master_w13_stride * es;
     if (L.fused_slab) {
@@ -139,39 +166,92 @@ int issue_copies(Layer& L, const int32_t* pairs, int n, hipStream_t cs, double* 
 void harvest_pagein_timing(Layer& L) {
   if (!L.pin_pending) return;
   float ms = 0.f;
-  if (hipEventElapsedTime(&ms, L.ev_pin_start, L.ev_pin_end) == hipSuccess) {
+  if (hipEventSynchronize(L.ev_pin_end) == hipSuccess &&
+      hipEventElapsedTime(&ms, L.ev_pin_start, L.ev_pin_end) == hipSuccess) {
     L.pin_ms_total += ms;
     L.pin_bytes_total += L.pin_bytes_pending;
-    L.pin_calls += 1;
   }
   L.pin_pending = false;
   L.pin_bytes_pending = 0;
 }
 
-int experts(Layer& L, const void* x, int T, int K, const float* w, const int32_t* slots,
-            void* act, void* out, int algo, hipStream_t st, bool timed) {
-  const wisp_layer_desc& d = L.d;
-  ProfSlot* p = timed && T > 0 ? prof_begin(L) : nullptr;
-  const StageEvents* se = p ? &p->se : nullptr;
-  int rc;
-  if (algo == WISP_ALGO_MFMA)
-    rc = experts_mfma(x, T, d.hidden, d.inter, K, w, slots, d.scratch_w13, d.scratch_w13_stride,
-                      d.scratch_w2, d.scratch_w2_stride, act, out, st, se);
-  else
-    rc = experts_gemv(x, d.dtype, T, d.hidden, d.inter, K, w, slots, d.scratch_w13,
-                      d.scratch_w13_stride, d.scratch_w2, d.scratch_w2_stride, act, out, st, se);
+// Page-in of `n` pairs.  On the caller's stream the copies simply follow
+// the queued kernels.  On side streams every copy stream first waits on
+// `after` (if any), copies run, and `st` waits for all of them; `slot` picks
+// the event ring entry.
+int page_in(Layer& L, const int32_t* pairs, int n, hipEvent_t after, int slot, hipStream_t st) {
+  harvest_pagein_timing(L);
+  if (L.nstreams == 0) {
+    WISP_HIP_TRY(hipEventRecord(L.ev_pin_start, st));
+    int rc = issue_copies(L, pairs, n, &L.pin_bytes_pending, st);
+    if (rc != WISP_OK) return rc;
+    WISP_HIP_TRY(hipEventRecord(L.ev_pin_end, st));
+    L.pin_pending = true;
+    return WISP_OK;
+  }
+  if (after)
+    for (int c = 0; c < L.nstreams; ++c)
+      WISP_HIP_TRY(hipStreamWaitEvent(L.copy[c], after, 0));
+  WISP_HIP_TRY(hipEventRecord(L.ev_pin_start, L.copy[0]));
+  for (int c = 1; c < L.nstreams; ++c)
+    WISP_HIP_TRY(hipStreamWaitEvent(L.copy[c], L.ev_pin_start, 0));
+  int rc = issue_copies(L, pairs, n, &L.pin_bytes_pending, st);
   if (rc != WISP_OK) return rc;
-  if (p) p->pending = true;
+  for (int c = 1; c < L.nstreams; ++c) {
+    WISP_HIP_TRY(hipEventRecord(L.ev_copy[c][slot % kEventRing], L.copy[c]));
+    WISP_HIP_TRY(hipStreamWaitEvent(L.copy[0], L.ev_copy[c][slot % kEventRing], 0));
+  }
+  WISP_HIP_TRY(hipEventRecord(L.ev_pin_end, L.copy[0]));
+  L.pin_pending = true;
+  WISP_HIP_TRY(hipStreamWaitEvent(st, L.ev_pin_end, 0));
   return WISP_OK;
 }
 
-// Kernel choice depends only on the whole call's T and the dtype, never on
-// the grouping, so paged and resident runs of one batch use one kernel.
-int choose_algo(int algo, int dtype, int T) {
-  (void)dtype;
+int w13(Layer& L, const void* x, int T, int K, const int32_t* slots, void* act, hipStream_t st,
+        const int32_t* filter, int want) {
+  const wisp_layer_desc& d = L.d;
+  ProfLaunch* p = prof_begin(L, 0);
+  int rc = gemv_w13(x, d.dtype, T, d.hidden, d.inter, K, slots, d.scratch_w13,
+                    d.scratch_w13_stride, act, st, p ? p->start : nullptr,
+                    p ? p->stop : nullptr, filter, want);
+  if (p && rc == WISP_OK) p->pending = true;
+  return rc;
+}
+
+int w2(Layer& L, const void* act, int T, int K, const float* w, const int32_t* slots, void* out,
+       hipStream_t st, const int32_t* skip_if, ProfLaunch** launched) {
+  const wisp_layer_desc& d = L.d;
+  ProfLaunch* p = prof_begin(L, 1);
+  int rc = gemv_w2(act, d.dtype, T, d.hidden, d.inter, K, w, slots, d.scratch_w2,
+                   d.scratch_w2_stride, out, st, p ? p->start : nullptr, p ? p->stop : nullptr,
+                   skip_if);
+  if (p && rc == WISP_OK) p->pending = true;
+  if (launched) *launched = p;
+  return rc;
+}
+
+// Both expert stages for T tokens (any algorithm, no filters).
+int experts(Layer& L, const void* x, int T, int K, const float* w, const int32_t* slots,
+            void* act, void* out, int algo, hipStream_t st) {
+  const wisp_layer_desc& d = L.d;
+  if (algo == WISP_ALGO_MFMA)
+    return experts_mfma(x, T, d.hidden, d.inter, K, w, slots, d.scratch_w13, d.scratch_w13_stride,
+                        d.scratch_w2, d.scratch_w2_stride, act, out, st, nullptr);
+  int rc = w13(L, x, T, K, slots, act, st, nullptr, 0);
+  if (rc != WISP_OK) return rc;
+  return w2(L, act, T, K, w, slots, out, st, nullptr, nullptr);
+}
+
+// Kernel choice depends only on the whole call's T, K and the dtype, never
+// on the grouping or the slots, so paged and resident runs of one batch use
+// one kernel.
+int choose_algo(const Layer& L, int algo, int T, int K) {
+  (void)L;
   (void)T;
-  if (algo != WISP_ALGO_AUTO) return algo;
-  return WISP_ALGO_GEMV;
+  (void)K;
+  if (algo == WISP_ALGO_AUTO) return WISP_ALGO_GEMV;
+  if (algo != WISP_ALGO_GEMV && algo != WISP_ALGO_MFMA) return -1;
+  return algo;
 }
 
 // Copies and expert kernels for groups [0, ngroups) of a decision record.
@@ -181,36 +261,21 @@ int run_groups(Layer& L, const int32_t* rec, int T, int K, int ngroups, bool com
   const RecordLayout RL(T, K);
   const size_t row = (size_t)L.d.hidden * L.es;
   int last_gemm = -1;
-  bool timing_started = false;
   for (int g = 0; g < ngroups; ++g) {
     const int32_t* G = rec + RL.group_base(g);
     const int t0 = G[0], t1 = G[1], ld_off = G[6], n_ld = G[7];
     if (n_ld > 0) {
-      if (last_gemm >= 0)
-        WISP_HIP_TRY(hipStreamWaitEvent(L.copy_stream, L.ev_gemm[last_gemm % kEventRing], 0));
-      if (!timing_started) {
-        harvest_pagein_timing(L);
-        WISP_HIP_TRY(hipEventRecord(L.ev_pin_start, L.copy_stream));
-        timing_started = true;
-      }
-      int rc = issue_copies(L, rec + RL.loaded_base() + 2 * ld_off, n_ld, L.copy_stream,
-                            &L.pin_bytes_pending);
+      int rc = page_in(L, rec + RL.loaded_base() + 2 * ld_off, n_ld,
+                       last_gemm >= 0 ? L.ev_gemm[last_gemm % kEventRing] : nullptr, g, st);
       if (rc != WISP_OK) return rc;
-      WISP_HIP_TRY(hipEventRecord(L.ev_copy[g % kEventRing], L.copy_stream));
-      WISP_HIP_TRY(hipStreamWaitEvent(st, L.ev_copy[g % kEventRing], 0));
     }
     if (compute && t1 > t0) {
       int rc = experts(L, (const char*)x + (size_t)t0 * row, t1 - t0, K, topk_w + (size_t)t0 * K,
-                       slots + (size_t)t0 * K, act, (char*)out + (size_t)t0 * row, algo, st,
-                       g == 0);
+                       slots + (size_t)t0 * K, act, (char*)out + (size_t)t0 * row, algo, st);
       if (rc != WISP_OK) return rc;
       WISP_HIP_TRY(hipEventRecord(L.ev_gemm[g % kEventRing], st));
       last_gemm = g;
     }
-  }
-  if (timing_started) {
-    WISP_HIP_TRY(hipEventRecord(L.ev_pin_end, L.copy_stream));
-    L.pin_pending = true;
   }
   return WISP_OK;
 }
@@ -226,7 +291,8 @@ int32_t* record_device_ptr(int32_t* rec) {
 
 int check_ws(const wisp_workspace* ws, int T, int K) {
   if (!ws || (int64_t)T * K > ws->max_pairs || !ws->topk_w || !ws->topk_ids || !ws->slots ||
-      !ws->act || !ws->record || ws->record_words < RecordLayout(T, K).words()) {
+      !ws->flags || !ws->act || !ws->record ||
+      ws->record_words < RecordLayout(T, K).words()) {
     wisp_set_last_error("workspace too small or missing", "wisp_layer_forward");
     return WISP_ERR_INVALID;
   }
@@ -252,7 +318,8 @@ extern "C" int wisp_layer_create(const wisp_layer_desc* desc, void** handle) {
       !d.lru_tick || !d.counters || d.scratch_w13_stride < d.w13_elems ||
       d.scratch_w2_stride < d.w2_elems || d.master_w13_stride < d.w13_elems ||
       d.master_w2_stride < d.w2_elems ||
-      (d.mode == WISP_MODE_RESIDENT && d.cap != d.num_experts)) {
+      (d.mode == WISP_MODE_RESIDENT && d.cap != d.num_experts) || d.pagein_streams < 0 ||
+      d.pagein_streams > kCopyStreams) {
     wisp_set_last_error("invalid layer descriptor", "wisp_layer_create");
     return WISP_ERR_INVALID;
   }
@@ -260,17 +327,20 @@ extern "C" int wisp_layer_create(const wisp_layer_desc* desc, void** handle) {
   Layer* L = new Layer();
   L->d = d;
   L->es = es;
+  L->nstreams = d.pagein_streams;
   const size_t w13_elems = d.w13_elems;
   L->fused_slab = d.master_w13_stride == d.master_w2_stride &&
                   d.scratch_w13_stride == d.scratch_w2_stride &&
                   (const char*)d.master_w2 == (const char*)d.master_w13 + w13_elems * es &&
                   (const char*)d.scratch_w2 == (const char*)d.scratch_w13 + w13_elems * es;
-  hipError_t e = hipStreamCreateWithFlags(&L->copy_stream, hipStreamNonBlocking);
-  if (e == hipSuccess) e = hipEventCreateWithFlags(&L->ev_decided, hipEventDisableTiming);
-  for (int i = 0; i < kEventRing && e == hipSuccess; ++i) {
-    e = hipEventCreateWithFlags(&L->ev_copy[i], hipEventDisableTiming);
-    if (e == hipSuccess) e = hipEventCreateWithFlags(&L->ev_gemm[i], hipEventDisableTiming);
+  hipError_t e = hipEventCreateWithFlags(&L->ev_decided, hipEventDisableTiming);
+  for (int c = 0; c < kCopyStreams && e == hipSuccess; ++c) {
+    e = hipStreamCreateWithFlags(&L->copy[c], hipStreamNonBlocking);
+    for (int i = 0; i < kEventRing && e == hipSuccess; ++i)
+      e = hipEventCreateWithFlags(&L->ev_copy[c][i], hipEventDisableTiming);
   }
+  for (int i = 0; i < kEventRing && e == hipSuccess; ++i)
+    e = hipEventCreateWithFlags(&L->ev_gemm[i], hipEventDisableTiming);
   if (e == hipSuccess) e = hipEventCreate(&L->ev_pin_start);
   if (e == hipSuccess) e = hipEventCreate(&L->ev_pin_end);
   if (e != hipSuccess) {
@@ -283,32 +353,38 @@ extern "C" int wisp_layer_create(const wisp_layer_desc* desc, void** handle) {
 }
 
 extern "C" int wisp_layer_destroy(void* handle) {
+  using namespace wisp;
   Layer* L = (Layer*)handle;
   if (!L) return WISP_OK;
-  if (L->copy_stream) (void)hipStreamSynchronize(L->copy_stream);
-  for (int i = 0; i < wisp::kEventRing; ++i) {
-    if (L->ev_copy[i]) (void)hipEventDestroy(L->ev_copy[i]);
+  for (int c = 0; c < kCopyStreams; ++c)
+    if (L->copy[c]) (void)hipStreamSynchronize(L->copy[c]);
+  for (int i = 0; i < kEventRing; ++i) {
+    for (int c = 0; c < kCopyStreams; ++c)
+      if (L->ev_copy[c][i]) (void)hipEventDestroy(L->ev_copy[c][i]);
     if (L->ev_gemm[i]) (void)hipEventDestroy(L->ev_gemm[i]);
   }
   if (L->ev_decided) (void)hipEventDestroy(L->ev_decided);
   if (L->ev_pin_start) (void)hipEventDestroy(L->ev_pin_start);
   if (L->ev_pin_end) (void)hipEventDestroy(L->ev_pin_end);
-  for (int i = 0; i < wisp::kProfRing; ++i)
-    for (int j = 0; j < 4; ++j)
-      if (L->prof[i].se.ev[j]) (void)hipEventDestroy(L->prof[i].se.ev[j]);
-  if (L->copy_stream) (void)hipStreamDestroy(L->copy_stream);
+  for (int i = 0; i < kProfRing; ++i) {
+    if (L->prof[i].start) (void)hipEventDestroy(L->prof[i].start);
+    if (L->prof[i].stop) (void)hipEventDestroy(L->prof[i].stop);
+  }
+  for (int c = 0; c < kCopyStreams; ++c)
+    if (L->copy[c]) (void)hipStreamDestroy(L->copy[c]);
   delete L;
   return WISP_OK;
 }
 
 extern "C" int wisp_layer_set_scratch(void* handle, void* scratch_w13, void* scratch_w2, int cap,
                                       int32_t* slot_to_expert, int64_t* lru_tick) {
+  using namespace wisp;
   Layer* L = (Layer*)handle;
   if (!L || !scratch_w13 || !scratch_w2 || cap < 1 || cap > L->d.num_experts ||
       !slot_to_expert || !lru_tick)
     return WISP_ERR_INVALID;
-  (void)hipStreamSynchronize(L->copy_stream);
-  L->pin_pending = false;
+  for (int c = 0; c < kCopyStreams; ++c) (void)hipStreamSynchronize(L->copy[c]);
+  harvest_pagein_timing(*L);
   const size_t es = L->es, w13_elems = L->d.w13_elems;
   L->d.scratch_w13 = scratch_w13;
   L->d.scratch_w2 = scratch_w2;
@@ -346,30 +422,65 @@ extern "C" int wisp_layer_forward(void* handle, const void* x, const void* logit
                         "wisp_layer_forward");
     return WISP_ERR_UNSUPPORTED;
   }
-  const int a = choose_algo(algo, d.dtype, T);
-  if (a == WISP_ALGO_MFMA && d.dtype != WISP_BF16) return WISP_ERR_UNSUPPORTED;
+  const int a = choose_algo(*L, algo, T, K);
+  if (a < 0 || (a == WISP_ALGO_MFMA && d.dtype != WISP_BF16)) {
+    wisp_set_last_error("requested expert algorithm does not cover this call",
+                        "wisp_layer_forward");
+    return WISP_ERR_UNSUPPORTED;
+  }
+  if (L->profile) L->prof_calls += 1;
 
   if (d.mode == WISP_MODE_RESIDENT) {
     rc = wisp_route_topk_softmax(logits, logits_dtype, T, d.num_experts, K, renormalize,
                                  ws->topk_w, ws->topk_ids, d.counters + kForward, stream);
     if (rc != WISP_OK) return rc;
-    return experts(*L, x, T, K, ws->topk_w, ws->topk_ids, ws->act, out, a, st, true);
+    return experts(*L, x, T, K, ws->topk_w, ws->topk_ids, ws->act, out, a, st);
   }
 
-  rc = wisp_route_topk_softmax(logits, logits_dtype, T, d.num_experts, K, renormalize,
-                               ws->topk_w, ws->topk_ids, nullptr, stream);
-  if (rc != WISP_OK) return rc;
-  rc = launch_pager(ws->topk_ids, T, K, d.num_experts, d.cap, 0, d.expert_map,
-                    d.slot_to_expert, d.lru_tick, d.counters, ws->slots,
-                    record_device_ptr(ws->record), ws->record_words, st);
+  const bool fuse_route = T <= kFusedRouteTokens;
+  if (!fuse_route) {
+    rc = wisp_route_topk_softmax(logits, logits_dtype, T, d.num_experts, K, renormalize,
+                                 ws->topk_w, ws->topk_ids, nullptr, stream);
+    if (rc != WISP_OK) return rc;
+  }
+  int32_t* rec_dev = record_device_ptr(ws->record);
+  rc = launch_pager(ws->topk_ids, fuse_route ? logits : nullptr, logits_dtype, renormalize,
+                    ws->topk_w, ws->topk_ids, T, K, d.num_experts, d.cap, 0, d.expert_map,
+                    d.slot_to_expert, d.lru_tick, d.counters, ws->slots, ws->flags, rec_dev,
+                    ws->record_words, st);
   if (rc != WISP_OK) return rc;
   WISP_HIP_TRY(hipEventRecord(L->ev_decided, st));
+
+  // One group is certain when every routed pair could be distinct and still
+  // fit: then the expert kernels go in right behind the pager.
+  const bool speculate = a == WISP_ALGO_GEMV && T > 0 && (int64_t)T * K <= d.cap;
+  ProfLaunch* spec_w2 = nullptr;
+  if (speculate) {
+    rc = w13(*L, x, T, K, ws->slots, ws->act, st, ws->flags + 1, 0);
+    if (rc == WISP_OK)
+      rc = w2(*L, ws->act, T, K, ws->topk_w, ws->slots, out, st, ws->flags, &spec_w2);
+    if (rc != WISP_OK) return rc;
+  }
+
   WISP_HIP_TRY(hipEventSynchronize(L->ev_decided));
   const int32_t* rec = ws->record;
   const int status = rec[kRecStatus];
   if (status == WISP_ERR_INVALID) {
     wisp_set_last_error("routed expert id out of range", "wisp_layer_forward");
     return status;
+  }
+  if (speculate) {
+    if (status != WISP_OK) return status;
+    const RecordLayout RL(T, K);
+    const int32_t* G = rec + RL.group_base(0);
+    const int n_ld = rec[kRecGroupsDone] > 0 ? G[7] : 0;
+    if (n_ld == 0) return WISP_OK;  // the queued kernels computed everything
+    if (spec_w2) spec_w2->counted = false;  // it found loads and exited
+    rc = page_in(*L, rec + RL.loaded_base() + 2 * G[6], n_ld, nullptr, 0, st);
+    if (rc != WISP_OK) return rc;
+    rc = w13(*L, x, T, K, ws->slots, ws->act, st, ws->flags + 1, 1);
+    if (rc == WISP_OK) rc = w2(*L, ws->act, T, K, ws->topk_w, ws->slots, out, st, nullptr, nullptr);
+    return rc;
   }
   rc = run_groups(*L, rec, T, K, rec[kRecGroupsDone], status == WISP_OK, x, ws->topk_w,
                   ws->slots, ws->act, out, a, st);
@@ -389,9 +500,9 @@ extern "C" int wisp_layer_ensure_resident(void* handle, const int32_t* ids, int 
     return WISP_ERR_INVALID;
   hipStream_t st = (hipStream_t)stream;
   const wisp_layer_desc& d = L->d;
-  int rc = launch_pager(ids, n, 1, d.num_experts, d.cap, 1, d.expert_map, d.slot_to_expert,
-                        d.lru_tick, d.counters, nullptr, record_device_ptr(ws->record),
-                        ws->record_words, st);
+  int rc = launch_pager(ids, nullptr, WISP_F32, 0, nullptr, nullptr, n, 1, d.num_experts, d.cap,
+                        1, d.expert_map, d.slot_to_expert, d.lru_tick, d.counters, nullptr,
+                        nullptr, record_device_ptr(ws->record), ws->record_words, st);
   if (rc != WISP_OK) return rc;
   WISP_HIP_TRY(hipEventRecord(L->ev_decided, st));
   WISP_HIP_TRY(hipEventSynchronize(L->ev_decided));
@@ -402,15 +513,8 @@ extern "C" int wisp_layer_ensure_resident(void* handle, const int32_t* ids, int 
   const RecordLayout RL(n, 1);
   const int32_t* G = rec + RL.group_base(0);
   if (rec[kRecGroupsDone] > 0 && G[7] > 0) {
-    harvest_pagein_timing(*L);
-    WISP_HIP_TRY(hipEventRecord(L->ev_pin_start, L->copy_stream));
-    rc = issue_copies(*L, rec + RL.loaded_base() + 2 * G[6], G[7], L->copy_stream,
-                      &L->pin_bytes_pending);
+    rc = page_in(*L, rec + RL.loaded_base() + 2 * G[6], G[7], nullptr, 0, st);
     if (rc != WISP_OK) return rc;
-    WISP_HIP_TRY(hipEventRecord(L->ev_pin_end, L->copy_stream));
-    L->pin_pending = true;
-    WISP_HIP_TRY(hipEventRecord(L->ev_copy[0], L->copy_stream));
-    WISP_HIP_TRY(hipStreamWaitEvent(st, L->ev_copy[0], 0));
   }
   if (status == WISP_ERR_SUBBATCH)
     wisp_set_last_error("working set exceeds cap_experts; the caller must sub-batch",
@@ -433,13 +537,10 @@ extern "C" int wisp_layer_prime_identity(void* handle, wisp_stream_t stream) {
     pairs[2 * e] = e;
     pairs[2 * e + 1] = e;
   }
-  double bytes = 0;
-  int rc = issue_copies(*L, pairs.data(), d.num_experts, L->copy_stream, &bytes);
+  int rc = page_in(*L, pairs.data(), d.num_experts, nullptr, 0, st);
   if (rc != WISP_OK) return rc;
-  WISP_HIP_TRY(hipEventRecord(L->ev_copy[0], L->copy_stream));
-  WISP_HIP_TRY(hipStreamWaitEvent(st, L->ev_copy[0], 0));
   hipLaunchKernelGGL(identity_kernel, dim3((d.num_experts + 255) / 256), dim3(256), 0, st,
-                     d.expert_map, d.slot_to_expert, d.lru_tick, d.num_experts);
+                     d.expert_map, d.slot_to_expert, d.num_experts);
   WISP_HIP_TRY(hipGetLastError());
   return WISP_OK;
 }
@@ -452,20 +553,19 @@ extern "C" int wisp_layer_last_pagein(void* handle, float* ms, double* bytes) {
   if (bytes) *bytes = L->pin_bytes_total;
   L->pin_ms_total = 0;
   L->pin_bytes_total = 0;
-  L->pin_calls = 0;
   return WISP_OK;
 }
 
 extern "C" int wisp_layer_profile(void* handle, int enable, double* w13_ms, double* w2_ms,
-                                  int64_t* launches) {
+                                  int64_t* calls) {
   Layer* L = (Layer*)handle;
   if (!L) return WISP_ERR_INVALID;
   for (int i = 0; i < wisp::kProfRing; ++i) wisp::prof_harvest(*L, L->prof[i]);
   if (w13_ms) *w13_ms = L->prof_ms[0];
   if (w2_ms) *w2_ms = L->prof_ms[1];
-  if (launches) *launches = L->prof_n;
+  if (calls) *calls = L->prof_calls;
   L->prof_ms[0] = L->prof_ms[1] = 0;
-  L->prof_n = 0;
+  L->prof_calls = 0;
   L->profile = enable != 0;
   return WISP_OK;
 }
@@ -515,7 +615,7 @@ extern "C" int wisp_moe_experts(const void* x, int dtype, int T, int H, int I, i
     wisp_set_last_error("H, I and buffers must be 16-byte aligned", "wisp_moe_experts");
     return WISP_ERR_UNSUPPORTED;
   }
-  const int a = choose_algo(algo, dtype, T);
+  const int a = algo == WISP_ALGO_AUTO ? WISP_ALGO_GEMV : algo;
   if (a == WISP_ALGO_MFMA) {
     if (dtype != WISP_BF16) return WISP_ERR_UNSUPPORTED;
     return experts_mfma(x, T, H, I, K, topk_w, slots, w13, w13_stride, w2, w2_stride, act, out,

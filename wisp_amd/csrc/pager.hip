@@ -20,6 +20,7 @@
 
 #include "common.h"
 #include "pager_core.h"
+#include "route_core.h"
 
 namespace wisp {
 
@@ -268,6 +269,7 @@ struct PagerSmem {
   int32_t s2e[kMaxExperts];
   int64_t tick[kMaxExperts];
   uint32_t need[kMaxExperts / 32];
+  uint32_t loaded[kMaxExperts / 32];
   int32_t keys[kMaxExperts];
   int32_t order[kMaxExperts];
   int32_t table[kMaxSetTable];
@@ -277,11 +279,25 @@ struct PagerSmem {
   int32_t sorted[kMaxExperts];
 };
 
+struct FusedRouteSmem {
+  int32_t ids[kFusedRouteTokens * kMaxTopK];
+};
+
+// One wavefront.  With `logits` non-null it first routes the T <= 8 tokens
+// (writing topk_w / topk_ids) and takes the ids from LDS; otherwise it reads
+// `ids_in`.  Outputs: device state, slots[p] (slot of pair p, -1 for pairs of
+// a group that was not completed), flags (optional): flags[0] = experts
+// loaded by this call, flags[1 + p] = 1 if pair p's expert was loaded by its
+// group, else 0; and the decision record.
+template <typename TL>
 __global__ __launch_bounds__(64) void pager_kernel(
-    const int32_t* __restrict__ ids, int T, int K, int E, int cap, int single_group,
-    int32_t* __restrict__ map_g, int32_t* __restrict__ s2e_g, int64_t* __restrict__ tick_g,
-    int64_t* __restrict__ ctr_g, int32_t* __restrict__ slots_g, int32_t* __restrict__ rec) {
+    const int32_t* __restrict__ ids_in, const TL* __restrict__ logits, int renorm,
+    float* __restrict__ w_out, int32_t* __restrict__ id_out, int T, int K, int E, int cap,
+    int single_group, int32_t* __restrict__ map_g, int32_t* __restrict__ s2e_g,
+    int64_t* __restrict__ tick_g, int64_t* __restrict__ ctr_g, int32_t* __restrict__ slots_g,
+    int32_t* __restrict__ flags_g, int32_t* __restrict__ rec) {
   __shared__ PagerSmem sm;
+  __shared__ FusedRouteSmem fr;
   const int lane = threadIdx.x;
   const int nwords = (E + 31) >> 5;
   const RecordLayout L(T, K);
@@ -295,6 +311,28 @@ __global__ __launch_bounds__(64) void pager_kernel(
   int64_t clock = ctr_g[kClock];
   int64_t n_forward = ctr_g[kForward], n_miss = ctr_g[kMiss], n_evict = ctr_g[kEvict],
           n_hits = ctr_g[kHits];
+  // Every pair starts as "not computed" (slot -1, not loaded); the same lane
+  // owns pair p for all later writes.
+  for (int p = lane; p < P; p += 64) {
+    if (slots_g) slots_g[p] = -1;
+    if (flags_g) flags_g[1 + p] = 0;
+  }
+
+  const int32_t* ids = ids_in;
+  if (logits) {
+    for (int t = 0; t < T; ++t) {
+      float w;
+      int id;
+      route_token_wave(logits + (size_t)t * E, E, K, renorm, lane, true, &w, &id);
+      if (lane < K) {
+        w_out[t * K + lane] = w;
+        id_out[t * K + lane] = id;
+        fr.ids[t * K + lane] = id;
+      }
+    }
+    wave_lds_sync();
+    ids = fr.ids;
+  }
 
   // Validate ids.
   bool bad = false;
@@ -313,8 +351,11 @@ __global__ __launch_bounds__(64) void pager_kernel(
     while (first || start < T) {
       first = false;
       // ---- plan one group: tokens [start, end) -----------------------
-      for (int w = lane; w < nwords; w += 64) sm.need[w] = 0u;
-      __syncthreads();
+      for (int w = lane; w < nwords; w += 64) {
+        sm.need[w] = 0u;
+        sm.loaded[w] = 0u;
+      }
+      wave_lds_sync();
       int end = start, cnt = 0;
       if (single_group) {
         for (int p = lane; p < P; p += 64) {
@@ -342,7 +383,7 @@ __global__ __launch_bounds__(64) void pager_kernel(
           }
         }
       }
-      __syncthreads();
+      wave_lds_sync();
       const int g = groups_planned++;
       const int t0 = start, t1 = end;
       start = end;
@@ -356,7 +397,7 @@ __global__ __launch_bounds__(64) void pager_kernel(
         if (in) sm.keys[U + popc_below(bb)] = e;
         U += __popcll(bb);
       }
-      __syncthreads();
+      wave_lds_sync();
       // ---- CPython set iteration order of the ascending keys ----------
       if (U <= 64) {
         const int key = lane < U ? sm.keys[lane] : -1;
@@ -365,7 +406,7 @@ __global__ __launch_bounds__(64) void pager_kernel(
       } else if (lane == 0) {
         cpython_set_order(sm.keys, U, sm.order, sm.table, kMaxSetTable);
       }
-      __syncthreads();
+      wave_lds_sync();
 
       // ---- missing experts, in set order -----------------------------
       int nmiss = 0;
@@ -388,7 +429,7 @@ __global__ __launch_bounds__(64) void pager_kernel(
         rec[gb + 0] = t0; rec[gb + 1] = t1; rec[gb + 2] = U; rec[gb + 3] = hits;
         rec[gb + 4] = ev_total; rec[gb + 5] = 0; rec[gb + 6] = ld_total; rec[gb + 7] = 0;
       }
-      __syncthreads();
+      wave_lds_sync();
 
       if (nmiss > 0) {
         // ---- free slots and eviction candidates, ascending slot --------
@@ -407,7 +448,7 @@ __global__ __launch_bounds__(64) void pager_kernel(
           nfree += __popcll(fbits);
           ncand += __popcll(cbits);
         }
-        __syncthreads();
+        wave_lds_sync();
         const int shortfall = nmiss - nfree;
         if (shortfall > ncand) {
           status = WISP_ERR_SUBBATCH;
@@ -426,7 +467,7 @@ __global__ __launch_bounds__(64) void pager_kernel(
             }
             sm.sorted[r] = sm.cand[i];
           }
-          __syncthreads();
+          wave_lds_sync();
           for (int r = lane; r < shortfall; r += 64) {
             const int s = sm.sorted[r];
             const int victim = sm.s2e[s];
@@ -441,7 +482,7 @@ __global__ __launch_bounds__(64) void pager_kernel(
           ev_total += shortfall;
           nfree += shortfall;
           if (lane == 0) rec[gb + 5] = shortfall;
-          __syncthreads();
+          wave_lds_sync();
         }
         clock += 1;
         for (int j = lane; j < nmiss; j += 64) {
@@ -450,6 +491,7 @@ __global__ __launch_bounds__(64) void pager_kernel(
           sm.s2e[s] = e;
           sm.map[e] = s;
           sm.tick[s] = clock;
+          atomicOr(&sm.loaded[e >> 5], 1u << (e & 31));
           const int o = L.loaded_base() + 2 * (ld_total + j);
           rec[o] = e;
           rec[o + 1] = s;
@@ -457,16 +499,20 @@ __global__ __launch_bounds__(64) void pager_kernel(
         n_miss += nmiss;
         ld_total += nmiss;
         if (lane == 0) rec[gb + 7] = nmiss;
-        __syncthreads();
+        wave_lds_sync();
       } else {
         clock += 1;
       }
       for (int j = lane; j < U; j += 64) sm.tick[sm.map[sm.keys[j]]] = clock;
-      __syncthreads();
-      if (slots_g)
-        for (int p = t0 * K + lane; p < t1 * K; p += 64) slots_g[p] = sm.map[ids[p]];
+      wave_lds_sync();
+      for (int p = lane; p < P; p += 64) {
+        if (p < t0 * K || p >= t1 * K) continue;
+        const int e = ids[p];
+        if (slots_g) slots_g[p] = sm.map[e];
+        if (flags_g) flags_g[1 + p] = (sm.loaded[e >> 5] >> (e & 31)) & 1u;
+      }
       groups_done = g + 1;
-      __syncthreads();
+      wave_lds_sync();
     }
   }
 
@@ -481,6 +527,7 @@ __global__ __launch_bounds__(64) void pager_kernel(
     ctr_g[kMiss] = n_miss;
     ctr_g[kEvict] = n_evict;
     ctr_g[kHits] = n_hits;
+    if (flags_g) flags_g[0] = ld_total;
     rec[kRecGroupsDone] = groups_done;
     rec[kRecGroupsPlanned] = groups_planned;
     rec[kRecFailGroup] = fail_group;
@@ -494,17 +541,28 @@ __global__ __launch_bounds__(64) void pager_kernel(
 
 }  // namespace
 
-int launch_pager(const int32_t* ids, int T, int K, int E, int cap, int single_group,
-                 int32_t* map, int32_t* s2e, int64_t* tick, int64_t* ctr, int32_t* slots,
-                 int32_t* rec, int rec_words, hipStream_t stream) {
+int launch_pager(const int32_t* ids, const void* logits, int logits_dtype, int renorm,
+                 float* topk_w, int32_t* topk_ids, int T, int K, int E, int cap,
+                 int single_group, int32_t* map, int32_t* s2e, int64_t* tick, int64_t* ctr,
+                 int32_t* slots, int32_t* flags, int32_t* rec, int rec_words,
+                 hipStream_t stream) {
   RecordLayout L(T, K);
   if (T < 0 || K < 1 || K > kMaxTopK || E < 1 || E > kMaxExperts || cap < 1 || cap > E ||
-      rec_words < L.words() || !map || !s2e || !tick || !ctr || !rec || (T > 0 && !ids)) {
+      rec_words < L.words() || !map || !s2e || !tick || !ctr || !rec ||
+      (T > 0 && !ids && !logits) ||
+      (logits && (T > kFusedRouteTokens || !topk_w || !topk_ids ||
+                  (logits_dtype != WISP_F32 && logits_dtype != WISP_BF16)))) {
     wisp_set_last_error("invalid pager arguments", "wisp_pager_decide");
     return WISP_ERR_INVALID;
   }
-  hipLaunchKernelGGL(pager_kernel, dim3(1), dim3(64), 0, stream, ids, T, K, E, cap,
-                     single_group, map, s2e, tick, ctr, slots, rec);
+  if (logits && logits_dtype == WISP_BF16)
+    hipLaunchKernelGGL(pager_kernel<uint16_t>, dim3(1), dim3(64), 0, stream, ids,
+                       (const uint16_t*)logits, renorm, topk_w, topk_ids, T, K, E, cap,
+                       single_group, map, s2e, tick, ctr, slots, flags, rec);
+  else
+    hipLaunchKernelGGL(pager_kernel<float>, dim3(1), dim3(64), 0, stream, ids,
+                       (const float*)logits, renorm, topk_w, topk_ids, T, K, E, cap,
+                       single_group, map, s2e, tick, ctr, slots, flags, rec);
   WISP_HIP_TRY(hipGetLastError());
   return WISP_OK;
 }
@@ -516,9 +574,9 @@ extern "C" int wisp_pager_decide(const int32_t* topk_ids, int T, int K, int E, i
                                  int32_t* slot_to_expert, int64_t* lru_tick,
                                  int64_t* counters, int32_t* slots, int32_t* record,
                                  int record_words, wisp_stream_t stream) {
-  return wisp::launch_pager(topk_ids, T, K, E, cap, single_group, expert_map, slot_to_expert,
-                            lru_tick, counters, slots, record, record_words,
-                            (hipStream_t)stream);
+  return wisp::launch_pager(topk_ids, nullptr, WISP_F32, 0, nullptr, nullptr, T, K, E, cap,
+                            single_group, expert_map, slot_to_expert, lru_tick, counters, slots,
+                            nullptr, record, record_words, (hipStream_t)stream);
 }
 
 extern "C" int wisp_pager_decide_host(const int32_t* topk_ids, int T, int K, int E, int cap,

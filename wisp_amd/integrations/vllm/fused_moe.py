@@ -79,6 +79,19 @@ def _resolve_cap_experts(num_experts: int) -> int:
     return max(2, min(cap, num_experts))
 
 
+def _resolve_pagein_streams() -> int:
+    """``WISP_PAGEIN_STREAMS``: 0 (default) issues page-in copies on the
+    caller's stream; 1 or 2 uses that many side copy streams fenced with
+    events (worth it only when independent work can overlap the copies)."""
+    raw = os.environ.get("WISP_PAGEIN_STREAMS", "0")
+    try:
+        n = int(raw)
+    except ValueError:
+        logger.warning("WISP_PAGEIN_STREAMS=%r is not an int; using 0", raw)
+        return 0
+    return max(0, min(2, n))
+
+
 _DTYPES = {torch.float32: _lib.WISP_F32, torch.bfloat16: _lib.WISP_BF16}
 
 
@@ -97,7 +110,7 @@ class _Workspace:
         self.pairs = 0
         self.record_words = 0
         self.struct = _lib.Workspace()
-        self.topk_w = self.topk_ids = self.slots = self.act = self.record = None
+        self.topk_w = self.topk_ids = self.slots = self.flags = self.act = self.record = None
 
     def ensure(self, T: int, K: int) -> "_lib.Workspace":
         pairs = max(1, T * K)
@@ -108,6 +121,7 @@ class _Workspace:
             self.topk_w = torch.empty(self.pairs, dtype=torch.float32, device=dev)
             self.topk_ids = torch.empty(self.pairs, dtype=torch.int32, device=dev)
             self.slots = torch.empty(self.pairs, dtype=torch.int32, device=dev)
+            self.flags = torch.zeros(self.pairs + 1, dtype=torch.int32, device=dev)
             self.act = torch.empty(self.pairs * self.inter, dtype=self.dtype, device=dev)
         if words > self.record_words:
             self.record_words = max(words, 2 * self.record_words)
@@ -116,6 +130,7 @@ class _Workspace:
         s.max_pairs = self.pairs
         s.topk_w, s.topk_ids = self.topk_w.data_ptr(), self.topk_ids.data_ptr()
         s.slots, s.act = self.slots.data_ptr(), self.act.data_ptr()
+        s.flags = self.flags.data_ptr()
         s.record, s.record_words = self.record.data_ptr(), self.record_words
         return s
 
@@ -192,6 +207,7 @@ class WispMoEState:
         d.num_experts, d.cap = self.num_experts, self.cap_experts
         d.hidden, d.inter = self.hidden, self.inter
         d.dtype = _DTYPES[self.dtype]
+        d.pagein_streams = _resolve_pagein_streams()
         d.w13_elems, d.w2_elems = self._w13_elems, self._w2_elems
         d.mode = _lib.WISP_MODE_RESIDENT if self.mode == _Mode.RESIDENT else _lib.WISP_MODE_PAGED
         d.scratch_w13, d.scratch_w13_stride = self.scratch_w13.data_ptr(), self._slab_elems
@@ -309,14 +325,14 @@ class WispMoEState:
               "pagein_stats")
         return float(ms.value), float(nbytes.value)
 
-    def profile(self, enable: bool = True) -> tuple[float, float, int]:
-        """Read and reset the HIP-event time (ms) spent in the w13 and the w2
-        expert kernels since the last read and the number of timed calls,
-        then switch per-call kernel timing on or off."""
+    def profile(self, enable: bool = True) -> dict:
+        """Read and reset the execution time (ms, dispatch timestamps) of the
+        ``w13`` and ``w2`` expert kernels of all layer calls since the last
+        read and the number of ``calls``; then switch timing on or off."""
         a, b, n = C.c_double(), C.c_double(), C.c_int64()
         check(lib().wisp_layer_profile(self._handle, int(enable), C.byref(a), C.byref(b),
                                        C.byref(n)), "profile")
-        return float(a.value), float(b.value), int(n.value)
+        return {"w13": float(a.value), "w2": float(b.value), "calls": int(n.value)}
 
     def resize_cap(self, new_cap: int) -> None:
         """Resize the scratch to ``new_cap`` slots at a drained barrier
