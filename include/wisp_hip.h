@@ -42,6 +42,15 @@ typedef struct ihipStream_t* wisp_stream_t; /* == hipStream_t */
 #define WISP_ALGO_GEMV 1  /* wave-per-row GEMV, decode shapes */
 #define WISP_ALGO_MFMA 2  /* bf16 MFMA grouped GEMM, batched/prefill shapes */
 
+/* page-in engines */
+#define WISP_PAGEIN_MEMCPY 0 /* hipMemcpyAsync per loaded expert, issued by the
+                                host after it has read the decision record */
+#define WISP_PAGEIN_KERNEL 1 /* a copy kernel reads the pinned masters through
+                                their device mapping; the load list stays on
+                                the GPU, so a call that is certain to be one
+                                token group (T*top_k <= cap) never waits for
+                                the host */
+
 /* ---- library -------------------------------------------------------- */
 
 /* Message of the last failing call on this thread ("" if none). */
@@ -137,7 +146,10 @@ typedef struct wisp_layer_desc {
   int pagein_streams;            /* 0: page-in copies run on the caller's
                                     stream (stream order fences them);
                                     1 or 2: on that many side streams,
-                                    fenced with events                    */
+                                    fenced with events (memcpy engine)    */
+  int pagein_engine;             /* WISP_PAGEIN_*; KERNEL falls back to
+                                    MEMCPY when the masters are not pinned,
+                                    device-mapped and 16-byte aligned     */
   size_t w13_elems, w2_elems;    /* elements of one expert's w13 / w2    */
   void* scratch_w13;             /* device, slot s at +s*stride [2I, H]  */
   size_t scratch_w13_stride;     /* elements                             */
@@ -161,6 +173,8 @@ typedef struct wisp_workspace {
   int32_t* flags;                /* device [1 + max_pairs]: experts loaded
                                     by the call, then per pair 1 if its
                                     expert was loaded by this call        */
+  int32_t* loads;                /* device [2*max_pairs]: (expert, slot)
+                                    pairs loaded by the call              */
   void* act;                     /* device [max_pairs*inter]             */
   int32_t* record;               /* pinned host [record_words]           */
   int record_words;
@@ -191,9 +205,13 @@ int wisp_layer_ensure_resident(void* handle, const int32_t* ids, int n,
  * Replaces: WispMoEState.prime_identity (fused_moe.py:242-258). */
 int wisp_layer_prime_identity(void* handle, wisp_stream_t stream);
 
-/* Milliseconds the last paged forward's copies took on the copy stream and
- * the bytes they moved (for page-in bandwidth reporting). */
+/* Milliseconds the page-in copies of the layer calls since the last query
+ * took (memcpy engine: from the first copy to the last; kernel engine: the
+ * copy kernels' execution) and the bytes they moved; then reset both. */
 int wisp_layer_last_pagein(void* handle, float* ms, double* bytes);
+
+/* The page-in engine the layer uses (WISP_PAGEIN_*), or -1 for a bad handle. */
+int wisp_layer_pagein_engine(void* handle);
 
 /* Read and reset the accumulated execution time (dispatch timestamps) of the
  * w13+SiLU kernels and of the w2+combine kernels of all layer calls since the

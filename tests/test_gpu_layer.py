@@ -70,34 +70,87 @@ def test_toy_fp32_layer_all_steps():
     drive(wl, 4, wl.steps, tol=1e-5)
 
 
-@pytest.mark.parametrize("streams", ["0", "1", "2"])
-def test_qwen3_bf16_layer_decode(monkeypatch, streams):
-    # page-in on the caller's stream (default) or on side streams with events
+@pytest.mark.parametrize("engine,streams", [("kernel", "0"), ("memcpy", "0"), ("memcpy", "1"),
+                                            ("memcpy", "2")])
+def test_qwen3_bf16_layer_decode(monkeypatch, engine, streams):
+    # copy kernel (default), or hipMemcpyAsync on the caller's stream or on
+    # side streams with events
+    monkeypatch.setenv("WISP_PAGEIN_ENGINE", engine)
     monkeypatch.setenv("WISP_PAGEIN_STREAMS", streams)
     wl = W.qwen3_decode(steps=48, pin=True)
     sts = drive(wl, 8, wl.steps, check_out_every=8, tol=1e-2)
+    assert sts["paged"].pagein_engine == engine
     ms, nbytes = sts["paged"].pagein_stats()
-    assert nbytes > 0 and ms > 0
+    assert ms > 0 and nbytes == sts["paged"].stats_miss * wl.shape.expert_bytes
 
 
-@pytest.mark.parametrize("streams", ["0", "2"])
-def test_batched_subbatching_matches_resident_bytes(monkeypatch, streams):
+@pytest.mark.parametrize("engine,streams", [("kernel", "0"), ("memcpy", "0"), ("memcpy", "2")])
+def test_batched_subbatching_matches_resident_bytes(monkeypatch, engine, streams):
+    monkeypatch.setenv("WISP_PAGEIN_ENGINE", engine)
     monkeypatch.setenv("WISP_PAGEIN_STREAMS", streams)
     # 16 tokens, cap 32 of 128 experts: several greedy groups per call
     wl = W.gaussian_logits("batch", seed=3, steps=3, tokens=16, pin=True)
-    drive(wl, 32, wl.steps, check_out_every=1, tol=1e-2)
+    sts = drive(wl, 32, wl.steps, check_out_every=1, tol=1e-2)
+    assert sts["paged"].pagein_engine == engine
 
 
-def test_mixtral_shape_decode_small_steps():
-    wl = W.mixtral(steps=6, pin=True)
-    drive(wl, 4, wl.steps, check_out_every=3, tol=1e-2)
-
-
-def test_overflow_token_raises_subbatch():
-    wl = W.toy(steps=2, pin=True)
+@pytest.mark.parametrize("engine", ["kernel", "memcpy"])
+def test_queued_decode_over_layers_matches_resident(monkeypatch, engine):
+    # Four layers share the masters and are called round-robin with no host
+    # synchronisation between calls, as a decode loop runs: every call's
+    # output must still equal the resident layer's bytes, and each layer's
+    # final pager state must equal its own oracle's.
+    monkeypatch.setenv("WISP_PAGEIN_ENGINE", engine)
+    wl = W.qwen3_decode(steps=40, pin=True)
     w13, w2 = wl.views()
-    st = WispMoEState(w13, w2, 2, "paged", DEV, 0)
-    x = wl.x[0].to(DEV)
-    with pytest.raises(RuntimeError, match="sub-batch"):
-        st.forward(x, wl.logits[0].to(DEV), 3, True)
+    K, nl = wl.shape.top_k, 4
+    paged = [WispMoEState(w13, w2, 8, "paged", DEV, i) for i in range(nl)]
+    res = WispMoEState(w13, w2, wl.shape.experts, "resident", DEV, nl)
+    res.prime_identity()
+    oras = [PagerOracle(wl.shape.experts, 8) for _ in range(nl)]
+    xs = [wl.x[t].to(DEV) for t in range(wl.steps)]
+    lgs = [wl.logits[t].to(DEV) for t in range(wl.steps)]
+    torch.cuda.synchronize()
+    outs, refs = [], []
+    for t in range(wl.steps):
+        outs.append(paged[t % nl].forward(xs[t], lgs[t], K, True))
+    for t in range(wl.steps):
+        refs.append(res.forward(xs[t], lgs[t], K, True))
+    torch.cuda.synchronize()
+    for t in range(wl.steps):
+        assert torch.equal(bits(outs[t]), bits(refs[t])), t
+        oras[t % nl].forward(route(wl.logits[t], K)[1].tolist())
+    for st, ora in zip(paged, oras):
+        assert st.pagein_engine == engine
+        assert st.slot_to_expert == ora.slot_to_expert and st.lru_tick == ora.lru_tick
+        assert (st.stats_forward, st.stats_miss, st.stats_evict, st.stats_hits) == \
+            (ora.stats_forward, ora.stats_miss, ora.stats_evict, ora.stats_hits)
 
+
+def test_kernel_engine_needs_pinned_masters():
+    # The copy kernel reads masters through their device mapping; a layer
+    # whose masters are pageable (or whose range leaves the pinned
+    # allocation) must be created with the hipMemcpyAsync engine instead.
+    import ctypes as C
+    from wisp_amd import _lib
+    wl = W.toy(steps=1, pin=True)
+    w13, w2 = wl.views()
+    st = WispMoEState(w13, w2, 4, "paged", DEV, 0)
+    assert st.pagein_engine == "kernel"
+    pageable = wl.slabs.clone()
+    assert not pageable.is_pinned()
+    cases = [(pageable.data_ptr(), pageable.data_ptr() + st._w13_elems * 4),
+             # starts where the pinned masters end, so the range runs past
+             # their allocation (the allocator rounds sizes up to at most 2x)
+             (wl.slabs.data_ptr() + wl.slabs.numel() * 4,
+              wl.slabs.data_ptr() + wl.slabs.numel() * 4 + st._w13_elems * 4)]
+    for m13, m2 in cases:
+        d = st._make_desc()
+        d.pagein_engine = _lib.WISP_PAGEIN_KERNEL
+        d.master_w13, d.master_w2 = m13, m2
+        h = C.c_void_p()
+        _lib.check(_lib.lib().wisp_layer_create(C.byref(d), C.byref(h)), "create")
+        try:
+            assert _lib.lib().wisp_layer_pagein_engine(h) == _lib.WISP_PAGEIN_MEMCPY
+        finally:
+            _lib.lib().wisp_layer_destroy(h)

@@ -26,6 +26,8 @@ WISP_MODE_RESIDENT = 1
 WISP_ALGO_AUTO = 0
 WISP_ALGO_GEMV = 1
 WISP_ALGO_MFMA = 2
+WISP_PAGEIN_MEMCPY = 0
+WISP_PAGEIN_KERNEL = 1
 
 # Decision-record header words (wisp_amd/csrc/pager_core.h).
 REC_STATUS, REC_GROUPS_DONE, REC_GROUPS_PLANNED, REC_FAIL_GROUP, REC_FAIL_UNIQUE, \
@@ -38,6 +40,7 @@ class LayerDesc(C.Structure):
     _fields_ = [
         ("num_experts", C.c_int), ("cap", C.c_int), ("hidden", C.c_int), ("inter", C.c_int),
         ("dtype", C.c_int), ("mode", C.c_int), ("pagein_streams", C.c_int),
+        ("pagein_engine", C.c_int),
         ("w13_elems", _sz), ("w2_elems", _sz),
         ("scratch_w13", _vp), ("scratch_w13_stride", _sz),
         ("scratch_w2", _vp), ("scratch_w2_stride", _sz),
@@ -50,7 +53,8 @@ class LayerDesc(C.Structure):
 class Workspace(C.Structure):
     _fields_ = [
         ("max_pairs", C.c_int), ("topk_w", _vp), ("topk_ids", _vp), ("slots", _vp),
-        ("flags", _vp), ("act", _vp), ("record", _vp), ("record_words", C.c_int),
+        ("flags", _vp), ("loads", _vp), ("act", _vp), ("record", _vp),
+        ("record_words", C.c_int),
     ]
 
 
@@ -78,6 +82,7 @@ SIGNATURES = {
     "wisp_layer_ensure_resident": (_i32, [_vp, _vp, _i32, C.POINTER(Workspace), _vp]),
     "wisp_layer_prime_identity": (_i32, [_vp, _vp]),
     "wisp_layer_last_pagein": (_i32, [_vp, _f32p, C.POINTER(C.c_double)]),
+    "wisp_layer_pagein_engine": (_i32, [_vp]),
     "wisp_layer_profile": (_i32, [_vp, _i32, C.POINTER(C.c_double), C.POINTER(C.c_double),
                                   C.POINTER(C.c_int64)]),
     "wisp_probe_h2d": (_i32, [_vp, _vp, _sz, _i32, _i32, _f32p]),

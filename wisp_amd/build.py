@@ -24,6 +24,7 @@ SOURCES = [
     "route.hip",
     "experts_gemv.hip",
     "experts_mfma.hip",
+    "pagein.hip",
     "layer.hip",
     "probes.hip",
 ]

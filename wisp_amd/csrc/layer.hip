@@ -1,11 +1,19 @@
-// The paged MoE layer call: routing, the GPU pager, page-in on side streams
-// and the expert kernels, orchestrated on the host in C++.
+// The paged MoE layer call: routing, the GPU pager, page-in and the expert
+// kernels, orchestrated on the host in C++.
 //
 // Replaces the reference's patched forward (src/wisp/integrations/vllm/
 // fused_moe.py:930-987, 990-1237) and the copy half of ensure_resident
 // (fused_moe.py:338-354).
 //
-// Paged call, one token group guaranteed (T*K <= cap, e.g. bs=1 decode):
+// Paged call, one token group guaranteed (T*K <= cap, e.g. bs=1 decode),
+// kernel page-in engine:
+//   caller's stream: [route+pager] [page-in copy kernel] [w13] [w2]
+// The pager leaves the (expert, slot) load list and its length in device
+// memory and the copy kernel reads them there, so the host enqueues the four
+// launches and returns: no host round trip, no copy-engine hand-off.  A call
+// that loads nothing pays one near-empty launch.
+//
+// Same call, memcpy engine (hipMemcpyAsync):
 //   caller's stream: [route+pager] [w13, pairs that hit] [w2 unless loads]
 //   host:            wait for the decision record; if experts were loaded:
 //                    the copies, then [w13, loaded pairs] [w2].
@@ -16,10 +24,10 @@
 // pager kernel wrote.
 //
 // Paged call, several groups possible: route (fused into the pager for
-// T <= 8), pager, one sync, then per group: copies, the group's expert
-// kernels.
+// T <= 8), pager, one sync, then per group: copies (copy kernel or
+// hipMemcpyAsync), the group's expert kernels.
 //
-// Page-in copies run by default on the caller's stream, where stream order
+// hipMemcpyAsync copies run by default on the caller's stream, where stream order
 // is both fences (a copy follows the kernels that read the slot before it;
 // the kernels that read the slot follow the copy).  With side streams
 // (pagein_streams 1 or 2) each copy stream first waits on an event recorded
@@ -36,6 +44,7 @@
 #include <vector>
 
 #include "common.h"
+#include "pagein.h"
 #include "pager_core.h"
 
 static thread_local std::string g_last_error;
@@ -52,7 +61,7 @@ namespace wisp {
 int launch_pager(const int32_t* ids, const void* logits, int logits_dtype, int renorm,
                  float* topk_w, int32_t* topk_ids, int T, int K, int E, int cap,
                  int single_group, int32_t* map, int32_t* s2e, int64_t* tick, int64_t* ctr,
-                 int32_t* slots, int32_t* flags, int32_t* rec, int rec_words,
+                 int32_t* slots, int32_t* flags, int32_t* loads, int32_t* rec, int rec_words,
                  hipStream_t stream);
 int gemv_w13(const void* x, int dtype, int T, int H, int I, int K, const int32_t* slots,
              const void* w13, size_t w13_stride, void* act, hipStream_t st,
@@ -72,6 +81,7 @@ namespace {
 constexpr int kEventRing = 4;
 constexpr int kCopyStreams = 2;
 constexpr int kProfRing = 512;
+constexpr int kPinRing = 64;
 
 size_t elem_size(int dtype) { return dtype == WISP_F32 ? 4 : 2; }
 
@@ -83,8 +93,23 @@ struct ProfLaunch {
   bool counted = true;   // false for a speculative launch that found nothing to do
 };
 
+// One copy-kernel launch: dispatch timestamps and the pinned word its first
+// block sets to the number of experts it copied.
+struct PinLaunch {
+  hipEvent_t start = nullptr, stop = nullptr;
+  bool pending = false;
+};
+
 struct Layer {
   wisp_layer_desc d;
+  // kernel page-in (engine WISP_PAGEIN_KERNEL and eligible masters)
+  bool kpin = false;
+  const char* m13_dev = nullptr;  // device addresses of the pinned masters
+  const char* m2_dev = nullptr;
+  int32_t* hist = nullptr;        // pinned host [kPinRing]
+  int32_t* hist_dev = nullptr;
+  int pin_next = 0;
+  PinLaunch pin[kPinRing];
   int nstreams = 0;  // side copy streams in use (0: the caller's stream)
   hipStream_t copy[kCopyStreams] = {};
   hipEvent_t ev_decided = nullptr;
@@ -175,6 +200,95 @@ void harvest_pagein_timing(Layer& L) {
   L.pin_bytes_pending = 0;
 }
 
+size_t expert_bytes(const Layer& L) { return (L.d.w13_elems + L.d.w2_elems) * L.es; }
+
+void harvest_pin(Layer& L, int i) {
+  PinLaunch& p = L.pin[i];
+  if (!p.pending) return;
+  float ms = 0.f;
+  if (hipEventSynchronize(p.stop) == hipSuccess &&
+      hipEventElapsedTime(&ms, p.start, p.stop) == hipSuccess) {
+    const int n = ((volatile int32_t*)L.hist)[i];
+    if (n > 0) {
+      L.pin_ms_total += ms;
+      L.pin_bytes_total += (double)n * (double)expert_bytes(L);
+    }
+  }
+  p.pending = false;
+}
+
+// Copy-kernel page-in on `st` of the (expert, slot) pairs at `loads` (device
+// memory); their number is *count (device) when count is non-null, else n.
+int page_in_kernel(Layer& L, const int32_t* loads, const int32_t* count, int n, hipStream_t st) {
+  const wisp_layer_desc& d = L.d;
+  const int i = L.pin_next;
+  L.pin_next = (L.pin_next + 1) % kPinRing;
+  harvest_pin(L, i);
+  PinLaunch& p = L.pin[i];
+  PageInArgs a;
+  a.loads = loads;
+  a.count = count;
+  a.n = n;
+  a.num_experts = d.num_experts;
+  a.cap = d.cap;
+  a.m13 = L.m13_dev;
+  a.m13_stride = d.master_w13_stride * L.es;
+  a.m2 = L.fused_slab ? nullptr : L.m2_dev;
+  a.m2_stride = d.master_w2_stride * L.es;
+  a.s13 = (char*)d.scratch_w13;
+  a.s13_stride = d.scratch_w13_stride * L.es;
+  a.s2 = (char*)d.scratch_w2;
+  a.s2_stride = d.scratch_w2_stride * L.es;
+  a.b13 = L.fused_slab ? expert_bytes(L) : d.w13_elems * L.es;
+  a.b2 = d.w2_elems * L.es;
+  a.hist = L.hist_dev + i;
+  int rc = launch_pagein(a, st, p.start, p.stop);
+  if (rc == WISP_OK) p.pending = true;
+  return rc;
+}
+
+// Enables the copy kernel when every master range is pinned, device-mapped
+// host memory and every copy is a whole number of aligned 16-byte units.
+void setup_kernel_pagein(Layer& L) {
+  const wisp_layer_desc& d = L.d;
+  const size_t es = L.es, b13 = d.w13_elems * es, b2 = d.w2_elems * es;
+  const size_t s13 = d.master_w13_stride * es, s2 = d.master_w2_stride * es;
+  const size_t last = (size_t)(d.num_experts - 1);
+  const bool aligned = b13 % 16 == 0 && b2 % 16 == 0 && s13 % 16 == 0 && s2 % 16 == 0 &&
+                       (d.scratch_w13_stride * es) % 16 == 0 &&
+                       (d.scratch_w2_stride * es) % 16 == 0 &&
+                       (uintptr_t)d.master_w13 % 16 == 0 && (uintptr_t)d.master_w2 % 16 == 0 &&
+                       (uintptr_t)d.scratch_w13 % 16 == 0 && (uintptr_t)d.scratch_w2 % 16 == 0;
+  if (d.pagein_engine != WISP_PAGEIN_KERNEL || !aligned) return;
+  const char* m13 = mapped_host_range(d.master_w13, last * s13 + (L.fused_slab ? b13 + b2 : b13));
+  const char* m2 = mapped_host_range(d.master_w2, last * s2 + b2);
+  if (!m13 || !m2) return;
+  void* h = nullptr;
+  if (hipHostMalloc(&h, kPinRing * sizeof(int32_t), hipHostMallocMapped) != hipSuccess) {
+    (void)hipGetLastError();
+    return;
+  }
+  void* hd = nullptr;
+  if (hipHostGetDevicePointer(&hd, h, 0) != hipSuccess || !hd) {
+    (void)hipGetLastError();
+    (void)hipHostFree(h);
+    return;
+  }
+  for (int i = 0; i < kPinRing; ++i) {
+    if (hipEventCreate(&L.pin[i].start) != hipSuccess ||
+        hipEventCreate(&L.pin[i].stop) != hipSuccess) {
+      (void)hipGetLastError();
+      return;  // the events made so far are released by wisp_layer_destroy
+    }
+  }
+  memset(h, 0, kPinRing * sizeof(int32_t));
+  L.hist = (int32_t*)h;
+  L.hist_dev = (int32_t*)hd;
+  L.m13_dev = m13;
+  L.m2_dev = m2;
+  L.kpin = true;
+}
+
 // Page-in of `n` pairs.  On the caller's stream the copies simply follow
 // the queued kernels.  On side streams every copy stream first waits on
 // `after` (if any), copies run, and `st` waits for all of them; `slot` picks
@@ -255,9 +369,9 @@ int choose_algo(const Layer& L, int algo, int T, int K) {
 }
 
 // Copies and expert kernels for groups [0, ngroups) of a decision record.
-int run_groups(Layer& L, const int32_t* rec, int T, int K, int ngroups, bool compute,
-               const void* x, const float* topk_w, const int32_t* slots, void* act, void* out,
-               int algo, hipStream_t st) {
+int run_groups(Layer& L, const int32_t* rec, const int32_t* loads, int T, int K, int ngroups,
+               bool compute, const void* x, const float* topk_w, const int32_t* slots, void* act,
+               void* out, int algo, hipStream_t st) {
   const RecordLayout RL(T, K);
   const size_t row = (size_t)L.d.hidden * L.es;
   int last_gemm = -1;
@@ -265,8 +379,10 @@ int run_groups(Layer& L, const int32_t* rec, int T, int K, int ngroups, bool com
     const int32_t* G = rec + RL.group_base(g);
     const int t0 = G[0], t1 = G[1], ld_off = G[6], n_ld = G[7];
     if (n_ld > 0) {
-      int rc = page_in(L, rec + RL.loaded_base() + 2 * ld_off, n_ld,
-                       last_gemm >= 0 ? L.ev_gemm[last_gemm % kEventRing] : nullptr, g, st);
+      int rc = L.kpin ? page_in_kernel(L, loads + 2 * ld_off, nullptr, n_ld, st)
+                      : page_in(L, rec + RL.loaded_base() + 2 * ld_off, n_ld,
+                                last_gemm >= 0 ? L.ev_gemm[last_gemm % kEventRing] : nullptr, g,
+                                st);
       if (rc != WISP_OK) return rc;
     }
     if (compute && t1 > t0) {
@@ -291,7 +407,7 @@ int32_t* record_device_ptr(int32_t* rec) {
 
 int check_ws(const wisp_workspace* ws, int T, int K) {
   if (!ws || (int64_t)T * K > ws->max_pairs || !ws->topk_w || !ws->topk_ids || !ws->slots ||
-      !ws->flags || !ws->act || !ws->record ||
+      !ws->flags || !ws->loads || !ws->act || !ws->record ||
       ws->record_words < RecordLayout(T, K).words()) {
     wisp_set_last_error("workspace too small or missing", "wisp_layer_forward");
     return WISP_ERR_INVALID;
@@ -319,7 +435,8 @@ extern "C" int wisp_layer_create(const wisp_layer_desc* desc, void** handle) {
       d.scratch_w2_stride < d.w2_elems || d.master_w13_stride < d.w13_elems ||
       d.master_w2_stride < d.w2_elems ||
       (d.mode == WISP_MODE_RESIDENT && d.cap != d.num_experts) || d.pagein_streams < 0 ||
-      d.pagein_streams > kCopyStreams) {
+      d.pagein_streams > kCopyStreams ||
+      (d.pagein_engine != WISP_PAGEIN_MEMCPY && d.pagein_engine != WISP_PAGEIN_KERNEL)) {
     wisp_set_last_error("invalid layer descriptor", "wisp_layer_create");
     return WISP_ERR_INVALID;
   }
@@ -348,6 +465,7 @@ extern "C" int wisp_layer_create(const wisp_layer_desc* desc, void** handle) {
     wisp_layer_destroy(L);
     return WISP_ERR_HIP;
   }
+  if (d.hidden > 0) setup_kernel_pagein(*L);
   *handle = L;
   return WISP_OK;
 }
@@ -370,6 +488,12 @@ extern "C" int wisp_layer_destroy(void* handle) {
     if (L->prof[i].start) (void)hipEventDestroy(L->prof[i].start);
     if (L->prof[i].stop) (void)hipEventDestroy(L->prof[i].stop);
   }
+  for (int i = 0; i < kPinRing; ++i) {
+    if (L->pin[i].pending) (void)hipEventSynchronize(L->pin[i].stop);
+    if (L->pin[i].start) (void)hipEventDestroy(L->pin[i].start);
+    if (L->pin[i].stop) (void)hipEventDestroy(L->pin[i].stop);
+  }
+  if (L->hist) (void)hipHostFree(L->hist);
   for (int c = 0; c < kCopyStreams; ++c)
     if (L->copy[c]) (void)hipStreamDestroy(L->copy[c]);
   delete L;
@@ -385,6 +509,7 @@ extern "C" int wisp_layer_set_scratch(void* handle, void* scratch_w13, void* scr
     return WISP_ERR_INVALID;
   for (int c = 0; c < kCopyStreams; ++c) (void)hipStreamSynchronize(L->copy[c]);
   harvest_pagein_timing(*L);
+  for (int i = 0; i < kPinRing; ++i) harvest_pin(*L, i);
   const size_t es = L->es, w13_elems = L->d.w13_elems;
   L->d.scratch_w13 = scratch_w13;
   L->d.scratch_w2 = scratch_w2;
@@ -392,6 +517,7 @@ extern "C" int wisp_layer_set_scratch(void* handle, void* scratch_w13, void* scr
                   L->d.scratch_w13_stride == L->d.scratch_w2_stride &&
                   (const char*)L->d.master_w2 == (const char*)L->d.master_w13 + w13_elems * es &&
                   (const char*)scratch_w2 == (const char*)scratch_w13 + w13_elems * es;
+  if (((uintptr_t)scratch_w13) % 16 || ((uintptr_t)scratch_w2) % 16) L->kpin = false;
   L->d.cap = cap;
   L->d.slot_to_expert = slot_to_expert;
   L->d.lru_tick = lru_tick;
@@ -446,14 +572,22 @@ extern "C" int wisp_layer_forward(void* handle, const void* x, const void* logit
   int32_t* rec_dev = record_device_ptr(ws->record);
   rc = launch_pager(ws->topk_ids, fuse_route ? logits : nullptr, logits_dtype, renormalize,
                     ws->topk_w, ws->topk_ids, T, K, d.num_experts, d.cap, 0, d.expert_map,
-                    d.slot_to_expert, d.lru_tick, d.counters, ws->slots, ws->flags, rec_dev,
-                    ws->record_words, st);
+                    d.slot_to_expert, d.lru_tick, d.counters, ws->slots, ws->flags, ws->loads,
+                    rec_dev, ws->record_words, st);
   if (rc != WISP_OK) return rc;
-  WISP_HIP_TRY(hipEventRecord(L->ev_decided, st));
 
   // One group is certain when every routed pair could be distinct and still
-  // fit: then the expert kernels go in right behind the pager.
-  const bool speculate = a == WISP_ALGO_GEMV && T > 0 && (int64_t)T * K <= d.cap;
+  // fit (the ids come from the router, so they are in range and the pager
+  // cannot fail): then the rest of the call goes in right behind the pager.
+  const bool one_group = T > 0 && (int64_t)T * K <= d.cap;
+  if (one_group && L->kpin) {
+    rc = page_in_kernel(*L, ws->loads, ws->flags, 0, st);
+    if (rc != WISP_OK) return rc;
+    return experts(*L, x, T, K, ws->topk_w, ws->slots, ws->act, out, a, st);
+  }
+  WISP_HIP_TRY(hipEventRecord(L->ev_decided, st));
+
+  const bool speculate = a == WISP_ALGO_GEMV && one_group;
   ProfLaunch* spec_w2 = nullptr;
   if (speculate) {
     rc = w13(*L, x, T, K, ws->slots, ws->act, st, ws->flags + 1, 0);
@@ -482,8 +616,8 @@ extern "C" int wisp_layer_forward(void* handle, const void* x, const void* logit
     if (rc == WISP_OK) rc = w2(*L, ws->act, T, K, ws->topk_w, ws->slots, out, st, nullptr, nullptr);
     return rc;
   }
-  rc = run_groups(*L, rec, T, K, rec[kRecGroupsDone], status == WISP_OK, x, ws->topk_w,
-                  ws->slots, ws->act, out, a, st);
+  rc = run_groups(*L, rec, ws->loads, T, K, rec[kRecGroupsDone], status == WISP_OK, x,
+                  ws->topk_w, ws->slots, ws->act, out, a, st);
   if (rc != WISP_OK) return rc;
   if (status == WISP_ERR_SUBBATCH)
     wisp_set_last_error("one token routes to more experts than cap; sub-batching cannot help",
@@ -502,7 +636,7 @@ extern "C" int wisp_layer_ensure_resident(void* handle, const int32_t* ids, int 
   const wisp_layer_desc& d = L->d;
   int rc = launch_pager(ids, nullptr, WISP_F32, 0, nullptr, nullptr, n, 1, d.num_experts, d.cap,
                         1, d.expert_map, d.slot_to_expert, d.lru_tick, d.counters, nullptr,
-                        nullptr, record_device_ptr(ws->record), ws->record_words, st);
+                        nullptr, nullptr, record_device_ptr(ws->record), ws->record_words, st);
   if (rc != WISP_OK) return rc;
   WISP_HIP_TRY(hipEventRecord(L->ev_decided, st));
   WISP_HIP_TRY(hipEventSynchronize(L->ev_decided));
@@ -549,11 +683,18 @@ extern "C" int wisp_layer_last_pagein(void* handle, float* ms, double* bytes) {
   Layer* L = (Layer*)handle;
   if (!L) return WISP_ERR_INVALID;
   wisp::harvest_pagein_timing(*L);
+  for (int i = 0; i < wisp::kPinRing; ++i) wisp::harvest_pin(*L, i);
   if (ms) *ms = (float)L->pin_ms_total;
   if (bytes) *bytes = L->pin_bytes_total;
   L->pin_ms_total = 0;
   L->pin_bytes_total = 0;
   return WISP_OK;
+}
+
+extern "C" int wisp_layer_pagein_engine(void* handle) {
+  Layer* L = (Layer*)handle;
+  if (!L) return -1;
+  return L->kpin ? WISP_PAGEIN_KERNEL : WISP_PAGEIN_MEMCPY;
 }
 
 extern "C" int wisp_layer_profile(void* handle, int enable, double* w13_ms, double* w2_ms,

@@ -288,14 +288,15 @@ struct FusedRouteSmem {
 // `ids_in`.  Outputs: device state, slots[p] (slot of pair p, -1 for pairs of
 // a group that was not completed), flags (optional): flags[0] = experts
 // loaded by this call, flags[1 + p] = 1 if pair p's expert was loaded by its
-// group, else 0; and the decision record.
+// group, else 0; loads (optional): the (expert, slot) pairs loaded, in the
+// record's order; and the decision record.
 template <typename TL>
 __global__ __launch_bounds__(64) void pager_kernel(
     const int32_t* __restrict__ ids_in, const TL* __restrict__ logits, int renorm,
     float* __restrict__ w_out, int32_t* __restrict__ id_out, int T, int K, int E, int cap,
     int single_group, int32_t* __restrict__ map_g, int32_t* __restrict__ s2e_g,
     int64_t* __restrict__ tick_g, int64_t* __restrict__ ctr_g, int32_t* __restrict__ slots_g,
-    int32_t* __restrict__ flags_g, int32_t* __restrict__ rec) {
+    int32_t* __restrict__ flags_g, int32_t* __restrict__ loads_g, int32_t* __restrict__ rec) {
   __shared__ PagerSmem sm;
   __shared__ FusedRouteSmem fr;
   const int lane = threadIdx.x;
@@ -495,6 +496,10 @@ __global__ __launch_bounds__(64) void pager_kernel(
           const int o = L.loaded_base() + 2 * (ld_total + j);
           rec[o] = e;
           rec[o + 1] = s;
+          if (loads_g) {
+            loads_g[2 * (ld_total + j)] = e;
+            loads_g[2 * (ld_total + j) + 1] = s;
+          }
         }
         n_miss += nmiss;
         ld_total += nmiss;
@@ -544,7 +549,7 @@ __global__ __launch_bounds__(64) void pager_kernel(
 int launch_pager(const int32_t* ids, const void* logits, int logits_dtype, int renorm,
                  float* topk_w, int32_t* topk_ids, int T, int K, int E, int cap,
                  int single_group, int32_t* map, int32_t* s2e, int64_t* tick, int64_t* ctr,
-                 int32_t* slots, int32_t* flags, int32_t* rec, int rec_words,
+                 int32_t* slots, int32_t* flags, int32_t* loads, int32_t* rec, int rec_words,
                  hipStream_t stream) {
   RecordLayout L(T, K);
   if (T < 0 || K < 1 || K > kMaxTopK || E < 1 || E > kMaxExperts || cap < 1 || cap > E ||
@@ -558,11 +563,11 @@ int launch_pager(const int32_t* ids, const void* logits, int logits_dtype, int r
   if (logits && logits_dtype == WISP_BF16)
     hipLaunchKernelGGL(pager_kernel<uint16_t>, dim3(1), dim3(64), 0, stream, ids,
                        (const uint16_t*)logits, renorm, topk_w, topk_ids, T, K, E, cap,
-                       single_group, map, s2e, tick, ctr, slots, flags, rec);
+                       single_group, map, s2e, tick, ctr, slots, flags, loads, rec);
   else
     hipLaunchKernelGGL(pager_kernel<float>, dim3(1), dim3(64), 0, stream, ids,
                        (const float*)logits, renorm, topk_w, topk_ids, T, K, E, cap,
-                       single_group, map, s2e, tick, ctr, slots, flags, rec);
+                       single_group, map, s2e, tick, ctr, slots, flags, loads, rec);
   WISP_HIP_TRY(hipGetLastError());
   return WISP_OK;
 }
@@ -576,7 +581,7 @@ extern "C" int wisp_pager_decide(const int32_t* topk_ids, int T, int K, int E, i
                                  int record_words, wisp_stream_t stream) {
   return wisp::launch_pager(topk_ids, nullptr, WISP_F32, 0, nullptr, nullptr, T, K, E, cap,
                             single_group, expert_map, slot_to_expert, lru_tick, counters, slots,
-                            nullptr, record, record_words, (hipStream_t)stream);
+                            nullptr, nullptr, record, record_words, (hipStream_t)stream);
 }
 
 extern "C" int wisp_pager_decide_host(const int32_t* topk_ids, int T, int K, int E, int cap,

@@ -92,6 +92,18 @@ def _resolve_pagein_streams() -> int:
     return max(0, min(2, n))
 
 
+def _resolve_pagein_engine() -> int:
+    """``WISP_PAGEIN_ENGINE``: ``kernel`` (default) copies loaded experts with
+    a GPU kernel that reads the pinned masters directly, so decode calls never
+    wait for the host; ``memcpy`` uses hipMemcpyAsync issued by the host after
+    it has read the pager's decision (the side-stream option applies to it)."""
+    raw = os.environ.get("WISP_PAGEIN_ENGINE", "kernel").strip().lower()
+    if raw not in ("kernel", "memcpy"):
+        logger.warning("WISP_PAGEIN_ENGINE=%r is not 'kernel' or 'memcpy'; using kernel", raw)
+        raw = "kernel"
+    return _lib.WISP_PAGEIN_KERNEL if raw == "kernel" else _lib.WISP_PAGEIN_MEMCPY
+
+
 _DTYPES = {torch.float32: _lib.WISP_F32, torch.bfloat16: _lib.WISP_BF16}
 
 
@@ -110,7 +122,8 @@ class _Workspace:
         self.pairs = 0
         self.record_words = 0
         self.struct = _lib.Workspace()
-        self.topk_w = self.topk_ids = self.slots = self.flags = self.act = self.record = None
+        self.topk_w = self.topk_ids = self.slots = self.flags = self.loads = None
+        self.act = self.record = None
 
     def ensure(self, T: int, K: int) -> "_lib.Workspace":
         pairs = max(1, T * K)
@@ -122,6 +135,7 @@ class _Workspace:
             self.topk_ids = torch.empty(self.pairs, dtype=torch.int32, device=dev)
             self.slots = torch.empty(self.pairs, dtype=torch.int32, device=dev)
             self.flags = torch.zeros(self.pairs + 1, dtype=torch.int32, device=dev)
+            self.loads = torch.zeros(2 * self.pairs, dtype=torch.int32, device=dev)
             self.act = torch.empty(self.pairs * self.inter, dtype=self.dtype, device=dev)
         if words > self.record_words:
             self.record_words = max(words, 2 * self.record_words)
@@ -130,7 +144,7 @@ class _Workspace:
         s.max_pairs = self.pairs
         s.topk_w, s.topk_ids = self.topk_w.data_ptr(), self.topk_ids.data_ptr()
         s.slots, s.act = self.slots.data_ptr(), self.act.data_ptr()
-        s.flags = self.flags.data_ptr()
+        s.flags, s.loads = self.flags.data_ptr(), self.loads.data_ptr()
         s.record, s.record_words = self.record.data_ptr(), self.record_words
         return s
 
@@ -208,6 +222,7 @@ class WispMoEState:
         d.hidden, d.inter = self.hidden, self.inter
         d.dtype = _DTYPES[self.dtype]
         d.pagein_streams = _resolve_pagein_streams()
+        d.pagein_engine = _resolve_pagein_engine()
         d.w13_elems, d.w2_elems = self._w13_elems, self._w2_elems
         d.mode = _lib.WISP_MODE_RESIDENT if self.mode == _Mode.RESIDENT else _lib.WISP_MODE_PAGED
         d.scratch_w13, d.scratch_w13_stride = self.scratch_w13.data_ptr(), self._slab_elems
@@ -268,8 +283,17 @@ class WispMoEState:
 
     @property
     def last_record(self) -> torch.Tensor:
-        """The pinned decision record of the last paged call."""
+        """The pinned decision record of the last paged call (waits for the
+        device to finish the calls already queued)."""
+        torch.cuda.synchronize(self.device)
         return self._ws.record
+
+    @property
+    def pagein_engine(self) -> str:
+        """``"kernel"`` or ``"memcpy"``: the page-in engine in use (the kernel
+        engine falls back to memcpy for masters that are not pinned)."""
+        eng = lib().wisp_layer_pagein_engine(self._handle)
+        return "kernel" if eng == _lib.WISP_PAGEIN_KERNEL else "memcpy"
 
     # -- reference API ------------------------------------------------------
     def prime_identity(self) -> None:
