@@ -125,16 +125,24 @@ int wisp_pagein_issue(const int32_t* record, int record_words, int T, int K, int
 /* Slot-remapped SwiGLU experts with the routing-order combine:
  *   act[t,k] = silu(W13[s] x[t])[:I] * (W13[s] x[t])[I:],  s = slots[t,k]
  *   out[t]   = sum_{k=0..K-1} topk_w[t,k] * (W2[s] act[t,k])  (k ascending)
- * A slot of -1 contributes zero.  W13 of slot s is at w13 + s*w13_stride
- * ([2I, H] row-major), W2 at w2 + s*w2_stride ([H, I] row-major); strides in
- * elements.  act: workspace of T*K*I elements.  dtype WISP_F32 or WISP_BF16
- * (x, weights, act and out share it).
+ * A slot of -1 contributes zero; slots are < nslots.  W13 of slot s is at
+ * w13 + s*w13_stride ([2I, H] row-major), W2 at w2 + s*w2_stride ([H, I]
+ * row-major); strides in elements.  act: workspace of T*K*I elements.  dtype
+ * WISP_F32 or WISP_BF16 (x, weights, act and out share it).  work: device
+ * buffer, 256-byte aligned, of wisp_moe_work_bytes(T, K, H, nslots) bytes
+ * (used by WISP_ALGO_MFMA; may be NULL for the GEMV kernels).
  * Replaces: vLLM fused_experts(..., expert_map=...) at
  *           fused_moe.py:1106-1118 and 1155-1167. */
 int wisp_moe_experts(const void* x, int dtype, int T, int H, int I, int K,
-                     const float* topk_w, const int32_t* slots,
+                     const float* topk_w, const int32_t* slots, int nslots,
                      const void* w13, size_t w13_stride, const void* w2, size_t w2_stride,
-                     void* act, void* out, int algo, wisp_stream_t stream);
+                     void* act, void* out, void* work, size_t work_bytes, int algo,
+                     wisp_stream_t stream);
+
+/* Bytes of the work buffer the MFMA expert path needs for T tokens x K over
+ * nslots slots at hidden size H: per-slot pair lists and fp32 per-pair
+ * outputs.  No reference counterpart (vLLM allocates its own). */
+size_t wisp_moe_work_bytes(int T, int K, int H, int nslots);
 
 /* ---- group 3: the layer call --------------------------------------- */
 
@@ -178,6 +186,10 @@ typedef struct wisp_workspace {
   void* act;                     /* device [max_pairs*inter]             */
   int32_t* record;               /* pinned host [record_words]           */
   int record_words;
+  void* work;                    /* device, 256-byte aligned: MFMA path
+                                    work buffer (wisp_moe_work_bytes with
+                                    nslots = cap)                         */
+  size_t work_bytes;
 } wisp_workspace;
 
 /* Create / destroy the per-layer context (copy stream, events). */

@@ -112,13 +112,16 @@ def run_experts(x, w, slots, w13, w2, algo=_lib.WISP_ALGO_GEMV):
     T, H = x.shape
     K = w.shape[1]
     I = w2.shape[2]
+    E = w13.shape[0]
     act = torch.empty(max(1, T * K) * I, dtype=x.dtype, device=DEV)
     out = torch.empty_like(x)
+    nbytes = _lib.lib().wisp_moe_work_bytes(max(1, T), K, H, E)
+    work = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
     dt = _lib.WISP_F32 if x.dtype == torch.float32 else _lib.WISP_BF16
     _lib.check(_lib.lib().wisp_moe_experts(
-        x.data_ptr(), dt, T, H, I, K, w.data_ptr(), slots.data_ptr(), w13.data_ptr(),
-        w13.stride(0), w2.data_ptr(), w2.stride(0), act.data_ptr(), out.data_ptr(), algo,
-        _lib.stream_handle()), "experts")
+        x.data_ptr(), dt, T, H, I, K, w.data_ptr(), slots.data_ptr(), E, w13.data_ptr(),
+        w13.stride(0), w2.data_ptr(), w2.stride(0), act.data_ptr(), out.data_ptr(),
+        work.data_ptr(), nbytes, algo, _lib.stream_handle()), "experts")
     torch.cuda.synchronize()
     return out
 
@@ -178,3 +181,53 @@ def test_output_bytes_independent_of_slot_placement(dtype):
                     w13[perm].to(DEV), w2[perm].to(DEV))
     assert torch.equal(a.view(torch.int16 if dtype == torch.bfloat16 else torch.int32),
                        b.view(torch.int16 if dtype == torch.bfloat16 else torch.int32))
+
+
+MFMA = _lib.WISP_ALGO_MFMA
+
+
+def _dev_case(x, w, ids, w13, w2):
+    return (x.to(DEV), torch.tensor(w, dtype=torch.float32, device=DEV),
+            torch.tensor(ids, dtype=torch.int32, device=DEV), w13.to(DEV), w2.to(DEV))
+
+
+# (T, H, I, E, K): one 16-token tile, several tiles, a multi-pass slot
+# (more than 128 tokens on one expert), a tiny call
+@pytest.mark.parametrize("T,H,I,E,K", [(16, 2048, 768, 16, 8), (64, 2048, 768, 32, 8),
+                                        (300, 512, 256, 4, 2), (5, 512, 256, 8, 2),
+                                        (40, 1024, 512, 128, 8)])
+def test_experts_mfma_bf16(T, H, I, E, K):
+    x, w, ids, w13, w2 = _expert_case(T * 13 + E, T, H, I, E, K, torch.bfloat16)
+    out = run_experts(*_dev_case(x, w, ids, w13, w2), algo=MFMA)
+    assert rel_err(out, moe_forward(x, w, ids, w13, w2)) < 1e-2
+    assert rel_err(out, moe_forward(x, w, ids, w13, w2, act_round="bf16")) < 4e-3
+
+
+def test_experts_mfma_absent_slot_contributes_zero():
+    x, w, ids, w13, w2 = _expert_case(6, 20, 512, 256, 8, 2, torch.bfloat16)
+    slots = torch.tensor(ids, dtype=torch.int32)
+    slots[3, 1] = -1
+    slots[7, 0] = -1
+    wt = torch.tensor(w, dtype=torch.float32)
+    out = run_experts(x.to(DEV), wt.to(DEV), slots.to(DEV), w13.to(DEV), w2.to(DEV), algo=MFMA)
+    wz = wt.clone()
+    wz[3, 1] = 0
+    wz[7, 0] = 0
+    assert rel_err(out, moe_forward(x, wz.numpy(), ids, w13, w2, act_round="bf16")) < 4e-3
+
+
+def test_mfma_bytes_independent_of_slots_and_grouping():
+    # A token's output must not depend on its slot numbers nor on which other
+    # tokens share the call: this is what makes paged == resident bytes.
+    x, w, ids, w13, w2 = _expert_case(12, 48, 2048, 768, 16, 8, torch.bfloat16)
+    xd, wd, idd, w13d, w2d = _dev_case(x, w, ids, w13, w2)
+    whole = run_experts(xd, wd, idd, w13d, w2d, algo=MFMA)
+    perm = torch.randperm(16, generator=torch.Generator().manual_seed(2))
+    inv = torch.argsort(perm)
+    moved = run_experts(xd, wd, inv[torch.as_tensor(ids)].to(torch.int32).to(DEV),
+                        w13[perm].to(DEV), w2[perm].to(DEV), algo=MFMA)
+    assert torch.equal(whole.view(torch.int16), moved.view(torch.int16))
+    for a, b in [(0, 5), (5, 21), (21, 48)]:
+        part = run_experts(xd[a:b].contiguous(), wd[a:b].contiguous(), idd[a:b].contiguous(),
+                           w13d, w2d, algo=MFMA)
+        assert torch.equal(part.view(torch.int16), whole[a:b].view(torch.int16)), (a, b)

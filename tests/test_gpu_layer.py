@@ -154,3 +154,37 @@ def test_kernel_engine_needs_pinned_masters():
             assert _lib.lib().wisp_layer_pagein_engine(h) == _lib.WISP_PAGEIN_MEMCPY
         finally:
             _lib.lib().wisp_layer_destroy(h)
+
+
+def test_prefill_chunk_layer_mfma():
+    # 96-token chunk at the Qwen3 shape, cap 32 of 128 experts: the call is
+    # split into greedy token groups and runs on the MFMA grouped GEMM
+    wl = W.batch_prefill(tokens=96, pin=True)
+    drive(wl, 32, 1, tol=1e-2)
+
+
+@pytest.mark.parametrize("algo", [1, 2], ids=["gemv", "mfma"])
+def test_batched_decode_explicit_algo(algo):
+    wl = W.batch_decode(steps=2, tokens=8, pin=True)
+    drive(wl, 32, wl.steps, tol=1e-2, algo=algo)
+
+
+def test_mixtral_shape_decode_small_steps():
+    wl = W.mixtral(steps=6, pin=True)
+    drive(wl, 4, wl.steps, check_out_every=3, tol=1e-2)
+
+
+def test_mixtral_shape_batch16_mfma():
+    # bs=16 at the Mixtral shape (8 experts, top-2, cap 4): sub-batched groups
+    # on the MFMA path
+    wl = W.mixtral(steps=2, tokens=16, pin=True)
+    drive(wl, 4, wl.steps, check_out_every=2, tol=1e-2)
+
+
+def test_overflow_token_raises_subbatch():
+    wl = W.toy(steps=2, pin=True)
+    w13, w2 = wl.views()
+    st = WispMoEState(w13, w2, 2, "paged", DEV, 0)
+    x = wl.x[0].to(DEV)
+    with pytest.raises(RuntimeError, match="sub-batch"):
+        st.forward(x, wl.logits[0].to(DEV), 3, True)

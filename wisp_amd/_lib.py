@@ -54,7 +54,7 @@ class Workspace(C.Structure):
     _fields_ = [
         ("max_pairs", C.c_int), ("topk_w", _vp), ("topk_ids", _vp), ("slots", _vp),
         ("flags", _vp), ("loads", _vp), ("act", _vp), ("record", _vp),
-        ("record_words", C.c_int),
+        ("record_words", C.c_int), ("work", _vp), ("work_bytes", _sz),
     ]
 
 
@@ -72,8 +72,9 @@ SIGNATURES = {
     "wisp_subbatch_plan": (_i32, [_vp, _i32, _i32, _i32, _vp]),
     "wisp_pagein_issue": (_i32, [_vp, _i32, _i32, _i32, _i32, _vp, _sz, _vp, _sz, _vp, _sz, _vp,
                                  _sz, _sz, _sz, _i32, _vp]),
-    "wisp_moe_experts": (_i32, [_vp, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _sz, _vp, _sz,
-                                _vp, _vp, _i32, _vp]),
+    "wisp_moe_experts": (_i32, [_vp, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _i32, _vp, _sz,
+                                _vp, _sz, _vp, _vp, _vp, _sz, _i32, _vp]),
+    "wisp_moe_work_bytes": (_sz, [_i32, _i32, _i32, _i32]),
     "wisp_layer_create": (_i32, [C.POINTER(LayerDesc), C.POINTER(_vp)]),
     "wisp_layer_destroy": (_i32, [_vp]),
     "wisp_layer_set_scratch": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp]),

@@ -1,15 +1,317 @@
-// Batched/prefill expert kernels on the bf16 MFMA units (grouped GEMM).
+// Batched/prefill expert kernels on the bf16 MFMA units: a grouped GEMM over
+// the slots present in the call.
+//
+// Replaces vLLM fused_experts for multi-token calls
+// (src/wisp/integrations/vllm/fused_moe.py:1106-1118, 1155-1167); same
+// arithmetic as the decode GEMV kernels:
+//   act[p]  = bf16(silu(W13[s][:I] x[t]) * (W13[s][I:] x[t]))   p = (t, k)
+//   y[p]    = W2[s] act[p]                                        (fp32)
+//   out[t]  = bf16(sum_{k ascending} w[t,k] * y[(t, k)])
+//
+// Four launches:
+//   1. gather: per slot s, the ascending list of pairs routed to s and its
+//      length (one wave per slot, ballot compaction - stable, deterministic);
+//   2. w13: block (i-panel of 64, slot s) streams the 64 gate rows and 64 up
+//      rows of the panel once and multiplies them against every token of s,
+//      16 tokens per MFMA tile (v_mfma_f32_16x16x32_bf16), with the gathered
+//      x rows staged in LDS 256 columns at a time; epilogue silu(g) * u;
+//   3. w2: block (h-panel of 64, slot s) likewise over act, writing fp32 y;
+//   4. combine: out[t] from y in routing order.
+// Each output element is one MFMA dot product chain over K in a fixed order,
+// independent of which other tokens share its tile, so a token's bytes do not
+// depend on the grouping or the slot numbers: paged calls (split into token
+// groups) give the same bytes as resident calls.
+//
+// At the Qwen3-30B-A3B shapes the expert weights are 9 MiB and a prefill
+// chunk routes ~32 tokens to each expert, about 32 FLOP per weight byte: far
+// below the bf16 ridge (~315 FLOP/B), so these kernels are HBM-bound and are
+// built to stream each weight byte once per call.
 #include "common.h"
 
 namespace wisp {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kKC = 256;             // K columns staged in LDS per chunk
+constexpr int kLdsRow = kKC + 8;     // padded LDS row (bf16): rows land on distinct banks
+constexpr int kPanel = 64;           // output columns per block: 4 waves x 16
+constexpr int kMaxMT = 8;            // 16-token tiles per pass (up to 128 tokens)
+
+__device__ inline u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ inline u32x4 ld16_stream(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+__device__ inline bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+__device__ inline uint16_t bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ inline float silu(float g) { return g / (1.0f + expf(-g)); }
+
+// Work buffer carve-up (bytes, each piece 256-byte aligned).
+struct WorkLayout {
+  size_t lists, counts, y, total;
+  WorkLayout(int P, int H, int nslots) {
+    auto up = [](size_t b) { return (b + 255) & ~(size_t)255; };
+    lists = 0;
+    counts = up((size_t)nslots * P * 4);
+    y = counts + up((size_t)nslots * 4);
+    total = y + up((size_t)P * H * 4);
+  }
+};
+
+// ---------------------------------------------------------------------------
+// 1. gather: lists[s * P + j] = j-th pair (ascending) with slots[p] == s.
+// grid = nslots, block = one wave.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(64) void gather_kernel(const int32_t* __restrict__ slots, int P,
+                                                    int32_t* __restrict__ lists,
+                                                    int32_t* __restrict__ counts) {
+  const int s = blockIdx.x, lane = threadIdx.x;
+  int32_t* L = lists + (size_t)s * P;
+  int n = 0;
+  for (int base = 0; base < P; base += 64) {
+    const int p = base + lane;
+    const bool m = p < P && slots[p] == s;
+    const uint64_t b = __ballot(m);
+    if (m) L[n + __popcll(b & ((1ull << lane) - 1ull))] = p;
+    n += __popcll(b);
+  }
+  if (lane == 0) counts[s] = n;
+}
+
+// Stages rows [m0, m0 + MT*16) of the A operand, columns [k0, k0 + kKC), into
+// LDS.  Row r is A_row(list[m0 + r]) of length ld; rows past `mrows` are zero.
+template <int MT, bool kTokenRows>
+__device__ inline void stage_a(uint16_t (*As)[kLdsRow], const uint16_t* __restrict__ A, int ld,
+                               int K, const int32_t* __restrict__ list, int m0, int mrows, int k0) {
+  constexpr int kVecs = kKC / 8;  // 16-byte vectors per row chunk
+  for (int idx = threadIdx.x; idx < MT * 16 * kVecs; idx += 256) {
+    const int r = idx / kVecs, c = idx % kVecs;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (r < mrows) {
+      const int p = list[m0 + r];
+      const int row = kTokenRows ? p / K : p;
+      v = ld16(A + (size_t)row * ld + k0 + c * 8);
+    }
+    *reinterpret_cast<u32x4*>(&As[r][c * 8]) = v;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 2. w13 + SiLU*mul.  grid = (I / 64, nslots); wave w owns i in
+// [blockIdx.x*64 + 16w, +16): gate rows i and up rows I + i.
+// ---------------------------------------------------------------------------
+template <int MT>
+__global__ __launch_bounds__(256) void mfma_w13_kernel(
+    const uint16_t* __restrict__ x, int H, int I, int K, int P, const int32_t* __restrict__ lists,
+    const int32_t* __restrict__ counts, const uint16_t* __restrict__ w13, size_t w13_stride,
+    uint16_t* __restrict__ act) {
+  __shared__ __attribute__((aligned(16))) uint16_t As[MT * 16][kLdsRow];
+  const int s = blockIdx.y;
+  const int M = counts[s];
+  if (M == 0) return;
+  const int32_t* list = lists + (size_t)s * P;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int i0 = blockIdx.x * kPanel + wave * 16;
+  const int kq = (lane >> 4) * 8;  // this lane's 8 columns of a 32-wide k-step
+  const uint16_t* Wg = w13 + (size_t)s * w13_stride + (size_t)(i0 + (lane & 15)) * H + kq;
+  const uint16_t* Wu = Wg + (size_t)I * H;
+
+  for (int m0 = 0; m0 < M; m0 += MT * 16) {
+    const int mrows = min(M - m0, MT * 16);
+    f32x4 ag[MT], au[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      ag[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+      au[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    for (int k0 = 0; k0 < H; k0 += kKC) {
+      u32x4 bg[kKC / 32], bu[kKC / 32];
+#pragma unroll
+      for (int j = 0; j < kKC / 32; ++j) {
+        bg[j] = ld16_stream(Wg + k0 + j * 32);
+        bu[j] = ld16_stream(Wu + k0 + j * 32);
+      }
+      __syncthreads();  // the previous chunk's A reads are done
+      stage_a<MT, true>(As, x, H, K, list, m0, mrows, k0);
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < kKC / 32; ++j) {
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          if (t * 16 < mrows) {
+            const bf16x8 a = *reinterpret_cast<const bf16x8*>(&As[t * 16 + (lane & 15)][j * 32 + kq]);
+            ag[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, as_bf16x8(bg[j]), ag[t], 0, 0, 0);
+            au[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, as_bf16x8(bu[j]), au[t], 0, 0, 0);
+          }
+        }
+      }
+    }
+    // C[row][col]: row = 16t + 4*(lane/16) + q, col = lane % 16
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = t * 16 + (lane >> 4) * 4 + q;
+        if (r < mrows) {
+          const int p = list[m0 + r];
+          act[(size_t)p * I + i0 + (lane & 15)] = bf16_rne(silu(ag[t][q]) * au[t][q]);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 3. w2: y[p, h] = W2[s][h, :] . act[p, :].  grid = (H / 64, nslots); wave w
+// owns h in [blockIdx.x*64 + 16w, +16).
+// ---------------------------------------------------------------------------
+template <int MT>
+__global__ __launch_bounds__(256) void mfma_w2_kernel(
+    const uint16_t* __restrict__ act, int H, int I, int P, const int32_t* __restrict__ lists,
+    const int32_t* __restrict__ counts, const uint16_t* __restrict__ w2, size_t w2_stride,
+    float* __restrict__ y) {
+  __shared__ __attribute__((aligned(16))) uint16_t As[MT * 16][kLdsRow];
+  const int s = blockIdx.y;
+  const int M = counts[s];
+  if (M == 0) return;
+  const int32_t* list = lists + (size_t)s * P;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int h0 = blockIdx.x * kPanel + wave * 16;
+  const int kq = (lane >> 4) * 8;
+  const uint16_t* Wr = w2 + (size_t)s * w2_stride + (size_t)(h0 + (lane & 15)) * I + kq;
+
+  for (int m0 = 0; m0 < M; m0 += MT * 16) {
+    const int mrows = min(M - m0, MT * 16);
+    f32x4 acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 0; k0 < I; k0 += kKC) {
+      u32x4 b[kKC / 32];
+#pragma unroll
+      for (int j = 0; j < kKC / 32; ++j) b[j] = ld16_stream(Wr + k0 + j * 32);
+      __syncthreads();
+      stage_a<MT, false>(As, act, I, 1, list, m0, mrows, k0);
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < kKC / 32; ++j) {
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          if (t * 16 < mrows) {
+            const bf16x8 a = *reinterpret_cast<const bf16x8*>(&As[t * 16 + (lane & 15)][j * 32 + kq]);
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, as_bf16x8(b[j]), acc[t], 0, 0, 0);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = t * 16 + (lane >> 4) * 4 + q;
+        if (r < mrows) y[(size_t)list[m0 + r] * H + h0 + (lane & 15)] = acc[t][q];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 4. combine: out[t, h] = bf16(sum_k w[t,k] * y[(t,k), h]), k ascending,
+// skipping pairs without a slot.  grid = (ceil(H / 256), T).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ y, int H, int K,
+                                                     int nslots, const float* __restrict__ topk_w,
+                                                     const int32_t* __restrict__ slots,
+                                                     uint16_t* __restrict__ out) {
+  const int t = blockIdx.y;
+  const int h = blockIdx.x * 256 + threadIdx.x;
+  if (h >= H) return;
+  float acc = 0.f;
+  for (int k = 0; k < K; ++k) {
+    const int p = t * K + k;
+    const int s = slots[p];
+    if (s < 0 || s >= nslots) continue;
+    acc = fmaf(topk_w[p], y[(size_t)p * H + h], acc);
+  }
+  out[(size_t)t * H + h] = bf16_rne(acc);
+}
+
+template <int MT>
+void launch_gemms(const uint16_t* x, int H, int I, int K, int P, int nslots, const int32_t* lists,
+                  const int32_t* counts, const uint16_t* w13, size_t w13_stride,
+                  const uint16_t* w2, size_t w2_stride, uint16_t* act, float* y, hipStream_t st,
+                  const StageEvents* ev) {
+  launch_timed(mfma_w13_kernel<MT>, dim3(I / kPanel, nslots), dim3(256), st,
+               ev ? ev->ev[0] : nullptr, ev ? ev->ev[1] : nullptr, x, H, I, K, P, lists, counts,
+               w13, w13_stride, act);
+  launch_timed(mfma_w2_kernel<MT>, dim3(H / kPanel, nslots), dim3(256), st,
+               ev ? ev->ev[2] : nullptr, ev ? ev->ev[3] : nullptr, act, H, I, P, lists, counts,
+               w2, w2_stride, y);
+}
+
+}  // namespace
+
+size_t mfma_work_bytes(int T, int K, int H, int nslots) {
+  if (T < 1 || K < 1 || H < 1 || nslots < 1) return 0;
+  return WorkLayout(T * K, H, nslots).total;
+}
+
+// Shapes the MFMA path covers (else the caller uses the GEMV kernels).
+bool mfma_supported(int H, int I) {
+  return H >= kKC && I >= kKC && H % kKC == 0 && I % kKC == 0;
+}
 
 int experts_mfma(const void* x, int T, int H, int I, int K, const float* topk_w,
-                 const int32_t* slots, const void* w13, size_t w13_stride, const void* w2,
-                 size_t w2_stride, void* act, void* out, hipStream_t st, const StageEvents* ev) {
-  (void)x; (void)T; (void)H; (void)I; (void)K; (void)topk_w; (void)slots; (void)w13;
-  (void)w13_stride; (void)w2; (void)w2_stride; (void)act; (void)out; (void)st; (void)ev;
-  wisp_set_last_error("MFMA expert path not built yet", "wisp_moe_experts");
-  return WISP_ERR_UNSUPPORTED;
+                 const int32_t* slots, int nslots, const void* w13, size_t w13_stride,
+                 const void* w2, size_t w2_stride, void* act, void* out, void* work,
+                 size_t work_bytes, hipStream_t st, const StageEvents* ev) {
+  if (T == 0) return WISP_OK;
+  if (!mfma_supported(H, I)) {
+    wisp_set_last_error("MFMA path needs hidden and intermediate sizes that are multiples of 256",
+                        "MFMA experts");
+    return WISP_ERR_UNSUPPORTED;
+  }
+  const int P = T * K;
+  const WorkLayout W(P, H, nslots);
+  if (nslots < 1 || nslots > 65535 || !work || work_bytes < W.total ||
+      ((uintptr_t)work) % 256) {
+    wisp_set_last_error("MFMA work buffer missing, misaligned or too small", "MFMA experts");
+    return WISP_ERR_INVALID;
+  }
+  int32_t* lists = (int32_t*)((char*)work + W.lists);
+  int32_t* counts = (int32_t*)((char*)work + W.counts);
+  float* y = (float*)((char*)work + W.y);
+  hipLaunchKernelGGL(gather_kernel, dim3(nslots), dim3(64), 0, st, slots, P, lists, counts);
+  // A slot holds a token at most once (a token's top-k experts are
+  // distinct), so T bounds the rows of any slot.
+  const uint16_t* xb = (const uint16_t*)x;
+  const uint16_t* a13 = (const uint16_t*)w13;
+  const uint16_t* a2 = (const uint16_t*)w2;
+  uint16_t* ab = (uint16_t*)act;
+  if (T <= 16)
+    launch_gemms<1>(xb, H, I, K, P, nslots, lists, counts, a13, w13_stride, a2, w2_stride, ab, y,
+                    st, ev);
+  else if (T <= 32)
+    launch_gemms<2>(xb, H, I, K, P, nslots, lists, counts, a13, w13_stride, a2, w2_stride, ab, y,
+                    st, ev);
+  else if (T <= 64)
+    launch_gemms<4>(xb, H, I, K, P, nslots, lists, counts, a13, w13_stride, a2, w2_stride, ab, y,
+                    st, ev);
+  else
+    launch_gemms<kMaxMT>(xb, H, I, K, P, nslots, lists, counts, a13, w13_stride, a2, w2_stride,
+                         ab, y, st, ev);
+  hipLaunchKernelGGL(combine_kernel, dim3((H + 255) / 256, T), dim3(256), 0, st, y, H, K, nslots,
+                     topk_w, slots, (uint16_t*)out);
+  WISP_HIP_TRY(hipGetLastError());
+  return WISP_OK;
 }
 
 }  // namespace wisp

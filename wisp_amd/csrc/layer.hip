@@ -73,8 +73,24 @@ int experts_gemv(const void* x, int dtype, int T, int H, int I, int K, const flo
                  const int32_t* slots, const void* w13, size_t w13_stride, const void* w2,
                  size_t w2_stride, void* act, void* out, hipStream_t st, const StageEvents* ev);
 int experts_mfma(const void* x, int T, int H, int I, int K, const float* topk_w,
-                 const int32_t* slots, const void* w13, size_t w13_stride, const void* w2,
-                 size_t w2_stride, void* act, void* out, hipStream_t st, const StageEvents* ev);
+                 const int32_t* slots, int nslots, const void* w13, size_t w13_stride,
+                 const void* w2, size_t w2_stride, void* act, void* out, void* work,
+                 size_t work_bytes, hipStream_t st, const StageEvents* ev);
+size_t mfma_work_bytes(int T, int K, int H, int nslots);
+bool mfma_supported(int H, int I);
+
+// Calls of at least this many tokens run the bf16 experts on the MFMA grouped
+// GEMM; fewer run the GEMV kernels, which stream each routed expert once per
+// token and win when the tokens of a call share few experts.
+constexpr int kMfmaMinTokens = 4;
+
+// The automatic expert-kernel choice.  It depends only on the call's dtype,
+// shape and token count, never on the grouping or the slots, so paged and
+// resident runs of one batch use one kernel.
+int auto_algo(int dtype, int H, int I, int T) {
+  return dtype == WISP_BF16 && mfma_supported(H, I) && T >= kMfmaMinTokens ? WISP_ALGO_MFMA
+                                                                          : WISP_ALGO_GEMV;
+}
 
 namespace {
 
@@ -346,24 +362,30 @@ int w2(Layer& L, const void* act, int T, int K, const float* w, const int32_t* s
 
 // Both expert stages for T tokens (any algorithm, no filters).
 int experts(Layer& L, const void* x, int T, int K, const float* w, const int32_t* slots,
-            void* act, void* out, int algo, hipStream_t st) {
+            void* act, void* out, int algo, const wisp_workspace* ws, hipStream_t st) {
   const wisp_layer_desc& d = L.d;
-  if (algo == WISP_ALGO_MFMA)
-    return experts_mfma(x, T, d.hidden, d.inter, K, w, slots, d.scratch_w13, d.scratch_w13_stride,
-                        d.scratch_w2, d.scratch_w2_stride, act, out, st, nullptr);
+  if (algo == WISP_ALGO_MFMA) {
+    ProfLaunch* p13 = prof_begin(L, 0);
+    ProfLaunch* p2 = prof_begin(L, 1);
+    StageEvents ev = {{p13 ? p13->start : nullptr, p13 ? p13->stop : nullptr,
+                       p2 ? p2->start : nullptr, p2 ? p2->stop : nullptr}};
+    int rc = experts_mfma(x, T, d.hidden, d.inter, K, w, slots, d.cap, d.scratch_w13,
+                          d.scratch_w13_stride, d.scratch_w2, d.scratch_w2_stride, act, out,
+                          ws->work, ws->work_bytes, st, (p13 && p2) ? &ev : nullptr);
+    if (rc == WISP_OK && p13 && p2) p13->pending = p2->pending = true;
+    return rc;
+  }
   int rc = w13(L, x, T, K, slots, act, st, nullptr, 0);
   if (rc != WISP_OK) return rc;
   return w2(L, act, T, K, w, slots, out, st, nullptr, nullptr);
 }
 
-// Kernel choice depends only on the whole call's T, K and the dtype, never
-// on the grouping or the slots, so paged and resident runs of one batch use
-// one kernel.
-int choose_algo(const Layer& L, int algo, int T, int K) {
-  (void)L;
-  (void)T;
-  (void)K;
-  if (algo == WISP_ALGO_AUTO) return WISP_ALGO_GEMV;
+// The expert algorithm of a layer call (-1: the request does not cover it).
+int choose_algo(const Layer& L, int algo, int T) {
+  const wisp_layer_desc& d = L.d;
+  if (algo == WISP_ALGO_AUTO) return auto_algo(d.dtype, d.hidden, d.inter, T);
+  if (algo == WISP_ALGO_MFMA && (d.dtype != WISP_BF16 || !mfma_supported(d.hidden, d.inter)))
+    return -1;
   if (algo != WISP_ALGO_GEMV && algo != WISP_ALGO_MFMA) return -1;
   return algo;
 }
@@ -371,7 +393,7 @@ int choose_algo(const Layer& L, int algo, int T, int K) {
 // Copies and expert kernels for groups [0, ngroups) of a decision record.
 int run_groups(Layer& L, const int32_t* rec, const int32_t* loads, int T, int K, int ngroups,
                bool compute, const void* x, const float* topk_w, const int32_t* slots, void* act,
-               void* out, int algo, hipStream_t st) {
+               void* out, int algo, const wisp_workspace* ws, hipStream_t st) {
   const RecordLayout RL(T, K);
   const size_t row = (size_t)L.d.hidden * L.es;
   int last_gemm = -1;
@@ -387,7 +409,7 @@ int run_groups(Layer& L, const int32_t* rec, const int32_t* loads, int T, int K,
     }
     if (compute && t1 > t0) {
       int rc = experts(L, (const char*)x + (size_t)t0 * row, t1 - t0, K, topk_w + (size_t)t0 * K,
-                       slots + (size_t)t0 * K, act, (char*)out + (size_t)t0 * row, algo, st);
+                       slots + (size_t)t0 * K, act, (char*)out + (size_t)t0 * row, algo, ws, st);
       if (rc != WISP_OK) return rc;
       WISP_HIP_TRY(hipEventRecord(L.ev_gemm[g % kEventRing], st));
       last_gemm = g;
@@ -548,8 +570,8 @@ extern "C" int wisp_layer_forward(void* handle, const void* x, const void* logit
                         "wisp_layer_forward");
     return WISP_ERR_UNSUPPORTED;
   }
-  const int a = choose_algo(*L, algo, T, K);
-  if (a < 0 || (a == WISP_ALGO_MFMA && d.dtype != WISP_BF16)) {
+  const int a = choose_algo(*L, algo, T);
+  if (a < 0) {
     wisp_set_last_error("requested expert algorithm does not cover this call",
                         "wisp_layer_forward");
     return WISP_ERR_UNSUPPORTED;
@@ -560,7 +582,7 @@ extern "C" int wisp_layer_forward(void* handle, const void* x, const void* logit
     rc = wisp_route_topk_softmax(logits, logits_dtype, T, d.num_experts, K, renormalize,
                                  ws->topk_w, ws->topk_ids, d.counters + kForward, stream);
     if (rc != WISP_OK) return rc;
-    return experts(*L, x, T, K, ws->topk_w, ws->topk_ids, ws->act, out, a, st);
+    return experts(*L, x, T, K, ws->topk_w, ws->topk_ids, ws->act, out, a, ws, st);
   }
 
   const bool fuse_route = T <= kFusedRouteTokens;
@@ -583,7 +605,7 @@ extern "C" int wisp_layer_forward(void* handle, const void* x, const void* logit
   if (one_group && L->kpin) {
     rc = page_in_kernel(*L, ws->loads, ws->flags, 0, st);
     if (rc != WISP_OK) return rc;
-    return experts(*L, x, T, K, ws->topk_w, ws->slots, ws->act, out, a, st);
+    return experts(*L, x, T, K, ws->topk_w, ws->slots, ws->act, out, a, ws, st);
   }
   WISP_HIP_TRY(hipEventRecord(L->ev_decided, st));
 
@@ -617,7 +639,7 @@ extern "C" int wisp_layer_forward(void* handle, const void* x, const void* logit
     return rc;
   }
   rc = run_groups(*L, rec, ws->loads, T, K, rec[kRecGroupsDone], status == WISP_OK, x,
-                  ws->topk_w, ws->slots, ws->act, out, a, st);
+                  ws->topk_w, ws->slots, ws->act, out, a, ws, st);
   if (rc != WISP_OK) return rc;
   if (status == WISP_ERR_SUBBATCH)
     wisp_set_last_error("one token routes to more experts than cap; sub-batching cannot help",
@@ -742,11 +764,13 @@ extern "C" int wisp_pagein_issue(const int32_t* record, int record_words, int T,
 }
 
 extern "C" int wisp_moe_experts(const void* x, int dtype, int T, int H, int I, int K,
-                                const float* topk_w, const int32_t* slots, const void* w13,
-                                size_t w13_stride, const void* w2, size_t w2_stride, void* act,
-                                void* out, int algo, wisp_stream_t stream) {
+                                const float* topk_w, const int32_t* slots, int nslots,
+                                const void* w13, size_t w13_stride, const void* w2,
+                                size_t w2_stride, void* act, void* out, void* work,
+                                size_t work_bytes, int algo, wisp_stream_t stream) {
   using namespace wisp;
-  if (T < 0 || H < 1 || I < 1 || K < 1 || (dtype != WISP_F32 && dtype != WISP_BF16) ||
+  if (T < 0 || H < 1 || I < 1 || K < 1 || nslots < 1 ||
+      (dtype != WISP_F32 && dtype != WISP_BF16) ||
       (T > 0 && (!x || !topk_w || !slots || !w13 || !w2 || !act || !out)))
     return WISP_ERR_INVALID;
   const size_t es = elem_size(dtype);
@@ -756,12 +780,20 @@ extern "C" int wisp_moe_experts(const void* x, int dtype, int T, int H, int I, i
     wisp_set_last_error("H, I and buffers must be 16-byte aligned", "wisp_moe_experts");
     return WISP_ERR_UNSUPPORTED;
   }
-  const int a = algo == WISP_ALGO_AUTO ? WISP_ALGO_GEMV : algo;
+  const int a = algo == WISP_ALGO_AUTO ? auto_algo(dtype, H, I, T) : algo;
   if (a == WISP_ALGO_MFMA) {
-    if (dtype != WISP_BF16) return WISP_ERR_UNSUPPORTED;
-    return experts_mfma(x, T, H, I, K, topk_w, slots, w13, w13_stride, w2, w2_stride, act, out,
-                        (hipStream_t)stream, nullptr);
+    if (dtype != WISP_BF16) {
+      wisp_set_last_error("the MFMA path computes in bf16 only", "wisp_moe_experts");
+      return WISP_ERR_UNSUPPORTED;
+    }
+    return experts_mfma(x, T, H, I, K, topk_w, slots, nslots, w13, w13_stride, w2, w2_stride,
+                        act, out, work, work_bytes, (hipStream_t)stream, nullptr);
   }
+  if (a != WISP_ALGO_GEMV) return WISP_ERR_INVALID;
   return experts_gemv(x, dtype, T, H, I, K, topk_w, slots, w13, w13_stride, w2, w2_stride, act,
                       out, (hipStream_t)stream, nullptr);
+}
+
+extern "C" size_t wisp_moe_work_bytes(int T, int K, int H, int nslots) {
+  return wisp::mfma_work_bytes(T, K, H, nslots);
 }

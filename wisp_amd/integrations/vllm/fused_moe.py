@@ -117,15 +117,18 @@ def _check_master(t: torch.Tensor, name: str) -> None:
 class _Workspace:
     """Per-layer device workspaces and the pinned decision record, grown on demand."""
 
-    def __init__(self, device: torch.device, inter: int, dtype: torch.dtype) -> None:
-        self.device, self.inter, self.dtype = device, inter, dtype
+    def __init__(self, device: torch.device, hidden: int, inter: int,
+                 dtype: torch.dtype) -> None:
+        self.device, self.hidden, self.inter, self.dtype = device, hidden, inter, dtype
         self.pairs = 0
         self.record_words = 0
+        self.work_bytes = 0
+        self.work = None
         self.struct = _lib.Workspace()
         self.topk_w = self.topk_ids = self.slots = self.flags = self.loads = None
         self.act = self.record = None
 
-    def ensure(self, T: int, K: int) -> "_lib.Workspace":
+    def ensure(self, T: int, K: int, nslots: int) -> "_lib.Workspace":
         pairs = max(1, T * K)
         words = lib().wisp_record_words(T, K)
         if pairs > self.pairs:
@@ -140,12 +143,21 @@ class _Workspace:
         if words > self.record_words:
             self.record_words = max(words, 2 * self.record_words)
             self.record = torch.zeros(self.record_words, dtype=torch.int32, pin_memory=True)
+        # the bf16 MFMA path's per-slot pair lists and fp32 per-pair outputs
+        need = 0
+        if self.dtype == torch.bfloat16 and self.hidden > 0:
+            need = lib().wisp_moe_work_bytes(max(1, T), K, self.hidden, nslots)
+        if need > self.work_bytes:
+            self.work_bytes = max(need, 2 * self.work_bytes)
+            self.work = torch.empty(self.work_bytes, dtype=torch.uint8, device=self.device)
         s = self.struct
         s.max_pairs = self.pairs
         s.topk_w, s.topk_ids = self.topk_w.data_ptr(), self.topk_ids.data_ptr()
         s.slots, s.act = self.slots.data_ptr(), self.act.data_ptr()
         s.flags, s.loads = self.flags.data_ptr(), self.loads.data_ptr()
         s.record, s.record_words = self.record.data_ptr(), self.record_words
+        s.work = self.work.data_ptr() if self.work is not None else None
+        s.work_bytes = self.work_bytes
         return s
 
 
@@ -198,7 +210,7 @@ class WispMoEState:
         self._counters = torch.zeros(8, dtype=torch.int64, device=dev)
         self.stats_pred_hits = 0
         self.stats_pred_total = 0
-        self._ws = _Workspace(dev, max(1, I), self.dtype)
+        self._ws = _Workspace(dev, self.hidden, max(1, I), self.dtype)
         self._last_pairs = 0
         self._handle = C.c_void_p()
         self._desc = self._make_desc()
@@ -310,7 +322,7 @@ class WispMoEState:
         when more distinct experts are needed than ``cap_experts``."""
         ids = needed_experts.reshape(-1).to(device=self.device, dtype=torch.int32).contiguous()
         n = ids.numel()
-        ws = self._ws.ensure(n, 1)
+        ws = self._ws.ensure(n, 1, self.cap_experts)
         rc = lib().wisp_layer_ensure_resident(self._handle, ids.data_ptr() if n else None, n,
                                               C.byref(ws), _lib.stream_handle())
         check(rc, "ensure_resident")
@@ -333,7 +345,7 @@ class WispMoEState:
         T = x.shape[0]
         if out is None:
             out = torch.empty_like(x)
-        ws = self._ws.ensure(T, top_k)
+        ws = self._ws.ensure(T, top_k, self.cap_experts)
         rc = lib().wisp_layer_forward(self._handle, x.data_ptr(), router_logits.data_ptr(),
                                       _DTYPES[router_logits.dtype], T, int(top_k),
                                       int(bool(renormalize)), out.data_ptr(), C.byref(ws),
@@ -551,10 +563,13 @@ def _route_and_experts(x, router_logits, top_k, renormalize, w13, w2) -> torch.T
                                         topk_ids.data_ptr(), None, st), "route")
     act = torch.empty((max(1, T * top_k), I), dtype=x.dtype, device=dev)
     out = torch.empty_like(x)
+    nbytes = lib().wisp_moe_work_bytes(max(1, T), top_k, H, E)
+    work = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     check(lib().wisp_moe_experts(x.data_ptr(), _DTYPES[x.dtype], T, H, I, top_k,
-                                 topk_w.data_ptr(), topk_ids.data_ptr(), w13.data_ptr(),
+                                 topk_w.data_ptr(), topk_ids.data_ptr(), E, w13.data_ptr(),
                                  w13.stride(0), w2.data_ptr(), w2.stride(0), act.data_ptr(),
-                                 out.data_ptr(), _lib.WISP_ALGO_AUTO, st), "experts")
+                                 out.data_ptr(), work.data_ptr(), nbytes, _lib.WISP_ALGO_AUTO,
+                                 st), "experts")
     return out
 
 
