@@ -12,9 +12,9 @@
 //   1. gather: per slot s, the ascending list of pairs routed to s and its
 //      length (one wave per slot, ballot compaction - stable, deterministic);
 //   2. w13: block (i-panel of 64, slot s) streams the 64 gate rows and 64 up
-//      rows of the panel once and multiplies them against every token of s,
-//      16 tokens per MFMA tile (v_mfma_f32_16x16x32_bf16), with the gathered
-//      x rows staged in LDS 256 columns at a time; epilogue silu(g) * u;
+//      rows of the panel once per 64 tokens of s and multiplies them against
+//      those tokens, 16 per MFMA tile (v_mfma_f32_16x16x32_bf16), with the
+//      token fragments read from the L2-resident x rows; epilogue silu(g) * u;
 //   3. w2: block (h-panel of 64, slot s) likewise over act, writing fp32 y;
 //   4. combine: out[t] from y in routing order.
 // Each output element is one MFMA dot product chain over K in a fixed order,
@@ -35,10 +35,10 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kKC = 256;             // K columns staged in LDS per chunk
-constexpr int kLdsRow = kKC + 8;     // padded LDS row (bf16): rows land on distinct banks
+constexpr int kKAlign = 256;         // H and I must be multiples (up to 8 k-steps per iteration)
 constexpr int kPanel = 64;           // output columns per block: 4 waves x 16
-constexpr int kMaxMT = 8;            // 16-token tiles per pass (up to 128 tokens)
+constexpr int kMaxMT = 4;            // 16-token tiles per pass (64 tokens); more tokens
+                                     // on a slot take further passes over its weights
 
 __device__ inline u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ inline u32x4 ld16_stream(const void* p) {
@@ -87,70 +87,82 @@ __global__ __launch_bounds__(64) void gather_kernel(const int32_t* __restrict__ 
   if (lane == 0) counts[s] = n;
 }
 
-// Stages rows [m0, m0 + MT*16) of the A operand, columns [k0, k0 + kKC), into
-// LDS.  Row r is A_row(list[m0 + r]) of length ld; rows past `mrows` are zero.
+// Row pointers of this lane's A rows (row lane%16 of each 16-token tile of
+// the pass starting at m0), offset to the lane's 8 columns of a k-step; null
+// for rows past the slot's last token (they read as zero).
 template <int MT, bool kTokenRows>
-__device__ inline void stage_a(uint16_t (*As)[kLdsRow], const uint16_t* __restrict__ A, int ld,
-                               int K, const int32_t* __restrict__ list, int m0, int mrows, int k0) {
-  constexpr int kVecs = kKC / 8;  // 16-byte vectors per row chunk
-  for (int idx = threadIdx.x; idx < MT * 16 * kVecs; idx += 256) {
-    const int r = idx / kVecs, c = idx % kVecs;
-    u32x4 v = {0u, 0u, 0u, 0u};
+__device__ inline void a_rows(const uint16_t* (&ap)[MT], const uint16_t* __restrict__ A, int ld,
+                              int K, const int32_t* __restrict__ list, int m0, int mrows,
+                              int lane) {
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    const int r = t * 16 + (lane & 15);
+    ap[t] = nullptr;
     if (r < mrows) {
       const int p = list[m0 + r];
-      const int row = kTokenRows ? p / K : p;
-      v = ld16(A + (size_t)row * ld + k0 + c * 8);
+      ap[t] = A + (size_t)(kTokenRows ? p / K : p) * ld + (lane >> 4) * 8;
     }
-    *reinterpret_cast<u32x4*>(&As[r][c * 8]) = v;
   }
+}
+
+__device__ inline u32x4 ld16_or_zero(const uint16_t* p, int off) {
+  if (!p) return u32x4{0u, 0u, 0u, 0u};
+  return ld16(p + off);
 }
 
 // ---------------------------------------------------------------------------
 // 2. w13 + SiLU*mul.  grid = (I / 64, nslots); wave w owns i in
-// [blockIdx.x*64 + 16w, +16): gate rows i and up rows I + i.
+// [blockIdx.x*64 + 16w, +16): gate rows i and up rows I + i.  Each wave
+// streams its 32 weight rows once per pass of up to MT*16 tokens, U k-steps
+// of 32 columns per iteration (16-byte loads per lane), and fetches the token
+// fragments of the same k-steps from x (small and shared: L2-resident).
+// No LDS, no barriers: waves are independent streams.
 // ---------------------------------------------------------------------------
-template <int MT>
+template <int MT, int U>
 __global__ __launch_bounds__(256) void mfma_w13_kernel(
     const uint16_t* __restrict__ x, int H, int I, int K, int P, const int32_t* __restrict__ lists,
     const int32_t* __restrict__ counts, const uint16_t* __restrict__ w13, size_t w13_stride,
     uint16_t* __restrict__ act) {
-  __shared__ __attribute__((aligned(16))) uint16_t As[MT * 16][kLdsRow];
   const int s = blockIdx.y;
   const int M = counts[s];
   if (M == 0) return;
   const int32_t* list = lists + (size_t)s * P;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int i0 = blockIdx.x * kPanel + wave * 16;
-  const int kq = (lane >> 4) * 8;  // this lane's 8 columns of a 32-wide k-step
-  const uint16_t* Wg = w13 + (size_t)s * w13_stride + (size_t)(i0 + (lane & 15)) * H + kq;
+  const uint16_t* Wg = w13 + (size_t)s * w13_stride + (size_t)(i0 + (lane & 15)) * H +
+                       (lane >> 4) * 8;
   const uint16_t* Wu = Wg + (size_t)I * H;
 
   for (int m0 = 0; m0 < M; m0 += MT * 16) {
     const int mrows = min(M - m0, MT * 16);
+    const uint16_t* ap[MT];
+    a_rows<MT, true>(ap, x, H, K, list, m0, mrows, lane);
     f32x4 ag[MT], au[MT];
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
       ag[t] = f32x4{0.f, 0.f, 0.f, 0.f};
       au[t] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    for (int k0 = 0; k0 < H; k0 += kKC) {
-      u32x4 bg[kKC / 32], bu[kKC / 32];
+    for (int k0 = 0; k0 < H; k0 += 32 * U) {
+      u32x4 bg[U], bu[U], a[U][MT];
 #pragma unroll
-      for (int j = 0; j < kKC / 32; ++j) {
-        bg[j] = ld16_stream(Wg + k0 + j * 32);
-        bu[j] = ld16_stream(Wu + k0 + j * 32);
+      for (int u = 0; u < U; ++u) {
+        bg[u] = ld16_stream(Wg + k0 + u * 32);
+        bu[u] = ld16_stream(Wu + k0 + u * 32);
       }
-      __syncthreads();  // the previous chunk's A reads are done
-      stage_a<MT, true>(As, x, H, K, list, m0, mrows, k0);
-      __syncthreads();
 #pragma unroll
-      for (int j = 0; j < kKC / 32; ++j) {
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) a[u][t] = ld16_or_zero(ap[t], k0 + u * 32);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
           if (t * 16 < mrows) {
-            const bf16x8 a = *reinterpret_cast<const bf16x8*>(&As[t * 16 + (lane & 15)][j * 32 + kq]);
-            ag[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, as_bf16x8(bg[j]), ag[t], 0, 0, 0);
-            au[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, as_bf16x8(bu[j]), au[t], 0, 0, 0);
+            ag[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a[u][t]), as_bf16x8(bg[u]),
+                                                            ag[t], 0, 0, 0);
+            au[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a[u][t]), as_bf16x8(bu[u]),
+                                                            au[t], 0, 0, 0);
           }
         }
       }
@@ -172,43 +184,44 @@ __global__ __launch_bounds__(256) void mfma_w13_kernel(
 
 // ---------------------------------------------------------------------------
 // 3. w2: y[p, h] = W2[s][h, :] . act[p, :].  grid = (H / 64, nslots); wave w
-// owns h in [blockIdx.x*64 + 16w, +16).
+// owns h in [blockIdx.x*64 + 16w, +16); same streaming scheme over act.
 // ---------------------------------------------------------------------------
-template <int MT>
+template <int MT, int U>
 __global__ __launch_bounds__(256) void mfma_w2_kernel(
     const uint16_t* __restrict__ act, int H, int I, int P, const int32_t* __restrict__ lists,
     const int32_t* __restrict__ counts, const uint16_t* __restrict__ w2, size_t w2_stride,
     float* __restrict__ y) {
-  __shared__ __attribute__((aligned(16))) uint16_t As[MT * 16][kLdsRow];
   const int s = blockIdx.y;
   const int M = counts[s];
   if (M == 0) return;
   const int32_t* list = lists + (size_t)s * P;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int h0 = blockIdx.x * kPanel + wave * 16;
-  const int kq = (lane >> 4) * 8;
-  const uint16_t* Wr = w2 + (size_t)s * w2_stride + (size_t)(h0 + (lane & 15)) * I + kq;
+  const uint16_t* Wr = w2 + (size_t)s * w2_stride + (size_t)(h0 + (lane & 15)) * I +
+                       (lane >> 4) * 8;
 
   for (int m0 = 0; m0 < M; m0 += MT * 16) {
     const int mrows = min(M - m0, MT * 16);
+    const uint16_t* ap[MT];
+    a_rows<MT, false>(ap, act, I, 1, list, m0, mrows, lane);
     f32x4 acc[MT];
 #pragma unroll
     for (int t = 0; t < MT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int k0 = 0; k0 < I; k0 += kKC) {
-      u32x4 b[kKC / 32];
+    for (int k0 = 0; k0 < I; k0 += 32 * U) {
+      u32x4 b[U], a[U][MT];
 #pragma unroll
-      for (int j = 0; j < kKC / 32; ++j) b[j] = ld16_stream(Wr + k0 + j * 32);
-      __syncthreads();
-      stage_a<MT, false>(As, act, I, 1, list, m0, mrows, k0);
-      __syncthreads();
+      for (int u = 0; u < U; ++u) b[u] = ld16_stream(Wr + k0 + u * 32);
 #pragma unroll
-      for (int j = 0; j < kKC / 32; ++j) {
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) a[u][t] = ld16_or_zero(ap[t], k0 + u * 32);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
-          if (t * 16 < mrows) {
-            const bf16x8 a = *reinterpret_cast<const bf16x8*>(&As[t * 16 + (lane & 15)][j * 32 + kq]);
-            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, as_bf16x8(b[j]), acc[t], 0, 0, 0);
-          }
+          if (t * 16 < mrows)
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a[u][t]), as_bf16x8(b[u]),
+                                                             acc[t], 0, 0, 0);
         }
       }
     }
@@ -244,15 +257,15 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
   out[(size_t)t * H + h] = bf16_rne(acc);
 }
 
-template <int MT>
+template <int MT, int U>
 void launch_gemms(const uint16_t* x, int H, int I, int K, int P, int nslots, const int32_t* lists,
                   const int32_t* counts, const uint16_t* w13, size_t w13_stride,
                   const uint16_t* w2, size_t w2_stride, uint16_t* act, float* y, hipStream_t st,
                   const StageEvents* ev) {
-  launch_timed(mfma_w13_kernel<MT>, dim3(I / kPanel, nslots), dim3(256), st,
+  launch_timed(mfma_w13_kernel<MT, U>, dim3(I / kPanel, nslots), dim3(256), st,
                ev ? ev->ev[0] : nullptr, ev ? ev->ev[1] : nullptr, x, H, I, K, P, lists, counts,
                w13, w13_stride, act);
-  launch_timed(mfma_w2_kernel<MT>, dim3(H / kPanel, nslots), dim3(256), st,
+  launch_timed(mfma_w2_kernel<MT, U>, dim3(H / kPanel, nslots), dim3(256), st,
                ev ? ev->ev[2] : nullptr, ev ? ev->ev[3] : nullptr, act, H, I, P, lists, counts,
                w2, w2_stride, y);
 }
@@ -266,7 +279,7 @@ size_t mfma_work_bytes(int T, int K, int H, int nslots) {
 
 // Shapes the MFMA path covers (else the caller uses the GEMV kernels).
 bool mfma_supported(int H, int I) {
-  return H >= kKC && I >= kKC && H % kKC == 0 && I % kKC == 0;
+  return H >= kKAlign && I >= kKAlign && H % kKAlign == 0 && I % kKAlign == 0;
 }
 
 int experts_mfma(const void* x, int T, int H, int I, int K, const float* topk_w,
@@ -296,18 +309,18 @@ int experts_mfma(const void* x, int T, int H, int I, int K, const float* topk_w,
   const uint16_t* a13 = (const uint16_t*)w13;
   const uint16_t* a2 = (const uint16_t*)w2;
   uint16_t* ab = (uint16_t*)act;
+  // (tiles per pass, k-steps per iteration), measured at the Qwen3 shapes on
+  // MI355X: more tiles per pass cost registers (fewer waves in flight) but
+  // save passes over the weights once slots hold more than 32 tokens.
   if (T <= 16)
-    launch_gemms<1>(xb, H, I, K, P, nslots, lists, counts, a13, w13_stride, a2, w2_stride, ab, y,
-                    st, ev);
-  else if (T <= 32)
-    launch_gemms<2>(xb, H, I, K, P, nslots, lists, counts, a13, w13_stride, a2, w2_stride, ab, y,
-                    st, ev);
-  else if (T <= 64)
-    launch_gemms<4>(xb, H, I, K, P, nslots, lists, counts, a13, w13_stride, a2, w2_stride, ab, y,
-                    st, ev);
+    launch_gemms<1, 8>(xb, H, I, K, P, nslots, lists, counts, a13, w13_stride, a2, w2_stride, ab,
+                       y, st, ev);
+  else if (T <= 128)
+    launch_gemms<2, 4>(xb, H, I, K, P, nslots, lists, counts, a13, w13_stride, a2, w2_stride, ab,
+                       y, st, ev);
   else
-    launch_gemms<kMaxMT>(xb, H, I, K, P, nslots, lists, counts, a13, w13_stride, a2, w2_stride,
-                         ab, y, st, ev);
+    launch_gemms<kMaxMT, 2>(xb, H, I, K, P, nslots, lists, counts, a13, w13_stride, a2,
+                            w2_stride, ab, y, st, ev);
   hipLaunchKernelGGL(combine_kernel, dim3((H + 255) / 256, T), dim3(256), 0, st, y, H, K, nslots,
                      topk_w, slots, (uint16_t*)out);
   WISP_HIP_TRY(hipGetLastError());
