@@ -17,7 +17,14 @@ stream from HBM rather than from the 256 MB last-level cache.
 Printed: one JSON line with tok/s (layer calls per second), the live
 HIP-event roofline of the dominant expert kernel, page-in bandwidth against
 the measured host link, and the CPU baseline (oracle pager + torch CPU
-fused-MoE on a bounded sample, timed on this host's cores).
+fused-MoE on a time-bounded sample, timed on this host's cores).
+
+``--workload`` selects other layer configurations for measurement runs (the
+default line above is the one the benchmark is quoted on):
+  prefill   one 512-token prefill chunk, Qwen3 layer, cap=32 paged and resident
+  batch32   bs=32 decode, Qwen3 layer, cap=32 paged and resident
+  mixtral   Mixtral-8x7B layer, cap=4, bs=1 and bs=16 decode
+  stack     48 Qwen3 layers, cap=24 each, bs=1 decode through the stack
 """
 from __future__ import annotations
 
@@ -37,40 +44,60 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def cpu_baseline(wl, steps: int) -> dict:
+def cpu_name() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(routes, w13, w2, seconds: float, warm: int = 4) -> dict:
+    """Oracle routing + LRU pager + torch CPU SwiGLU experts over the decode
+    routing sequences (one pager per sequence, round-robin, as on the GPU),
+    until ``seconds`` of timed work; throughput = timed steps / timed time."""
     import torch
 
     from oracle.moe import moe_forward_fast, route
     from oracle.pager import PagerOracle
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    w13, w2 = wl.views()
-    K = wl.shape.top_k
-    pager = PagerOracle(wl.shape.experts, wl.shape.cap)
-    times = []
-    warm = 4
-    for t in range(min(steps + warm, wl.steps)):
+    K = routes[0].shape.top_k
+    pagers = [PagerOracle(wl.shape.experts, wl.shape.cap) for wl in routes]
+    R, per = len(routes), routes[0].steps
+    n = timed = 0
+    spent = 0.0
+    while spent < seconds and n < 64 * R * per:
+        r, pos = n % R, (n // R) % per
         t0 = time.perf_counter()
-        w, ids = route(wl.logits[t], K)
-        pager.forward(ids.tolist())
-        moe_forward_fast(wl.x[t], w, ids, w13, w2)
-        if t >= warm:
-            times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
-    cpu = "unknown"
+        w, ids = route(routes[r].logits[pos], K)
+        pagers[r].forward(ids.tolist())
+        moe_forward_fast(routes[r].x[pos], w, ids, w13, w2)
+        if n >= warm:
+            spent += time.perf_counter() - t0
+            timed += 1
+        n += 1
+    return {"value": round(timed / spent, 2), "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": f"{timed} bs=1 decode steps of the qwen3 layer after {warm} warm-up steps, "
+                      f"round-robin over {R} routing sequences with one pager each, time-bounded "
+                      f"to {seconds:.0f} s (oracle routing + LRU pager + torch CPU SwiGLU "
+                      f"experts on bf16 weights in host memory, so no page-in); {cpu_name()}"}
+
+
+def pmc_traffic(path: str, kernel: str):
+    """HBM bytes per launch of ``kernel`` from a committed profiler summary
+    (FETCH_SIZE + WRITE_SIZE per dispatch, calibrated against a copy kernel
+    of known size), or None."""
     try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    cpu = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
-    return {"value": round(1.0 / med, 2), "unit": "tok/s", "cores": cores, "kind": "port",
-            "sample": f"{len(times)} bs=1 decode steps of the qwen3 layer after {warm} warm-up "
-                      f"steps (oracle routing + LRU pager + torch CPU SwiGLU experts, bf16 "
-                      f"weights in host memory, no page-in); median step "
-                      f"{med * 1e3:.2f} ms; {cpu}"}
+        with open(path) as f:
+            d = json.load(f)
+        k = d["kernels"][kernel]
+        return int(round(k["fetch_bytes"] + k["write_bytes"]))
+    except (OSError, KeyError, ValueError, TypeError):
+        return None
 
 
 def h2d_link(nbytes: int, iters: int = 20, streams: int = 1) -> float:
@@ -88,6 +115,237 @@ def h2d_link(nbytes: int, iters: int = 20, streams: int = 1) -> float:
     return nbytes / (statistics.median(list(ms)[2:]) * 1e-3) / 1e9
 
 
+# ---------------------------------------------------------------------------
+# Measurement runs of the other layer configurations (--workload).
+# ---------------------------------------------------------------------------
+
+def _collect(states) -> dict:
+    """Kernel time (ms), calls, page-in ms/bytes and pager counters summed
+    over the states since profiling was switched on."""
+    agg = {"w13_ms": 0.0, "w2_ms": 0.0, "calls": 0, "pin_ms": 0.0, "pin_bytes": 0.0,
+           "miss": 0, "hits": 0}
+    for st in states:
+        p = st.profile(False)
+        agg["w13_ms"] += p["w13"]
+        agg["w2_ms"] += p["w2"]
+        agg["calls"] += p["calls"]
+        ms, nb = st.pagein_stats()
+        agg["pin_ms"] += ms
+        agg["pin_bytes"] += nb
+        agg["miss"] += st.stats_miss
+        agg["hits"] += st.stats_hits
+    return agg
+
+
+def _timed(fn, n_warm: int, n: int, states) -> tuple[float, dict]:
+    import torch
+    for i in range(n_warm):
+        fn(i)
+    torch.cuda.synchronize()
+    for st in states:
+        st.profile(True)
+        st.pagein_stats()
+    t0 = time.perf_counter()
+    for i in range(n_warm, n_warm + n):
+        fn(i)
+    torch.cuda.synchronize()
+    return time.perf_counter() - t0, _collect(states)
+
+
+def _gemm_report(agg: dict, shape, tokens_per_call: int, distinct_per_call: float,
+                 kernels: str) -> dict:
+    calls = max(1, agg["calls"])
+    t = (agg["w13_ms"] + agg["w2_ms"]) / calls * 1e-3
+    flops = 2.0 * tokens_per_call * shape.top_k * 3 * shape.hidden * shape.inter
+    byts = distinct_per_call * shape.expert_bytes
+    return {"kernels": kernels, "avg_us_per_call": round(t * 1e6, 2),
+            "w13_us": round(agg["w13_ms"] / calls * 1e3, 2),
+            "w2_us": round(agg["w2_ms"] / calls * 1e3, 2),
+            "achieved_TFLOPs": round(flops / t / 1e12, 2) if t else None,
+            "frac_bf16_mfma_peak": round(flops / t / 1e12 / BF16_PEAK_TFLOPS, 4) if t else None,
+            "achieved_GBps": round(byts / t / 1e9, 1) if t else None,
+            "frac_hbm_peak": round(byts / t / 1e9 / HBM_PEAK_GBPS, 4) if t else None,
+            "bytes_per_call": int(byts), "flops_per_call": int(flops)}
+
+
+def _pagein_report(agg: dict) -> dict:
+    gbps = agg["pin_bytes"] / (agg["pin_ms"] * 1e-3) / 1e9 if agg["pin_ms"] else 0.0
+    return {"bytes": agg["pin_bytes"], "achieved_GBps": round(gbps, 2), "misses": agg["miss"],
+            "hits": agg["hits"]}
+
+
+def _distinct(logits, K: int) -> int:
+    """Distinct experts routed to by the tokens of one call (``logits [T, E]``):
+    the expert weights one call of the grouped GEMM streams."""
+    import torch
+    return int(torch.unique(torch.topk(logits.float(), K, dim=-1).indices).numel())
+
+
+def _line(metric, value, unit, args, steps, elapsed, config, **extra) -> dict:
+    line = {"metric": metric, "value": round(value, 2), "unit": unit, "n_gpus": 1,
+            "steps": steps, "warmup": args.warmup,
+            "ms_per_step": round(elapsed / max(1, steps) * 1e3, 4), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+            "config": config}
+    line.update(extra)
+    return line
+
+
+def _cpu_layer(wl, cap: int, calls: int) -> dict:
+    """Oracle routing + pager (with greedy sub-batching) + torch CPU experts
+    over ``calls`` layer calls of the workload."""
+    import torch
+
+    from oracle.moe import moe_forward_fast, route
+    from oracle.pager import PagerOracle
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    w13, w2 = wl.views()
+    K = wl.shape.top_k
+    pager = PagerOracle(wl.shape.experts, cap)
+    t0 = time.perf_counter()
+    for c in range(calls):
+        w, ids = route(wl.logits[c % wl.steps], K)
+        pager.forward(ids.tolist())
+        moe_forward_fast(wl.x[c % wl.steps], w, ids, w13, w2)
+    dt = time.perf_counter() - t0
+    return {"value": round(calls * wl.tokens / dt, 2), "unit": "tok/s", "cores": cores,
+            "kind": "port", "sample": f"{calls} layer calls of {wl.tokens} tokens (oracle routing "
+            f"+ LRU pager with sub-batching + torch CPU SwiGLU experts, weights in host memory); "
+            f"{cpu_name()}"}
+
+
+def _state_run(wl, cap: int, mode: str, n_warm: int, n: int):
+    """Times ``n`` layer calls (call i uses step i % steps, after ``n_warm``
+    untimed calls) of ``wl`` on a fresh state: paged with ``cap`` slots, or
+    resident with every expert primed."""
+    import torch
+
+    from wisp_amd.integrations.vllm.fused_moe import WispMoEState
+    dev = torch.device("cuda", 0)
+    w13, w2 = wl.views()
+    K = wl.shape.top_k
+    xs, lgs = wl.x.to(dev), wl.logits.to(dev)
+    out = torch.empty_like(xs[0])
+    st = WispMoEState(w13, w2, wl.shape.experts if mode == "resident" else cap, mode, dev, 0)
+    if mode == "resident":
+        st.prime_identity()
+    r = _timed(lambda i: st.forward(xs[i % wl.steps], lgs[i % wl.steps], K, True, out=out),
+               n_warm, n, [st])
+    del st
+    torch.cuda.empty_cache()
+    return r
+
+
+def bench_prefill(args) -> dict:
+    from wisp_amd import workloads as W
+    wl = W.gaussian_logits("batch", seed=0, steps=3, tokens=512, pin=True)
+    sh = wl.shape
+    pe, pa = _state_run(wl, sh.cap, "paged", 1, 2)
+    re_, ra = _state_run(wl, sh.cap, "resident", 2, 20)
+    dist = sum(_distinct(wl.logits[i], 8) for i in range(wl.steps)) / wl.steps
+    cpu = None if args.no_cpu_baseline else _cpu_layer(wl, sh.cap, 1)
+    return _line("MoE prefill tok/s, Qwen3-30B-A3B shape, 512-token chunk, cap=32 paged",
+                 2 * 512 / pe, "tok/s", args, 2, pe,
+                 {"workload": "qwen3 moe layer, 512-token prefill chunk, router logits N(0,1)",
+                  "hidden": sh.hidden, "expert_intermediate": sh.inter, "experts": sh.experts,
+                  "top_k": sh.top_k, "cap": sh.cap, "tokens": 512},
+                 pagein=_pagein_report(pa),
+                 resident={"tok_per_s": round(20 * 512 / re_, 1),
+                           "expert_gemm": _gemm_report(ra, sh, 512, dist,
+                                                       "mfma_w13_kernel + mfma_w2_kernel")},
+                 cpu_baseline=cpu)
+
+
+def bench_batch32(args) -> dict:
+    from wisp_amd import workloads as W
+    wl = W.batch_decode(steps=24, tokens=32, pin=True)
+    sh = wl.shape
+    pe, pa = _state_run(wl, sh.cap, "paged", 2, 16)
+    re_, ra = _state_run(wl, sh.cap, "resident", 2, 128)
+    cpu = None if args.no_cpu_baseline else _cpu_layer(wl, sh.cap, 4)
+    dist = sum(_distinct(wl.logits[i], 8) for i in range(wl.steps)) / wl.steps
+    return _line("MoE batched decode tok/s, Qwen3-30B-A3B shape, bs=32, cap=32 paged",
+                 16 * 32 / pe, "tok/s", args, 16, pe,
+                 {"workload": "qwen3 moe layer, bs=32 decode, router logits N(0,1)",
+                  "hidden": sh.hidden, "expert_intermediate": sh.inter, "experts": sh.experts,
+                  "top_k": sh.top_k, "cap": sh.cap, "batch": 32},
+                 pagein=_pagein_report(pa),
+                 resident={"tok_per_s": round(128 * 32 / re_, 1),
+                           "expert_gemm": _gemm_report(ra, sh, 32, dist,
+                                                       "mfma_w13_kernel + mfma_w2_kernel")},
+                 cpu_baseline=cpu)
+
+
+def bench_mixtral(args) -> dict:
+    from wisp_amd import workloads as W
+    wl = W.mixtral(steps=40, tokens=1, pin=True)
+    sh = wl.shape
+    pe, pa = _state_run(wl, sh.cap, "paged", 4, 32)
+    re_, ra = _state_run(wl, sh.cap, "resident", 4, 32)
+    wl16 = W.mixtral(steps=10, tokens=16, pin=False, weights=False)
+    wl16.slabs = wl.slabs
+    pe16, pa16 = _state_run(wl16, sh.cap, "paged", 2, 8)
+    re16, ra16 = _state_run(wl16, sh.cap, "resident", 2, 8)
+    cpu = None if args.no_cpu_baseline else _cpu_layer(wl, sh.cap, 8)
+    return _line("MoE decode tok/s, Mixtral-8x7B shape bs=1 cap=4 paged", 32 / pe, "tok/s",
+                 args, 32, pe,
+                 {"workload": "mixtral-8x7b moe layer decode, router N(0,1) + bias N(0,0.5)",
+                  "hidden": sh.hidden, "expert_intermediate": sh.inter, "experts": sh.experts,
+                  "top_k": sh.top_k, "cap": sh.cap, "batch": 1},
+                 pagein=_pagein_report(pa),
+                 resident={"tok_per_s": round(32 / re_, 1),
+                           "expert_gemm": _gemm_report(ra, sh, 1, 2.0,
+                                                       "w13_silu_kernel + w2_combine_kernel")},
+                 bs16={"paged_tok_per_s": round(8 * 16 / pe16, 2), "pagein": _pagein_report(pa16),
+                       "resident_tok_per_s": round(8 * 16 / re16, 1),
+                       "resident_expert_gemm": _gemm_report(
+                           ra16, sh, 16, sum(_distinct(wl16.logits[i], 2) for i in range(10)) / 10,
+                           "mfma_w13_kernel + mfma_w2_kernel")},
+                 cpu_baseline=cpu)
+
+
+def bench_stack(args) -> dict:
+    """48 MoE layers (own scratch of 24 slots and own pager each, one shared
+    set of pinned masters): each token runs through the 48 layers in order,
+    the output of layer L being the input of layer L+1."""
+    import torch
+
+    from wisp_amd import workloads as W
+    from wisp_amd.integrations.vllm.fused_moe import WispMoEState
+    sh = W.SHAPES["stack"]
+    layers, tokens = 48, 512
+    t_setup = time.perf_counter()
+    base = W.qwen3_decode(steps=1, pin=True)
+    w13, w2 = base.views()
+    dev = torch.device("cuda", 0)
+    lg = torch.from_numpy(W.stack_routing(seed=0, layers=layers, tokens=tokens)).to(dev)
+    x0 = torch.randn((tokens, 1, sh.hidden), generator=torch.Generator().manual_seed(1)) \
+        .to(sh.dtype).to(dev)
+    states = [WispMoEState(w13, w2, sh.cap, "paged", dev, L) for L in range(layers)]
+    log(f"stack setup {time.perf_counter() - t_setup:.1f}s")
+    n_warm = 8
+
+    def token(i: int) -> None:
+        h = x0[i]
+        for L in range(layers):
+            h = states[L].forward(h, lg[L, i:i + 1], sh.top_k, True)
+
+    elapsed, agg = _timed(token, n_warm, tokens - n_warm, states)
+    n = tokens - n_warm
+    calls = max(1, agg["calls"])
+    return _line("MoE-only 48-layer stack decode tok/s, Qwen3-30B-A3B shape bs=1 cap=24",
+                 n / elapsed, "tok/s", args, n, elapsed,
+                 {"workload": "48 qwen3 moe layers, bs=1 decode, Dirichlet(0.3) layer-conditioned "
+                              "routing, one shared set of pinned masters",
+                  "hidden": sh.hidden, "expert_intermediate": sh.inter, "experts": sh.experts,
+                  "top_k": sh.top_k, "cap": sh.cap, "layers": layers, "tokens": n},
+                 layer_calls_per_s=round(n * layers / elapsed, 1),
+                 pagein=_pagein_report(agg),
+                 expert_gemm_us_per_layer_call=round((agg["w13_ms"] + agg["w2_ms"]) / calls * 1e3,
+                                                     2))
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -95,13 +353,22 @@ def main() -> int:
                     help="timed layer calls (default: 8 instances x 256 decode steps)")
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--replicas", type=int, default=8)
-    ap.add_argument("--cpu-sample", type=int, default=24)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="time bound of the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--workload", default="qwen3",
+                    choices=["qwen3", "prefill", "batch32", "mixtral", "stack"])
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
               "(the paged MoE path has no multi-GPU mode)", file=sys.stderr)
         return 2
+
+    if args.workload != "qwen3":
+        line = {"prefill": bench_prefill, "batch32": bench_batch32, "mixtral": bench_mixtral,
+                "stack": bench_stack}[args.workload](args)
+        print(json.dumps(line), flush=True)
+        return 0
 
     import torch
 
@@ -175,8 +442,10 @@ def main() -> int:
     cpu = None
     if not args.no_cpu_baseline:
         t_cpu = time.perf_counter()
-        cpu = cpu_baseline(base, args.cpu_sample)
+        cpu = cpu_baseline(routes, w13, w2, args.cpu_seconds)
         log(f"cpu baseline {time.perf_counter() - t_cpu:.1f}s")
+    traffic = pmc_traffic(os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                                       "qwen3_decode_pmc.json"), "w13_silu_kernel")
 
     value = args.steps / elapsed
     line = {
@@ -205,7 +474,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(a13 / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": traffic,
             "bytes_per_call": w13_bytes,
             "avg_us_per_call": round(t13 * 1e6, 3),
         },
