@@ -206,14 +206,21 @@ __device__ inline int probe_insert(uint64_t& lo, uint64_t& hi, uint32_t mask, in
   uint32_t perturb = (uint32_t)key;
   uint32_t i = (uint32_t)key & mask;
   for (;;) {
-    const int n = (i + 9 <= mask) ? 10 : 1;
-    for (int d = 0; d < n; ++d) {
-      const uint32_t s = i + d;
-      const uint64_t bit = 1ull << (s & 63);
-      uint64_t& w = s < 64 ? lo : hi;
+    if (i + 9 <= mask) {
+      // the 10 linear probes at once: occupancy bits i .. i+9
+      const uint64_t w = i >= 64 ? hi >> (i - 64) : i == 0 ? lo : (lo >> i) | (hi << (64 - i));
+      const uint32_t free = ~(uint32_t)w & 0x3FFu;
+      if (free) {
+        const uint32_t s = i + (uint32_t)__builtin_ctz(free);
+        if (s < 64) lo |= 1ull << s; else hi |= 1ull << (s - 64);
+        return (int)s;
+      }
+    } else {
+      uint64_t& w = i < 64 ? lo : hi;
+      const uint64_t bit = 1ull << (i & 63);
       if (!(w & bit)) {
         w |= bit;
-        return (int)s;
+        return (int)i;
       }
     }
     perturb >>= 5;
@@ -290,7 +297,7 @@ struct FusedRouteSmem {
 // loaded by this call, flags[1 + p] = 1 if pair p's expert was loaded by its
 // group, else 0; loads (optional): the (expert, slot) pairs loaded, in the
 // record's order; and the decision record.
-template <typename TL>
+template <typename TL, int VALS>
 __global__ __launch_bounds__(64) void pager_kernel(
     const int32_t* __restrict__ ids_in, const TL* __restrict__ logits, int renorm,
     float* __restrict__ w_out, int32_t* __restrict__ id_out, int T, int K, int E, int cap,
@@ -324,7 +331,7 @@ __global__ __launch_bounds__(64) void pager_kernel(
     for (int t = 0; t < T; ++t) {
       float w;
       int id;
-      route_token_wave(logits + (size_t)t * E, E, K, renorm, lane, true, &w, &id);
+      route_token_wave<TL, VALS>(logits + (size_t)t * E, E, K, renorm, lane, true, &w, &id);
       if (lane < K) {
         w_out[t * K + lane] = w;
         id_out[t * K + lane] = id;
@@ -400,12 +407,23 @@ __global__ __launch_bounds__(64) void pager_kernel(
       }
       wave_lds_sync();
       // ---- CPython set iteration order of the ascending keys ----------
-      if (U <= 64) {
-        const int key = lane < U ? sm.keys[lane] : -1;
-        const int pos = set_positions_wave(key, U, lane);
-        if (lane < U) sm.order[pos] = key;
-      } else if (lane == 0) {
-        cpython_set_order(sm.keys, U, sm.order, sm.table, kMaxSetTable);
+      // It only decides which free slot each missing expert takes, so it is
+      // computed when two or more are missing; otherwise any order will do.
+      int nmiss_any = 0;
+      for (int base = 0; base < U; base += 64) {
+        const int j = base + lane;
+        nmiss_any += __popcll(ballot(j < U && sm.map[sm.keys[j]] < 0));
+      }
+      const int32_t* ord = sm.keys;
+      if (nmiss_any >= 2) {
+        if (U <= 64) {
+          const int key = lane < U ? sm.keys[lane] : -1;
+          const int pos = set_positions_wave(key, U, lane);
+          if (lane < U) sm.order[pos] = key;
+        } else if (lane == 0) {
+          cpython_set_order(sm.keys, U, sm.order, sm.table, kMaxSetTable);
+        }
+        ord = sm.order;
       }
       wave_lds_sync();
 
@@ -416,7 +434,7 @@ __global__ __launch_bounds__(64) void pager_kernel(
         int e = -1;
         bool m = false;
         if (j < U) {
-          e = sm.order[j];
+          e = ord[j];
           m = sm.map[e] < 0;
         }
         const uint64_t mb = ballot(m);
@@ -560,14 +578,17 @@ int launch_pager(const int32_t* ids, const void* logits, int logits_dtype, int r
     wisp_set_last_error("invalid pager arguments", "wisp_pager_decide");
     return WISP_ERR_INVALID;
   }
-  if (logits && logits_dtype == WISP_BF16)
-    hipLaunchKernelGGL(pager_kernel<uint16_t>, dim3(1), dim3(64), 0, stream, ids,
-                       (const uint16_t*)logits, renorm, topk_w, topk_ids, T, K, E, cap,
-                       single_group, map, s2e, tick, ctr, slots, flags, loads, rec);
-  else
-    hipLaunchKernelGGL(pager_kernel<float>, dim3(1), dim3(64), 0, stream, ids,
-                       (const float*)logits, renorm, topk_w, topk_ids, T, K, E, cap,
-                       single_group, map, s2e, tick, ctr, slots, flags, loads, rec);
+  with_route_vals(logits ? E : 1, [&](auto vals) {
+    constexpr int V = decltype(vals)::value;
+    if (logits && logits_dtype == WISP_BF16)
+      hipLaunchKernelGGL((pager_kernel<uint16_t, V>), dim3(1), dim3(64), 0, stream, ids,
+                         (const uint16_t*)logits, renorm, topk_w, topk_ids, T, K, E, cap,
+                         single_group, map, s2e, tick, ctr, slots, flags, loads, rec);
+    else
+      hipLaunchKernelGGL((pager_kernel<float, V>), dim3(1), dim3(64), 0, stream, ids,
+                         (const float*)logits, renorm, topk_w, topk_ids, T, K, E, cap,
+                         single_group, map, s2e, tick, ctr, slots, flags, loads, rec);
+  });
   WISP_HIP_TRY(hipGetLastError());
   return WISP_OK;
 }

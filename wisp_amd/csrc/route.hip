@@ -13,7 +13,7 @@
 namespace wisp {
 namespace {
 
-template <typename TL>
+template <typename TL, int VALS>
 __global__ __launch_bounds__(256) void route_kernel(const TL* __restrict__ logits, int T, int E,
                                                      int K, int renorm, float* __restrict__ w_out,
                                                      int32_t* __restrict__ id_out,
@@ -24,7 +24,8 @@ __global__ __launch_bounds__(256) void route_kernel(const TL* __restrict__ logit
   const bool active = t < T;
   float w;
   int id;
-  route_token_wave(logits + (size_t)(active ? t : 0) * E, E, K, renorm, lane, active, &w, &id);
+  route_token_wave<TL, VALS>(logits + (size_t)(active ? t : 0) * E, E, K, renorm, lane, active,
+                             &w, &id);
   if (active && lane < K) {
     w_out[(size_t)t * K + lane] = w;
     id_out[(size_t)t * K + lane] = id;
@@ -46,14 +47,17 @@ extern "C" int wisp_route_topk_softmax(const void* logits, int logits_dtype, int
   }
   const int blocks = T > 0 ? (T + 3) / 4 : (forward_counter ? 1 : 0);
   if (blocks == 0) return WISP_OK;
-  if (logits_dtype == WISP_F32)
-    hipLaunchKernelGGL(route_kernel<float>, dim3(blocks), dim3(256), 0, (hipStream_t)stream,
-                       (const float*)logits, T, E, K, renormalize, topk_w, topk_ids,
-                       forward_counter);
-  else
-    hipLaunchKernelGGL(route_kernel<uint16_t>, dim3(blocks), dim3(256), 0, (hipStream_t)stream,
-                       (const uint16_t*)logits, T, E, K, renormalize, topk_w, topk_ids,
-                       forward_counter);
+  with_route_vals(E, [&](auto vals) {
+    constexpr int V = decltype(vals)::value;
+    if (logits_dtype == WISP_F32)
+      hipLaunchKernelGGL((route_kernel<float, V>), dim3(blocks), dim3(256), 0, (hipStream_t)stream,
+                         (const float*)logits, T, E, K, renormalize, topk_w, topk_ids,
+                         forward_counter);
+    else
+      hipLaunchKernelGGL((route_kernel<uint16_t, V>), dim3(blocks), dim3(256), 0,
+                         (hipStream_t)stream, (const uint16_t*)logits, T, E, K, renormalize,
+                         topk_w, topk_ids, forward_counter);
+  });
   WISP_HIP_TRY(hipGetLastError());
   return WISP_OK;
 }

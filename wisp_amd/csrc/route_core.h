@@ -9,17 +9,36 @@
 // (xor 1, xor 2, half-mirror, mirror - after each step both partners hold
 // the same bits, since IEEE add and max are commutative), then the four row
 // results are combined with readlane in a fixed order.  The result is
-// deterministic and identical in every lane.  The argmax of each top-k
-// round is the wave max followed by a ballot for the lowest id holding it.
+// deterministic and identical in every lane.  The softmax maximum is the
+// first top-k value, so the denominator pass follows the top-k rounds.
 #pragma once
 
 #include <math.h>
+
+#include <type_traits>
 
 #include "common.h"
 
 namespace wisp {
 
-constexpr int kRouteVals = kMaxExperts / 64;
+// Logits per lane a router instance holds: 2 (E <= 128), 4 (E <= 256) or 8
+// (E <= 512).  The top-k rescans and the softmax sum are unrolled over them,
+// so the smallest instance that covers E keeps the serial path short.
+template <int VALS>
+struct RouteVals {
+  static_assert(VALS == 2 || VALS == 4 || VALS == 8, "2, 4 or 8 logits per lane");
+};
+
+// Calls f(std::integral_constant<int, VALS>) with the smallest VALS covering E.
+template <typename F>
+__host__ inline void with_route_vals(int E, F&& f) {
+  if (E <= 128)
+    f(std::integral_constant<int, 2>());
+  else if (E <= 256)
+    f(std::integral_constant<int, 4>());
+  else
+    f(std::integral_constant<int, 8>());
+}
 
 template <typename TL>
 __device__ inline float load_logit(const TL* p);
@@ -59,18 +78,34 @@ __device__ inline float wave_max_f32(float v) {
                fmaxf(readlane_f32(v, 32), readlane_f32(v, 48)));
 }
 
+// Minimum over the 64 lanes (same value in every lane).
+__device__ inline int wave_min_i32(int v) {
+  v = min(v, __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false));
+  v = min(v, __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false));
+  v = min(v, __builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, false));
+  v = min(v, __builtin_amdgcn_mov_dpp(v, 0x140, 0xF, 0xF, false));
+  return min(min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+             min(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+
 // Routes one token.  Lanes < K return (weight, id) of routing position
 // `lane`; other lanes return (0, -1).  Needs no shared memory; all lanes of
 // the wave must call it.
-template <typename TL>
+//
+// Top-k: each lane keeps the best of its own not-yet-taken entries (value
+// and the lowest position j holding it).  A round takes the wave max of the
+// lane bests; the winner is the lowest id e = 64 j + lane among the lanes
+// holding that value, and only the winning lane rescans its entries.
+template <typename TL, int VALS>
 __device__ inline void route_token_wave(const TL* __restrict__ logits_row, int E, int K,
                                         int renorm, int lane, bool active, float* w_out,
                                         int* id_out) {
-  const int per = (E + 63) >> 6;
-  float v[kRouteVals];
+  (void)RouteVals<VALS>();
+  const int per = min((E + 63) >> 6, VALS);
+  float v[VALS];
   uint32_t taken = 0;  // bit j: entry j of this lane is not eligible
 #pragma unroll
-  for (int j = 0; j < kRouteVals; ++j) {
+  for (int j = 0; j < VALS; ++j) {
     const int e = j * 64 + lane;
     float x = -INFINITY;
     if (active && j < per && e < E) {
@@ -85,38 +120,50 @@ __device__ inline void route_token_wave(const TL* __restrict__ logits_row, int E
   *id_out = -1;
   if (!active) return;
 
-  float lmax = -INFINITY;
+  // best eligible entry of this lane: value lb at position lbj (-1: none)
+  float lb = -INFINITY;
+  int lbj = -1;
+  auto rescan = [&]() {
+    lb = -INFINITY;
+    lbj = -1;
 #pragma unroll
-  for (int j = 0; j < kRouteVals; ++j)
-    if (!(taken & (1u << j))) lmax = fmaxf(lmax, v[j]);
-  const float m = wave_max_f32(lmax);
-  float ls = 0.f;
-#pragma unroll
-  for (int j = 0; j < kRouteVals; ++j)
-    if (!(taken & (1u << j))) ls += expf(v[j] - m);
-  const float s = wave_sum_f32(ls);
+    for (int j = VALS - 1; j >= 0; --j)
+      if (!(taken & (1u << j)) && (lbj < 0 || v[j] >= lb)) {
+        lb = v[j];
+        lbj = j;
+      }
+  };
+  rescan();
 
+  float m = 0.f;
   int my_id = -1;
   float my_v = 0.f;
   for (int r = 0; r < K; ++r) {
-    float best = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < kRouteVals; ++j)
-      if (!(taken & (1u << j))) best = fmaxf(best, v[j]);
-    const float bm = wave_max_f32(best);
-    int e = -1;
-#pragma unroll
-    for (int j = 0; j < kRouteVals; ++j) {
-      if (j >= per || e >= 0) continue;
-      const uint64_t b = __ballot(!(taken & (1u << j)) && v[j] == bm);
-      if (b) e = j * 64 + __builtin_ctzll(b);
+    const float bm = wave_max_f32(lbj >= 0 ? lb : -INFINITY);
+    if (r == 0) m = bm;
+    const bool cand = lbj >= 0 && lb == bm;
+    const uint64_t cb = __ballot(cand);
+    int e;
+    if (__popcll(cb) == 1) {
+      const int wl = __builtin_ctzll(cb);
+      e = __builtin_amdgcn_readlane(lbj, wl) * 64 + wl;
+    } else {
+      e = wave_min_i32(cand ? lbj * 64 + lane : 0x7fffffff);
     }
-    if (e >= 0 && (e & 63) == lane) taken |= 1u << (e >> 6);
+    if (lane == (e & 63)) {
+      taken |= 1u << (e >> 6);
+      rescan();
+    }
     if (lane == r) {
       my_id = e;
       my_v = bm;
     }
   }
+  float ls = 0.f;
+#pragma unroll
+  for (int j = 0; j < VALS; ++j)
+    if (j < per && j * 64 + lane < E) ls += expf(v[j] - m);
+  const float s = wave_sum_f32(ls);
   float p = lane < K ? expf(my_v - m) / s : 0.f;
   if (renorm) p = p / wave_sum_f32(p);
   if (lane < K) {
