@@ -69,9 +69,12 @@ __device__ inline float silu(float g) { return g / (1.0f + expf(-g)); }
 // consecutive i (gate row i and up row I + i) of one (token, k) pair; each
 // lane covers CH chunks of 16 bytes of a row (chunk c*64 + lane).
 // grid = (ceil(I / (4 * RW)), T * K).  One row pair per wave (RW = 1) gives
-// the most waves in flight, which is what a pure weight stream needs.
+// the most waves in flight, which is what a pure weight stream needs.  FULL:
+// a row is exactly CH chunks per lane, so the loads carry no bounds guard
+// (a guarded load sits in its own exec-masked block, which costs ~0.7 us per
+// launch at the Qwen3 shape by keeping the loads from issuing back to back).
 // ---------------------------------------------------------------------------
-template <typename T, int CH, int RW>
+template <typename T, int CH, int RW, bool FULL>
 __global__ __launch_bounds__(256) void w13_silu_kernel(const T* __restrict__ x, int H, int I,
                                                         int K, const int32_t* __restrict__ slots,
                                                         const T* __restrict__ w13,
@@ -99,7 +102,7 @@ __global__ __launch_bounds__(256) void w13_silu_kernel(const T* __restrict__ x, 
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     const int ch = c * 64 + lane;
-    xv[c] = ch < nch ? ld16(xr + (size_t)ch * V) : make_uint4(0, 0, 0, 0);
+    xv[c] = (FULL || ch < nch) ? ld16(xr + (size_t)ch * V) : make_uint4(0, 0, 0, 0);
   }
 #pragma unroll
   for (int r = 0; r < RW; ++r) {
@@ -107,7 +110,7 @@ __global__ __launch_bounds__(256) void w13_silu_kernel(const T* __restrict__ x, 
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
       const int ch = c * 64 + lane;
-      if (ch < nch) {
+      if (FULL || ch < nch) {
         wg[r][c] = ld16_stream(W + (size_t)i * H + (size_t)ch * V);
         wu[r][c] = ld16_stream(W + (size_t)(I + i) * H + (size_t)ch * V);
       } else {
@@ -158,7 +161,7 @@ __global__ __launch_bounds__(256) void w13_silu_kernel(const T* __restrict__ x, 
 // ---------------------------------------------------------------------------
 constexpr int kMaxKw2 = 16;
 
-template <typename T, int LPR, int CH>
+template <typename T, int LPR, int CH, bool FULL>
 __global__ __launch_bounds__(1024) void w2_combine_kernel(const T* __restrict__ act, int H, int I,
                                                            int K, const float* __restrict__ topk_w,
                                                            const int32_t* __restrict__ slots,
@@ -187,7 +190,7 @@ __global__ __launch_bounds__(1024) void w2_combine_kernel(const T* __restrict__ 
 #pragma unroll
       for (int c = 0; c < CH; ++c) {
         const int ch = c * LPR + l;
-        if (ch < nch) {
+        if (FULL || ch < nch) {
           wv[c] = ld16(wrow + (size_t)ch * V);
           av[c] = ld16(arow + (size_t)ch * V);
         } else {
@@ -243,8 +246,12 @@ void launch_w13(const T* x, int T_, int H, int I, int K, const int32_t* slots, c
                 size_t w13_stride, T* act, hipStream_t st, const LaunchCtl& c) {
   constexpr int RW = 1;
   dim3 grid((I + 4 * RW - 1) / (4 * RW), T_ * K);
-  launch_timed(w13_silu_kernel<T, CH, RW>, grid, dim3(256), st, c.start, c.stop, x, H, I, K,
-               slots, w13, w13_stride, act, c.pair_filter, c.want);
+  if (H == CH * 64 * Vec<T>::N)
+    launch_timed(w13_silu_kernel<T, CH, RW, true>, grid, dim3(256), st, c.start, c.stop, x, H, I,
+                 K, slots, w13, w13_stride, act, c.pair_filter, c.want);
+  else
+    launch_timed(w13_silu_kernel<T, CH, RW, false>, grid, dim3(256), st, c.start, c.stop, x, H, I,
+                 K, slots, w13, w13_stride, act, c.pair_filter, c.want);
 }
 
 template <typename T>
@@ -269,8 +276,12 @@ void launch_w2(const T* act, int T_, int H, int I, int K, const float* w, const 
                const T* w2, size_t w2_stride, T* out, hipStream_t st, const LaunchCtl& c) {
   constexpr int RPW = 64 / LPR;
   dim3 grid((H + RPW - 1) / RPW, T_);
-  launch_timed(w2_combine_kernel<T, LPR, CH>, grid, dim3(64 * K), st, c.start, c.stop, act, H,
-               I, K, w, slots, w2, w2_stride, out, c.skip_if);
+  if (CH > 0 && I == CH * LPR * Vec<T>::N)
+    launch_timed(w2_combine_kernel<T, LPR, CH, true>, grid, dim3(64 * K), st, c.start, c.stop, act,
+                 H, I, K, w, slots, w2, w2_stride, out, c.skip_if);
+  else
+    launch_timed(w2_combine_kernel<T, LPR, CH, false>, grid, dim3(64 * K), st, c.start, c.stop,
+                 act, H, I, K, w, slots, w2, w2_stride, out, c.skip_if);
 }
 
 template <typename T>
