@@ -237,6 +237,173 @@ __global__ __launch_bounds__(256) void mfma_w2_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Software-pipelined variants for slots with many tokens (prefill).  The
+// token tile of the pass (MT*16 rows) is staged through double-buffered LDS,
+// 32*U columns at a time and shared by the four waves; each wave keeps the
+// next chunk's weight fragments in flight in registers while it runs the
+// MFMAs of the current chunk.  One barrier per chunk.
+// ---------------------------------------------------------------------------
+template <int MT, int U>
+struct PipeA {
+  static constexpr int kCols = 32 * U;
+  static constexpr int kLd = kCols + 8;                  // padded row (bf16)
+  static constexpr int kVecs = MT * 16 * kCols / 8;      // 16-byte vectors per chunk
+  static constexpr int kPer = (kVecs + 255) / 256;       // per thread
+};
+
+// Loads this thread's share of the A chunk at column k0 into registers.
+template <int MT, int U, bool kTokenRows, int NPER>
+__device__ inline void pipe_load_a(u32x4 (&r)[NPER], const uint16_t* __restrict__ A, int ld,
+                                   int K, const int32_t* __restrict__ list, int m0, int mrows,
+                                   int k0) {
+  constexpr int kRowVecs = PipeA<MT, U>::kCols / 8;
+#pragma unroll
+  for (int q = 0; q < PipeA<MT, U>::kPer; ++q) {
+    const int idx = threadIdx.x + q * 256;
+    const int row = idx / kRowVecs, c = idx % kRowVecs;
+    r[q] = u32x4{0u, 0u, 0u, 0u};
+    if (idx < PipeA<MT, U>::kVecs && row < mrows) {
+      const int p = list[m0 + row];
+      r[q] = ld16(A + (size_t)(kTokenRows ? p / K : p) * ld + k0 + c * 8);
+    }
+  }
+}
+
+template <int MT, int U, int NPER, int LD>
+__device__ inline void pipe_store_a(uint16_t (*As)[LD], const u32x4 (&r)[NPER]) {
+  constexpr int kRowVecs = PipeA<MT, U>::kCols / 8;
+#pragma unroll
+  for (int q = 0; q < PipeA<MT, U>::kPer; ++q) {
+    const int idx = threadIdx.x + q * 256;
+    if (idx < PipeA<MT, U>::kVecs)
+      *reinterpret_cast<u32x4*>(&As[idx / kRowVecs][(idx % kRowVecs) * 8]) = r[q];
+  }
+}
+
+// NB: the weight operand rows of one wave are W[row0 + lane%16]; NW such row
+// groups (NW = 2 for gate/up, 1 for w2) share the A tile.
+template <int MT, int U, int NW, bool kTokenRows, int LD>
+__device__ inline void pipe_gemm(const uint16_t* __restrict__ A, int ld_a, int K, int Kdim,
+                                 const int32_t* __restrict__ list, int m0, int mrows,
+                                 const uint16_t* const (&Wr)[NW], f32x4 (&acc)[NW][MT],
+                                 uint16_t (*As)[MT * 16][LD]) {
+  using PA = PipeA<MT, U>;
+  const int lane = threadIdx.x & 63;
+  const int kq = (lane >> 4) * 8;
+  u32x4 b[NW][U], bn[NW][U], ar[PA::kPer];
+#pragma unroll
+  for (int w = 0; w < NW; ++w)
+#pragma unroll
+    for (int u = 0; u < U; ++u) b[w][u] = ld16_stream(Wr[w] + u * 32);
+  pipe_load_a<MT, U, kTokenRows>(ar, A, ld_a, K, list, m0, mrows, 0);
+  __syncthreads();  // the previous pass's readers of buffer 0 are done
+  pipe_store_a<MT, U>(As[0], ar);
+  __syncthreads();
+  int buf = 0;
+  for (int k0 = 0; k0 < Kdim; k0 += PA::kCols) {
+    const bool more = k0 + PA::kCols < Kdim;
+    if (more) {
+#pragma unroll
+      for (int w = 0; w < NW; ++w)
+#pragma unroll
+        for (int u = 0; u < U; ++u) bn[w][u] = ld16_stream(Wr[w] + k0 + PA::kCols + u * 32);
+      pipe_load_a<MT, U, kTokenRows>(ar, A, ld_a, K, list, m0, mrows, k0 + PA::kCols);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        if (t * 16 < mrows) {
+          const bf16x8 a =
+              *reinterpret_cast<const bf16x8*>(&As[buf][t * 16 + (lane & 15)][u * 32 + kq]);
+#pragma unroll
+          for (int w = 0; w < NW; ++w)
+            acc[w][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, as_bf16x8(b[w][u]), acc[w][t],
+                                                                0, 0, 0);
+        }
+      }
+    }
+    if (more) {
+      pipe_store_a<MT, U>(As[buf ^ 1], ar);
+      __syncthreads();
+      buf ^= 1;
+#pragma unroll
+      for (int w = 0; w < NW; ++w)
+#pragma unroll
+        for (int u = 0; u < U; ++u) b[w][u] = bn[w][u];
+    }
+  }
+}
+
+template <int MT, int U>
+__global__ __launch_bounds__(256) void mfma_w13_pipe_kernel(
+    const uint16_t* __restrict__ x, int H, int I, int K, int P, const int32_t* __restrict__ lists,
+    const int32_t* __restrict__ counts, const uint16_t* __restrict__ w13, size_t w13_stride,
+    uint16_t* __restrict__ act) {
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][MT * 16][PipeA<MT, U>::kLd];
+  const int s = blockIdx.y;
+  const int M = counts[s];
+  if (M == 0) return;
+  const int32_t* list = lists + (size_t)s * P;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int i0 = blockIdx.x * kPanel + wave * 16;
+  const uint16_t* Wg = w13 + (size_t)s * w13_stride + (size_t)(i0 + (lane & 15)) * H +
+                       (lane >> 4) * 8;
+  const uint16_t* const Wr[2] = {Wg, Wg + (size_t)I * H};
+  for (int m0 = 0; m0 < M; m0 += MT * 16) {
+    const int mrows = min(M - m0, MT * 16);
+    f32x4 acc[2][MT];
+#pragma unroll
+    for (int w = 0; w < 2; ++w)
+#pragma unroll
+      for (int t = 0; t < MT; ++t) acc[w][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    pipe_gemm<MT, U, 2, true>(x, H, K, H, list, m0, mrows, Wr, acc, As);
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = t * 16 + (lane >> 4) * 4 + q;
+        if (r < mrows) {
+          const int p = list[m0 + r];
+          act[(size_t)p * I + i0 + (lane & 15)] = bf16_rne(silu(acc[0][t][q]) * acc[1][t][q]);
+        }
+      }
+    }
+  }
+}
+
+template <int MT, int U>
+__global__ __launch_bounds__(256) void mfma_w2_pipe_kernel(
+    const uint16_t* __restrict__ act, int H, int I, int P, const int32_t* __restrict__ lists,
+    const int32_t* __restrict__ counts, const uint16_t* __restrict__ w2, size_t w2_stride,
+    float* __restrict__ y) {
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][MT * 16][PipeA<MT, U>::kLd];
+  const int s = blockIdx.y;
+  const int M = counts[s];
+  if (M == 0) return;
+  const int32_t* list = lists + (size_t)s * P;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int h0 = blockIdx.x * kPanel + wave * 16;
+  const uint16_t* const Wr[1] = {w2 + (size_t)s * w2_stride + (size_t)(h0 + (lane & 15)) * I +
+                                 (lane >> 4) * 8};
+  for (int m0 = 0; m0 < M; m0 += MT * 16) {
+    const int mrows = min(M - m0, MT * 16);
+    f32x4 acc[1][MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[0][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    pipe_gemm<MT, U, 1, false>(act, I, 1, I, list, m0, mrows, Wr, acc, As);
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = t * 16 + (lane >> 4) * 4 + q;
+        if (r < mrows) y[(size_t)list[m0 + r] * H + h0 + (lane & 15)] = acc[0][t][q];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // 4. combine: out[t, h] = bf16(sum_k w[t,k] * y[(t,k), h]), k ascending,
 // skipping pairs without a slot.  grid = (ceil(H / 256), T).
 // ---------------------------------------------------------------------------
@@ -257,17 +424,24 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
   out[(size_t)t * H + h] = bf16_rne(acc);
 }
 
-template <int MT, int U>
+template <int MT, int U, bool kPipe>
 void launch_gemms(const uint16_t* x, int H, int I, int K, int P, int nslots, const int32_t* lists,
                   const int32_t* counts, const uint16_t* w13, size_t w13_stride,
                   const uint16_t* w2, size_t w2_stride, uint16_t* act, float* y, hipStream_t st,
                   const StageEvents* ev) {
-  launch_timed(mfma_w13_kernel<MT, U>, dim3(I / kPanel, nslots), dim3(256), st,
-               ev ? ev->ev[0] : nullptr, ev ? ev->ev[1] : nullptr, x, H, I, K, P, lists, counts,
-               w13, w13_stride, act);
-  launch_timed(mfma_w2_kernel<MT, U>, dim3(H / kPanel, nslots), dim3(256), st,
-               ev ? ev->ev[2] : nullptr, ev ? ev->ev[3] : nullptr, act, H, I, P, lists, counts,
-               w2, w2_stride, y);
+  hipEvent_t e0 = ev ? ev->ev[0] : nullptr, e1 = ev ? ev->ev[1] : nullptr;
+  hipEvent_t e2 = ev ? ev->ev[2] : nullptr, e3 = ev ? ev->ev[3] : nullptr;
+  if (kPipe) {
+    launch_timed(mfma_w13_pipe_kernel<MT, U>, dim3(I / kPanel, nslots), dim3(256), st, e0, e1, x,
+                 H, I, K, P, lists, counts, w13, w13_stride, act);
+    launch_timed(mfma_w2_pipe_kernel<MT, U>, dim3(H / kPanel, nslots), dim3(256), st, e2, e3, act,
+                 H, I, P, lists, counts, w2, w2_stride, y);
+  } else {
+    launch_timed(mfma_w13_kernel<MT, U>, dim3(I / kPanel, nslots), dim3(256), st, e0, e1, x, H, I,
+                 K, P, lists, counts, w13, w13_stride, act);
+    launch_timed(mfma_w2_kernel<MT, U>, dim3(H / kPanel, nslots), dim3(256), st, e2, e3, act, H,
+                 I, P, lists, counts, w2, w2_stride, y);
+  }
 }
 
 }  // namespace
@@ -309,18 +483,19 @@ int experts_mfma(const void* x, int T, int H, int I, int K, const float* topk_w,
   const uint16_t* a13 = (const uint16_t*)w13;
   const uint16_t* a2 = (const uint16_t*)w2;
   uint16_t* ab = (uint16_t*)act;
-  // (tiles per pass, k-steps per iteration), measured at the Qwen3 shapes on
-  // MI355X: more tiles per pass cost registers (fewer waves in flight) but
-  // save passes over the weights once slots hold more than 32 tokens.
+  // (tiles per pass, k-steps per iteration, pipelined), measured at the Qwen3
+  // shapes on MI355X: more tiles per pass cost registers (fewer waves in
+  // flight) but save passes over the weights once slots hold more than 32
+  // tokens, where staging the token tile in LDS also pays.
   if (T <= 16)
-    launch_gemms<1, 8>(xb, H, I, K, P, nslots, lists, counts, a13, w13_stride, a2, w2_stride, ab,
-                       y, st, ev);
+    launch_gemms<1, 8, false>(xb, H, I, K, P, nslots, lists, counts, a13, w13_stride, a2,
+                              w2_stride, ab, y, st, ev);
   else if (T <= 128)
-    launch_gemms<2, 4>(xb, H, I, K, P, nslots, lists, counts, a13, w13_stride, a2, w2_stride, ab,
-                       y, st, ev);
+    launch_gemms<2, 4, false>(xb, H, I, K, P, nslots, lists, counts, a13, w13_stride, a2,
+                              w2_stride, ab, y, st, ev);
   else
-    launch_gemms<kMaxMT, 2>(xb, H, I, K, P, nslots, lists, counts, a13, w13_stride, a2,
-                            w2_stride, ab, y, st, ev);
+    launch_gemms<kMaxMT, 4, true>(xb, H, I, K, P, nslots, lists, counts, a13, w13_stride, a2,
+                                  w2_stride, ab, y, st, ev);
   hipLaunchKernelGGL(combine_kernel, dim3((H + 255) / 256, T), dim3(256), 0, st, y, H, K, nslots,
                      topk_w, slots, (uint16_t*)out);
   WISP_HIP_TRY(hipGetLastError());
