@@ -235,6 +235,62 @@ int wisp_layer_profile(void* handle, int enable, double* w13_ms, double* w2_ms,
 
 /* ---- group 4: probes ----------------------------------------------- */
 
+/* ---- group 4: cross-layer speculative prefetch ------------------------ */
+
+/* Dense expert co-activation table and the current step's observations, all
+ * in device memory (owned by the caller). */
+typedef struct wisp_cooccur {
+  int layers, experts;
+  int32_t* count;     /* [layers][experts][layers][experts]: steps in which
+                         expert e_src fired at L_src and e_dst at L_dst, for
+                         L_dst > L_src                                        */
+  int32_t* total;     /* [layers][experts]: steps in which (L, e) fired        */
+  int32_t* obs_keys;  /* [layers][experts]: the current step's experts of each
+                         layer, in the iteration order of the set the forward
+                         built (ascending insertion)                           */
+  int32_t* obs_n;     /* [layers]: their number, 0 when not seen this step     */
+  int32_t* obs_seq;   /* [layers]: the order in which the step saw the layers  */
+  int32_t* meta;      /* [4]: [0] layers seen this step, [1] steps learned     */
+} wisp_cooccur;
+
+/* Record layer `layer`'s experts for the current step (nothing for n == 0):
+ * ordered == 0: the set built from the ascending unique of ids[n] (what the
+ * forward does); ordered != 0: ids[n] as given, in that iteration order.
+ * Replaces: _CURRENT_STEP_OBS[layer_idx] = last_set (fused_moe.py:1174-1199). */
+int wisp_cooccur_observe_layer(const wisp_cooccur* table, int layer, const int32_t* ids, int n,
+                               int ordered, wisp_stream_t stream);
+
+/* Top-k experts predicted at target_layer from the step's observations:
+ * out_ids[0..*out_n) in rank order.  weights[d] (device, double) weighs
+ * sources d+1 layers below the target (decay ** d).
+ * Replaces: predict_layer (src/wisp/oracle/cooccur.py:233-287). */
+int wisp_cooccur_predict(const wisp_cooccur* table, int target_layer, int k,
+                         const double* weights, int normalize, int only_prev_layer,
+                         int32_t* out_ids, int32_t* out_n, wisp_stream_t stream);
+
+/* End of a step: add its pairs and marginals to the table when `learn`, then
+ * clear the observations.  Replaces: table.observe_step(_CURRENT_STEP_OBS);
+ * _CURRENT_STEP_OBS.clear() (fused_moe.py:1224-1233, cooccur.py:79-104). */
+int wisp_cooccur_end_step(const wisp_cooccur* table, int learn, wisp_stream_t stream);
+
+/* Words of a prefetch record for up to max_predicted predictions:
+ * [0] evicted, [1] loaded, [2] clock advanced, [3] predictions taken, then
+ * max_predicted evicted (expert, slot) pairs, then max_predicted loaded. */
+int wisp_prefetch_record_words(int max_predicted);
+
+/* Speculatively page predicted[0..n) (device; length *n_predicted when that
+ * device pointer is non-NULL, else n) into the layer: the decisions run on
+ * `stream`, the copies on the layer's side stream; the layer's next call
+ * waits for them before it touches its scratch.  ordered != 0: the list is
+ * already a set's iteration order; else it is the insertion order of
+ * set(predicted).  last_ids[n_last] (device): the layer's last routed
+ * experts (never evicted here).  count_pred != 0 adds the prediction count
+ * to the layer's counters.  record: device [wisp_prefetch_record_words(n)].
+ * Replaces: WispMoEState.prefetch_async (fused_moe.py:360-433). */
+int wisp_layer_prefetch(void* handle, const int32_t* predicted, const int32_t* n_predicted,
+                        int n, int ordered, int count_pred, const int32_t* last_ids,
+                        int n_last, int32_t* record, int record_words, wisp_stream_t stream);
+
 /* Pinned host -> device hipMemcpyAsync bandwidth: `iters` copies of `bytes`
  * on `streams` streams; writes the per-iteration milliseconds.
  * Replaces: scripts/m3_11_anvil_bandwidth_probe.py:42-82. */

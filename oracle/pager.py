@@ -5,6 +5,7 @@ Follows ``src/wisp/integrations/vllm/fused_moe.py`` of the reference:
 * ``PagerOracle.ensure_resident``  <- ``WispMoEState.ensure_resident`` (264-358)
 * ``PagerOracle.prime_identity``   <- ``WispMoEState.prime_identity`` (242-258)
 * ``PagerOracle.resize_cap``       <- ``WispMoEState.resize_cap`` (439-490)
+* ``PagerOracle.prefetch_async``   <- ``WispMoEState.prefetch_async`` (360-433)
 * ``plan_groups``                  <- greedy first-fit sub-batching (1119-1140)
 * ``PagerOracle.forward``          <- working-set check + fast path / sub-batch
                                       loop of ``_wisp_forward_cuda_paged``
@@ -56,6 +57,9 @@ class PagerOracle:
         self.stats_miss = 0
         self.stats_evict = 0
         self.stats_hits = 0
+        # post-forward bookkeeping (fused_moe.py:1173-1177) and prefetch count
+        self.last_unique_experts: set[int] = set()
+        self.stats_pred_total = 0
 
     # -- expert_map_device view (fused_moe.py:196-204, 333, 353) -----------
     def expert_map(self) -> list[int]:
@@ -127,6 +131,54 @@ class PagerOracle:
         rec.update(self.snapshot())
         return rec
 
+    # -- fused_moe.py:360-433 ---------------------------------------------
+    def prefetch_async(self, predicted_experts: set) -> dict:
+        """Speculative load of ``predicted_experts`` (a set; its iteration
+        order fixes which slot each expert takes).  Evicts by LRU tick among
+        slots whose expert is neither in ``last_unique_experts`` nor
+        predicted; loads what fits; bumps the clock once if anything was
+        missing.  Returns ``{"evicted": [(e, s)], "loaded": [(e, s)]}``."""
+        rec = {"evicted": [], "loaded": []}
+        if not predicted_experts:
+            return rec
+        to_load = [e for e in predicted_experts if e not in self.expert_to_slot]
+        if not to_load:
+            return rec
+        free_slots = [s for s in range(self.cap_experts) if self.slot_to_expert[s] == -1]
+        candidates = sorted(
+            (
+                (self.lru_tick[s], s)
+                for s in range(self.cap_experts)
+                if self.slot_to_expert[s] != -1
+                and self.slot_to_expert[s] not in self.last_unique_experts
+                and self.slot_to_expert[s] not in predicted_experts
+            ),
+            key=lambda ts: ts[0],
+        )
+        need = len(to_load) - len(free_slots)
+        if need > 0:
+            if need > len(candidates):
+                # speculative: load only what fits (first in set order)
+                to_load = to_load[: len(candidates) + len(free_slots)]
+                need = len(to_load) - len(free_slots)
+            for _tick, s in candidates[:need]:
+                victim = self.slot_to_expert[s]
+                self.expert_to_slot.pop(victim, None)
+                self.slot_to_expert[s] = -1
+                free_slots.append(s)
+                self.stats_evict += 1
+                rec["evicted"].append((victim, s))
+        self.lru_clock += 1
+        for e in to_load:
+            if not free_slots:
+                break
+            s = free_slots.pop()
+            self.slot_to_expert[s] = int(e)
+            self.expert_to_slot[int(e)] = s
+            self.lru_tick[s] = self.lru_clock
+            rec["loaded"].append((int(e), s))
+        return rec
+
     # -- fused_moe.py:439-490 ---------------------------------------------
     def resize_cap(self, new_cap: int) -> None:
         new_cap = max(2, min(int(new_cap), self.num_experts))
@@ -159,6 +211,8 @@ class PagerOracle:
             records.append(rec)
             for row in ids[t0:t1]:
                 slots.append([self.expert_to_slot[e] for e in row])
+        # post-forward (fused_moe.py:1173-1177): built from the sorted unique ids
+        self.last_unique_experts = {int(e) for e in sorted({e for row in ids for e in row})}
         return {"groups": groups, "records": records, "slots": slots}
 
 

@@ -50,6 +50,13 @@ class LayerDesc(C.Structure):
     ]
 
 
+class Cooccur(C.Structure):
+    _fields_ = [
+        ("layers", C.c_int), ("experts", C.c_int), ("count", _vp), ("total", _vp),
+        ("obs_keys", _vp), ("obs_n", _vp), ("obs_seq", _vp), ("meta", _vp),
+    ]
+
+
 class Workspace(C.Structure):
     _fields_ = [
         ("max_pairs", C.c_int), ("topk_w", _vp), ("topk_ids", _vp), ("slots", _vp),
@@ -86,6 +93,12 @@ SIGNATURES = {
     "wisp_layer_pagein_engine": (_i32, [_vp]),
     "wisp_layer_profile": (_i32, [_vp, _i32, C.POINTER(C.c_double), C.POINTER(C.c_double),
                                   C.POINTER(C.c_int64)]),
+    "wisp_cooccur_observe_layer": (_i32, [C.POINTER(Cooccur), _i32, _vp, _i32, _i32, _vp]),
+    "wisp_cooccur_predict": (_i32, [C.POINTER(Cooccur), _i32, _i32, _vp, _i32, _i32, _vp, _vp,
+                                    _vp]),
+    "wisp_cooccur_end_step": (_i32, [C.POINTER(Cooccur), _i32, _vp]),
+    "wisp_prefetch_record_words": (_i32, [_i32]),
+    "wisp_layer_prefetch": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, _vp, _i32, _vp, _i32, _vp]),
     "wisp_probe_h2d": (_i32, [_vp, _vp, _sz, _i32, _i32, _f32p]),
     "wisp_probe_hbm_copy": (_i32, [_vp, _vp, _sz, _vp]),
 }

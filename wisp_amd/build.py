@@ -25,6 +25,7 @@ SOURCES = [
     "experts_gemv.hip",
     "experts_mfma.hip",
     "pagein.hip",
+    "prefetch.hip",
     "layer.hip",
     "probes.hip",
 ]

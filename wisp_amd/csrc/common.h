@@ -28,6 +28,7 @@ enum Counter : int {
   kMiss = 2,
   kEvict = 3,
   kHits = 4,
+  kPredTotal = 5,  // experts predicted for this layer by cross-layer prefetch
   kNumCounters = 8,
 };
 

@@ -77,6 +77,11 @@ int experts_mfma(const void* x, int T, int H, int I, int K, const float* topk_w,
                  const void* w2, size_t w2_stride, void* act, void* out, void* work,
                  size_t work_bytes, hipStream_t st, const StageEvents* ev);
 size_t mfma_work_bytes(int T, int K, int H, int nslots);
+int launch_prefetch(const int32_t* predicted, const int32_t* n_pred_ptr, int n_pred, int ordered,
+                    int count_pred, const int32_t* last_ids, int n_last, int E, int cap,
+                    int max_pred, int32_t* map, int32_t* s2e, int64_t* tick, int64_t* ctr,
+                    int32_t* rec, hipStream_t st);
+int prefetch_record_words(int max_pred);
 bool mfma_supported(int H, int I);
 
 // Calls of at least this many tokens run the bf16 experts on the MFMA grouped
@@ -128,6 +133,9 @@ struct Layer {
   int32_t* hist_dev = nullptr;
   int pin_next = 0;
   PinLaunch pin[kPinRing];
+  // cross-layer prefetch: copies on copy[0], fenced by events
+  hipEvent_t ev_pf_decided = nullptr, ev_pf_done = nullptr;
+  bool pf_pending = false;
   int nstreams = 0;  // side copy streams in use (0: the caller's stream)
   hipStream_t copy[kCopyStreams] = {};
   hipEvent_t ev_decided = nullptr;
@@ -233,6 +241,15 @@ void harvest_pin(Layer& L, int i) {
     }
   }
   p.pending = false;
+}
+
+// Orders `st` after the layer's outstanding prefetch copies (before anything
+// that reads or writes the scratch).
+int wait_prefetch(Layer& L, hipStream_t st) {
+  if (!L.pf_pending) return WISP_OK;
+  WISP_HIP_TRY(hipStreamWaitEvent(st, L.ev_pf_done, 0));
+  L.pf_pending = false;
+  return WISP_OK;
 }
 
 // Copy-kernel page-in on `st` of the (expert, slot) pairs at `loads` (device
@@ -482,6 +499,8 @@ extern "C" int wisp_layer_create(const wisp_layer_desc* desc, void** handle) {
   }
   for (int i = 0; i < kEventRing && e == hipSuccess; ++i)
     e = hipEventCreateWithFlags(&L->ev_gemm[i], hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&L->ev_pf_decided, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&L->ev_pf_done, hipEventDisableTiming);
   if (e == hipSuccess) e = hipEventCreate(&L->ev_pin_start);
   if (e == hipSuccess) e = hipEventCreate(&L->ev_pin_end);
   if (e != hipSuccess) {
@@ -506,6 +525,8 @@ extern "C" int wisp_layer_destroy(void* handle) {
     if (L->ev_gemm[i]) (void)hipEventDestroy(L->ev_gemm[i]);
   }
   if (L->ev_decided) (void)hipEventDestroy(L->ev_decided);
+  if (L->ev_pf_decided) (void)hipEventDestroy(L->ev_pf_decided);
+  if (L->ev_pf_done) (void)hipEventDestroy(L->ev_pf_done);
   if (L->ev_pin_start) (void)hipEventDestroy(L->ev_pin_start);
   if (L->ev_pin_end) (void)hipEventDestroy(L->ev_pin_end);
   for (int i = 0; i < kProfRing; ++i) {
@@ -603,6 +624,8 @@ extern "C" int wisp_layer_forward(void* handle, const void* x, const void* logit
   // One group is certain when every routed pair could be distinct and still
   // fit (the ids come from the router, so they are in range and the pager
   // cannot fail): then the rest of the call goes in right behind the pager.
+  rc = wait_prefetch(*L, st);
+  if (rc != WISP_OK) return rc;
   const bool one_group = T > 0 && (int64_t)T * K <= d.cap;
   if (one_group && L->kpin) {
     rc = page_in_kernel(*L, ws->loads, ws->flags, 0, st);
@@ -670,6 +693,8 @@ extern "C" int wisp_layer_ensure_resident(void* handle, const int32_t* ids, int 
   // ensure_resident is a single call: one group, planned over n tokens x 1.
   const RecordLayout RL(n, 1);
   const int32_t* G = rec + RL.group_base(0);
+  rc = wait_prefetch(*L, st);
+  if (rc != WISP_OK) return rc;
   if (rec[kRecGroupsDone] > 0 && G[7] > 0) {
     rc = page_in(*L, rec + RL.loaded_base() + 2 * G[6], G[7], nullptr, 0, st);
     if (rc != WISP_OK) return rc;
@@ -695,7 +720,9 @@ extern "C" int wisp_layer_prime_identity(void* handle, wisp_stream_t stream) {
     pairs[2 * e] = e;
     pairs[2 * e + 1] = e;
   }
-  int rc = page_in(*L, pairs.data(), d.num_experts, nullptr, 0, st);
+  int rc = wait_prefetch(*L, st);
+  if (rc != WISP_OK) return rc;
+  rc = page_in(*L, pairs.data(), d.num_experts, nullptr, 0, st);
   if (rc != WISP_OK) return rc;
   hipLaunchKernelGGL(identity_kernel, dim3((d.num_experts + 255) / 256), dim3(256), 0, st,
                      d.expert_map, d.slot_to_expert, d.num_experts);
@@ -712,6 +739,43 @@ extern "C" int wisp_layer_last_pagein(void* handle, float* ms, double* bytes) {
   if (bytes) *bytes = L->pin_bytes_total;
   L->pin_ms_total = 0;
   L->pin_bytes_total = 0;
+  return WISP_OK;
+}
+
+extern "C" int wisp_layer_prefetch(void* handle, const int32_t* predicted,
+                                   const int32_t* n_predicted, int n, int ordered,
+                                   int count_pred, const int32_t* last_ids, int n_last,
+                                   int32_t* record, int record_words, wisp_stream_t stream) {
+  using namespace wisp;
+  Layer* L = (Layer*)handle;
+  if (!L || n < 0 || n > kMaxExperts || (n > 0 && !predicted) || n_last < 0 ||
+      (n_last > 0 && !last_ids) || !record || record_words < prefetch_record_words(n))
+    return WISP_ERR_INVALID;
+  const wisp_layer_desc& d = L->d;
+  if (d.mode == WISP_MODE_RESIDENT || d.hidden < 1) return WISP_OK;  // nothing to page
+  hipStream_t st = (hipStream_t)stream;
+  int rc = launch_prefetch(predicted, n_predicted, n, ordered, count_pred, last_ids, n_last,
+                           d.num_experts, d.cap, n, d.expert_map, d.slot_to_expert, d.lru_tick,
+                           d.counters, record, st);
+  if (rc != WISP_OK) return rc;
+  int32_t* loads = record + 4 + 2 * n;
+  WISP_HIP_TRY(hipEventRecord(L->ev_pf_decided, st));
+  hipStream_t side = L->copy[0];
+  WISP_HIP_TRY(hipStreamWaitEvent(side, L->ev_pf_decided, 0));
+  if (L->kpin) {
+    rc = page_in_kernel(*L, loads, record + 1, 0, side);
+    if (rc != WISP_OK) return rc;
+  } else {
+    // hipMemcpyAsync needs the decisions on the host
+    std::vector<int32_t> h(4 + 4 * (size_t)n);
+    WISP_HIP_TRY(hipEventSynchronize(L->ev_pf_decided));
+    WISP_HIP_TRY(hipMemcpy(h.data(), record, h.size() * sizeof(int32_t), hipMemcpyDeviceToHost));
+    double bytes = 0;
+    rc = issue_copies(*L, h.data() + 4 + 2 * n, h[1], &bytes, side);
+    if (rc != WISP_OK) return rc;
+  }
+  WISP_HIP_TRY(hipEventRecord(L->ev_pf_done, side));
+  L->pf_pending = true;
   return WISP_OK;
 }
 

@@ -209,7 +209,9 @@ class WispMoEState:
         self.expert_map_device = torch.full((E,), -1, dtype=torch.int32, device=dev)
         self._counters = torch.zeros(8, dtype=torch.int64, device=dev)
         self.stats_pred_hits = 0
-        self.stats_pred_total = 0
+        self._pf_record: torch.Tensor | None = None
+        self._pf_words = 0
+        self._pf_n = 0
         self._ws = _Workspace(dev, self.hidden, max(1, I), self.dtype)
         self._last_pairs = 0
         self._handle = C.c_void_p()
@@ -270,6 +272,7 @@ class WispMoEState:
     stats_miss = property(lambda self: self._ctr(2), lambda self, v: self._set_ctr(2, v))
     stats_evict = property(lambda self: self._ctr(3), lambda self, v: self._set_ctr(3, v))
     stats_hits = property(lambda self: self._ctr(4), lambda self, v: self._set_ctr(4, v))
+    stats_pred_total = property(lambda self: self._ctr(5), lambda self, v: self._set_ctr(5, v))
 
     @property
     def expert_to_slot(self) -> dict[int, int]:
@@ -353,6 +356,47 @@ class WispMoEState:
         self._last_pairs, self._last_shape = T * top_k, (T, top_k)
         check(rc, "wisp_layer_forward")
         return out
+
+    def prefetch_async(self, predicted_experts) -> None:
+        """Speculatively page ``predicted_experts`` into this layer (reference
+        360-433): the decisions run on the current stream, the copies on the
+        layer's side stream, and the layer's next call waits for them.  The
+        iteration order of ``predicted_experts`` fixes which slot each expert
+        takes; experts of the last call and the predicted ones are never
+        evicted."""
+        ids = [int(e) for e in predicted_experts]
+        if not ids:
+            self._pf_n = 0  # nothing predicted: no decisions (last_prefetch is empty)
+            return
+        t = torch.tensor(ids, dtype=torch.int32, device=self.device)
+        self._prefetch(t, None, len(ids), ordered=True, count_pred=False)
+
+    def _prefetch(self, ids: torch.Tensor, n_dev: torch.Tensor | None, n: int, ordered: bool,
+                  count_pred: bool) -> None:
+        words = lib().wisp_prefetch_record_words(n)
+        if self._pf_record is None or self._pf_words < words:
+            self._pf_words = max(words, lib().wisp_prefetch_record_words(self.num_experts))
+            self._pf_record = torch.zeros(self._pf_words, dtype=torch.int32, device=self.device)
+        self._pf_n = n
+        last = self._ws.topk_ids if self._last_pairs else None
+        check(lib().wisp_layer_prefetch(
+            self._handle, ids.data_ptr(), n_dev.data_ptr() if n_dev is not None else None, n,
+            int(bool(ordered)), int(bool(count_pred)),
+            last.data_ptr() if last is not None else None, self._last_pairs,
+            self._pf_record.data_ptr(), self._pf_words, _lib.stream_handle()), "prefetch")
+
+    @property
+    def last_prefetch(self) -> dict:
+        """Decisions of the last prefetch: ``{"evicted": [(e, s)], "loaded":
+        [(e, s)], "clock": bool}`` (waits for the device)."""
+        if self._pf_record is None or self._pf_n == 0:
+            return {"evicted": [], "loaded": [], "clock": False}
+        r = self._pf_record.cpu().tolist()
+        n = self._pf_n
+        ev, ld = r[4:4 + 2 * n], r[4 + 2 * n:4 + 4 * n]
+        return {"evicted": [(ev[2 * i], ev[2 * i + 1]) for i in range(r[0])],
+                "loaded": [(ld[2 * i], ld[2 * i + 1]) for i in range(r[1])],
+                "clock": bool(r[2])}
 
     def pagein_stats(self) -> tuple[float, float]:
         """(milliseconds, bytes) of page-in copies since the last query."""
@@ -642,7 +686,79 @@ def _wisp_forward_cuda_paged(self, layer: torch.nn.Module, x: torch.Tensor,
     _check_supported(a)
     if getattr(layer, "zero_expert_num", 0):
         raise NotImplementedError("wisp: zero experts are not supported")
-    return state.forward(x, a["router_logits"], a["top_k"], a["renormalize"])
+    out = state.forward(x, a["router_logits"], a["top_k"], a["renormalize"])
+    if state.mode == _Mode.PAGED:
+        _prefetch_after_forward(state)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Cross-layer speculative prefetch (reference 596-650, 1173-1233)
+# ---------------------------------------------------------------------------
+
+_COOCCUR_TABLE: Any = None  # None: not loaded yet; False: disabled
+
+
+def _flag(name: str) -> bool:
+    return os.environ.get(name, "0").strip().lower() in ("1", "true", "yes")
+
+
+def _maybe_load_cooccur(state: WispMoEState) -> Any:
+    """The process-wide co-occurrence table, sized for the registered
+    layers: warm from ``WISP_COOCCUR_PATH`` or cold when
+    ``WISP_COOCCUR_ONLINE`` is set; None when neither (prefetch then does
+    nothing, as in the reference)."""
+    global _COOCCUR_TABLE
+    if _COOCCUR_TABLE is not None:
+        return _COOCCUR_TABLE or None
+    from .cooccur import CooccurTable
+    path = os.environ.get("WISP_COOCCUR_PATH", "").strip()
+    online = _flag("WISP_COOCCUR_ONLINE")
+    if not path and not online:
+        return None
+    layers = max(len(_LAYER_STATES), state.layer_idx + 1)
+    try:
+        if path and os.path.isfile(path):
+            _COOCCUR_TABLE = CooccurTable.load(path, layers, state.num_experts, state.device)
+            logger.info("wisp.vllm: loaded warm cooccur table from %s (%d observed steps)",
+                        path, _COOCCUR_TABLE.num_steps_observed)
+        else:
+            _COOCCUR_TABLE = CooccurTable(layers, state.num_experts, state.device)
+            logger.info("wisp.vllm: cooccur table starts cold (online=%s)", online)
+    except Exception as e:  # pragma: no cover - bad file
+        logger.warning("wisp.vllm: cooccur init failed: %s - disabling", e)
+        _COOCCUR_TABLE = False
+        return None
+    return _COOCCUR_TABLE
+
+
+def _reset_cooccur() -> None:
+    """Forget the process-wide table (the next paged call reloads it)."""
+    global _COOCCUR_TABLE
+    _COOCCUR_TABLE = None
+
+
+def _prefetch_after_forward(state: WispMoEState) -> None:
+    """Post-forward step of a paged layer with ``WISP_PREFETCH`` set
+    (reference 1173-1233): record this layer's experts for the step, predict
+    the next layer's ``max(8, cap // 2)`` experts (normalised, decay 0.5) and
+    prefetch them into it; at the last layer learn the step when
+    ``WISP_COOCCUR_ONLINE`` is set, then clear it.  All of it is queued on
+    the current stream; nothing waits for the device."""
+    if not _flag("WISP_PREFETCH") or state._last_pairs == 0:
+        return
+    table = _maybe_load_cooccur(state)
+    if table is None or state.layer_idx >= table.layers:
+        return
+    table.observe_layer(state.layer_idx, state._ws.topk_ids, state._last_pairs)
+    nxt = state.layer_idx + 1
+    if nxt < len(_LAYER_STATES) and nxt < table.layers:
+        ns = _LAYER_STATES[nxt]
+        k = max(8, ns.cap_experts // 2)
+        ids, n_dev = table.predict_device(nxt, k, normalize=True, decay=0.5)
+        ns._prefetch(ids, n_dev, min(k, table.experts), ordered=False, count_pred=True)
+    if state.layer_idx == len(_LAYER_STATES) - 1:
+        table.end_step(_flag("WISP_COOCCUR_ONLINE"))
 
 
 # ---------------------------------------------------------------------------
