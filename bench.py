@@ -325,11 +325,22 @@ def bench_stack(args) -> dict:
     states = [WispMoEState(w13, w2, sh.cap, "paged", dev, L) for L in range(layers)]
     log(f"stack setup {time.perf_counter() - t_setup:.1f}s")
     n_warm = 8
+    after = None
+    if args.prefetch:
+        from wisp_amd.integrations.vllm import fused_moe as fm
+        os.environ["WISP_PREFETCH"] = "1"
+        os.environ["WISP_COOCCUR_ONLINE"] = "1"
+        os.environ.pop("WISP_COOCCUR_PATH", None)
+        fm._reset_cooccur()
+        fm._LAYER_STATES = states
+        after = fm._prefetch_after_forward
 
     def token(i: int) -> None:
         h = x0[i]
         for L in range(layers):
             h = states[L].forward(h, lg[L, i:i + 1], sh.top_k, True)
+            if after is not None:
+                after(states[L])
 
     elapsed, agg = _timed(token, n_warm, tokens - n_warm, states)
     n = tokens - n_warm
@@ -341,6 +352,9 @@ def bench_stack(args) -> dict:
                   "hidden": sh.hidden, "expert_intermediate": sh.inter, "experts": sh.experts,
                   "top_k": sh.top_k, "cap": sh.cap, "layers": layers, "tokens": n},
                  layer_calls_per_s=round(n * layers / elapsed, 1),
+                 prefetch={"enabled": bool(args.prefetch),
+                           "predicted": sum(st.stats_pred_total for st in states),
+                           "evicted": sum(st.stats_evict for st in states)},
                  pagein=_pagein_report(agg),
                  expert_gemm_us_per_layer_call=round((agg["w13_ms"] + agg["w2_ms"]) / calls * 1e3,
                                                      2))
@@ -358,6 +372,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", default="qwen3",
                     choices=["qwen3", "prefill", "batch32", "mixtral", "stack"])
+    ap.add_argument("--prefetch", action="store_true",
+                    help="stack workload: cross-layer speculative prefetch with a co-occurrence "
+                         "table learned online (WISP_PREFETCH=1, WISP_COOCCUR_ONLINE=1)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
