@@ -32,6 +32,8 @@ typedef struct ihipStream_t* wisp_stream_t; /* == hipStream_t */
 /* element types */
 #define WISP_F32 0
 #define WISP_BF16 1
+#define WISP_FP8_E4M3 2 /* layer dtype: expert weights float8_e4m3fn (OCP) with
+                           float32 block scales; x, act and out bfloat16 */
 
 /* layer modes (WISP_MODE, fused_moe.py:76-79) */
 #define WISP_MODE_PAGED 0
@@ -55,7 +57,8 @@ typedef struct ihipStream_t* wisp_stream_t; /* == hipStream_t */
 
 /* Message of the last failing call on this thread ("" if none). */
 const char* wisp_last_error(void);
-/* ABI version of this library. */
+/* ABI version of this library: 2 (wisp_layer_desc carries the block-FP8
+ * fields). */
 int wisp_abi_version(void);
 /* int32 words a decision record needs for a call of T tokens x K experts. */
 int wisp_record_words(int T, int K);
@@ -139,6 +142,40 @@ int wisp_moe_experts(const void* x, int dtype, int T, int H, int I, int K,
                      void* act, void* out, void* work, size_t work_bytes, int algo,
                      wisp_stream_t stream);
 
+/* Block-FP8 (w8a8) SwiGLU experts with the routing-order combine, as vLLM's
+ * fused_experts computes them with an fp8_w8a8 block quant config:
+ *   activations quantised per token and group of 128 columns to e4m3fn
+ *   (s = max(max|x|, 1e-10) / 448), then per k-block kb
+ *   acc += (dot(q_x[kb], W[n, kb]) * s_x[kb]) * S[n / block_n][kb];
+ *   h13 = bf16(acc); act = bf16(bf16(silu(gate)) * up); act quantised as x;
+ *   y = bf16(W2-stage acc * topk_w); out[t] = moe_sum_k y[t,k] (bf16 adds
+ *   for K in {2,3,4}, else one float32 sum rounded once), k ascending.
+ * x, act, out: bfloat16.  W13 of slot s: w13 + s*w13_stride bytes
+ * ([2I, H] e4m3fn), its scales s13 + s*s13_stride floats
+ * ([2I/block_n, H/128]); W2 [H, I] and s2 [H/block_n, I/128] likewise.
+ * Requires block_k == 128, block_n a multiple of 16 dividing I, H and I
+ * multiples of 128.  A slot of -1 contributes zero.  work / work_bytes:
+ * reserved for larger-batch kernels (may be NULL / 0).
+ * Replaces: vLLM fused_experts(..., quant_config=fp8_w8a8_moe_quant_config(
+ *           w1_scale=scratch_s13, w2_scale=scratch_s2, block_shape=...))
+ *           at src/wisp/integrations/vllm/fused_moe_fp8.py:245-249,316-326. */
+int wisp_moe_experts_fp8(const void* x, int T, int H, int I, int K, const float* topk_w,
+                         const int32_t* slots, int nslots, const void* w13, size_t w13_stride,
+                         const float* s13, size_t s13_stride, const void* w2, size_t w2_stride,
+                         const float* s2, size_t s2_stride, int block_n, int block_k, void* act,
+                         void* out, void* work, size_t work_bytes, int algo,
+                         wisp_stream_t stream);
+
+/* Dynamic per-row, per-group fp8 quantisation: x [rows, cols] (WISP_F32 or
+ * WISP_BF16, row stride cols) -> q [rows, cols] e4m3fn codes and
+ * scales [rows, cols / group] float32, s = max(max|x_g|, 1e-10) / 448,
+ * q = e4m3fn(clamp(x / s, -448, 448)) rounded to nearest even.  group == 128
+ * and cols a multiple of it.
+ * Replaces: vLLM per_token_group_quant_fp8 (the activation quantisation of
+ *           the fp8_w8a8 block path at fused_moe_fp8.py:316-326). */
+int wisp_quant_fp8_groups(const void* x, int dtype, int rows, int cols, int group, uint8_t* q,
+                          float* scales, wisp_stream_t stream);
+
 /* Bytes of the work buffer the MFMA expert path needs for T tokens x K over
  * nslots slots at hidden size H: per-slot pair lists and fp32 per-pair
  * outputs.  No reference counterpart (vLLM allocates its own). */
@@ -147,7 +184,10 @@ size_t wisp_moe_work_bytes(int T, int K, int H, int nslots);
 /* ---- group 3: the layer call --------------------------------------- */
 
 typedef struct wisp_layer_desc {
-  int num_experts, cap;
+  int num_experts, cap;          /* cap in [1, 512]; it may exceed
+                                    num_experts (the FP8 clamp
+                                    max(8, min(cap, E)), fused_moe_fp8.py:58);
+                                    resident mode needs cap == num_experts */
   int hidden, inter;             /* expert MLP shape; 0 for a pager-only
                                     state (the forward call then fails)  */
   int dtype, mode;
@@ -171,6 +211,20 @@ typedef struct wisp_layer_desc {
   int32_t* slot_to_expert;       /* device [cap]                         */
   int64_t* lru_tick;             /* device [cap]                         */
   int64_t* counters;             /* device [8]                           */
+  /* block-FP8 experts (dtype WISP_FP8_E4M3; zero / NULL otherwise).  The
+     weights above are then float8_e4m3fn (strides in bytes) and each expert
+     carries float32 block scales: s13 [2*ceil(I/bn), ceil(H/bk)],
+     s2 [ceil(H/bn), ceil(I/bk)] (fused_moe_fp8.py:188-202). */
+  int block_n, block_k;          /* weight block [rows, cols]            */
+  size_t s13_elems, s2_elems;    /* scale elements of one expert         */
+  float* scratch_s13;            /* device, slot s at +s*stride          */
+  size_t scratch_s13_stride;     /* elements                             */
+  float* scratch_s2;
+  size_t scratch_s2_stride;      /* elements                             */
+  const float* master_s13;       /* host, expert e at +e*stride          */
+  size_t master_s13_stride;      /* elements                             */
+  const float* master_s2;
+  size_t master_s2_stride;       /* elements                             */
 } wisp_layer_desc;
 
 typedef struct wisp_workspace {
@@ -195,7 +249,9 @@ typedef struct wisp_workspace {
 /* Create / destroy the per-layer context (copy stream, events). */
 int wisp_layer_create(const wisp_layer_desc* desc, void** handle);
 int wisp_layer_destroy(void* handle);
-/* Re-point the context at a new scratch / cap (after a resize). */
+/* Re-point the context at a new scratch / cap (after a resize).  Layers of
+ * dtype WISP_FP8_E4M3 have no resize (the reference's FP8 state has none):
+ * WISP_ERR_UNSUPPORTED. */
 int wisp_layer_set_scratch(void* handle, void* scratch_w13, void* scratch_w2, int cap,
                            int32_t* slot_to_expert, int64_t* lru_tick);
 
@@ -232,8 +288,6 @@ int wisp_layer_pagein_engine(void* handle);
  * and exited is not counted. */
 int wisp_layer_profile(void* handle, int enable, double* w13_ms, double* w2_ms,
                        int64_t* calls);
-
-/* ---- group 4: probes ----------------------------------------------- */
 
 /* ---- group 4: cross-layer speculative prefetch ------------------------ */
 
@@ -290,6 +344,8 @@ int wisp_prefetch_record_words(int max_predicted);
 int wisp_layer_prefetch(void* handle, const int32_t* predicted, const int32_t* n_predicted,
                         int n, int ordered, int count_pred, const int32_t* last_ids,
                         int n_last, int32_t* record, int record_words, wisp_stream_t stream);
+
+/* ---- group 5: probes ----------------------------------------------- */
 
 /* Pinned host -> device hipMemcpyAsync bandwidth: `iters` copies of `bytes`
  * on `streams` streams; writes the per-iteration milliseconds.

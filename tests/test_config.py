@@ -87,3 +87,64 @@ def test_unsupported_call_arguments():
     with pytest.raises(NotImplementedError):
         fm._check_supported({"use_grouped_topk": True})
     fm._check_supported({"scoring_func": "softmax", "topk_group": None})
+
+
+# --- block-FP8 path (reference fused_moe_fp8.py:48-58, 362-390) -------------
+
+f8m = importlib.import_module("wisp_amd.integrations.vllm.fused_moe_fp8")
+
+
+@pytest.mark.parametrize("raw,E,want", [(None, 128, 24), (None, 8, 8), ("8", 128, 8),
+                                        ("2", 128, 8), ("2", 4, 8), ("999", 128, 128),
+                                        ("abc", 128, 24), ("abc", 16, 16), ("-5", 16, 8)])
+def test_resolve_cap_fp8(monkeypatch, raw, E, want):
+    if raw is None:
+        monkeypatch.delenv("WISP_CAP_EXPERTS", raising=False)
+    else:
+        monkeypatch.setenv("WISP_CAP_EXPERTS", raw)
+    assert f8m._resolve_cap_experts(E) == want
+
+
+def test_fp8_slab_layout_qwen3_shape():
+    lay = f8m.Fp8SlabLayout(2048, 768, (128, 128))
+    assert lay.s13_shape == (12, 16) and lay.s2_shape == (16, 6)
+    assert lay.o_w2 == 2 * 768 * 2048 and lay.o_s13 == 3 * 768 * 2048
+    assert lay.o_s2 == lay.o_s13 + 4 * 12 * 16 and lay.used == lay.o_s2 + 4 * 16 * 6
+    assert lay.slab % 256 == 0 and lay.slab - lay.used < 256
+    import torch
+    buf = torch.zeros((3, lay.slab), dtype=torch.uint8)
+    w13, w2, s13, s2 = lay.views(buf)
+    assert w13.shape == (3, 1536, 2048) and w13.dtype == torch.float8_e4m3fn
+    assert s2.shape == (3, 16, 6) and s2.dtype == torch.float32
+    s2[1].fill_(2.0)
+    raw = buf[1, lay.o_s2:lay.used].view(torch.float32)
+    assert torch.equal(raw, torch.full((96,), 2.0))
+    # DeepSeek-V3-shaped and block_n 64 layouts keep the scales 16-byte aligned
+    for H, I, blk in ((7168, 2048, (128, 128)), (1024, 384, (64, 128))):
+        lay = f8m.Fp8SlabLayout(H, I, blk)
+        assert lay.o_s13 % 16 == 0 and lay.o_s2 % 4 == 0
+
+
+def test_install_fp8_patches_standin_once():
+    from wisp_amd.integrations.vllm import layer
+    cls = layer.Fp8MoEMethod
+    names = ("create_weights", "process_weights_after_loading", "apply")
+    orig = {n: cls.__dict__[n] for n in names}
+    was = getattr(cls, f8m._PATCHED_FLAG, False)
+    try:
+        if was:
+            for n in names:
+                setattr(cls, n, getattr(cls, "_wisp_original_" + n))
+            delattr(cls, f8m._PATCHED_FLAG)
+        assert f8m.install_wisp_fp8() is True and f8m.is_fp8_installed()
+        assert f8m.install_wisp_fp8() is False
+        assert cls.apply is f8m._patched_apply
+        assert cls._wisp_original_apply is (orig["apply"] if not was
+                                           else getattr(cls, "_wisp_original_apply"))
+    finally:
+        for n, f in orig.items():
+            setattr(cls, n, f)
+        if was:
+            setattr(cls, f8m._PATCHED_FLAG, True)
+        elif hasattr(cls, f8m._PATCHED_FLAG):
+            delattr(cls, f8m._PATCHED_FLAG)

@@ -1,0 +1,286 @@
+"""Block-FP8 paged path on the GPU: the activation quantiser bit-exact with the
+oracle, the expert kernels within the bf16 tolerance of the oracle's
+restatement of vLLM's w8a8 block math (oracle/fp8.py), outputs independent
+of slot placement and batching (byte-identical), pager decisions of the FP8
+state bit-exact with the reference pager, and the FP8 plug-in surface."""
+import ctypes as C
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import fp8 as F
+from oracle.moe import route
+from oracle.pager import PagerOracle
+from wisp_amd import _lib
+from wisp_amd import workloads as W
+from wisp_amd.integrations.vllm import fused_moe_fp8 as f8m
+from wisp_amd.integrations.vllm.fused_moe_fp8 import WispMoEStateFP8, fp8_slab_masters
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+# bf16 outputs: the tolerance the paged path is held to
+REL_TOL = 1e-2
+
+
+def _rel(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def _experts(E, H, I, block, seed=0, gain=True):
+    """Host slabs of E block-FP8 experts with block scales that differ by up
+    to 16x between blocks."""
+    buf, w13, w2, s13, s2 = fp8_slab_masters(E, H, I, block, pin=False)
+    g = torch.Generator().manual_seed(seed)
+    bn, bk = block
+    for e in range(E):
+        for dst, sdst, shape in ((w13, s13, (2 * I, H)), (w2, s2, (H, I))):
+            w = torch.randn(shape, generator=g) * 0.05
+            if gain:
+                gb = 2.0 ** (torch.rand((shape[0] // bn, shape[1] // bk), generator=g) * 4 - 2)
+                w = w * gb.repeat_interleave(bn, 0).repeat_interleave(bk, 1)
+            q, s = W.block_quant_fp8(w, block)
+            dst[e].copy_(q)
+            sdst[e].copy_(s)
+    return buf, w13, w2, s13, s2
+
+
+def _rows(t, idx):
+    """Rows ``idx`` of a CPU tensor (fp8 through its bytes)."""
+    idx = torch.as_tensor(np.asarray(idx, dtype=np.int64))
+    if t.dtype == torch.float8_e4m3fn:
+        return t.view(torch.uint8)[idx].view(t.dtype)
+    return t[idx]
+
+
+def _routing(T, E, K, seed):
+    rng = np.random.default_rng(seed)
+    ids = np.stack([rng.permutation(E)[:K] for _ in range(T)]).astype(np.int32)
+    w = rng.uniform(0.05, 1.0, (T, K)).astype(np.float32)
+    return ids, w
+
+
+def _run_experts(x, ids, tw, w13, w2, s13, s2, block, slots=None, nslots=None):
+    """wisp_moe_experts_fp8 through the C ABI on device copies; returns
+    (out, act) as float32 CPU tensors."""
+    T, H = x.shape
+    K = ids.shape[1]
+    E, I = w13.shape[0], w2.shape[2]
+    d13, d2 = w13.to(DEV), w2.to(DEV)
+    ds13, ds2 = s13.to(DEV), s2.to(DEV)
+    sl = torch.from_numpy(ids if slots is None else slots).to(DEV).contiguous()
+    twd = torch.from_numpy(tw).to(DEV).contiguous()
+    xd = x.to(DEV).contiguous()
+    act = torch.full((max(1, T * K), I), float("nan"), dtype=torch.bfloat16, device=DEV)
+    out = torch.empty((T, H), dtype=torch.bfloat16, device=DEV)
+    rc = _lib.lib().wisp_moe_experts_fp8(
+        xd.data_ptr(), T, H, I, K, twd.data_ptr(), sl.data_ptr(), E if nslots is None else nslots,
+        d13.data_ptr(), d13.stride(0), ds13.data_ptr(), ds13.stride(0), d2.data_ptr(),
+        d2.stride(0), ds2.data_ptr(), ds2.stride(0), block[0], block[1], act.data_ptr(),
+        out.data_ptr(), None, 0, _lib.WISP_ALGO_AUTO, _lib.stream_handle())
+    _lib.check(rc, "wisp_moe_experts_fp8")
+    torch.cuda.synchronize()
+    return out.float().cpu(), act.float().cpu().view(T, K, I)
+
+
+def test_quant_groups_bit_exact():
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn((37, 1024), generator=g) * torch.logspace(-3, 3, 37).view(37, 1)
+    x[5, 256:384] = 0.0
+    x[6, :128] = 448.0
+    for dt, code in ((torch.bfloat16, _lib.WISP_BF16), (torch.float32, _lib.WISP_F32)):
+        xd = x.to(dt).to(DEV).contiguous()
+        q = torch.empty((37, 1024), dtype=torch.uint8, device=DEV)
+        s = torch.empty((37, 8), dtype=torch.float32, device=DEV)
+        _lib.check(_lib.lib().wisp_quant_fp8_groups(xd.data_ptr(), code, 37, 1024, 128,
+                                                    q.data_ptr(), s.data_ptr(),
+                                                    _lib.stream_handle()), "quant")
+        torch.cuda.synchronize()
+        wq, ws = F.quant_groups(xd.float().cpu().numpy(), 128)
+        assert np.array_equal(q.cpu().numpy(), wq), dt
+        assert np.array_equal(s.cpu().numpy(), ws), dt
+
+
+SHAPES = [  # T, H, I, E, K, block
+    (1, 2048, 768, 12, 8, (128, 128)),   # Qwen3-30B-A3B-FP8 decode shape, fewer experts
+    (3, 256, 256, 8, 2, (128, 128)),     # K = 2: bf16 adds in moe_sum
+    (4, 1024, 384, 10, 3, (64, 128)),    # block_n 64, K = 3
+    (2, 4096, 256, 6, 1, (128, 128)),    # eight w13 waves, K = 1
+    (9, 512, 256, 12, 6, (128, 128)),    # batch of 9, shared experts
+]
+
+
+@pytest.mark.parametrize("T,H,I,E,K,block", SHAPES)
+def test_experts_fp8_match_oracle(T, H, I, E, K, block):
+    _, w13, w2, s13, s2 = _experts(E, H, I, block, seed=T * 31 + K)
+    ids, tw = _routing(T, E, K, seed=T + H)
+    x = (torch.randn((T, H), generator=torch.Generator().manual_seed(5)) * 2).to(torch.bfloat16)
+    out, act = _run_experts(x, ids, tw, w13, w2, s13, s2, block)
+    want, want_act = F.moe_forward_fp8(x, tw, ids, w13, w2, s13, s2, block, return_act=True)
+    assert _rel(act, want_act) < REL_TOL
+    # the MFMA's own rounding moves a few bf16 ulps; most act values are equal
+    same = float(np.mean(act.numpy() == want_act))
+    assert same > 0.95, same
+    assert _rel(out, want) < REL_TOL, _rel(out, want)
+
+
+def test_experts_fp8_absent_slot_and_slot_placement():
+    T, H, I, E, K, block = 4, 512, 256, 10, 4, (128, 128)
+    _, w13, w2, s13, s2 = _experts(E, H, I, block, seed=3)
+    ids, tw = _routing(T, E, K, seed=4)
+    x = torch.randn((T, H), generator=torch.Generator().manual_seed(6)).to(torch.bfloat16)
+    base, _ = _run_experts(x, ids, tw, w13, w2, s13, s2, block)
+    # the same experts at other slots: byte-identical
+    perm = np.random.default_rng(7).permutation(E)
+    inv = np.argsort(perm)
+    moved, _ = _run_experts(x, ids, tw, _rows(w13, perm), _rows(w2, perm), _rows(s13, perm),
+                            _rows(s2, perm), block, slots=inv[ids].astype(np.int32))
+    assert torch.equal(base.view(torch.int32), moved.view(torch.int32))
+    # a slot of -1 contributes nothing (vLLM's expert_map == -1)
+    sl = ids.copy()
+    sl[1, 2] = -1
+    sl[3, 0] = -1
+    got, _ = _run_experts(x, ids, tw, w13, w2, s13, s2, block, slots=sl)
+    # oracle: the absent pairs route to an extra expert the map marks absent
+    ext = list(range(E)) + [0]
+    emap = np.concatenate([np.zeros(E, np.int32), [-1]])
+    want = F.moe_forward_fp8(x, tw, np.where(sl < 0, E, ids), _rows(w13, ext), _rows(w2, ext),
+                             _rows(s13, ext), _rows(s2, ext), block, expert_map=emap)
+    assert _rel(got, want) < REL_TOL
+
+
+def test_experts_fp8_batching_is_byte_invariant():
+    """A token's output does not depend on the other tokens of the launch
+    (MFMA columns are independent), so grouping never changes bytes."""
+    T, H, I, E, K, block = 6, 1024, 512, 8, 4, (128, 128)
+    _, w13, w2, s13, s2 = _experts(E, H, I, block, seed=8)
+    ids, tw = _routing(T, E, K, seed=9)
+    x = torch.randn((T, H), generator=torch.Generator().manual_seed(10)).to(torch.bfloat16)
+    full, _ = _run_experts(x, ids, tw, w13, w2, s13, s2, block)
+    for t in range(T):
+        one, _ = _run_experts(x[t:t + 1], ids[t:t + 1], tw[t:t + 1], w13, w2, s13, s2, block)
+        assert torch.equal(one[0].view(torch.int32), full[t].view(torch.int32)), t
+
+
+def _fp8_state(wl, cap):
+    w13, w2, s13, s2 = wl.views()
+    return WispMoEStateFP8(w13, w2, s13, s2, cap, DEV, 0)
+
+
+@pytest.fixture(scope="module")
+def small_fp8():
+    """Qwen3-shaped block-FP8 layer with 32 experts, 48 decode steps, pinned."""
+    base = W.qwen3_decode(seed=2, steps=48, weights=False)
+    base.logits = base.logits[:, :, :32].contiguous()
+    return W.fp8_layer(base, pin=True, experts=32)
+
+
+@pytest.mark.parametrize("engine", ["kernel", "memcpy"])
+def test_fp8_state_decode_matches_oracle(monkeypatch, small_fp8, engine):
+    monkeypatch.setenv("WISP_PAGEIN_ENGINE", engine)
+    wl = small_fp8
+    E, K, cap = 32, wl.shape.top_k, 8
+    st = _fp8_state(wl, cap)
+    assert st.pagein_engine == engine
+    full = _fp8_state(wl, E)
+    ora = PagerOracle(E, cap)
+    w13, w2, s13, s2 = wl.views()
+    for t in range(wl.steps):
+        x, lg = wl.x[t].to(DEV), wl.logits[t].to(DEV)
+        out = st.forward(x, lg, K, True)
+        ref = full.forward(x, lg, K, True)
+        res = ora.forward(route(wl.logits[t], K)[1].tolist())
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), t
+        assert st.slot_to_expert == ora.slot_to_expert and st.lru_tick == ora.lru_tick, t
+        assert (st.stats_miss, st.stats_evict, st.stats_hits) == \
+            (ora.stats_miss, ora.stats_evict, ora.stats_hits), t
+        if t % 16 == 0:
+            tw, ids = route(wl.logits[t], K)
+            want = F.moe_forward_fp8(wl.x[t], tw.astype(np.float32), ids, w13, w2, s13, s2)
+            assert _rel(out.float().cpu(), want) < REL_TOL, t
+    assert ora.stats_miss > cap  # the trace pages
+
+
+def test_fp8_state_subbatches_like_the_reference(small_fp8):
+    """A batch whose experts overflow cap runs as greedy token groups."""
+    wl = small_fp8
+    E, K, cap = 32, wl.shape.top_k, 12
+    st = _fp8_state(wl, cap)
+    full = _fp8_state(wl, E)
+    ora = PagerOracle(E, cap)
+    x = wl.x[:6, 0].to(DEV)
+    lg = wl.logits[:6, 0].to(DEV)
+    out = st.forward(x, lg, K, True)
+    ref = full.forward(x, lg, K, True)
+    res = ora.forward(route(wl.logits[:6, 0], K)[1].tolist())
+    torch.cuda.synchronize()
+    assert len(res["groups"]) > 1
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    assert st.slot_to_expert == ora.slot_to_expert and st.lru_tick == ora.lru_tick
+
+
+def test_fp8_cap_clamp_above_num_experts(monkeypatch):
+    """WISP_CAP_EXPERTS=2 with E=4 clamps to 8 slots (> E); the misses take
+    the top free slots, as in the reference."""
+    H, I, E, K = 256, 256, 4, 2
+    _, w13, w2, s13, s2 = _experts(E, H, I, (128, 128), seed=11)
+    monkeypatch.setenv("WISP_CAP_EXPERTS", "2")
+    cap = f8m._resolve_cap_experts(E)
+    assert cap == 8
+    st = WispMoEStateFP8(w13, w2, s13, s2, cap, DEV, 0)
+    ora = PagerOracle(E, cap)
+    g = torch.Generator().manual_seed(12)
+    for t in range(6):
+        lg = torch.randn((1, E), generator=g)
+        x = torch.randn((1, H), generator=g).to(torch.bfloat16)
+        st.forward(x.to(DEV), lg.to(DEV), K, True)
+        ora.forward(route(lg, K)[1].tolist())
+        torch.cuda.synchronize()
+        assert st.slot_to_expert == ora.slot_to_expert, t
+    n = sum(e >= 0 for e in st.slot_to_expert)
+    assert n >= K and st.slot_to_expert[:cap - n] == [-1] * (cap - n)
+
+
+def test_install_wisp_fp8_standin_layer_matches_resident():
+    from wisp_amd.integrations.vllm.layer import Fp8FusedMoE, Fp8MoEMethod
+    E, H, I, K, block = 16, 512, 256, 4, (128, 128)
+    _, w13, w2, s13, s2 = _experts(E, H, I, block, seed=13)
+    g = torch.Generator().manual_seed(14)
+    x = torch.randn((3, H), generator=g).to(torch.bfloat16).to(DEV)
+    lg = torch.randn((3, E), generator=g).to(DEV)
+    names = ("create_weights", "process_weights_after_loading", "apply")
+    saved = {n: Fp8MoEMethod.__dict__[n] for n in names}
+    was_patched = getattr(Fp8MoEMethod, f8m._PATCHED_FLAG, False)
+    if was_patched:  # an earlier install_wisp_moe() also patched the FP8 method
+        for n in names:
+            setattr(Fp8MoEMethod, n, getattr(Fp8MoEMethod, "_wisp_original_" + n))
+        delattr(Fp8MoEMethod, f8m._PATCHED_FLAG)
+    try:
+        plain = Fp8FusedMoE(E, K, H, I, block)  # unpatched: every expert on the GPU
+        plain.load_weights(w13, w2, s13, s2)
+        plain.process_weights_after_loading()
+        ref = plain(x, lg)
+        assert f8m.install_wisp_fp8() and f8m.is_fp8_installed()
+        assert not f8m.install_wisp_fp8()  # idempotent
+        paged = Fp8FusedMoE(E, K, H, I, block)
+        assert paged.w13_weight.device.type == "cpu" and paged.w13_weight.is_pinned()
+        paged.load_weights(w13, w2, s13, s2)
+        paged.process_weights_after_loading()
+        st = paged._wisp_fp8_state
+        assert st.cap_experts == min(E, 24) and st.pagein_engine == "kernel"
+        assert paged.w13_weight.numel() == 0  # device placeholder
+        out = paged(x, lg)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+        with pytest.raises(NotImplementedError):
+            paged.quant_method.apply(paged, x, lg, K, True, expert_map=torch.zeros(E))
+    finally:
+        for n, f in saved.items():
+            setattr(Fp8MoEMethod, n, f)
+        if was_patched:
+            setattr(Fp8MoEMethod, f8m._PATCHED_FLAG, True)
+        elif hasattr(Fp8MoEMethod, f8m._PATCHED_FLAG):
+            delattr(Fp8MoEMethod, f8m._PATCHED_FLAG)
+        f8m._FP8_LAYER_STATES.clear()

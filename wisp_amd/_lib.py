@@ -19,6 +19,7 @@ WISP_ERR_UNSUPPORTED = 4
 
 WISP_F32 = 0
 WISP_BF16 = 1
+WISP_FP8_E4M3 = 2
 
 WISP_MODE_PAGED = 0
 WISP_MODE_RESIDENT = 1
@@ -47,6 +48,11 @@ class LayerDesc(C.Structure):
         ("master_w13", _vp), ("master_w13_stride", _sz),
         ("master_w2", _vp), ("master_w2_stride", _sz),
         ("expert_map", _vp), ("slot_to_expert", _vp), ("lru_tick", _vp), ("counters", _vp),
+        ("block_n", C.c_int), ("block_k", C.c_int), ("s13_elems", _sz), ("s2_elems", _sz),
+        ("scratch_s13", _vp), ("scratch_s13_stride", _sz),
+        ("scratch_s2", _vp), ("scratch_s2_stride", _sz),
+        ("master_s13", _vp), ("master_s13_stride", _sz),
+        ("master_s2", _vp), ("master_s2_stride", _sz),
     ]
 
 
@@ -82,6 +88,10 @@ SIGNATURES = {
     "wisp_moe_experts": (_i32, [_vp, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _i32, _vp, _sz,
                                 _vp, _sz, _vp, _vp, _vp, _sz, _i32, _vp]),
     "wisp_moe_work_bytes": (_sz, [_i32, _i32, _i32, _i32]),
+    "wisp_moe_experts_fp8": (_i32, [_vp, _i32, _i32, _i32, _i32, _vp, _vp, _i32, _vp, _sz, _vp,
+                                    _sz, _vp, _sz, _vp, _sz, _i32, _i32, _vp, _vp, _vp, _sz, _i32,
+                                    _vp]),
+    "wisp_quant_fp8_groups": (_i32, [_vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp]),
     "wisp_layer_create": (_i32, [C.POINTER(LayerDesc), C.POINTER(_vp)]),
     "wisp_layer_destroy": (_i32, [_vp]),
     "wisp_layer_set_scratch": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp]),

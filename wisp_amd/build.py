@@ -24,6 +24,7 @@ SOURCES = [
     "route.hip",
     "experts_gemv.hip",
     "experts_mfma.hip",
+    "experts_fp8.hip",
     "pagein.hip",
     "prefetch.hip",
     "layer.hip",

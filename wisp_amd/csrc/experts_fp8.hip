@@ -1,0 +1,610 @@
+// Block-FP8 (w8a8) expert kernels for decode and small batches on gfx950.
+//
+// Replaces vLLM's fused_experts with an fp8_w8a8 block quant config, as the
+// reference's FP8 path calls it on the Triton backend
+// (src/wisp/integrations/vllm/fused_moe_fp8.py:245-249, 316-326):
+//   x quantised per token and 128-column group (per_token_group_quant_fp8):
+//     s = max(max|x_g|, 1e-10) / 448,  q = e4m3fn(clamp(x / s, -448, 448))
+//   h = bf16(sum_kb (dot(q_x[kb], W13[n, kb]) * s_x[kb]) * S13[n / bn][kb])
+//   act = bf16(bf16(silu(gate)) * up)                         (silu_and_mul)
+//   y_k = bf16((W2-stage sum on the quantised act) * topk_w[t, k])
+//   out[t] = moe_sum_k y_k: bf16 adds for K in {2, 3, 4}, otherwise one
+//            float32 sum rounded once; k ascending.
+//
+// Both GEMMs run on v_mfma_f32_16x16x128_f8f6f4.  One instruction multiplies
+// a 16-row weight tile by up to 16 activation columns over one 128-wide
+// k-block, which is exactly one block of the weight scales, so the scaling
+// happens once per instruction result, in the order vLLM's kernel uses:
+//   acc += (D * s_act[column]) * s_w[tile's row block][kb]
+// Operand layout (checked on MI355X): lane l feeds row (A) / column (B)
+// l % 16 with the 32 consecutive k at 32 * (l / 16); the result lane l holds
+// rows 4 * (l / 16) + j, j < 4, of column l % 16.  The instruction does not
+// round like an exact float32 sum (measured: up to ~1e-4 of the largest
+// result on full-range codes), but it is deterministic and its result for
+// one output does not depend on the other columns, so outputs depend only on
+// the pair's token and the weights read: paged and resident runs agree byte
+// for byte.
+//
+// w13 kernel: grid (I / 16 row tiles, T*K pairs).  The block of the lowest
+// pair routed to a slot computes every pair of that slot, up to NCOL per
+// MFMA column set, and the other pairs' blocks exit, so each weight tile is
+// read once per launch.  NW waves split the k-blocks of H; each wave
+// quantises the activation groups it consumes into its own LDS slice, so no
+// separate quantisation launch precedes the GEMM.  Partial sums meet in LDS
+// in wave order; the epilogue rounds gate and up to bf16 and applies
+// silu_and_mul with vLLM's roundings.
+//
+// w2 kernel: grid (H / 16 row tiles, T tokens).  The block quantises the
+// token's K act rows into LDS, waves take (pair, k-range) jobs over I, and
+// the block scales each pair by its routing weight, rounds to bf16 and sums
+// the K results in routing order.
+#include "common.h"
+
+#pragma clang fp contract(off)  // keep vLLM's separate multiply and add roundings
+
+namespace wisp {
+
+int experts_fp8(const void* x, int T, int H, int I, int K, const float* topk_w,
+                const int32_t* slots, int nslots, const void* w13, size_t w13_stride,
+                const float* s13, size_t s13_stride, const void* w2, size_t w2_stride,
+                const float* s2, size_t s2_stride, int block_n, void* act, void* out,
+                hipStream_t st, const StageEvents* ev);
+const char* fp8_unsupported(int H, int I, int K, int block_n, int block_k);
+
+namespace {
+
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kE4m3Max = 448.f;
+constexpr float kQuantEps = 1e-10f;
+constexpr int kKB = 128;         // k-block: the MFMA's K and the scale block's width
+constexpr int kKC = 4;           // k-blocks a w13 wave loads before it computes
+constexpr int kKC2 = 8;          // k-blocks a w2 wave loads before it computes
+constexpr int kW2Waves = 8;
+constexpr size_t kMaxLds = 160 * 1024;
+
+__device__ inline float bf16f(uint32_t b) { return __uint_as_float(b << 16); }
+
+__device__ inline uint16_t bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ inline float round_bf16(float f) { return bf16f(bf16_rne(f)); }
+
+__device__ inline float silu(float g) { return g / (1.0f + expf(-g)); }
+
+__device__ inline f32x4 mfma_fp8(const i32x8& a, const i32x8& b) {
+  const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+  // formats 0/0: both operands e4m3; zero scale operands select the
+  // unscaled instruction
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, z, 0, 0, 0, 0, 0, 0);
+}
+
+__device__ inline i32x8 join(const u32x4& a, const u32x4& b) {
+  i32x8 r;
+  r[0] = (int)a.x; r[1] = (int)a.y; r[2] = (int)a.z; r[3] = (int)a.w;
+  r[4] = (int)b.x; r[5] = (int)b.y; r[6] = (int)b.z; r[7] = (int)b.w;
+  return r;
+}
+
+// 32 bytes of a weight row, streamed (each byte is read once per launch).
+__device__ inline i32x8 ld32_stream(const uint8_t* p) {
+  const u32x4 a = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  const u32x4 b = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p + 16));
+  return join(a, b);
+}
+
+__device__ inline i32x8 lds32(const uint8_t* p) {
+  return join(*reinterpret_cast<const u32x4*>(p), *reinterpret_cast<const u32x4*>(p + 16));
+}
+
+__device__ inline i32x8 zero8() {
+  i32x8 r;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = 0;
+  return r;
+}
+
+// Max over the 16 lanes of this lane's quarter-wave.
+__device__ inline float quarter_max(float v) {
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+// Quantises one 128-value group held 8 values per lane by the 16 lanes of a
+// quarter-wave (per_token_group_quant_fp8): returns the scale and the 8 codes
+// of this lane as two words (code of value i in byte i).
+__device__ inline float quant8(const float* v, uint32_t* q) {
+  float m = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[i]));
+  m = quarter_max(m);
+  const float s = fmaxf(m, kQuantEps) / kE4m3Max;
+  float c[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) c[i] = fminf(fmaxf(v[i] / s, -kE4m3Max), kE4m3Max);
+  int w0 = __builtin_amdgcn_cvt_pk_fp8_f32(c[0], c[1], 0, false);
+  w0 = __builtin_amdgcn_cvt_pk_fp8_f32(c[2], c[3], w0, true);
+  int w1 = __builtin_amdgcn_cvt_pk_fp8_f32(c[4], c[5], 0, false);
+  w1 = __builtin_amdgcn_cvt_pk_fp8_f32(c[6], c[7], w1, true);
+  q[0] = (uint32_t)w0;
+  q[1] = (uint32_t)w1;
+  return s;
+}
+
+__device__ inline void unpack_bf16x8(const u32x4& u, float* f) {
+  f[0] = bf16f(u.x & 0xffffu); f[1] = bf16f(u.x >> 16);
+  f[2] = bf16f(u.y & 0xffffu); f[3] = bf16f(u.y >> 16);
+  f[4] = bf16f(u.z & 0xffffu); f[5] = bf16f(u.z >> 16);
+  f[6] = bf16f(u.w & 0xffffu); f[7] = bf16f(u.w >> 16);
+}
+
+// ---------------------------------------------------------------------------
+// Standalone group quantiser: one quarter-wave per 128-value group.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void quant_groups_kernel(const T* __restrict__ x, int rows,
+                                                           int cols, uint8_t* __restrict__ q,
+                                                           float* __restrict__ scales) {
+  const int ng = cols / kKB;
+  const long job = (long)blockIdx.x * 16 + (threadIdx.x >> 4);
+  if (job >= (long)rows * ng) return;
+  const int r = (int)(job / ng), g = (int)(job % ng), sub = threadIdx.x & 15;
+  const size_t off = (size_t)r * cols + (size_t)g * kKB + sub * 8;
+  float v[8];
+  if constexpr (sizeof(T) == 2) {
+    unpack_bf16x8(*reinterpret_cast<const u32x4*>(x + off), v);
+  } else {
+    const u32x4 a = *reinterpret_cast<const u32x4*>(x + off);
+    const u32x4 b = *reinterpret_cast<const u32x4*>(x + off + 4);
+    v[0] = __uint_as_float(a.x); v[1] = __uint_as_float(a.y);
+    v[2] = __uint_as_float(a.z); v[3] = __uint_as_float(a.w);
+    v[4] = __uint_as_float(b.x); v[5] = __uint_as_float(b.y);
+    v[6] = __uint_as_float(b.z); v[7] = __uint_as_float(b.w);
+  }
+  uint32_t c[2];
+  const float s = quant8(v, c);
+  *reinterpret_cast<uint2*>(q + off) = make_uint2(c[0], c[1]);
+  if (sub == 0) scales[(size_t)r * ng + g] = s;
+}
+
+// ---------------------------------------------------------------------------
+// w13 + silu_and_mul.
+// Dynamic LDS: red [NW][2][64][4] f32, then per wave xs [kKC][ncol] f32 and
+// xq [kKC][ncol][kKB] codes.
+// ---------------------------------------------------------------------------
+
+// Pair index of rank `rank` among the pairs routed to slot s (-1 if none),
+// and their number; wave-uniform loop over the P pairs.
+__device__ inline int pair_of_rank(const int32_t* __restrict__ slots, int P, int s, int rank,
+                                   int lane, int* total) {
+  int found = -1, seen = 0;
+  for (int b = 0; b < P; b += 64) {
+    const int q = b + lane;
+    unsigned long long bal = __ballot(q < P && slots[q] == s);
+    const int c = __popcll(bal);
+    const int want = rank - seen;
+    if (found < 0 && want >= 0 && want < c) {
+      for (int i = 0; i < want; ++i) bal &= bal - 1;
+      found = b + __ffsll((long long)bal) - 1;
+    }
+    seen += c;
+  }
+  *total = seen;
+  return found;
+}
+
+template <int NW>
+__global__ __launch_bounds__(NW * 64) void fp8_w13_kernel(
+    const uint16_t* __restrict__ x, int H, int I, int K, int P, const int32_t* __restrict__ slots,
+    int nslots, const uint8_t* __restrict__ w13, size_t w13_stride, const float* __restrict__ s13,
+    size_t s13_stride, int block_n, int ncol, uint16_t* __restrict__ act) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  float* red = reinterpret_cast<float*>(smem);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int col = lane & 15, grp = lane >> 4;
+  const int p = blockIdx.y, i0 = blockIdx.x * 16;
+  const int s = slots[p];
+  if (s < 0 || s >= nslots) {  // this pair reads no expert
+    if (threadIdx.x < 16) act[(size_t)p * I + i0 + threadIdx.x] = 0;
+    return;
+  }
+  int total = 0;
+  if (pair_of_rank(slots, P, s, 0, lane, &total) != p) return;  // not the slot's leader
+
+  float* xs = reinterpret_cast<float*>(smem + NW * 2 * 64 * 4 * sizeof(float) +
+                                       (size_t)wave * kKC * ncol * (4 + kKB));
+  uint8_t* xq = reinterpret_cast<uint8_t*>(xs + kKC * ncol);
+  const int nkb = H / kKB;
+  const int per = (nkb + NW - 1) / NW;
+  const int kb0 = min(nkb, wave * per), kb1 = min(nkb, kb0 + per);
+  const uint8_t* W = w13 + (size_t)s * w13_stride;
+  const float* Sg = s13 + (size_t)s * s13_stride + (size_t)(i0 / block_n) * nkb;
+  const float* Su = s13 + (size_t)s * s13_stride + (size_t)((I + i0) / block_n) * nkb;
+  const uint8_t* rowg = W + (size_t)(i0 + col) * H + grp * 32;
+  const uint8_t* rowu = W + (size_t)(I + i0 + col) * H + grp * 32;
+
+  for (int rank0 = 0; rank0 < total; rank0 += ncol) {
+    const int npc = min(ncol, total - rank0);
+    // column `col` of this set computes the pair of rank rank0 + col (every
+    // lane runs the ballots; lanes past the set's width get -1)
+    const int r = pair_of_rank(slots, P, s, rank0 + col, lane, &total);
+    const int mypair = col < npc ? r : -1;
+    const int mytok = mypair >= 0 ? mypair / K : 0;
+    f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
+    for (int kc = kb0; kc < kb1; kc += kKC) {
+      const int nk = min(kKC, kb1 - kc);
+      // activation groups of this chunk: job j = (column j / nk, k-block j % nk),
+      // four jobs per pass (a quarter-wave each, 8 values per lane), four
+      // passes per round
+      const int njobs = npc * nk, npass = (njobs + 3) >> 2;
+      u32x4 xv[4];
+      auto load_round = [&](int r0) {
+#pragma unroll
+        for (int it = 0; it < 4; ++it) {
+          if (r0 + it < npass) {  // wave-uniform
+            const int j = (r0 + it) * 4 + grp;
+            const int c = j < njobs ? j / nk : 0, kbi = j < njobs ? j % nk : 0;
+            const int tok = __shfl(mytok, c);  // the token of column c (lane c)
+            // here lane & 15 is the lane's eighth of the 128-value group
+            xv[it] = j < njobs ? *reinterpret_cast<const u32x4*>(
+                                     x + (size_t)tok * H + (size_t)(kc + kbi) * kKB + col * 8)
+                               : u32x4{0u, 0u, 0u, 0u};
+          }
+        }
+      };
+      auto quant_round = [&](int r0) {
+#pragma unroll
+        for (int it = 0; it < 4; ++it) {
+          if (r0 + it < npass) {
+            const int j = (r0 + it) * 4 + grp;
+            float v[8];
+            unpack_bf16x8(xv[it], v);
+            uint32_t q[2];
+            const float sc = quant8(v, q);
+            if (j < njobs) {
+              const int c = j / nk, kbi = j % nk;
+              *reinterpret_cast<uint2*>(xq + ((size_t)kbi * ncol + c) * kKB + col * 8) =
+                  make_uint2(q[0], q[1]);
+              if (col == 0) xs[kbi * ncol + c] = sc;
+            }
+          }
+        }
+      };
+      // the first round's activations, then the weights, are in flight
+      // together; the quantisation waits only for the activations
+      load_round(0);
+      i32x8 wg[kKC], wu[kKC];
+#pragma unroll
+      for (int kbi = 0; kbi < kKC; ++kbi) {
+        if (kbi < nk) {
+          wg[kbi] = ld32_stream(rowg + (size_t)(kc + kbi) * kKB);
+          wu[kbi] = ld32_stream(rowu + (size_t)(kc + kbi) * kKB);
+        }
+      }
+      quant_round(0);
+      for (int r0 = 4; r0 < npass; r0 += 4) {
+        load_round(r0);
+        quant_round(r0);
+      }
+      wave_lds_sync();
+#pragma unroll
+      for (int kbi = 0; kbi < kKC; ++kbi) {
+        if (kbi < nk) {
+          const i32x8 b = col < npc ? lds32(xq + ((size_t)kbi * ncol + col) * kKB + grp * 32)
+                                    : zero8();
+          const float sa = col < npc ? xs[kbi * ncol + col] : 0.f;
+          const float sg = Sg[kc + kbi], su = Su[kc + kbi];
+          const f32x4 dg = mfma_fp8(wg[kbi], b);
+          const f32x4 du = mfma_fp8(wu[kbi], b);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            ag[j] = ag[j] + (dg[j] * sa) * sg;
+            au[j] = au[j] + (du[j] * sa) * su;
+          }
+        }
+      }
+      wave_lds_sync();  // the slice is rewritten by the next chunk
+    }
+    float* rw = red + ((size_t)wave * 2 * 64 + lane) * 4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      rw[j] = ag[j];
+      rw[64 * 4 + j] = au[j];
+    }
+    __syncthreads();
+    if (wave == 0 && col < npc) {
+      float g[4] = {0.f, 0.f, 0.f, 0.f}, u[4] = {0.f, 0.f, 0.f, 0.f};
+      for (int w = 0; w < NW; ++w) {
+        const float* r = red + ((size_t)w * 2 * 64 + lane) * 4;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          g[j] = g[j] + r[j];
+          u[j] = u[j] + r[64 * 4 + j];
+        }
+      }
+      uint16_t* arow = act + (size_t)mypair * I + i0 + grp * 4;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float hg = round_bf16(g[j]), hu = round_bf16(u[j]);
+        arow[j] = bf16_rne(round_bf16(silu(hg)) * hu);
+      }
+    }
+    __syncthreads();  // red is rewritten by the next column set
+  }
+}
+
+// ---------------------------------------------------------------------------
+// w2 + routing weight + moe_sum.
+// Dynamic LDS: aq [K][I] codes, as [K][nkb] f32, part [K][WP][16] f32.
+// ---------------------------------------------------------------------------
+template <int NW>
+__global__ __launch_bounds__(NW * 64) void fp8_w2_kernel(
+    const uint16_t* __restrict__ act, int H, int I, int K, const float* __restrict__ topk_w,
+    const int32_t* __restrict__ slots, int nslots, const uint8_t* __restrict__ w2,
+    size_t w2_stride,
+    const float* __restrict__ s2, size_t s2_stride, int block_n, int WP,
+    uint16_t* __restrict__ out) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int col = lane & 15, grp = lane >> 4;
+  const int t = blockIdx.y, h0 = blockIdx.x * 16;
+  const int nkb = I / kKB;
+  uint8_t* aq = smem;
+  float* as = reinterpret_cast<float*>(smem + (size_t)K * I);
+  float* part = as + (size_t)K * nkb;
+
+  // this wave's jobs: (pair k, k-block part q), q < WP; the first job's
+  // first chunk of weights is loaded before the act is quantised
+  const int njob = K * WP;
+  const int per = (nkb + WP - 1) / WP;
+  i32x8 a[kKC2];
+  int j0 = wave;
+  int s0 = -1, kbs0 = 0, kbe0 = 0;
+  if (j0 < njob) {
+    s0 = slots[(size_t)t * K + j0 / WP];
+    if (s0 >= nslots) s0 = -1;
+    kbs0 = min(nkb, (j0 % WP) * per);
+    kbe0 = min(nkb, kbs0 + per);
+    if (s0 >= 0) {
+      const uint8_t* row = w2 + (size_t)s0 * w2_stride + (size_t)(h0 + col) * I + grp * 32;
+#pragma unroll
+      for (int kbi = 0; kbi < kKC2; ++kbi)
+        if (kbs0 + kbi < kbe0) a[kbi] = ld32_stream(row + (size_t)(kbs0 + kbi) * kKB);
+    }
+  }
+
+  // quantise the token's K act rows: one quarter-wave per 128-value group
+  const int ngroups = K * nkb;
+  for (int g0 = wave * 4; g0 < ngroups; g0 += NW * 4) {
+    const int g = g0 + grp;
+    if (g < ngroups) {
+      const int k = g / nkb, kb = g % nkb;
+      const u32x4 u = *reinterpret_cast<const u32x4*>(act + ((size_t)t * K + k) * I +
+                                                      (size_t)kb * kKB + col * 8);
+      float v[8];
+      unpack_bf16x8(u, v);
+      uint32_t q[2];
+      const float sc = quant8(v, q);
+      *reinterpret_cast<uint2*>(aq + (size_t)k * I + (size_t)kb * kKB + col * 8) =
+          make_uint2(q[0], q[1]);
+      if (col == 0) as[k * nkb + kb] = sc;
+    }  // the shuffles of quant8 stay inside one quarter-wave, which branches as one
+  }
+  __syncthreads();
+
+  for (int j = wave; j < njob; j += NW) {
+    const int k = j / WP;
+    int s = j == j0 ? s0 : slots[(size_t)t * K + k];
+    if (s >= nslots) s = -1;  // out of the scratch: contributes zero
+    const int kbs = j == j0 ? kbs0 : min(nkb, (j % WP) * per);
+    const int kbe = j == j0 ? kbe0 : min(nkb, kbs + per);
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    if (s >= 0) {
+      const uint8_t* row = w2 + (size_t)s * w2_stride + (size_t)(h0 + col) * I + grp * 32;
+      const float* S = s2 + (size_t)s * s2_stride + (size_t)(h0 / block_n) * nkb;
+      const float* sa = as + (size_t)k * nkb;
+      const uint8_t* aqk = aq + (size_t)k * I + grp * 32;
+      for (int kc = kbs; kc < kbe; kc += kKC2) {
+        if (!(j == j0 && kc == kbs)) {
+#pragma unroll
+          for (int kbi = 0; kbi < kKC2; ++kbi)
+            if (kc + kbi < kbe) a[kbi] = ld32_stream(row + (size_t)(kc + kbi) * kKB);
+        }
+#pragma unroll
+        for (int kbi = 0; kbi < kKC2; ++kbi) {
+          if (kc + kbi < kbe) {
+            const i32x8 b = col == 0 ? lds32(aqk + (size_t)(kc + kbi) * kKB) : zero8();
+            const f32x4 d = mfma_fp8(a[kbi], b);
+            const float sc = sa[kc + kbi], sw = S[kc + kbi];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) acc[q] = acc[q] + (d[q] * sc) * sw;
+          }
+        }
+      }
+    }
+    if (col == 0) {
+      float* pr = part + ((size_t)k * WP + (j % WP)) * 16 + grp * 4;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) pr[q] = acc[q];
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    const int r = threadIdx.x;
+    const float* w = topk_w + (size_t)t * K;
+    const bool bf16_adds = K >= 2 && K <= 4;
+    float sum = 0.f;
+    for (int k = 0; k < K; ++k) {
+      float y = 0.f;
+      const int sk = slots[(size_t)t * K + k];
+      if (sk >= 0 && sk < nslots) {
+        float v = 0.f;
+        for (int q = 0; q < WP; ++q) v = v + part[((size_t)k * WP + q) * 16 + r];
+        y = round_bf16(v * w[k]);
+      }
+      sum = bf16_adds ? round_bf16(sum + y) : sum + y;
+    }
+    out[(size_t)t * H + h0 + r] = bf16_rne(sum);
+  }
+}
+
+size_t w13_lds(int NW, int ncol) {
+  return (size_t)NW * 2 * 64 * 4 * sizeof(float) + (size_t)NW * kKC * ncol * (4 + kKB);
+}
+
+size_t w2_lds(int K, int I, int WP) {
+  return (size_t)K * I + (size_t)K * (I / kKB) * sizeof(float) + (size_t)K * WP * 16 * sizeof(float);
+}
+
+// Waves per w13 block: four up to H = 2048, eight above (a wave then loops
+// over chunks of kKC k-blocks; sixteen waves would cap a wave at 128 VGPRs).
+int w13_waves(int H) { return H / kKB <= 4 * kKC ? 4 : 8; }
+
+// Allows a kernel more than the default 64 KiB of dynamic LDS (once).
+template <typename Kern>
+hipError_t allow_lds(Kern kernel, size_t lds, bool* done) {
+  if (lds <= 64 * 1024 || *done) return hipSuccess;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds);
+  if (e == hipSuccess) *done = true;
+  return e;
+}
+
+template <int NW>
+hipError_t launch_w13(dim3 grid, size_t lds, hipStream_t st, hipEvent_t e0, hipEvent_t e1,
+                      const uint16_t* x, int H, int I, int K, int P, const int32_t* slots,
+                      int nslots, const uint8_t* w13, size_t w13_stride, const float* s13,
+                      size_t s13_stride,
+                      int block_n, int ncol, uint16_t* act) {
+  static bool big_lds = false;
+  hipError_t e = allow_lds(fp8_w13_kernel<NW>, lds, &big_lds);
+  if (e != hipSuccess) return e;
+  if (e0)
+    hipExtLaunchKernelGGL(fp8_w13_kernel<NW>, grid, dim3(NW * 64), lds, st, e0, e1, 0, x, H, I, K,
+                          P, slots, nslots, w13, w13_stride, s13, s13_stride, block_n, ncol, act);
+  else
+    hipLaunchKernelGGL(fp8_w13_kernel<NW>, grid, dim3(NW * 64), lds, st, x, H, I, K, P, slots,
+                       nslots, w13, w13_stride, s13, s13_stride, block_n, ncol, act);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+const char* fp8_unsupported(int H, int I, int K, int block_n, int block_k) {
+  if (block_k != kKB) return "block-FP8 kernels need block_k == 128";
+  if (block_n < 16 || block_n % 16) return "block-FP8 kernels need block_n a multiple of 16";
+  if (H < kKB || I < kKB || H % kKB || I % kKB)
+    return "block-FP8 kernels need H and I multiples of 128";
+  if (I % block_n)
+    return "block-FP8 experts need I a multiple of block_n (the w13 scale rows of gate and up)";
+  if (K < 1 || w2_lds(K, I, 1) > kMaxLds) return "top_k * I exceeds the w2 kernel's LDS";
+  return nullptr;
+}
+
+int experts_fp8(const void* x, int T, int H, int I, int K, const float* topk_w,
+                const int32_t* slots, int nslots, const void* w13, size_t w13_stride,
+                const float* s13, size_t s13_stride, const void* w2, size_t w2_stride,
+                const float* s2, size_t s2_stride, int block_n, void* act, void* out,
+                hipStream_t st, const StageEvents* ev) {
+  if (T == 0) return WISP_OK;
+  const int P = T * K;
+  const int NW = w13_waves(H);
+  const int ncol = min(T, 16);
+  const size_t l13 = w13_lds(NW, ncol);
+  const dim3 g13(I / 16, P);
+  hipEvent_t e0 = ev ? ev->ev[0] : nullptr, e1 = ev ? ev->ev[1] : nullptr;
+  const uint16_t* xb = (const uint16_t*)x;
+  const uint8_t* w13b = (const uint8_t*)w13;
+  uint16_t* actb = (uint16_t*)act;
+  if (NW == 4)
+    WISP_HIP_TRY(launch_w13<4>(g13, l13, st, e0, e1, xb, H, I, K, P, slots, nslots, w13b,
+                               w13_stride, s13, s13_stride, block_n, ncol, actb));
+  else
+    WISP_HIP_TRY(launch_w13<8>(g13, l13, st, e0, e1, xb, H, I, K, P, slots, nslots, w13b,
+                               w13_stride, s13, s13_stride, block_n, ncol, actb));
+
+  // waves per pair: split I's k-blocks when there are fewer pairs than waves
+  int WP = K >= kW2Waves ? 1 : kW2Waves / K;
+  while (WP > 1 && w2_lds(K, I, WP) > kMaxLds) WP >>= 1;
+  const size_t l2 = w2_lds(K, I, WP);
+  const dim3 g2(H / 16, T);
+  static bool big_lds2 = false;
+  WISP_HIP_TRY(allow_lds(fp8_w2_kernel<kW2Waves>, l2, &big_lds2));
+  if (ev && ev->ev[2])
+    hipExtLaunchKernelGGL(fp8_w2_kernel<kW2Waves>, g2, dim3(kW2Waves * 64), l2, st, ev->ev[2],
+                          ev->ev[3], 0, (const uint16_t*)act, H, I, K, topk_w, slots, nslots,
+                          (const uint8_t*)w2, w2_stride, s2, s2_stride, block_n, WP,
+                          (uint16_t*)out);
+  else
+    hipLaunchKernelGGL(fp8_w2_kernel<kW2Waves>, g2, dim3(kW2Waves * 64), l2, st,
+                       (const uint16_t*)act, H, I, K, topk_w, slots, nslots,
+                       (const uint8_t*)w2, w2_stride, s2, s2_stride, block_n, WP, (uint16_t*)out);
+  WISP_HIP_TRY(hipGetLastError());
+  return WISP_OK;
+}
+
+}  // namespace wisp
+
+extern "C" int wisp_quant_fp8_groups(const void* x, int dtype, int rows, int cols, int group,
+                                     uint8_t* q, float* scales, wisp_stream_t stream) {
+  using namespace wisp;
+  if (rows < 0 || cols < 0 || (rows > 0 && cols > 0 && (!x || !q || !scales)) ||
+      (dtype != WISP_F32 && dtype != WISP_BF16))
+    return WISP_ERR_INVALID;
+  if (group != kKB || cols % kKB || ((uintptr_t)x) % 16 || ((uintptr_t)q) % 8) {
+    wisp_set_last_error("group must be 128, cols a multiple of it, x 16-byte and q 8-byte "
+                        "aligned", "wisp_quant_fp8_groups");
+    return WISP_ERR_UNSUPPORTED;
+  }
+  const long jobs = (long)rows * (cols / kKB);
+  if (jobs == 0) return WISP_OK;
+  const dim3 grid((unsigned)((jobs + 15) / 16));
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == WISP_BF16)
+    hipLaunchKernelGGL(quant_groups_kernel<uint16_t>, grid, dim3(256), 0, st,
+                       (const uint16_t*)x, rows, cols, q, scales);
+  else
+    hipLaunchKernelGGL(quant_groups_kernel<float>, grid, dim3(256), 0, st, (const float*)x, rows,
+                       cols, q, scales);
+  WISP_HIP_TRY(hipGetLastError());
+  return WISP_OK;
+}
+
+extern "C" int wisp_moe_experts_fp8(const void* x, int T, int H, int I, int K,
+                                    const float* topk_w, const int32_t* slots, int nslots,
+                                    const void* w13, size_t w13_stride, const float* s13,
+                                    size_t s13_stride, const void* w2, size_t w2_stride,
+                                    const float* s2, size_t s2_stride, int block_n, int block_k,
+                                    void* act, void* out, void* work, size_t work_bytes,
+                                    int algo, wisp_stream_t stream) {
+  using namespace wisp;
+  (void)work;
+  (void)work_bytes;
+  if (T < 0 || K < 1 || K > kMaxTopK || nslots < 1 ||
+      (T > 0 && (!x || !topk_w || !slots || !w13 || !w2 || !s13 || !s2 || !act || !out)))
+    return WISP_ERR_INVALID;
+  if (algo != WISP_ALGO_AUTO && algo != WISP_ALGO_GEMV) {
+    wisp_set_last_error("block-FP8 experts have one kernel pair (WISP_ALGO_GEMV)",
+                        "wisp_moe_experts_fp8");
+    return WISP_ERR_UNSUPPORTED;
+  }
+  const char* why = fp8_unsupported(H, I, K, block_n, block_k);
+  if (!why && (w13_stride % 16 || w2_stride % 16 || ((uintptr_t)w13) % 16 ||
+               ((uintptr_t)w2) % 16 || ((uintptr_t)s13) % 4 || ((uintptr_t)s2) % 4 ||
+               (T > 0 && (((uintptr_t)x) % 16 || ((uintptr_t)act) % 16 ||
+                          ((uintptr_t)out) % 16))))
+    why = "weights, strides and buffers must be 16-byte aligned";
+  if (why) {
+    wisp_set_last_error(why, "wisp_moe_experts_fp8");
+    return WISP_ERR_UNSUPPORTED;
+  }
+  return experts_fp8(x, T, H, I, K, topk_w, slots, nslots, w13, w13_stride, s13, s13_stride, w2,
+                     w2_stride, s2, s2_stride, block_n, act, out, (hipStream_t)stream, nullptr);
+}

@@ -54,7 +54,7 @@ void wisp_set_last_error(const char* what, const char* where) {
 }
 
 extern "C" const char* wisp_last_error(void) { return g_last_error.c_str(); }
-extern "C" int wisp_abi_version(void) { return 1; }
+extern "C" int wisp_abi_version(void) { return 2; }
 
 namespace wisp {
 
@@ -77,6 +77,12 @@ int experts_mfma(const void* x, int T, int H, int I, int K, const float* topk_w,
                  const void* w2, size_t w2_stride, void* act, void* out, void* work,
                  size_t work_bytes, hipStream_t st, const StageEvents* ev);
 size_t mfma_work_bytes(int T, int K, int H, int nslots);
+int experts_fp8(const void* x, int T, int H, int I, int K, const float* topk_w,
+                const int32_t* slots, int nslots, const void* w13, size_t w13_stride,
+                const float* s13, size_t s13_stride, const void* w2, size_t w2_stride,
+                const float* s2, size_t s2_stride, int block_n, void* act, void* out,
+                hipStream_t st, const StageEvents* ev);
+const char* fp8_unsupported(int H, int I, int K, int block_n, int block_k);
 int launch_prefetch(const int32_t* predicted, const int32_t* n_pred_ptr, int n_pred, int ordered,
                     int count_pred, const int32_t* last_ids, int n_last, int E, int cap,
                     int max_pred, int32_t* map, int32_t* s2e, int64_t* tick, int64_t* ctr,
@@ -95,6 +101,7 @@ constexpr int kMfmaMinTokens = 16;
 // shape and token count, never on the grouping or the slots, so paged and
 // resident runs of one batch use one kernel.
 int auto_algo(int dtype, int H, int I, int T) {
+  if (dtype == WISP_FP8_E4M3) return WISP_ALGO_GEMV;
   return dtype == WISP_BF16 && mfma_supported(H, I) && T >= kMfmaMinTokens ? WISP_ALGO_MFMA
                                                                           : WISP_ALGO_GEMV;
 }
@@ -106,7 +113,21 @@ constexpr int kCopyStreams = 2;
 constexpr int kProfRing = 512;
 constexpr int kPinRing = 64;
 
-size_t elem_size(int dtype) { return dtype == WISP_F32 ? 4 : 2; }
+// Bytes of one weight element, and of one activation element (x, act, out).
+size_t elem_size(int dtype) { return dtype == WISP_F32 ? 4 : dtype == WISP_FP8_E4M3 ? 1 : 2; }
+size_t act_size(int dtype) { return dtype == WISP_F32 ? 4 : 2; }
+
+// One tensor of an expert as the page-in moves it (see PageInPlane): host
+// master address (and its device mapping, for the copy kernel), scratch
+// address, byte strides and bytes per expert.
+struct Plane {
+  const char* host = nullptr;
+  const char* dev = nullptr;
+  size_t m_stride = 0;
+  char* d = nullptr;
+  size_t d_stride = 0;
+  size_t bytes = 0;
+};
 
 // One timed kernel launch (dispatch timestamps).
 struct ProfLaunch {
@@ -125,10 +146,13 @@ struct PinLaunch {
 
 struct Layer {
   wisp_layer_desc d;
+  bool fp8 = false;
+  // the tensors one page-in moves per expert, merged where they are adjacent
+  int nplanes = 0;
+  Plane planes[kMaxPlanes];
+  size_t expert_bytes = 0;  // weight (and scale) bytes of one expert
   // kernel page-in (engine WISP_PAGEIN_KERNEL and eligible masters)
   bool kpin = false;
-  const char* m13_dev = nullptr;  // device addresses of the pinned masters
-  const char* m2_dev = nullptr;
   int32_t* hist = nullptr;        // pinned host [kPinRing]
   int32_t* hist_dev = nullptr;
   int pin_next = 0;
@@ -145,8 +169,7 @@ struct Layer {
   bool pin_pending = false;
   double pin_bytes_pending = 0;
   double pin_ms_total = 0, pin_bytes_total = 0;
-  bool fused_slab = false;
-  size_t es = 2;
+  size_t es = 2;  // bytes of one weight element
   bool profile = false;
   int prof_next = 0;
   ProfLaunch prof[kProfRing];
@@ -189,9 +212,6 @@ __global__ void identity_kernel(int32_t* map, int32_t* s2e, int E) {
 // Copies of `n` loaded (expert, slot) pairs on `st`, or alternating over the
 // side streams so one engine's per-copy setup overlaps the other's transfer.
 int issue_copies(Layer& L, const int32_t* pairs, int n, double* bytes, hipStream_t st) {
-  const size_t es = L.es;
-  const size_t w13_bytes = L.d.w13_elems * es;
-  const size_t w2_bytes = L.d.w2_elems * es;
   for (int j = 0; j < n; ++j) {
     const int e = pairs[2 * j], s = pairs[2 * j + 1];
     if (e < 0 || e >= L.d.num_experts || s < 0 || s >= L.d.cap) {
@@ -199,19 +219,52 @@ int issue_copies(Layer& L, const int32_t* pairs, int n, double* bytes, hipStream
       return WISP_ERR_INVALID;
     }
     hipStream_t cs = L.nstreams ? L.copy[j % L.nstreams] : st;
-    char* d13 = (char*)L.d.scratch_w13 + (size_t)s * L.d.scratch_w13_stride * es;
-    const char* m13 = (const char*)L.d.master_w13 + (size_t)e * L.d.master_w13_stride * es;
-    if (L.fused_slab) {
-      WISP_HIP_TRY(hipMemcpyAsync(d13, m13, w13_bytes + w2_bytes, hipMemcpyHostToDevice, cs));
-    } else {
-      char* d2 = (char*)L.d.scratch_w2 + (size_t)s * L.d.scratch_w2_stride * es;
-      const char* m2 = (const char*)L.d.master_w2 + (size_t)e * L.d.master_w2_stride * es;
-      WISP_HIP_TRY(hipMemcpyAsync(d13, m13, w13_bytes, hipMemcpyHostToDevice, cs));
-      WISP_HIP_TRY(hipMemcpyAsync(d2, m2, w2_bytes, hipMemcpyHostToDevice, cs));
+    for (int q = 0; q < L.nplanes; ++q) {
+      const Plane& p = L.planes[q];
+      WISP_HIP_TRY(hipMemcpyAsync(p.d + (size_t)s * p.d_stride, p.host + (size_t)e * p.m_stride,
+                                  p.bytes, hipMemcpyHostToDevice, cs));
     }
-    *bytes += (double)(w13_bytes + w2_bytes);
+    *bytes += (double)L.expert_bytes;
   }
   return WISP_OK;
+}
+
+// The layer's tensors as page-in planes: w13, w2 and (block-FP8) the two
+// scale tensors, merged when one starts where the previous ends in both the
+// master and the scratch with equal strides, so a [w13 | w2 | s13 | s2] slab
+// per expert moves as one copy.  A single merged plane is padded to 16 bytes
+// when both strides leave room, so the copy kernel can move it.
+void build_planes(Layer& L) {
+  const wisp_layer_desc& d = L.d;
+  const size_t wb = L.es;
+  Plane raw[kMaxPlanes];
+  int n = 0;
+  raw[n++] = {(const char*)d.master_w13, nullptr, d.master_w13_stride * wb,
+              (char*)d.scratch_w13, d.scratch_w13_stride * wb, d.w13_elems * wb};
+  raw[n++] = {(const char*)d.master_w2, nullptr, d.master_w2_stride * wb, (char*)d.scratch_w2,
+              d.scratch_w2_stride * wb, d.w2_elems * wb};
+  if (L.fp8) {
+    raw[n++] = {(const char*)d.master_s13, nullptr, d.master_s13_stride * 4,
+                (char*)d.scratch_s13, d.scratch_s13_stride * 4, d.s13_elems * 4};
+    raw[n++] = {(const char*)d.master_s2, nullptr, d.master_s2_stride * 4, (char*)d.scratch_s2,
+                d.scratch_s2_stride * 4, d.s2_elems * 4};
+  }
+  L.expert_bytes = 0;
+  for (int i = 0; i < n; ++i) L.expert_bytes += raw[i].bytes;
+  L.nplanes = 0;
+  for (int i = 0; i < n; ++i) {
+    Plane* cur = L.nplanes ? &L.planes[L.nplanes - 1] : nullptr;
+    if (cur && raw[i].host == cur->host + cur->bytes && raw[i].d == cur->d + cur->bytes &&
+        raw[i].m_stride == cur->m_stride && raw[i].d_stride == cur->d_stride)
+      cur->bytes += raw[i].bytes;
+    else
+      L.planes[L.nplanes++] = raw[i];
+  }
+  if (L.nplanes == 1) {
+    Plane& p = L.planes[0];
+    const size_t padded = (p.bytes + 15) & ~(size_t)15;
+    if (padded <= p.m_stride && padded <= p.d_stride) p.bytes = padded;
+  }
 }
 
 void harvest_pagein_timing(Layer& L) {
@@ -226,8 +279,6 @@ void harvest_pagein_timing(Layer& L) {
   L.pin_bytes_pending = 0;
 }
 
-size_t expert_bytes(const Layer& L) { return (L.d.w13_elems + L.d.w2_elems) * L.es; }
-
 void harvest_pin(Layer& L, int i) {
   PinLaunch& p = L.pin[i];
   if (!p.pending) return;
@@ -237,7 +288,7 @@ void harvest_pin(Layer& L, int i) {
     const int n = ((volatile int32_t*)L.hist)[i];
     if (n > 0) {
       L.pin_ms_total += ms;
-      L.pin_bytes_total += (double)n * (double)expert_bytes(L);
+      L.pin_bytes_total += (double)n * (double)L.expert_bytes;
     }
   }
   p.pending = false;
@@ -266,16 +317,11 @@ int page_in_kernel(Layer& L, const int32_t* loads, const int32_t* count, int n, 
   a.n = n;
   a.num_experts = d.num_experts;
   a.cap = d.cap;
-  a.m13 = L.m13_dev;
-  a.m13_stride = d.master_w13_stride * L.es;
-  a.m2 = L.fused_slab ? nullptr : L.m2_dev;
-  a.m2_stride = d.master_w2_stride * L.es;
-  a.s13 = (char*)d.scratch_w13;
-  a.s13_stride = d.scratch_w13_stride * L.es;
-  a.s2 = (char*)d.scratch_w2;
-  a.s2_stride = d.scratch_w2_stride * L.es;
-  a.b13 = L.fused_slab ? expert_bytes(L) : d.w13_elems * L.es;
-  a.b2 = d.w2_elems * L.es;
+  a.nplanes = L.nplanes;
+  for (int q = 0; q < L.nplanes; ++q) {
+    const Plane& pl = L.planes[q];
+    a.p[q] = {pl.dev, pl.m_stride, pl.d, pl.d_stride, pl.bytes};
+  }
   a.hist = L.hist_dev + i;
   int rc = launch_pagein(a, st, p.start, p.stop);
   if (rc == WISP_OK) p.pending = true;
@@ -286,18 +332,17 @@ int page_in_kernel(Layer& L, const int32_t* loads, const int32_t* count, int n, 
 // host memory and every copy is a whole number of aligned 16-byte units.
 void setup_kernel_pagein(Layer& L) {
   const wisp_layer_desc& d = L.d;
-  const size_t es = L.es, b13 = d.w13_elems * es, b2 = d.w2_elems * es;
-  const size_t s13 = d.master_w13_stride * es, s2 = d.master_w2_stride * es;
+  if (d.pagein_engine != WISP_PAGEIN_KERNEL) return;
   const size_t last = (size_t)(d.num_experts - 1);
-  const bool aligned = b13 % 16 == 0 && b2 % 16 == 0 && s13 % 16 == 0 && s2 % 16 == 0 &&
-                       (d.scratch_w13_stride * es) % 16 == 0 &&
-                       (d.scratch_w2_stride * es) % 16 == 0 &&
-                       (uintptr_t)d.master_w13 % 16 == 0 && (uintptr_t)d.master_w2 % 16 == 0 &&
-                       (uintptr_t)d.scratch_w13 % 16 == 0 && (uintptr_t)d.scratch_w2 % 16 == 0;
-  if (d.pagein_engine != WISP_PAGEIN_KERNEL || !aligned) return;
-  const char* m13 = mapped_host_range(d.master_w13, last * s13 + (L.fused_slab ? b13 + b2 : b13));
-  const char* m2 = mapped_host_range(d.master_w2, last * s2 + b2);
-  if (!m13 || !m2) return;
+  const char* dev[kMaxPlanes] = {};
+  for (int q = 0; q < L.nplanes; ++q) {
+    const Plane& p = L.planes[q];
+    if (p.bytes % 16 || p.m_stride % 16 || p.d_stride % 16 || (uintptr_t)p.host % 16 ||
+        (uintptr_t)p.d % 16)
+      return;
+    dev[q] = mapped_host_range(p.host, last * p.m_stride + p.bytes);
+    if (!dev[q]) return;
+  }
   void* h = nullptr;
   if (hipHostMalloc(&h, kPinRing * sizeof(int32_t), hipHostMallocMapped) != hipSuccess) {
     (void)hipGetLastError();
@@ -319,8 +364,7 @@ void setup_kernel_pagein(Layer& L) {
   memset(h, 0, kPinRing * sizeof(int32_t));
   L.hist = (int32_t*)h;
   L.hist_dev = (int32_t*)hd;
-  L.m13_dev = m13;
-  L.m2_dev = m2;
+  for (int q = 0; q < L.nplanes; ++q) L.planes[q].dev = dev[q];
   L.kpin = true;
 }
 
@@ -383,6 +427,18 @@ int w2(Layer& L, const void* act, int T, int K, const float* w, const int32_t* s
 int experts(Layer& L, const void* x, int T, int K, const float* w, const int32_t* slots,
             void* act, void* out, int algo, const wisp_workspace* ws, hipStream_t st) {
   const wisp_layer_desc& d = L.d;
+  if (L.fp8) {
+    ProfLaunch* p13 = prof_begin(L, 0);
+    ProfLaunch* p2 = prof_begin(L, 1);
+    StageEvents ev = {{p13 ? p13->start : nullptr, p13 ? p13->stop : nullptr,
+                       p2 ? p2->start : nullptr, p2 ? p2->stop : nullptr}};
+    int rc = experts_fp8(x, T, d.hidden, d.inter, K, w, slots, d.cap, d.scratch_w13,
+                         d.scratch_w13_stride, d.scratch_s13, d.scratch_s13_stride, d.scratch_w2,
+                         d.scratch_w2_stride, d.scratch_s2, d.scratch_s2_stride, d.block_n, act,
+                         out, st, (p13 && p2) ? &ev : nullptr);
+    if (rc == WISP_OK && p13 && p2) p13->pending = p2->pending = true;
+    return rc;
+  }
   if (algo == WISP_ALGO_MFMA) {
     ProfLaunch* p13 = prof_begin(L, 0);
     ProfLaunch* p2 = prof_begin(L, 1);
@@ -404,7 +460,7 @@ int choose_algo(const Layer& L, int algo, int T) {
   const wisp_layer_desc& d = L.d;
   if (algo == WISP_ALGO_AUTO) return auto_algo(d.dtype, d.hidden, d.inter, T);
   if (algo == WISP_ALGO_MFMA && (d.dtype != WISP_BF16 || !mfma_supported(d.hidden, d.inter)))
-    return -1;
+    return -1;  // block-FP8 experts have one kernel pair, selected as GEMV
   if (algo != WISP_ALGO_GEMV && algo != WISP_ALGO_MFMA) return -1;
   return algo;
 }
@@ -414,7 +470,7 @@ int run_groups(Layer& L, const int32_t* rec, const int32_t* loads, int T, int K,
                bool compute, const void* x, const float* topk_w, const int32_t* slots, void* act,
                void* out, int algo, const wisp_workspace* ws, hipStream_t st) {
   const RecordLayout RL(T, K);
-  const size_t row = (size_t)L.d.hidden * L.es;
+  const size_t row = (size_t)L.d.hidden * act_size(L.d.dtype);
   int last_gemm = -1;
   for (int g = 0; g < ngroups; ++g) {
     const int32_t* G = rec + RL.group_base(g);
@@ -461,15 +517,32 @@ int check_ws(const wisp_workspace* ws, int T, int K) {
 
 using wisp::Layer;
 
+namespace wisp {
+// Block-FP8 fields of a descriptor: scale shapes consistent with the MLP
+// shape and the block, scale buffers present.
+static bool fp8_desc_ok(const wisp_layer_desc& d) {
+  if (d.block_n < 1 || d.block_k < 1 || !d.scratch_s13 || !d.scratch_s2 || !d.master_s13 ||
+      !d.master_s2 || d.s13_elems < 1 || d.s2_elems < 1 ||
+      d.scratch_s13_stride < d.s13_elems || d.scratch_s2_stride < d.s2_elems ||
+      d.master_s13_stride < d.s13_elems || d.master_s2_stride < d.s2_elems)
+    return false;
+  if (d.hidden == 0) return true;
+  const size_t H = d.hidden, I = d.inter, bn = d.block_n, bk = d.block_k;
+  return d.s13_elems == 2 * ((I + bn - 1) / bn) * ((H + bk - 1) / bk) &&
+         d.s2_elems == ((H + bn - 1) / bn) * ((I + bk - 1) / bk);
+}
+}  // namespace wisp
+
 extern "C" int wisp_layer_create(const wisp_layer_desc* desc, void** handle) {
   using namespace wisp;
   if (!desc || !handle) return WISP_ERR_INVALID;
   const wisp_layer_desc& d = *desc;
-  if (d.num_experts < 1 || d.num_experts > kMaxExperts || d.cap < 1 || d.cap > d.num_experts ||
+  if (d.num_experts < 1 || d.num_experts > kMaxExperts || d.cap < 1 || d.cap > kMaxExperts ||
       d.hidden < 0 || d.inter < 0 || d.w13_elems < 1 || d.w2_elems < 1 ||
       (d.hidden > 0 && (d.w13_elems != (size_t)2 * d.inter * d.hidden ||
                         d.w2_elems != (size_t)d.hidden * d.inter)) ||
-      (d.dtype != WISP_F32 && d.dtype != WISP_BF16) ||
+      (d.dtype != WISP_F32 && d.dtype != WISP_BF16 && d.dtype != WISP_FP8_E4M3) ||
+      (d.dtype == WISP_FP8_E4M3 && !fp8_desc_ok(d)) ||
       (d.mode != WISP_MODE_PAGED && d.mode != WISP_MODE_RESIDENT) || !d.scratch_w13 ||
       !d.scratch_w2 || !d.master_w13 || !d.master_w2 || !d.expert_map || !d.slot_to_expert ||
       !d.lru_tick || !d.counters || d.scratch_w13_stride < d.w13_elems ||
@@ -481,16 +554,12 @@ extern "C" int wisp_layer_create(const wisp_layer_desc* desc, void** handle) {
     wisp_set_last_error("invalid layer descriptor", "wisp_layer_create");
     return WISP_ERR_INVALID;
   }
-  const size_t es = elem_size(d.dtype);
   Layer* L = new Layer();
   L->d = d;
-  L->es = es;
+  L->fp8 = d.dtype == WISP_FP8_E4M3;
+  L->es = elem_size(d.dtype);
   L->nstreams = d.pagein_streams;
-  const size_t w13_elems = d.w13_elems;
-  L->fused_slab = d.master_w13_stride == d.master_w2_stride &&
-                  d.scratch_w13_stride == d.scratch_w2_stride &&
-                  (const char*)d.master_w2 == (const char*)d.master_w13 + w13_elems * es &&
-                  (const char*)d.scratch_w2 == (const char*)d.scratch_w13 + w13_elems * es;
+  build_planes(*L);
   hipError_t e = hipEventCreateWithFlags(&L->ev_decided, hipEventDisableTiming);
   for (int c = 0; c < kCopyStreams && e == hipSuccess; ++c) {
     e = hipStreamCreateWithFlags(&L->copy[c], hipStreamNonBlocking);
@@ -549,20 +618,32 @@ extern "C" int wisp_layer_set_scratch(void* handle, void* scratch_w13, void* scr
                                       int32_t* slot_to_expert, int64_t* lru_tick) {
   using namespace wisp;
   Layer* L = (Layer*)handle;
-  if (!L || !scratch_w13 || !scratch_w2 || cap < 1 || cap > L->d.num_experts ||
+  if (!L || !scratch_w13 || !scratch_w2 || cap < 1 || cap > kMaxExperts ||
       !slot_to_expert || !lru_tick)
     return WISP_ERR_INVALID;
+  if (L->fp8) {
+    wisp_set_last_error("block-FP8 layers are not resized", "wisp_layer_set_scratch");
+    return WISP_ERR_UNSUPPORTED;
+  }
   for (int c = 0; c < kCopyStreams; ++c) (void)hipStreamSynchronize(L->copy[c]);
   harvest_pagein_timing(*L);
   for (int i = 0; i < kPinRing; ++i) harvest_pin(*L, i);
-  const size_t es = L->es, w13_elems = L->d.w13_elems;
   L->d.scratch_w13 = scratch_w13;
   L->d.scratch_w2 = scratch_w2;
-  L->fused_slab = L->d.master_w13_stride == L->d.master_w2_stride &&
-                  L->d.scratch_w13_stride == L->d.scratch_w2_stride &&
-                  (const char*)L->d.master_w2 == (const char*)L->d.master_w13 + w13_elems * es &&
-                  (const char*)scratch_w2 == (const char*)scratch_w13 + w13_elems * es;
-  if (((uintptr_t)scratch_w13) % 16 || ((uintptr_t)scratch_w2) % 16) L->kpin = false;
+  // the masters (and their device mappings) are unchanged; only the scratch
+  // side of each plane moves
+  const char* dev[kMaxPlanes];
+  for (int q = 0; q < L->nplanes; ++q) dev[q] = L->planes[q].dev;
+  const int old_n = L->nplanes;
+  build_planes(*L);
+  if (L->nplanes != old_n) {
+    L->kpin = false;
+  } else {
+    for (int q = 0; q < L->nplanes; ++q) {
+      L->planes[q].dev = dev[q];
+      if (((uintptr_t)L->planes[q].d) % 16 || L->planes[q].d_stride % 16) L->kpin = false;
+    }
+  }
   L->d.cap = cap;
   L->d.slot_to_expert = slot_to_expert;
   L->d.lru_tick = lru_tick;
@@ -583,8 +664,9 @@ extern "C" int wisp_layer_forward(void* handle, const void* x, const void* logit
   if (rc != WISP_OK) return rc;
   hipStream_t st = (hipStream_t)stream;
   const wisp_layer_desc& d = L->d;
-  const size_t es = L->es;
+  const size_t es = L->es, as = act_size(d.dtype);
   if (d.hidden < 1 || d.inter < 1 || (d.hidden * es) % 16 || (d.inter * es) % 16 ||
+      (d.hidden * as) % 16 || (d.inter * as) % 16 ||
       (d.scratch_w13_stride * es) % 16 || (d.scratch_w2_stride * es) % 16 ||
       ((uintptr_t)d.scratch_w13) % 16 || ((uintptr_t)d.scratch_w2) % 16 ||
       (T > 0 && (((uintptr_t)x) % 16 || ((uintptr_t)out) % 16))) {
@@ -592,6 +674,15 @@ extern "C" int wisp_layer_forward(void* handle, const void* x, const void* logit
                         "be multiples of 16 bytes, buffers 16-byte aligned)",
                         "wisp_layer_forward");
     return WISP_ERR_UNSUPPORTED;
+  }
+  if (L->fp8) {
+    const char* why = fp8_unsupported(d.hidden, d.inter, K, d.block_n, d.block_k);
+    if (!why && (((uintptr_t)d.scratch_s13) % 16 || ((uintptr_t)d.scratch_s2) % 16))
+      why = "scale scratch must be 16-byte aligned";
+    if (why) {
+      wisp_set_last_error(why, "wisp_layer_forward");
+      return WISP_ERR_UNSUPPORTED;
+    }
   }
   const int a = choose_algo(*L, algo, T);
   if (a < 0) {
@@ -634,7 +725,7 @@ extern "C" int wisp_layer_forward(void* handle, const void* x, const void* logit
   }
   WISP_HIP_TRY(hipEventRecord(L->ev_decided, st));
 
-  const bool speculate = a == WISP_ALGO_GEMV && one_group;
+  const bool speculate = a == WISP_ALGO_GEMV && one_group && !L->fp8;
   ProfLaunch* spec_w2 = nullptr;
   if (speculate) {
     rc = w13(*L, x, T, K, ws->slots, ws->act, st, ws->flags + 1, 0);

@@ -7,25 +7,32 @@ namespace wisp {
 
 constexpr int kPageInBlocks = 64;
 
+// One tensor of an expert that moves as a unit: expert e's bytes
+// [m + e*m_stride, +bytes) of the pinned master (device address of its
+// mapping) go to slot s at [d + s*d_stride, +bytes) of the HBM scratch.
+// Strides and sizes are in bytes, all multiples of 16.
+struct PageInPlane {
+  const char* m;
+  size_t m_stride;
+  char* d;
+  size_t d_stride;
+  size_t bytes;
+};
+
+// At most four tensors per expert: w13, w2 and, for block-FP8 experts,
+// their two scale tensors.  A layer whose tensors sit back to back in one
+// slab per expert (in master and scratch alike) copies them as one plane.
+constexpr int kMaxPlanes = 4;
+
 // One page-in launch.  The load list holds (expert, slot) pairs; its length
 // is *count when count is non-null (written by the pager kernel), else n.
-// m13/m2 are device addresses of the pinned masters (m2 null: each expert's
-// w13 and w2 are one contiguous range of b13 bytes in both master and
-// scratch).  Strides and sizes are in bytes, all multiples of 16.
 struct PageInArgs {
   const int32_t* loads;
   const int32_t* count;
   int n;
   int num_experts, cap;
-  const char* m13;
-  size_t m13_stride;
-  const char* m2;
-  size_t m2_stride;
-  char* s13;
-  size_t s13_stride;
-  char* s2;
-  size_t s2_stride;
-  size_t b13, b2;
+  int nplanes;
+  PageInPlane p[kMaxPlanes];
   int32_t* hist;  // device address of a pinned host word that receives n, or null
 };
 

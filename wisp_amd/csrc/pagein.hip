@@ -4,7 +4,8 @@
 //
 // Replaces the per-miss copies of ensure_resident
 // (src/wisp/integrations/vllm/fused_moe.py:338-354: scratch_w13[slot].copy_,
-// scratch_w2[slot].copy_ on the copy stream).  The load list comes from the
+// scratch_w2[slot].copy_ on the copy stream; for block-FP8 experts also the
+// two scale tensors, fused_moe_fp8.py:135-141).  The load list comes from the
 // pager kernel in device memory, so a decode call needs no host round trip
 // between the decision and the copy: the layer enqueues pager, page-in, w13
 // and w2 back to back on one stream.  64 blocks of 16-byte loads keep about
@@ -52,11 +53,11 @@ __global__ __launch_bounds__(256) void pagein_kernel(PageInArgs a) {
   for (int j = 0; j < n; ++j) {
     const int e = a.loads[2 * j], s = a.loads[2 * j + 1];
     if (e < 0 || e >= a.num_experts || s < 0 || s >= a.cap) continue;
-    copy_range(a.m13 + (size_t)e * a.m13_stride, a.s13 + (size_t)s * a.s13_stride, a.b13,
-               blockIdx.x, gridDim.x);
-    if (a.m2)
-      copy_range(a.m2 + (size_t)e * a.m2_stride, a.s2 + (size_t)s * a.s2_stride, a.b2, blockIdx.x,
-                 gridDim.x);
+    for (int q = 0; q < a.nplanes; ++q) {
+      const PageInPlane& pl = a.p[q];
+      copy_range(pl.m + (size_t)e * pl.m_stride, pl.d + (size_t)s * pl.d_stride, pl.bytes,
+                 blockIdx.x, gridDim.x);
+    }
   }
 }
 

@@ -116,7 +116,7 @@ int ensure_group_host(PagerView& st, const std::vector<int32_t>& needed, HostRec
 int pager_decide_host(PagerView st, const int32_t* ids, int T, int K, int single_group,
                       int32_t* slots, int32_t* rec, int rec_words) {
   RecordLayout L(T, K);
-  if (T < 0 || K < 1 || st.E < 1 || st.E > kMaxExperts || st.cap < 1 || st.cap > st.E ||
+  if (T < 0 || K < 1 || st.E < 1 || st.E > kMaxExperts || st.cap < 1 || st.cap > kMaxExperts ||
       rec_words < L.words())
     return WISP_ERR_INVALID;
   for (int w = 0; w < 8; ++w) rec[w] = 0;
@@ -492,7 +492,7 @@ int launch_pager(const int32_t* ids, const void* logits, int logits_dtype, int r
                  int32_t* slots, int32_t* flags, int32_t* loads, int32_t* rec, int rec_words,
                  hipStream_t stream) {
   RecordLayout L(T, K);
-  if (T < 0 || K < 1 || K > kMaxTopK || E < 1 || E > kMaxExperts || cap < 1 || cap > E ||
+  if (T < 0 || K < 1 || K > kMaxTopK || E < 1 || E > kMaxExperts || cap < 1 || cap > kMaxExperts ||
       rec_words < L.words() || !map || !s2e || !tick || !ctr || !rec ||
       (T > 0 && !ids && !logits) ||
       (logits && (T > kFusedRouteTokens || !topk_w || !topk_ids ||

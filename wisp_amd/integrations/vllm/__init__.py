@@ -8,5 +8,6 @@ Same import surface as the reference's ``wisp.integrations.vllm``
     install_wisp_moe()   # before the model is built
 """
 from .fused_moe import install_wisp_moe, is_installed
+from .fused_moe_fp8 import install_wisp_fp8, is_fp8_installed
 
-__all__ = ["install_wisp_moe", "is_installed"]
+__all__ = ["install_wisp_moe", "is_installed", "install_wisp_fp8", "is_fp8_installed"]

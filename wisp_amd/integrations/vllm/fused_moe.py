@@ -798,6 +798,13 @@ def install_wisp_moe(*, mode: str | None = None, cap_experts: int | None = None)
     setattr(cls, _PATCHED_FLAG, True)
     logger.info("wisp: patched %s.%s (mode=%s cap_experts=%s)", cls.__module__, cls.__name__,
                 _WISP_RUNTIME_CONFIG["mode"], cap_experts)
+    # Also page the block-FP8 MoE method, best effort, as the reference does
+    # (1297-1303): a failure there must not break the unquantised path.
+    try:
+        from .fused_moe_fp8 import install_wisp_fp8
+        install_wisp_fp8()
+    except Exception as e:  # pragma: no cover - depends on the host's vLLM
+        logger.warning("wisp: FP8 MoE patch not applied (%s)", e)
     return True
 
 

@@ -14,6 +14,10 @@ batch  Qwen3 layer, 512-token prefill + bs=32 x128  2048    768  128   8    32
 mixtral Mixtral-8x7B layer, 256 steps bs=1 / bs=16  4096  14336    8   2     4
 =====  ==========================================  ====  =====  ===  ==  ====
 
+``fp8_layer`` makes the block-FP8 twin of any of them (e4m3fn weights with
+float32 [128, 128] block scales, one ``[w13 | w2 | s13 | s2]`` slab per
+expert); ``qwen3_fp8_decode`` is the Qwen3-30B-A3B-FP8 decode layer.
+
 Expert weights are stored one contiguous *slab* per expert:
 ``[w13 (2I x H) | w2 (H x I)]`` row-major, so one copy moves one expert.
 ``slab_views`` returns the ``w13 [E, 2I, H]`` / ``w2 [E, H, I]`` views the
@@ -218,6 +222,88 @@ def stack_routing(seed: int = 0, layers: int = 48, tokens: int = 512, experts: i
             out[L, t] = lg
             prev = drawn
     return out
+
+
+# ---------------------------------------------------------------------------
+# Block-FP8 layers: float8_e4m3fn weights with float32 [128, 128] block scales
+# ---------------------------------------------------------------------------
+
+FP8_BLOCK = (128, 128)
+
+
+def block_quant_fp8(w: torch.Tensor, block=FP8_BLOCK):
+    """Dense ``[N, Kd]`` float32 -> ``(e4m3fn codes, float32 scales)`` the way
+    block-FP8 checkpoints are made: per block ``s = absmax / 448``,
+    ``q = e4m3fn(w / s)`` (N and Kd multiples of the block)."""
+    bn, bk = block
+    N, Kd = w.shape
+    blocks = w.reshape(N // bn, bn, Kd // bk, bk)
+    s = (blocks.abs().amax(dim=(1, 3)).clamp_min(1e-12) / 448.0).to(torch.float32)
+    q = (blocks / s[:, None, :, None]).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+    return q.reshape(N, Kd), s
+
+
+@dataclass
+class Fp8Workload:
+    name: str
+    shape: LayerShape        # dtype: the activations' (bfloat16)
+    block: tuple
+    x: torch.Tensor          # [steps, T, H] bfloat16
+    logits: torch.Tensor     # [steps, T, E] float32
+    slabs: torch.Tensor      # [E, slab] uint8: [w13 | w2 | s13 | s2] per expert
+
+    @property
+    def steps(self) -> int:
+        return self.x.shape[0]
+
+    @property
+    def layout(self):
+        from .integrations.vllm.fused_moe_fp8 import Fp8SlabLayout
+        return Fp8SlabLayout(self.shape.hidden, self.shape.inter, self.block)
+
+    def views(self):
+        """``(w13, w2, s13, s2)`` views of the slabs."""
+        return self.layout.views(self.slabs)
+
+    @property
+    def expert_bytes(self) -> int:
+        """Weight and scale bytes of one expert (what one miss moves)."""
+        lay = self.layout
+        return lay.w13_bytes + lay.w2_bytes + 4 * (lay.s13_elems + lay.s2_elems)
+
+
+def fill_fp8_experts(views, shape: LayerShape, gen: torch.Generator, block=FP8_BLOCK,
+                     scale: float = 0.02) -> None:
+    """W13 for every expert, then W2 for every expert, each ~ N(0, scale^2)
+    in float32, block-quantised to e4m3fn with their scales."""
+    w13, w2, s13, s2 = views
+    for e in range(w13.shape[0]):
+        q, s = block_quant_fp8(torch.randn(w13.shape[1:], generator=gen) * scale, block)
+        w13[e].copy_(q)
+        s13[e].copy_(s)
+    for e in range(w2.shape[0]):
+        q, s = block_quant_fp8(torch.randn(w2.shape[1:], generator=gen) * scale, block)
+        w2[e].copy_(q)
+        s2[e].copy_(s)
+
+
+def fp8_layer(base: Workload, pin: bool = False, seed: int = 7, experts: int | None = None,
+              block=FP8_BLOCK) -> Fp8Workload:
+    """The block-FP8 twin of a bf16 workload: same activations and router
+    logits, weights drawn from their own seeded generator and quantised."""
+    from .integrations.vllm.fused_moe_fp8 import fp8_slab_masters
+    sh = base.shape
+    E = sh.experts if experts is None else experts
+    buf, w13, w2, s13, s2 = fp8_slab_masters(E, sh.hidden, sh.inter, block, pin=pin)
+    fill_fp8_experts((w13, w2, s13, s2), sh, torch.Generator().manual_seed(seed), block)
+    fsh = LayerShape(sh.hidden, sh.inter, sh.experts, sh.top_k, sh.cap, torch.bfloat16)
+    x = base.x.to(torch.bfloat16)
+    return Fp8Workload(base.name + "-fp8", fsh, tuple(block), x, base.logits, buf)
+
+
+def qwen3_fp8_decode(seed: int = 0, steps: int = 256, pin: bool = False) -> Fp8Workload:
+    """Qwen3-30B-A3B-FP8 layer at bs=1 (the routing trace of ``qwen3_decode``)."""
+    return fp8_layer(qwen3_decode(seed, steps, weights=False), pin=pin)
 
 
 def algorithmic_bytes(shape: LayerShape, unique_experts: int) -> int:
