@@ -25,6 +25,8 @@ default line above is the one the benchmark is quoted on):
   batch32   bs=32 decode, Qwen3 layer, cap=32 paged and resident
   mixtral   Mixtral-8x7B layer, cap=4, bs=1 and bs=16 decode
   stack     48 Qwen3 layers, cap=24 each, bs=1 decode through the stack
+  fp8       the default decode line on the Qwen3-30B-A3B-FP8 layer (e4m3fn
+            weights with [128, 128] float32 block scales, w8a8)
 """
 from __future__ import annotations
 
@@ -360,6 +362,125 @@ def bench_stack(args) -> dict:
                                                      2))
 
 
+def _calibration_copy(dev) -> None:
+    """A plain 256 MiB device copy: the calibration dispatch for the
+    profiler's HBM byte counters (FETCH_SIZE / WRITE_SIZE of a copy of known
+    size)."""
+    import torch
+
+    from wisp_amd import _lib
+    cal = torch.empty(2, 256 << 20, dtype=torch.uint8, device=dev)
+    _lib.check(_lib.lib().wisp_probe_hbm_copy(cal[1].data_ptr(), cal[0].data_ptr(), 256 << 20,
+                                              _lib.stream_handle()), "hbm copy")
+    torch.cuda.synchronize()
+    del cal
+
+
+def cpu_baseline_fp8(routes, views, seconds: float, warm: int = 2) -> dict:
+    """Oracle routing + LRU pager + the oracle's block-FP8 experts (numpy,
+    float64 dots) over the decode routing sequences, time-bounded."""
+    import numpy as np
+    import torch
+
+    from oracle.fp8 import moe_forward_fp8
+    from oracle.moe import route
+    from oracle.pager import PagerOracle
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    w13, w2, s13, s2 = views
+    K = routes[0].shape.top_k
+    pagers = [PagerOracle(wl.shape.experts, wl.shape.cap) for wl in routes]
+    R, per = len(routes), routes[0].steps
+    n = timed = 0
+    spent = 0.0
+    while spent < seconds and n < 8 * R * per:
+        r, pos = n % R, (n // R) % per
+        t0 = time.perf_counter()
+        w, ids = route(routes[r].logits[pos], K)
+        pagers[r].forward(ids.tolist())
+        moe_forward_fp8(routes[r].x[pos], w.astype(np.float32), ids, w13, w2, s13, s2)
+        if n >= warm:
+            spent += time.perf_counter() - t0
+            timed += 1
+        n += 1
+    return {"value": round(timed / spent, 2), "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": f"{timed} bs=1 decode steps of the qwen3-fp8 layer after {warm} warm-up "
+                      f"steps, round-robin over {R} routing sequences with one pager each, "
+                      f"time-bounded to {seconds:.0f} s (oracle routing + LRU pager + the "
+                      f"oracle's block-FP8 experts in numpy, weights in host memory, so no "
+                      f"page-in); {cpu_name()}"}
+
+
+def bench_fp8(args) -> dict:
+    """The default decode measurement on the block-FP8 twin of the Qwen3
+    layer: same routing sequences, eight layer instances sharing one set of
+    pinned FP8 masters."""
+    import torch
+
+    from wisp_amd import workloads as W
+    from wisp_amd.integrations.vllm.fused_moe_fp8 import WispMoEStateFP8
+    R = args.replicas
+    per = -(-(args.warmup + args.steps) // R)
+    t_setup = time.perf_counter()
+    routes = [W.qwen3_decode(seed=r, steps=per, weights=False) for r in range(R)]
+    wl = W.fp8_layer(routes[0], pin=True)
+    sh = wl.shape
+    views = wl.views()
+    dev = torch.device("cuda", 0)
+    xs = torch.stack([r.x for r in routes]).to(dev)
+    lgs = torch.stack([r.logits for r in routes]).to(dev)
+    states = [WispMoEStateFP8(*views, sh.cap, dev, r) for r in range(R)]
+    outs = [torch.empty((1, sh.hidden), dtype=torch.bfloat16, device=dev) for _ in range(R)]
+    log(f"fp8 setup {time.perf_counter() - t_setup:.1f}s: engine {states[0].pagein_engine}")
+
+    def call(i: int) -> None:
+        r, pos = i % R, i // R
+        states[r].forward(xs[r, pos], lgs[r, pos], sh.top_k, True, out=outs[r])
+
+    elapsed, agg = _timed(call, args.warmup, args.steps, states)
+    _calibration_copy(dev)
+    lay = wl.layout
+    K = sh.top_k
+    calls = max(1, agg["calls"])
+    t13 = agg["w13_ms"] / calls * 1e-3
+    t2 = agg["w2_ms"] / calls * 1e-3
+    w13_bytes = K * (lay.w13_bytes + 4 * lay.s13_elems)
+    w2_bytes = K * (lay.w2_bytes + 4 * lay.s2_elems)
+    a13 = w13_bytes / t13 / 1e9 if t13 > 0 else 0.0
+    agemm = (w13_bytes + w2_bytes) / (t13 + t2) / 1e9 if t13 + t2 > 0 else 0.0
+    link = h2d_link(wl.expert_bytes)
+    cpu = None
+    if not args.no_cpu_baseline:
+        t_cpu = time.perf_counter()
+        croutes = [W.Workload(r.name, sh, r.x, r.logits, wl.slabs) for r in routes]
+        cpu = cpu_baseline_fp8(croutes, views, args.cpu_seconds)
+        log(f"cpu baseline {time.perf_counter() - t_cpu:.1f}s")
+    line = _line("MoE decode tok/s, Qwen3-30B-A3B-FP8 shape bs=1 cap=8 (block-FP8 w8a8)",
+                 args.steps / elapsed, "tok/s", args, args.steps, elapsed,
+                 {"workload": "qwen3-30b-a3b-fp8 moe layer decode, bs=1, cap=8, paged from "
+                              "pinned host",
+                  "hidden": sh.hidden, "expert_intermediate": sh.inter, "experts": sh.experts,
+                  "top_k": K, "cap": sh.cap, "batch": 1, "layer_instances": R,
+                  "weight_block": list(wl.block),
+                  "routing": "zipf(1.1) bias + 0.6 reuse of previous top-8"},
+                 roofline={"kernel": "fp8_w13_kernel (gate/up block-FP8 MFMA + SiLU*mul)",
+                           "bound": "hbm", "achieved": round(a13, 1), "peak": HBM_PEAK_GBPS,
+                           "unit": "GB/s", "frac": round(a13 / HBM_PEAK_GBPS, 4),
+                           "traffic": None, "bytes_per_call": w13_bytes,
+                           "avg_us_per_call": round(t13 * 1e6, 3)},
+                 expert_gemm={"kernels": "fp8_w13_kernel + fp8_w2_kernel",
+                              "bytes_per_token": w13_bytes + w2_bytes,
+                              "avg_us": round((t13 + t2) * 1e6, 3),
+                              "achieved_GBps": round(agemm, 1),
+                              "frac_hbm_peak": round(agemm / HBM_PEAK_GBPS, 4),
+                              "w2_avg_us": round(t2 * 1e6, 3), "timed_calls": agg["calls"]},
+                 pagein=dict(_pagein_report(agg), link_GBps_p50=round(link, 2),
+                             expert_bytes=wl.expert_bytes),
+                 cpu_baseline=cpu)
+    line["dtype"] = "fp8_e4m3 (bf16 activations, f32 accumulate)"
+    return line
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -371,7 +492,7 @@ def main() -> int:
                     help="time bound of the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", default="qwen3",
-                    choices=["qwen3", "prefill", "batch32", "mixtral", "stack"])
+                    choices=["qwen3", "prefill", "batch32", "mixtral", "stack", "fp8"])
     ap.add_argument("--prefetch", action="store_true",
                     help="stack workload: cross-layer speculative prefetch with a co-occurrence "
                          "table learned online (WISP_PREFETCH=1, WISP_COOCCUR_ONLINE=1)")
@@ -383,7 +504,7 @@ def main() -> int:
 
     if args.workload != "qwen3":
         line = {"prefill": bench_prefill, "batch32": bench_batch32, "mixtral": bench_mixtral,
-                "stack": bench_stack}[args.workload](args)
+                "stack": bench_stack, "fp8": bench_fp8}[args.workload](args)
         print(json.dumps(line), flush=True)
         return 0
 
@@ -443,14 +564,7 @@ def main() -> int:
     a13 = w13_bytes / t13 / 1e9 if t13 > 0 else 0.0
     agemm = (w13_bytes + w2_bytes) / (t13 + t2) / 1e9 if t13 + t2 > 0 else 0.0
 
-    # A plain 256 MiB device copy: the calibration dispatch for the profiler's
-    # HBM byte counters (FETCH_SIZE / WRITE_SIZE of a copy of known size).
-    cal = torch.empty(2, 256 << 20, dtype=torch.uint8, device=dev)
-    from wisp_amd import _lib
-    _lib.check(_lib.lib().wisp_probe_hbm_copy(cal[1].data_ptr(), cal[0].data_ptr(), 256 << 20,
-                                              _lib.stream_handle()), "hbm copy")
-    torch.cuda.synchronize()
-    del cal
+    _calibration_copy(dev)
 
     link = h2d_link(sh.expert_bytes)
     link_big = h2d_link(256 << 20, iters=8)

@@ -61,7 +61,6 @@ constexpr float kE4m3Max = 448.f;
 constexpr float kQuantEps = 1e-10f;
 constexpr int kKB = 128;         // k-block: the MFMA's K and the scale block's width
 constexpr int kKC = 4;           // k-blocks a w13 wave loads before it computes
-constexpr int kKC2 = 8;          // k-blocks a w2 wave loads before it computes
 constexpr int kW2Waves = 8;
 constexpr size_t kMaxLds = 160 * 1024;
 
@@ -92,10 +91,12 @@ __device__ inline i32x8 join(const u32x4& a, const u32x4& b) {
   return r;
 }
 
-// 32 bytes of a weight row, streamed (each byte is read once per launch).
-__device__ inline i32x8 ld32_stream(const uint8_t* p) {
-  const u32x4 a = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
-  const u32x4 b = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p + 16));
+// 32 bytes of a weight row.  Plain loads: with the nontemporal hint the
+// decode kernels ran ~1.4 us slower each (measured on MI355X at the Qwen3
+// shape), unlike the bf16 GEMV, whose rows are read whole by one wave.
+__device__ inline i32x8 ld32(const uint8_t* p) {
+  const u32x4 a = *reinterpret_cast<const u32x4*>(p);
+  const u32x4 b = *reinterpret_cast<const u32x4*>(p + 16);
   return join(a, b);
 }
 
@@ -175,19 +176,47 @@ __global__ __launch_bounds__(256) void quant_groups_kernel(const T* __restrict__
 }
 
 // ---------------------------------------------------------------------------
-// w13 + silu_and_mul.
-// Dynamic LDS: red [NW][2][64][4] f32, then per wave xs [kKC][ncol] f32 and
-// xq [kKC][ncol][kKB] codes.
+// The launch's slot table.  Up to kPairRegs * 64 pairs it is read once into
+// registers (lane l holds pairs l, 64 + l, ...), so a block knows its slot,
+// whether it leads and its column set after one memory round trip; larger
+// launches (BIG) scan it in memory.
 // ---------------------------------------------------------------------------
+constexpr int kPairRegs = 4;
 
-// Pair index of rank `rank` among the pairs routed to slot s (-1 if none),
-// and their number; wave-uniform loop over the P pairs.
-__device__ inline int pair_of_rank(const int32_t* __restrict__ slots, int P, int s, int rank,
-                                   int lane, int* total) {
+template <bool BIG>
+__device__ inline void load_pairs(const int32_t* __restrict__ slots, int P, int lane,
+                                  int (&v)[kPairRegs]) {
+  // unguarded loads at clamped indices (no exec-masked branches), masked after
+  int raw[kPairRegs];
+#pragma unroll
+  for (int c = 0; c < kPairRegs; ++c) raw[c] = BIG ? -1 : slots[min(c * 64 + lane, P - 1)];
+#pragma unroll
+  for (int c = 0; c < kPairRegs; ++c) v[c] = (!BIG && c * 64 + lane < P) ? raw[c] : -1;
+}
+
+// Slot of pair p (wave-uniform).
+template <bool BIG>
+__device__ inline int slot_of(const int32_t* __restrict__ slots, const int (&v)[kPairRegs],
+                              int p) {
+  if constexpr (BIG) {
+    return slots[p];
+  } else {
+    int r = -1;
+#pragma unroll
+    for (int c = 0; c < kPairRegs; ++c)
+      if (p / 64 == c) r = __shfl(v[c], p % 64);
+    return r;
+  }
+}
+
+// Pair index of rank `rank` (per lane) among the pairs routed to slot s >= 0
+// (-1 if none), and their number.
+template <bool BIG>
+__device__ inline int pair_of_rank(const int32_t* __restrict__ slots, const int (&v)[kPairRegs],
+                                   int P, int s, int rank, int lane, int* total) {
   int found = -1, seen = 0;
-  for (int b = 0; b < P; b += 64) {
-    const int q = b + lane;
-    unsigned long long bal = __ballot(q < P && slots[q] == s);
+  auto step = [&](int b, bool m) {
+    unsigned long long bal = __ballot(m);
     const int c = __popcll(bal);
     const int want = rank - seen;
     if (found < 0 && want >= 0 && want < c) {
@@ -195,32 +224,51 @@ __device__ inline int pair_of_rank(const int32_t* __restrict__ slots, int P, int
       found = b + __ffsll((long long)bal) - 1;
     }
     seen += c;
+  };
+  if constexpr (BIG) {
+    for (int b = 0; b < P; b += 64) {
+      const int q = b + lane;
+      step(b, q < P && slots[q] == s);
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < kPairRegs; ++c) step(c * 64, v[c] == s);  // -1 past P never matches
   }
   *total = seen;
   return found;
 }
 
-template <int NW>
+// ---------------------------------------------------------------------------
+// w13 + silu_and_mul.
+// NCOL: MFMA columns per pass over the weights (1 for a one-token launch, 4,
+// or 16), a compile-time width so that every load is unguarded: a column or
+// k-block past the live ones loads a clamped copy that is never stored.
+// Dynamic LDS: red [NW][2][64][4] f32, then per wave xs [kKC][NCOL] f32 and
+// xq [kKC][NCOL][kKB] codes.
+// ---------------------------------------------------------------------------
+template <int NW, int NCOL, bool BIG>
 __global__ __launch_bounds__(NW * 64) void fp8_w13_kernel(
     const uint16_t* __restrict__ x, int H, int I, int K, int P, const int32_t* __restrict__ slots,
     int nslots, const uint8_t* __restrict__ w13, size_t w13_stride, const float* __restrict__ s13,
-    size_t s13_stride, int block_n, int ncol, uint16_t* __restrict__ act) {
+    size_t s13_stride, int block_n, uint16_t* __restrict__ act) {
   extern __shared__ __align__(16) unsigned char smem[];
   float* red = reinterpret_cast<float*>(smem);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int col = lane & 15, grp = lane >> 4;
   const int p = blockIdx.y, i0 = blockIdx.x * 16;
-  const int s = slots[p];
+  int sv[kPairRegs];
+  load_pairs<BIG>(slots, P, lane, sv);
+  const int s = slot_of<BIG>(slots, sv, p);
   if (s < 0 || s >= nslots) {  // this pair reads no expert
     if (threadIdx.x < 16) act[(size_t)p * I + i0 + threadIdx.x] = 0;
     return;
   }
   int total = 0;
-  if (pair_of_rank(slots, P, s, 0, lane, &total) != p) return;  // not the slot's leader
+  if (pair_of_rank<BIG>(slots, sv, P, s, 0, lane, &total) != p) return;  // not the leader
 
   float* xs = reinterpret_cast<float*>(smem + NW * 2 * 64 * 4 * sizeof(float) +
-                                       (size_t)wave * kKC * ncol * (4 + kKB));
-  uint8_t* xq = reinterpret_cast<uint8_t*>(xs + kKC * ncol);
+                                       (size_t)wave * kKC * NCOL * (4 + kKB));
+  uint8_t* xq = reinterpret_cast<uint8_t*>(xs + kKC * NCOL);
   const int nkb = H / kKB;
   const int per = (nkb + NW - 1) / NW;
   const int kb0 = min(nkb, wave * per), kb1 = min(nkb, kb0 + per);
@@ -230,83 +278,62 @@ __global__ __launch_bounds__(NW * 64) void fp8_w13_kernel(
   const uint8_t* rowg = W + (size_t)(i0 + col) * H + grp * 32;
   const uint8_t* rowu = W + (size_t)(I + i0 + col) * H + grp * 32;
 
-  for (int rank0 = 0; rank0 < total; rank0 += ncol) {
-    const int npc = min(ncol, total - rank0);
+  for (int rank0 = 0; rank0 < total; rank0 += NCOL) {
+    const int npc = min(NCOL, total - rank0);
     // column `col` of this set computes the pair of rank rank0 + col (every
     // lane runs the ballots; lanes past the set's width get -1)
-    const int r = pair_of_rank(slots, P, s, rank0 + col, lane, &total);
+    const int r = pair_of_rank<BIG>(slots, sv, P, s, rank0 + col, lane, &total);
     const int mypair = col < npc ? r : -1;
     const int mytok = mypair >= 0 ? mypair / K : 0;
     f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
     for (int kc = kb0; kc < kb1; kc += kKC) {
       const int nk = min(kKC, kb1 - kc);
-      // activation groups of this chunk: job j = (column j / nk, k-block j % nk),
-      // four jobs per pass (a quarter-wave each, 8 values per lane), four
-      // passes per round
-      const int njobs = npc * nk, npass = (njobs + 3) >> 2;
-      u32x4 xv[4];
-      auto load_round = [&](int r0) {
+      // activations: pass c quantises column c, quarter-wave g its k-block g
+      // (lane & 15 is then the lane's eighth of the 128-value group); the
+      // activation loads go first, then the weights and scales, so the
+      // quantisation waits only for the activations
+      u32x4 xv[NCOL];
 #pragma unroll
-        for (int it = 0; it < 4; ++it) {
-          if (r0 + it < npass) {  // wave-uniform
-            const int j = (r0 + it) * 4 + grp;
-            const int c = j < njobs ? j / nk : 0, kbi = j < njobs ? j % nk : 0;
-            const int tok = __shfl(mytok, c);  // the token of column c (lane c)
-            // here lane & 15 is the lane's eighth of the 128-value group
-            xv[it] = j < njobs ? *reinterpret_cast<const u32x4*>(
-                                     x + (size_t)tok * H + (size_t)(kc + kbi) * kKB + col * 8)
-                               : u32x4{0u, 0u, 0u, 0u};
-          }
-        }
-      };
-      auto quant_round = [&](int r0) {
-#pragma unroll
-        for (int it = 0; it < 4; ++it) {
-          if (r0 + it < npass) {
-            const int j = (r0 + it) * 4 + grp;
-            float v[8];
-            unpack_bf16x8(xv[it], v);
-            uint32_t q[2];
-            const float sc = quant8(v, q);
-            if (j < njobs) {
-              const int c = j / nk, kbi = j % nk;
-              *reinterpret_cast<uint2*>(xq + ((size_t)kbi * ncol + c) * kKB + col * 8) =
-                  make_uint2(q[0], q[1]);
-              if (col == 0) xs[kbi * ncol + c] = sc;
-            }
-          }
-        }
-      };
-      // the first round's activations, then the weights, are in flight
-      // together; the quantisation waits only for the activations
-      load_round(0);
+      for (int c = 0; c < NCOL; ++c) {
+        const int tok = __shfl(mytok, min(c, npc - 1));
+        xv[c] = *reinterpret_cast<const u32x4*>(x + (size_t)tok * H +
+                                                (size_t)(kc + min(grp, nk - 1)) * kKB + col * 8);
+      }
       i32x8 wg[kKC], wu[kKC];
+      float sg[kKC], su[kKC];
 #pragma unroll
       for (int kbi = 0; kbi < kKC; ++kbi) {
-        if (kbi < nk) {
-          wg[kbi] = ld32_stream(rowg + (size_t)(kc + kbi) * kKB);
-          wu[kbi] = ld32_stream(rowu + (size_t)(kc + kbi) * kKB);
-        }
+        const int kb = kc + min(kbi, nk - 1);
+        wg[kbi] = ld32(rowg + (size_t)kb * kKB);
+        wu[kbi] = ld32(rowu + (size_t)kb * kKB);
+        sg[kbi] = Sg[kb];
+        su[kbi] = Su[kb];
       }
-      quant_round(0);
-      for (int r0 = 4; r0 < npass; r0 += 4) {
-        load_round(r0);
-        quant_round(r0);
+#pragma unroll
+      for (int c = 0; c < NCOL; ++c) {
+        float v[8];
+        unpack_bf16x8(xv[c], v);
+        uint32_t q[2];
+        const float sc = quant8(v, q);
+        if (c < npc && grp < nk) {
+          *reinterpret_cast<uint2*>(xq + ((size_t)grp * NCOL + c) * kKB + col * 8) =
+              make_uint2(q[0], q[1]);
+          if (col == 0) xs[grp * NCOL + c] = sc;
+        }
       }
       wave_lds_sync();
 #pragma unroll
       for (int kbi = 0; kbi < kKC; ++kbi) {
         if (kbi < nk) {
-          const i32x8 b = col < npc ? lds32(xq + ((size_t)kbi * ncol + col) * kKB + grp * 32)
+          const i32x8 b = col < npc ? lds32(xq + ((size_t)kbi * NCOL + col) * kKB + grp * 32)
                                     : zero8();
-          const float sa = col < npc ? xs[kbi * ncol + col] : 0.f;
-          const float sg = Sg[kc + kbi], su = Su[kc + kbi];
+          const float sa = col < npc ? xs[kbi * NCOL + col] : 0.f;
           const f32x4 dg = mfma_fp8(wg[kbi], b);
           const f32x4 du = mfma_fp8(wu[kbi], b);
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            ag[j] = ag[j] + (dg[j] * sa) * sg;
-            au[j] = au[j] + (du[j] * sa) * su;
+            ag[j] = ag[j] + (dg[j] * sa) * sg[kbi];
+            au[j] = au[j] + (du[j] * sa) * su[kbi];
           }
         }
       }
@@ -322,11 +349,11 @@ __global__ __launch_bounds__(NW * 64) void fp8_w13_kernel(
     if (wave == 0 && col < npc) {
       float g[4] = {0.f, 0.f, 0.f, 0.f}, u[4] = {0.f, 0.f, 0.f, 0.f};
       for (int w = 0; w < NW; ++w) {
-        const float* r = red + ((size_t)w * 2 * 64 + lane) * 4;
+        const float* rr = red + ((size_t)w * 2 * 64 + lane) * 4;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          g[j] = g[j] + r[j];
-          u[j] = u[j] + r[64 * 4 + j];
+          g[j] = g[j] + rr[j];
+          u[j] = u[j] + rr[64 * 4 + j];
         }
       }
       uint16_t* arow = act + (size_t)mypair * I + i0 + grp * 4;
@@ -342,14 +369,17 @@ __global__ __launch_bounds__(NW * 64) void fp8_w13_kernel(
 
 // ---------------------------------------------------------------------------
 // w2 + routing weight + moe_sum.
+// KC2: k-blocks a wave loads before it computes (the job's k-range is a
+// whole number of chunks, or the last chunk loads clamped copies that are
+// never used).  QP: quantisation passes per round (4 act groups per pass),
+// sized so that a wave quantises few clamped copies.
 // Dynamic LDS: aq [K][I] codes, as [K][nkb] f32, part [K][WP][16] f32.
 // ---------------------------------------------------------------------------
-template <int NW>
+template <int NW, int KC2, int QP>
 __global__ __launch_bounds__(NW * 64) void fp8_w2_kernel(
     const uint16_t* __restrict__ act, int H, int I, int K, const float* __restrict__ topk_w,
     const int32_t* __restrict__ slots, int nslots, const uint8_t* __restrict__ w2,
-    size_t w2_stride,
-    const float* __restrict__ s2, size_t s2_stride, int block_n, int WP,
+    size_t w2_stride, const float* __restrict__ s2, size_t s2_stride, int block_n, int WP,
     uint16_t* __restrict__ out) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -360,49 +390,84 @@ __global__ __launch_bounds__(NW * 64) void fp8_w2_kernel(
   float* as = reinterpret_cast<float*>(smem + (size_t)K * I);
   float* part = as + (size_t)K * nkb;
 
-  // this wave's jobs: (pair k, k-block part q), q < WP; the first job's
-  // first chunk of weights is loaded before the act is quantised
-  const int njob = K * WP;
-  const int per = (nkb + WP - 1) / WP;
-  i32x8 a[kKC2];
-  int j0 = wave;
-  int s0 = -1, kbs0 = 0, kbe0 = 0;
-  if (j0 < njob) {
-    s0 = slots[(size_t)t * K + j0 / WP];
-    if (s0 >= nslots) s0 = -1;
-    kbs0 = min(nkb, (j0 % WP) * per);
-    kbe0 = min(nkb, kbs0 + per);
-    if (s0 >= 0) {
-      const uint8_t* row = w2 + (size_t)s0 * w2_stride + (size_t)(h0 + col) * I + grp * 32;
-#pragma unroll
-      for (int kbi = 0; kbi < kKC2; ++kbi)
-        if (kbs0 + kbi < kbe0) a[kbi] = ld32_stream(row + (size_t)(kbs0 + kbi) * kKB);
-    }
-  }
+  // the token's slots and routing weights, lane k holding pair k (K <= 64;
+  // lanes past K hold copies and are never read), loaded without branches; a
+  // slot outside the scratch contributes zero
+  const int kl = min(lane, K - 1);
+  int sk = slots[(size_t)t * K + kl];
+  const float wk = topk_w[(size_t)t * K + kl];
+  if (sk >= nslots) sk = -1;
 
-  // quantise the token's K act rows: one quarter-wave per 128-value group
+  // act groups to quantise: one quarter-wave per 128-value group, four per
+  // pass, QP passes per round; clamped copies past the last group are
+  // quantised and dropped
   const int ngroups = K * nkb;
-  for (int g0 = wave * 4; g0 < ngroups; g0 += NW * 4) {
-    const int g = g0 + grp;
-    if (g < ngroups) {
+  u32x4 av[QP];
+  auto load_round = [&](int g0) {
+#pragma unroll
+    for (int it = 0; it < QP; ++it) {
+      const int g = min(g0 + it * NW * 4 + grp, ngroups - 1);
       const int k = g / nkb, kb = g % nkb;
-      const u32x4 u = *reinterpret_cast<const u32x4*>(act + ((size_t)t * K + k) * I +
-                                                      (size_t)kb * kKB + col * 8);
+      av[it] = *reinterpret_cast<const u32x4*>(act + ((size_t)t * K + k) * I +
+                                               (size_t)kb * kKB + col * 8);
+    }
+  };
+  auto quant_round = [&](int g0) {
+#pragma unroll
+    for (int it = 0; it < QP; ++it) {
+      const int g = g0 + it * NW * 4 + grp;
       float v[8];
-      unpack_bf16x8(u, v);
+      unpack_bf16x8(av[it], v);
       uint32_t q[2];
       const float sc = quant8(v, q);
-      *reinterpret_cast<uint2*>(aq + (size_t)k * I + (size_t)kb * kKB + col * 8) =
-          make_uint2(q[0], q[1]);
-      if (col == 0) as[k * nkb + kb] = sc;
-    }  // the shuffles of quant8 stay inside one quarter-wave, which branches as one
+      if (g < ngroups) {
+        const int k = g / nkb, kb = g % nkb;
+        *reinterpret_cast<uint2*>(aq + (size_t)k * I + (size_t)kb * kKB + col * 8) =
+            make_uint2(q[0], q[1]);
+        if (col == 0) as[k * nkb + kb] = sc;
+      }
+    }
+  };
+  load_round(wave * 4);
+
+  // this wave's jobs: (pair k, k-block part q), q < WP; the first job's first
+  // chunk of weights and scales is in flight while the act is quantised
+  const int njob = K * WP;
+  const int per = (nkb + WP - 1) / WP;
+  i32x8 a[KC2];
+  float sw[KC2];
+  // The loads are unconditional (a wave without a first job, an absent slot
+  // or an empty k-range reads slot 0's first block and drops it): loads
+  // under a branch would make the wait before the quantisation below count
+  // them too.
+  const int j0 = wave;
+  const int s0 = j0 < njob ? __shfl(sk, min(j0, njob - 1) / WP) : -1;
+  const int kbs0 = min(nkb, (j0 % WP) * per);
+  const int kbe0 = min(nkb, kbs0 + per);
+  {
+    const bool live = s0 >= 0 && kbe0 > kbs0;
+    const int sl = live ? s0 : 0;
+    const uint8_t* row = w2 + (size_t)sl * w2_stride + (size_t)(h0 + col) * I + grp * 32;
+    const float* S = s2 + (size_t)sl * s2_stride + (size_t)(h0 / block_n) * nkb;
+    const int last = live ? min(KC2, kbe0 - kbs0) - 1 : 0;
+    const int base = live ? kbs0 : 0;
+#pragma unroll
+    for (int kbi = 0; kbi < KC2; ++kbi) {
+      const int kb = base + min(kbi, last);
+      a[kbi] = ld32(row + (size_t)kb * kKB);
+      sw[kbi] = S[kb];
+    }
+  }
+  quant_round(wave * 4);
+  for (int g0 = wave * 4 + QP * NW * 4; g0 < ngroups; g0 += QP * NW * 4) {
+    load_round(g0);
+    quant_round(g0);
   }
   __syncthreads();
 
   for (int j = wave; j < njob; j += NW) {
     const int k = j / WP;
-    int s = j == j0 ? s0 : slots[(size_t)t * K + k];
-    if (s >= nslots) s = -1;  // out of the scratch: contributes zero
+    const int s = j == j0 ? s0 : __shfl(sk, k);
     const int kbs = j == j0 ? kbs0 : min(nkb, (j % WP) * per);
     const int kbe = j == j0 ? kbe0 : min(nkb, kbs + per);
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -411,20 +476,24 @@ __global__ __launch_bounds__(NW * 64) void fp8_w2_kernel(
       const float* S = s2 + (size_t)s * s2_stride + (size_t)(h0 / block_n) * nkb;
       const float* sa = as + (size_t)k * nkb;
       const uint8_t* aqk = aq + (size_t)k * I + grp * 32;
-      for (int kc = kbs; kc < kbe; kc += kKC2) {
+      for (int kc = kbs; kc < kbe; kc += KC2) {
+        const int nk = min(KC2, kbe - kc);
         if (!(j == j0 && kc == kbs)) {
 #pragma unroll
-          for (int kbi = 0; kbi < kKC2; ++kbi)
-            if (kc + kbi < kbe) a[kbi] = ld32_stream(row + (size_t)(kc + kbi) * kKB);
+          for (int kbi = 0; kbi < KC2; ++kbi) {
+            const int kb = kc + min(kbi, nk - 1);
+            a[kbi] = ld32(row + (size_t)kb * kKB);
+            sw[kbi] = S[kb];
+          }
         }
 #pragma unroll
-        for (int kbi = 0; kbi < kKC2; ++kbi) {
-          if (kc + kbi < kbe) {
+        for (int kbi = 0; kbi < KC2; ++kbi) {
+          if (kbi < nk) {
             const i32x8 b = col == 0 ? lds32(aqk + (size_t)(kc + kbi) * kKB) : zero8();
             const f32x4 d = mfma_fp8(a[kbi], b);
-            const float sc = sa[kc + kbi], sw = S[kc + kbi];
+            const float sc = sa[kc + kbi];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) acc[q] = acc[q] + (d[q] * sc) * sw;
+            for (int q = 0; q < 4; ++q) acc[q] = acc[q] + (d[q] * sc) * sw[kbi];
           }
         }
       }
@@ -436,22 +505,22 @@ __global__ __launch_bounds__(NW * 64) void fp8_w2_kernel(
     }
   }
   __syncthreads();
-  if (threadIdx.x < 16) {
-    const int r = threadIdx.x;
-    const float* w = topk_w + (size_t)t * K;
+  if (wave == 0) {  // every lane runs the loop (shuffles); lanes < 16 store
+    const int r = lane & 15;
     const bool bf16_adds = K >= 2 && K <= 4;
     float sum = 0.f;
     for (int k = 0; k < K; ++k) {
+      const int s = __shfl(sk, k);
+      const float w = __shfl(wk, k);
       float y = 0.f;
-      const int sk = slots[(size_t)t * K + k];
-      if (sk >= 0 && sk < nslots) {
+      if (s >= 0) {
         float v = 0.f;
         for (int q = 0; q < WP; ++q) v = v + part[((size_t)k * WP + q) * 16 + r];
-        y = round_bf16(v * w[k]);
+        y = round_bf16(v * w);
       }
       sum = bf16_adds ? round_bf16(sum + y) : sum + y;
     }
-    out[(size_t)t * H + h0 + r] = bf16_rne(sum);
+    if (lane < 16) out[(size_t)t * H + h0 + r] = bf16_rne(sum);
   }
 }
 
@@ -460,11 +529,12 @@ size_t w13_lds(int NW, int ncol) {
 }
 
 size_t w2_lds(int K, int I, int WP) {
-  return (size_t)K * I + (size_t)K * (I / kKB) * sizeof(float) + (size_t)K * WP * 16 * sizeof(float);
+  return (size_t)K * I + (size_t)K * (I / kKB) * sizeof(float) +
+         (size_t)K * WP * 16 * sizeof(float);
 }
 
 // Waves per w13 block: four up to H = 2048, eight above (a wave then loops
-// over chunks of kKC k-blocks; sixteen waves would cap a wave at 128 VGPRs).
+// over chunks of kKC k-blocks).
 int w13_waves(int H) { return H / kKB <= 4 * kKC ? 4 : 8; }
 
 // Allows a kernel more than the default 64 KiB of dynamic LDS (once).
@@ -477,21 +547,65 @@ hipError_t allow_lds(Kern kernel, size_t lds, bool* done) {
   return e;
 }
 
-template <int NW>
-hipError_t launch_w13(dim3 grid, size_t lds, hipStream_t st, hipEvent_t e0, hipEvent_t e1,
-                      const uint16_t* x, int H, int I, int K, int P, const int32_t* slots,
-                      int nslots, const uint8_t* w13, size_t w13_stride, const float* s13,
-                      size_t s13_stride,
-                      int block_n, int ncol, uint16_t* act) {
+struct W13Args {
+  const uint16_t* x;
+  int H, I, K, P;
+  const int32_t* slots;
+  int nslots;
+  const uint8_t* w13;
+  size_t w13_stride;
+  const float* s13;
+  size_t s13_stride;
+  int block_n;
+  uint16_t* act;
+};
+
+template <int NW, int NCOL, bool BIG>
+hipError_t launch_w13(const W13Args& a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
   static bool big_lds = false;
-  hipError_t e = allow_lds(fp8_w13_kernel<NW>, lds, &big_lds);
+  const auto kern = &fp8_w13_kernel<NW, NCOL, BIG>;
+  const size_t lds = w13_lds(NW, NCOL);
+  hipError_t e = allow_lds(kern, lds, &big_lds);
   if (e != hipSuccess) return e;
+  const dim3 grid(a.I / 16, a.P), block(NW * 64);
   if (e0)
-    hipExtLaunchKernelGGL(fp8_w13_kernel<NW>, grid, dim3(NW * 64), lds, st, e0, e1, 0, x, H, I, K,
-                          P, slots, nslots, w13, w13_stride, s13, s13_stride, block_n, ncol, act);
+    hipExtLaunchKernelGGL(kern, grid, block, lds, st, e0, e1, 0, a.x, a.H, a.I, a.K, a.P, a.slots,
+                          a.nslots, a.w13, a.w13_stride, a.s13, a.s13_stride, a.block_n, a.act);
   else
-    hipLaunchKernelGGL(fp8_w13_kernel<NW>, grid, dim3(NW * 64), lds, st, x, H, I, K, P, slots,
-                       nslots, w13, w13_stride, s13, s13_stride, block_n, ncol, act);
+    hipLaunchKernelGGL(kern, grid, block, lds, st, a.x, a.H, a.I, a.K, a.P, a.slots, a.nslots,
+                       a.w13, a.w13_stride, a.s13, a.s13_stride, a.block_n, a.act);
+  return hipGetLastError();
+}
+
+struct W2Args {
+  const uint16_t* act;
+  int H, I, K, T;
+  const float* topk_w;
+  const int32_t* slots;
+  int nslots;
+  const uint8_t* w2;
+  size_t w2_stride;
+  const float* s2;
+  size_t s2_stride;
+  int block_n, WP;
+  uint16_t* out;
+};
+
+template <int KC2, int QP>
+hipError_t launch_w2(const W2Args& a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
+  static bool big_lds = false;
+  const auto kern = &fp8_w2_kernel<kW2Waves, KC2, QP>;
+  const size_t lds = w2_lds(a.K, a.I, a.WP);
+  hipError_t e = allow_lds(kern, lds, &big_lds);
+  if (e != hipSuccess) return e;
+  const dim3 grid(a.H / 16, a.T), block(kW2Waves * 64);
+  if (e0)
+    hipExtLaunchKernelGGL(kern, grid, block, lds, st, e0, e1, 0, a.act, a.H, a.I, a.K, a.topk_w,
+                          a.slots, a.nslots, a.w2, a.w2_stride, a.s2, a.s2_stride, a.block_n,
+                          a.WP, a.out);
+  else
+    hipLaunchKernelGGL(kern, grid, block, lds, st, a.act, a.H, a.I, a.K, a.topk_w, a.slots,
+                       a.nslots, a.w2, a.w2_stride, a.s2, a.s2_stride, a.block_n, a.WP, a.out);
   return hipGetLastError();
 }
 
@@ -515,38 +629,43 @@ int experts_fp8(const void* x, int T, int H, int I, int K, const float* topk_w,
                 hipStream_t st, const StageEvents* ev) {
   if (T == 0) return WISP_OK;
   const int P = T * K;
-  const int NW = w13_waves(H);
-  const int ncol = min(T, 16);
-  const size_t l13 = w13_lds(NW, ncol);
-  const dim3 g13(I / 16, P);
+  const W13Args a13 = {(const uint16_t*)x, H, I, K, P, slots, nslots, (const uint8_t*)w13,
+                       w13_stride, s13, s13_stride, block_n, (uint16_t*)act};
   hipEvent_t e0 = ev ? ev->ev[0] : nullptr, e1 = ev ? ev->ev[1] : nullptr;
-  const uint16_t* xb = (const uint16_t*)x;
-  const uint8_t* w13b = (const uint8_t*)w13;
-  uint16_t* actb = (uint16_t*)act;
-  if (NW == 4)
-    WISP_HIP_TRY(launch_w13<4>(g13, l13, st, e0, e1, xb, H, I, K, P, slots, nslots, w13b,
-                               w13_stride, s13, s13_stride, block_n, ncol, actb));
+  // MFMA columns per pass: a decode token needs one; pairs sharing a slot
+  // are at most T (a token's experts are distinct)
+  const int ncol = T == 1 ? 1 : T <= 4 ? 4 : 16;
+  const bool big = P > kPairRegs * 64;
+  using L13 = hipError_t (*)(const W13Args&, hipStream_t, hipEvent_t, hipEvent_t);
+  L13 l13;
+  if (w13_waves(H) == 4)
+    l13 = ncol == 1 ? &launch_w13<4, 1, false>
+        : ncol == 4 ? &launch_w13<4, 4, false>
+        : big ? &launch_w13<4, 16, true> : &launch_w13<4, 16, false>;
   else
-    WISP_HIP_TRY(launch_w13<8>(g13, l13, st, e0, e1, xb, H, I, K, P, slots, nslots, w13b,
-                               w13_stride, s13, s13_stride, block_n, ncol, actb));
+    l13 = ncol == 1 ? &launch_w13<8, 1, false>
+        : ncol == 4 ? &launch_w13<8, 4, false>
+        : big ? &launch_w13<8, 16, true> : &launch_w13<8, 16, false>;
+  WISP_HIP_TRY(l13(a13, st, e0, e1));
 
   // waves per pair: split I's k-blocks when there are fewer pairs than waves
   int WP = K >= kW2Waves ? 1 : kW2Waves / K;
   while (WP > 1 && w2_lds(K, I, WP) > kMaxLds) WP >>= 1;
-  const size_t l2 = w2_lds(K, I, WP);
-  const dim3 g2(H / 16, T);
-  static bool big_lds2 = false;
-  WISP_HIP_TRY(allow_lds(fp8_w2_kernel<kW2Waves>, l2, &big_lds2));
-  if (ev && ev->ev[2])
-    hipExtLaunchKernelGGL(fp8_w2_kernel<kW2Waves>, g2, dim3(kW2Waves * 64), l2, st, ev->ev[2],
-                          ev->ev[3], 0, (const uint16_t*)act, H, I, K, topk_w, slots, nslots,
-                          (const uint8_t*)w2, w2_stride, s2, s2_stride, block_n, WP,
-                          (uint16_t*)out);
+  const int per = (I / kKB + WP - 1) / WP;
+  const int kc2 = per <= 4 ? 4 : per <= 6 ? 6 : per <= 8 || per % 8 == 0 ? 8 : per % 6 == 0 ? 6 : 8;
+  const W2Args a2 = {(const uint16_t*)act, H, I, K, T, topk_w, slots, nslots, (const uint8_t*)w2,
+                     w2_stride, s2, s2_stride, block_n, WP, (uint16_t*)out};
+  // quantisation passes a wave needs (4 groups each), capped at 4 per round
+  const int passes = (K * (I / kKB) + kW2Waves * 4 - 1) / (kW2Waves * 4);
+  using L2 = hipError_t (*)(const W2Args&, hipStream_t, hipEvent_t, hipEvent_t);
+  L2 l2;
+  if (passes <= 1)
+    l2 = kc2 == 4 ? &launch_w2<4, 1> : kc2 == 6 ? &launch_w2<6, 1> : &launch_w2<8, 1>;
+  else if (passes <= 2)
+    l2 = kc2 == 4 ? &launch_w2<4, 2> : kc2 == 6 ? &launch_w2<6, 2> : &launch_w2<8, 2>;
   else
-    hipLaunchKernelGGL(fp8_w2_kernel<kW2Waves>, g2, dim3(kW2Waves * 64), l2, st,
-                       (const uint16_t*)act, H, I, K, topk_w, slots, nslots,
-                       (const uint8_t*)w2, w2_stride, s2, s2_stride, block_n, WP, (uint16_t*)out);
-  WISP_HIP_TRY(hipGetLastError());
+    l2 = kc2 == 4 ? &launch_w2<4, 4> : kc2 == 6 ? &launch_w2<6, 4> : &launch_w2<8, 4>;
+  WISP_HIP_TRY(l2(a2, st, ev ? ev->ev[2] : nullptr, ev ? ev->ev[3] : nullptr));
   return WISP_OK;
 }
 
