@@ -466,7 +466,10 @@ def bench_fp8(args) -> dict:
                  roofline={"kernel": "fp8_w13_kernel (gate/up block-FP8 MFMA + SiLU*mul)",
                            "bound": "hbm", "achieved": round(a13, 1), "peak": HBM_PEAK_GBPS,
                            "unit": "GB/s", "frac": round(a13 / HBM_PEAK_GBPS, 4),
-                           "traffic": None, "bytes_per_call": w13_bytes,
+                           "traffic": pmc_traffic(os.path.join(
+                               os.path.dirname(os.path.abspath(__file__)), "profiles",
+                               "qwen3_fp8_decode_pmc.json"), "fp8_w13_kernel"),
+                           "bytes_per_call": w13_bytes,
                            "avg_us_per_call": round(t13 * 1e6, 3)},
                  expert_gemm={"kernels": "fp8_w13_kernel + fp8_w2_kernel",
                               "bytes_per_token": w13_bytes + w2_bytes,
