@@ -154,8 +154,12 @@ int wisp_moe_experts(const void* x, int dtype, int T, int H, int I, int K,
  * ([2I, H] e4m3fn), its scales s13 + s*s13_stride floats
  * ([2I/block_n, H/128]); W2 [H, I] and s2 [H/block_n, I/128] likewise.
  * Requires block_k == 128, block_n a multiple of 16 dividing I, H and I
- * multiples of 128.  A slot of -1 contributes zero.  work / work_bytes:
- * reserved for larger-batch kernels (may be NULL / 0).
+ * multiples of 128.  A slot of -1 contributes zero.  algo: WISP_ALGO_GEMV
+ * runs the decode kernels (MFMA tiles of one token column per pair, no work
+ * buffer); WISP_ALGO_MFMA the grouped path (per-slot token lists, each
+ * weight tile once per 64 tokens), which needs work: device, 256-byte
+ * aligned, wisp_moe_fp8_work_bytes(T, K, H, I, nslots) bytes; AUTO picks
+ * the grouped path from 16 tokens.
  * Replaces: vLLM fused_experts(..., quant_config=fp8_w8a8_moe_quant_config(
  *           w1_scale=scratch_s13, w2_scale=scratch_s2, block_shape=...))
  *           at src/wisp/integrations/vllm/fused_moe_fp8.py:245-249,316-326. */
@@ -165,6 +169,11 @@ int wisp_moe_experts_fp8(const void* x, int T, int H, int I, int K, const float*
                          const float* s2, size_t s2_stride, int block_n, int block_k, void* act,
                          void* out, void* work, size_t work_bytes, int algo,
                          wisp_stream_t stream);
+
+/* Bytes of the work buffer the grouped block-FP8 path needs: per-slot pair
+ * lists, bf16 per-pair outputs, and the quantised x and act with their
+ * scales.  No reference counterpart (vLLM allocates its own). */
+size_t wisp_moe_fp8_work_bytes(int T, int K, int H, int I, int nslots);
 
 /* Dynamic per-row, per-group fp8 quantisation: x [rows, cols] (WISP_F32 or
  * WISP_BF16, row stride cols) -> q [rows, cols] e4m3fn codes and

@@ -61,7 +61,8 @@ def _routing(T, E, K, seed):
     return ids, w
 
 
-def _run_experts(x, ids, tw, w13, w2, s13, s2, block, slots=None, nslots=None):
+def _run_experts(x, ids, tw, w13, w2, s13, s2, block, slots=None, nslots=None,
+                 algo=_lib.WISP_ALGO_GEMV):
     """wisp_moe_experts_fp8 through the C ABI on device copies; returns
     (out, act) as float32 CPU tensors."""
     T, H = x.shape
@@ -74,11 +75,14 @@ def _run_experts(x, ids, tw, w13, w2, s13, s2, block, slots=None, nslots=None):
     xd = x.to(DEV).contiguous()
     act = torch.full((max(1, T * K), I), float("nan"), dtype=torch.bfloat16, device=DEV)
     out = torch.empty((T, H), dtype=torch.bfloat16, device=DEV)
+    ns = E if nslots is None else nslots
+    nbytes = _lib.lib().wisp_moe_fp8_work_bytes(max(1, T), K, H, I, ns)
+    work = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
     rc = _lib.lib().wisp_moe_experts_fp8(
-        xd.data_ptr(), T, H, I, K, twd.data_ptr(), sl.data_ptr(), E if nslots is None else nslots,
+        xd.data_ptr(), T, H, I, K, twd.data_ptr(), sl.data_ptr(), ns,
         d13.data_ptr(), d13.stride(0), ds13.data_ptr(), ds13.stride(0), d2.data_ptr(),
         d2.stride(0), ds2.data_ptr(), ds2.stride(0), block[0], block[1], act.data_ptr(),
-        out.data_ptr(), None, 0, _lib.WISP_ALGO_AUTO, _lib.stream_handle())
+        out.data_ptr(), work.data_ptr(), nbytes, algo, _lib.stream_handle())
     _lib.check(rc, "wisp_moe_experts_fp8")
     torch.cuda.synchronize()
     return out.float().cpu(), act.float().cpu().view(T, K, I)
@@ -125,23 +129,28 @@ def test_experts_fp8_match_oracle(T, H, I, E, K, block):
     assert _rel(out, want) < REL_TOL, _rel(out, want)
 
 
-def test_experts_fp8_absent_slot_and_slot_placement():
+ALGOS = [pytest.param(_lib.WISP_ALGO_GEMV, id="decode"),
+         pytest.param(_lib.WISP_ALGO_MFMA, id="grouped")]
+
+
+@pytest.mark.parametrize("algo", ALGOS)
+def test_experts_fp8_absent_slot_and_slot_placement(algo):
     T, H, I, E, K, block = 4, 512, 256, 10, 4, (128, 128)
     _, w13, w2, s13, s2 = _experts(E, H, I, block, seed=3)
     ids, tw = _routing(T, E, K, seed=4)
     x = torch.randn((T, H), generator=torch.Generator().manual_seed(6)).to(torch.bfloat16)
-    base, _ = _run_experts(x, ids, tw, w13, w2, s13, s2, block)
+    base, _ = _run_experts(x, ids, tw, w13, w2, s13, s2, block, algo=algo)
     # the same experts at other slots: byte-identical
     perm = np.random.default_rng(7).permutation(E)
     inv = np.argsort(perm)
     moved, _ = _run_experts(x, ids, tw, _rows(w13, perm), _rows(w2, perm), _rows(s13, perm),
-                            _rows(s2, perm), block, slots=inv[ids].astype(np.int32))
+                            _rows(s2, perm), block, slots=inv[ids].astype(np.int32), algo=algo)
     assert torch.equal(base.view(torch.int32), moved.view(torch.int32))
     # a slot of -1 contributes nothing (vLLM's expert_map == -1)
     sl = ids.copy()
     sl[1, 2] = -1
     sl[3, 0] = -1
-    got, _ = _run_experts(x, ids, tw, w13, w2, s13, s2, block, slots=sl)
+    got, _ = _run_experts(x, ids, tw, w13, w2, s13, s2, block, slots=sl, algo=algo)
     # oracle: the absent pairs route to an extra expert the map marks absent
     ext = list(range(E)) + [0]
     emap = np.concatenate([np.zeros(E, np.int32), [-1]])
@@ -150,17 +159,54 @@ def test_experts_fp8_absent_slot_and_slot_placement():
     assert _rel(got, want) < REL_TOL
 
 
-def test_experts_fp8_batching_is_byte_invariant():
+@pytest.mark.parametrize("algo", ALGOS)
+def test_experts_fp8_batching_is_byte_invariant(algo):
     """A token's output does not depend on the other tokens of the launch
     (MFMA columns are independent), so grouping never changes bytes."""
     T, H, I, E, K, block = 6, 1024, 512, 8, 4, (128, 128)
     _, w13, w2, s13, s2 = _experts(E, H, I, block, seed=8)
     ids, tw = _routing(T, E, K, seed=9)
     x = torch.randn((T, H), generator=torch.Generator().manual_seed(10)).to(torch.bfloat16)
-    full, _ = _run_experts(x, ids, tw, w13, w2, s13, s2, block)
+    full, _ = _run_experts(x, ids, tw, w13, w2, s13, s2, block, algo=algo)
     for t in range(T):
-        one, _ = _run_experts(x[t:t + 1], ids[t:t + 1], tw[t:t + 1], w13, w2, s13, s2, block)
+        one, _ = _run_experts(x[t:t + 1], ids[t:t + 1], tw[t:t + 1], w13, w2, s13, s2, block,
+                              algo=algo)
         assert torch.equal(one[0].view(torch.int32), full[t].view(torch.int32)), t
+    halves = [_run_experts(x[a:b], ids[a:b], tw[a:b], w13, w2, s13, s2, block, algo=algo)[0]
+              for a, b in ((0, 2), (2, 6))]
+    assert torch.equal(torch.cat(halves).view(torch.int32), full.view(torch.int32))
+
+
+GROUPED = [  # T, H, I, E, K, block: tile widths 1, 2 and 4 per pass, odd k-block counts
+    (16, 2048, 768, 32, 8, (128, 128)),
+    (70, 1024, 384, 16, 4, (64, 128)),
+    (200, 512, 256, 24, 8, (128, 128)),
+    (40, 384, 640, 12, 2, (128, 128)),
+]
+
+
+@pytest.mark.parametrize("T,H,I,E,K,block", GROUPED)
+def test_experts_fp8_grouped_match_oracle(T, H, I, E, K, block):
+    _, w13, w2, s13, s2 = _experts(E, H, I, block, seed=T + 1)
+    ids, tw = _routing(T, E, K, seed=T + 2)
+    x = torch.randn((T, H), generator=torch.Generator().manual_seed(T)).to(torch.bfloat16)
+    out, act = _run_experts(x, ids, tw, w13, w2, s13, s2, block, algo=_lib.WISP_ALGO_MFMA)
+    want, want_act = F.moe_forward_fp8(x, tw, ids, w13, w2, s13, s2, block, return_act=True)
+    assert _rel(act, want_act) < REL_TOL
+    assert float(np.mean(act.numpy() == want_act)) > 0.95
+    assert _rel(out, want) < REL_TOL, _rel(out, want)
+
+
+def test_experts_fp8_decode_kernels_over_256_pairs():
+    """The decode kernels' in-memory slot scan (launches of more than 256
+    pairs) against the oracle."""
+    T, H, I, E, K, block = 40, 512, 256, 16, 8, (128, 128)
+    _, w13, w2, s13, s2 = _experts(E, H, I, block, seed=21)
+    ids, tw = _routing(T, E, K, seed=22)
+    x = torch.randn((T, H), generator=torch.Generator().manual_seed(23)).to(torch.bfloat16)
+    out, _ = _run_experts(x, ids, tw, w13, w2, s13, s2, block, algo=_lib.WISP_ALGO_GEMV)
+    want = F.moe_forward_fp8(x, tw, ids, w13, w2, s13, s2, block)
+    assert _rel(out, want) < REL_TOL
 
 
 def _fp8_state(wl, cap):
@@ -219,6 +265,30 @@ def test_fp8_state_subbatches_like_the_reference(small_fp8):
     assert len(res["groups"]) > 1
     assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
     assert st.slot_to_expert == ora.slot_to_expert and st.lru_tick == ora.lru_tick
+
+
+def test_fp8_state_prefill_paged_equals_full(small_fp8):
+    """A 64-token prefill chunk (grouped path) through cap=16: token groups,
+    each group's experts paged in; bytes equal the cap=E run and decisions
+    equal the reference pager's."""
+    wl = small_fp8
+    E, K, cap = 32, wl.shape.top_k, 16
+    st = _fp8_state(wl, cap)
+    full = _fp8_state(wl, E)
+    ora = PagerOracle(E, cap)
+    x = wl.x[:, 0].repeat(2, 1)[:64].contiguous().to(DEV)    # 48 steps, twice
+    lg = wl.logits[:, 0].repeat(2, 1)[:64].contiguous().to(DEV)
+    out = st.forward(x, lg, K, True)
+    ref = full.forward(x, lg, K, True)
+    res = ora.forward(route(lg.cpu(), K)[1].tolist())
+    torch.cuda.synchronize()
+    assert len(res["groups"]) > 1
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    assert st.slot_to_expert == ora.slot_to_expert and st.lru_tick == ora.lru_tick
+    w13, w2, s13, s2 = wl.views()
+    tw, ids = route(lg.cpu(), K)
+    want = F.moe_forward_fp8(x.cpu(), tw.astype(np.float32), ids, w13, w2, s13, s2)
+    assert _rel(out.float().cpu(), want) < REL_TOL
 
 
 def test_fp8_cap_clamp_above_num_experts(monkeypatch):

@@ -92,6 +92,7 @@ SIGNATURES = {
                                     _sz, _vp, _sz, _vp, _sz, _i32, _i32, _vp, _vp, _vp, _sz, _i32,
                                     _vp]),
     "wisp_quant_fp8_groups": (_i32, [_vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp]),
+    "wisp_moe_fp8_work_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),
     "wisp_layer_create": (_i32, [C.POINTER(LayerDesc), C.POINTER(_vp)]),
     "wisp_layer_destroy": (_i32, [_vp]),
     "wisp_layer_set_scratch": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp]),

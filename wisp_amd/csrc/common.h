@@ -49,6 +49,13 @@ struct StageEvents {
   hipEvent_t ev[4];
 };
 
+// Per slot s < nslots, the ascending list of the pairs p < P with
+// slots[p] == s (lists[s * P + j]) and its length (counts[s]); one wave per
+// slot, ballot compaction (deterministic).  Defined with the bf16 grouped
+// GEMM; the block-FP8 grouped path shares it.
+void launch_gather(const int32_t* slots, int P, int nslots, int32_t* lists, int32_t* counts,
+                   hipStream_t st);
+
 // Launch with or without dispatch timestamps.
 template <typename Kern, typename... Args>
 inline void launch_timed(Kern kernel, dim3 grid, dim3 block, hipStream_t st, hipEvent_t start,

@@ -50,6 +50,13 @@ int experts_fp8(const void* x, int T, int H, int I, int K, const float* topk_w,
                 const float* s2, size_t s2_stride, int block_n, void* act, void* out,
                 hipStream_t st, const StageEvents* ev);
 const char* fp8_unsupported(int H, int I, int K, int block_n, int block_k);
+int experts_fp8_grouped(const void* x, int T, int H, int I, int K, const float* topk_w,
+                        const int32_t* slots, int nslots, const void* w13, size_t w13_stride,
+                        const float* s13, size_t s13_stride, const void* w2, size_t w2_stride,
+                        const float* s2, size_t s2_stride, int block_n, void* act, void* out,
+                        void* work, size_t work_bytes, hipStream_t st, const StageEvents* ev);
+size_t fp8_work_bytes(int T, int K, int H, int I, int nslots);
+int auto_algo(int dtype, int H, int I, int T);
 
 namespace {
 
@@ -524,6 +531,199 @@ __global__ __launch_bounds__(NW * 64) void fp8_w2_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Grouped path for batches and prefill chunks: per slot, the pairs routed to
+// it (gather), x and act quantised once by the group quantiser, and each
+// weight tile streamed once per pass of up to MT * 16 token columns.
+//   fp8_grouped_w13: grid (I / 64, nslots), wave w owns gate rows
+//     [64 * bx + 16w, +16) and the matching up rows; act written as bf16;
+//   fp8_grouped_w2: grid (H / 64, nslots), y[p] = bf16(acc * topk_w[p]);
+//   fp8_combine: out[t] = moe_sum over k of y[(t, k)].
+// An output element is one chain over the k-blocks in ascending order, the
+// same for every MT, U and grouping, so bytes do not depend on which tokens
+// share a launch.  U k-blocks are loaded per iteration (nkb % U == 0).
+// ---------------------------------------------------------------------------
+template <int MT, int U>
+__global__ __launch_bounds__(256) void fp8_grouped_w13_kernel(
+    const uint8_t* __restrict__ xq, const float* __restrict__ xs, int H, int I, int K, int P,
+    const int32_t* __restrict__ lists, const int32_t* __restrict__ counts,
+    const uint8_t* __restrict__ w13, size_t w13_stride, const float* __restrict__ s13,
+    size_t s13_stride, int block_n, uint16_t* __restrict__ act) {
+  const int s = blockIdx.y;
+  const int M = counts[s];
+  if (M == 0) return;
+  const int32_t* list = lists + (size_t)s * P;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int col = lane & 15, grp = lane >> 4;
+  const int i0 = blockIdx.x * 64 + wave * 16;
+  const int nkb = H / kKB;
+  const uint8_t* Wg = w13 + (size_t)s * w13_stride + (size_t)(i0 + col) * H + grp * 32;
+  const uint8_t* Wu = Wg + (size_t)I * H;
+  const float* Sg = s13 + (size_t)s * s13_stride + (size_t)(i0 / block_n) * nkb;
+  const float* Su = s13 + (size_t)s * s13_stride + (size_t)((I + i0) / block_n) * nkb;
+  for (int m0 = 0; m0 < M; m0 += MT * 16) {
+    const int mrows = min(M - m0, MT * 16);
+    // the token of this lane's column in each tile (past the last row: a
+    // clamped copy, computed and not stored)
+    int tok[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) tok[t] = list[m0 + min(t * 16 + col, mrows - 1)] / K;
+    f32x4 ag[MT], au[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      ag[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+      au[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    for (int kb0 = 0; kb0 < nkb; kb0 += U) {
+      i32x8 wgr[U], wur[U], b[U][MT];
+      float sg[U], su[U], sx[U][MT];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        wgr[u] = ld32(Wg + (size_t)(kb0 + u) * kKB);
+        wur[u] = ld32(Wu + (size_t)(kb0 + u) * kKB);
+        sg[u] = Sg[kb0 + u];
+        su[u] = Su[kb0 + u];
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          b[u][t] = ld32(xq + (size_t)tok[t] * H + (size_t)(kb0 + u) * kKB + grp * 32);
+          sx[u][t] = xs[(size_t)tok[t] * nkb + kb0 + u];
+        }
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          if (t * 16 < mrows) {
+            const f32x4 dg = mfma_fp8(wgr[u], b[u][t]);
+            const f32x4 du = mfma_fp8(wur[u], b[u][t]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              ag[t][j] = ag[t][j] + (dg[j] * sx[u][t]) * sg[u];
+              au[t][j] = au[t][j] + (du[j] * sx[u][t]) * su[u];
+            }
+          }
+        }
+    }
+    // D[row][col]: weight row i0 + 4 * grp + j, token column col
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const int r = t * 16 + col;
+      if (r < mrows) {
+        const int p = list[m0 + r];
+        uint16_t* arow = act + (size_t)p * I + i0 + grp * 4;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float hg = round_bf16(ag[t][j]), hu = round_bf16(au[t][j]);
+          arow[j] = bf16_rne(round_bf16(silu(hg)) * hu);
+        }
+      }
+    }
+  }
+}
+
+template <int MT, int U>
+__global__ __launch_bounds__(256) void fp8_grouped_w2_kernel(
+    const uint8_t* __restrict__ aq, const float* __restrict__ as, int H, int I, int P,
+    const int32_t* __restrict__ lists, const int32_t* __restrict__ counts,
+    const float* __restrict__ topk_w, const uint8_t* __restrict__ w2, size_t w2_stride,
+    const float* __restrict__ s2, size_t s2_stride, int block_n, uint16_t* __restrict__ y) {
+  const int s = blockIdx.y;
+  const int M = counts[s];
+  if (M == 0) return;
+  const int32_t* list = lists + (size_t)s * P;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int col = lane & 15, grp = lane >> 4;
+  const int h0 = blockIdx.x * 64 + wave * 16;
+  const int nkb = I / kKB;
+  const uint8_t* Wr = w2 + (size_t)s * w2_stride + (size_t)(h0 + col) * I + grp * 32;
+  const float* S = s2 + (size_t)s * s2_stride + (size_t)(h0 / block_n) * nkb;
+  for (int m0 = 0; m0 < M; m0 += MT * 16) {
+    const int mrows = min(M - m0, MT * 16);
+    int pr[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) pr[t] = list[m0 + min(t * 16 + col, mrows - 1)];
+    f32x4 acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int kb0 = 0; kb0 < nkb; kb0 += U) {
+      i32x8 a[U], b[U][MT];
+      float sw[U], sa[U][MT];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        a[u] = ld32(Wr + (size_t)(kb0 + u) * kKB);
+        sw[u] = S[kb0 + u];
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          b[u][t] = ld32(aq + (size_t)pr[t] * I + (size_t)(kb0 + u) * kKB + grp * 32);
+          sa[u][t] = as[(size_t)pr[t] * nkb + kb0 + u];
+        }
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          if (t * 16 < mrows) {
+            const f32x4 d = mfma_fp8(a[u], b[u][t]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[t][j] = acc[t][j] + (d[j] * sa[u][t]) * sw[u];
+          }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const int r = t * 16 + col;
+      if (r < mrows) {
+        const int p = list[m0 + r];
+        const float w = topk_w[p];
+        uint16_t* yr = y + (size_t)p * H + h0 + grp * 4;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) yr[j] = bf16_rne(acc[t][j] * w);
+      }
+    }
+  }
+}
+
+// out[t, h] = moe_sum over k ascending of y[(t, k), h]: bf16 adds for K in
+// {2, 3, 4}, else one float32 sum rounded once.  grid = (ceil(H / 256), T).
+__global__ __launch_bounds__(256) void fp8_combine_kernel(const uint16_t* __restrict__ y, int H,
+                                                          int K, int nslots,
+                                                          const int32_t* __restrict__ slots,
+                                                          uint16_t* __restrict__ out) {
+  const int t = blockIdx.y;
+  const int h = blockIdx.x * 256 + threadIdx.x;
+  if (h >= H) return;
+  const bool bf16_adds = K >= 2 && K <= 4;
+  float sum = 0.f;
+  for (int k = 0; k < K; ++k) {
+    const int p = t * K + k;
+    const int s = slots[p];
+    const float v = (s < 0 || s >= nslots) ? 0.f : bf16f(y[(size_t)p * H + h]);
+    sum = bf16_adds ? round_bf16(sum + v) : sum + v;
+  }
+  out[(size_t)t * H + h] = bf16_rne(sum);
+}
+
+// Work buffer of the grouped path (bytes, each piece 256-byte aligned).
+struct Fp8Work {
+  size_t lists, counts, y, xq, xs, aq, as, total;
+  Fp8Work(int T, int K, int H, int I, int nslots) {
+    auto up = [](size_t b) { return (b + 255) & ~(size_t)255; };
+    const size_t P = (size_t)T * K;
+    lists = 0;
+    counts = up((size_t)nslots * P * 4);
+    y = counts + up((size_t)nslots * 4);
+    xq = y + up(P * H * 2);
+    xs = xq + up((size_t)T * H);
+    aq = xs + up((size_t)T * (H / kKB) * 4);
+    as = aq + up(P * I);
+    total = as + up(P * (I / kKB) * 4);
+  }
+};
+
 size_t w13_lds(int NW, int ncol) {
   return (size_t)NW * 2 * 64 * 4 * sizeof(float) + (size_t)NW * kKC * ncol * (4 + kKB);
 }
@@ -622,6 +822,82 @@ const char* fp8_unsupported(int H, int I, int K, int block_n, int block_k) {
   return nullptr;
 }
 
+template <int MT, int U>
+void launch_grouped(const uint8_t* xq, const float* xs, uint8_t* aq, float* as, int T, int H,
+                    int I, int K, int nslots, const int32_t* lists, const int32_t* counts,
+                    const float* topk_w, const uint8_t* w13, size_t w13_stride, const float* s13,
+                    size_t s13_stride, const uint8_t* w2, size_t w2_stride, const float* s2,
+                    size_t s2_stride, int block_n, uint16_t* act, uint16_t* y, hipStream_t st,
+                    const StageEvents* ev) {
+  const int P = T * K;
+  hipEvent_t e0 = ev ? ev->ev[0] : nullptr, e1 = ev ? ev->ev[1] : nullptr;
+  hipEvent_t e2 = ev ? ev->ev[2] : nullptr, e3 = ev ? ev->ev[3] : nullptr;
+  launch_timed(fp8_grouped_w13_kernel<MT, U>, dim3(I / 64, nslots), dim3(256), st, e0, e1, xq, xs,
+               H, I, K, P, lists, counts, w13, w13_stride, s13, s13_stride, block_n, act);
+  const long jobs = (long)P * (I / kKB);
+  hipLaunchKernelGGL(quant_groups_kernel<uint16_t>, dim3((unsigned)((jobs + 15) / 16)),
+                     dim3(256), 0, st, (const uint16_t*)act, P, I, aq, as);
+  launch_timed(fp8_grouped_w2_kernel<MT, U>, dim3(H / 64, nslots), dim3(256), st, e2, e3, aq, as,
+               H, I, P, lists, counts, topk_w, w2, w2_stride, s2, s2_stride, block_n, y);
+}
+
+size_t fp8_work_bytes(int T, int K, int H, int I, int nslots) {
+  if (T < 1 || K < 1 || H < kKB || I < kKB || nslots < 1) return 0;
+  return Fp8Work(T, K, H, I, nslots).total;
+}
+
+int experts_fp8_grouped(const void* x, int T, int H, int I, int K, const float* topk_w,
+                        const int32_t* slots, int nslots, const void* w13, size_t w13_stride,
+                        const float* s13, size_t s13_stride, const void* w2, size_t w2_stride,
+                        const float* s2, size_t s2_stride, int block_n, void* act, void* out,
+                        void* work, size_t work_bytes, hipStream_t st, const StageEvents* ev) {
+  if (T == 0) return WISP_OK;
+  const Fp8Work W(T, K, H, I, nslots);
+  if (nslots > 65535 || !work || work_bytes < W.total || ((uintptr_t)work) % 256) {
+    wisp_set_last_error("block-FP8 grouped path: work buffer missing, misaligned or too small",
+                        "FP8 experts");
+    return WISP_ERR_INVALID;
+  }
+  char* wb = (char*)work;
+  int32_t* lists = (int32_t*)(wb + W.lists);
+  int32_t* counts = (int32_t*)(wb + W.counts);
+  uint16_t* y = (uint16_t*)(wb + W.y);
+  uint8_t* xq = (uint8_t*)(wb + W.xq);
+  float* xs = (float*)(wb + W.xs);
+  uint8_t* aq = (uint8_t*)(wb + W.aq);
+  float* as = (float*)(wb + W.as);
+  const int P = T * K;
+  launch_gather(slots, P, nslots, lists, counts, st);
+  const long jobs = (long)T * (H / kKB);
+  hipLaunchKernelGGL(quant_groups_kernel<uint16_t>, dim3((unsigned)((jobs + 15) / 16)),
+                     dim3(256), 0, st, (const uint16_t*)x, T, H, xq, xs);
+  const uint8_t* a13 = (const uint8_t*)w13;
+  const uint8_t* a2 = (const uint8_t*)w2;
+  uint16_t* ab = (uint16_t*)act;
+  // two k-blocks per iteration when both k extents allow it; 16-token tiles
+  // per pass: a slot holds at most T tokens
+  const bool u2 = (H / kKB) % 2 == 0 && (I / kKB) % 2 == 0;
+  const int mt = T <= 16 ? 1 : T <= 128 ? 2 : 4;
+#define WISP_GROUPED(MT_, U_)                                                                 \
+  launch_grouped<MT_, U_>(xq, xs, aq, as, T, H, I, K, nslots, lists, counts, topk_w, a13,    \
+                          w13_stride, s13, s13_stride, a2, w2_stride, s2, s2_stride, block_n, \
+                          ab, y, st, ev)
+  if (u2) {
+    if (mt == 1) WISP_GROUPED(1, 2);
+    else if (mt == 2) WISP_GROUPED(2, 2);
+    else WISP_GROUPED(4, 2);
+  } else {
+    if (mt == 1) WISP_GROUPED(1, 1);
+    else if (mt == 2) WISP_GROUPED(2, 1);
+    else WISP_GROUPED(4, 1);
+  }
+#undef WISP_GROUPED
+  hipLaunchKernelGGL(fp8_combine_kernel, dim3((H + 255) / 256, T), dim3(256), 0, st, y, H, K,
+                     nslots, slots, (uint16_t*)out);
+  WISP_HIP_TRY(hipGetLastError());
+  return WISP_OK;
+}
+
 int experts_fp8(const void* x, int T, int H, int I, int K, const float* topk_w,
                 const int32_t* slots, int nslots, const void* w13, size_t w13_stride,
                 const float* s13, size_t s13_stride, const void* w2, size_t w2_stride,
@@ -704,16 +980,11 @@ extern "C" int wisp_moe_experts_fp8(const void* x, int T, int H, int I, int K,
                                     void* act, void* out, void* work, size_t work_bytes,
                                     int algo, wisp_stream_t stream) {
   using namespace wisp;
-  (void)work;
-  (void)work_bytes;
   if (T < 0 || K < 1 || K > kMaxTopK || nslots < 1 ||
       (T > 0 && (!x || !topk_w || !slots || !w13 || !w2 || !s13 || !s2 || !act || !out)))
     return WISP_ERR_INVALID;
-  if (algo != WISP_ALGO_AUTO && algo != WISP_ALGO_GEMV) {
-    wisp_set_last_error("block-FP8 experts have one kernel pair (WISP_ALGO_GEMV)",
-                        "wisp_moe_experts_fp8");
-    return WISP_ERR_UNSUPPORTED;
-  }
+  if (algo != WISP_ALGO_AUTO && algo != WISP_ALGO_GEMV && algo != WISP_ALGO_MFMA)
+    return WISP_ERR_INVALID;
   const char* why = fp8_unsupported(H, I, K, block_n, block_k);
   if (!why && (w13_stride % 16 || w2_stride % 16 || ((uintptr_t)w13) % 16 ||
                ((uintptr_t)w2) % 16 || ((uintptr_t)s13) % 4 || ((uintptr_t)s2) % 4 ||
@@ -724,6 +995,15 @@ extern "C" int wisp_moe_experts_fp8(const void* x, int T, int H, int I, int K,
     wisp_set_last_error(why, "wisp_moe_experts_fp8");
     return WISP_ERR_UNSUPPORTED;
   }
+  const int a = algo == WISP_ALGO_AUTO ? auto_algo(WISP_FP8_E4M3, H, I, T) : algo;
+  if (a == WISP_ALGO_MFMA)
+    return experts_fp8_grouped(x, T, H, I, K, topk_w, slots, nslots, w13, w13_stride, s13,
+                               s13_stride, w2, w2_stride, s2, s2_stride, block_n, act, out, work,
+                               work_bytes, (hipStream_t)stream, nullptr);
   return experts_fp8(x, T, H, I, K, topk_w, slots, nslots, w13, w13_stride, s13, s13_stride, w2,
                      w2_stride, s2, s2_stride, block_n, act, out, (hipStream_t)stream, nullptr);
+}
+
+extern "C" size_t wisp_moe_fp8_work_bytes(int T, int K, int H, int I, int nslots) {
+  return wisp::fp8_work_bytes(T, K, H, I, nslots);
 }

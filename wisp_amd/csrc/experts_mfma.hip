@@ -446,6 +446,11 @@ void launch_gemms(const uint16_t* x, int H, int I, int K, int P, int nslots, con
 
 }  // namespace
 
+void launch_gather(const int32_t* slots, int P, int nslots, int32_t* lists, int32_t* counts,
+                   hipStream_t st) {
+  hipLaunchKernelGGL(gather_kernel, dim3(nslots), dim3(64), 0, st, slots, P, lists, counts);
+}
+
 size_t mfma_work_bytes(int T, int K, int H, int nslots) {
   if (T < 1 || K < 1 || H < 1 || nslots < 1) return 0;
   return WorkLayout(T * K, H, nslots).total;

@@ -83,6 +83,11 @@ int experts_fp8(const void* x, int T, int H, int I, int K, const float* topk_w,
                 const float* s2, size_t s2_stride, int block_n, void* act, void* out,
                 hipStream_t st, const StageEvents* ev);
 const char* fp8_unsupported(int H, int I, int K, int block_n, int block_k);
+int experts_fp8_grouped(const void* x, int T, int H, int I, int K, const float* topk_w,
+                        const int32_t* slots, int nslots, const void* w13, size_t w13_stride,
+                        const float* s13, size_t s13_stride, const void* w2, size_t w2_stride,
+                        const float* s2, size_t s2_stride, int block_n, void* act, void* out,
+                        void* work, size_t work_bytes, hipStream_t st, const StageEvents* ev);
 int launch_prefetch(const int32_t* predicted, const int32_t* n_pred_ptr, int n_pred, int ordered,
                     int count_pred, const int32_t* last_ids, int n_last, int E, int cap,
                     int max_pred, int32_t* map, int32_t* s2e, int64_t* tick, int64_t* ctr,
@@ -101,7 +106,7 @@ constexpr int kMfmaMinTokens = 16;
 // shape and token count, never on the grouping or the slots, so paged and
 // resident runs of one batch use one kernel.
 int auto_algo(int dtype, int H, int I, int T) {
-  if (dtype == WISP_FP8_E4M3) return WISP_ALGO_GEMV;
+  if (dtype == WISP_FP8_E4M3) return T >= kMfmaMinTokens ? WISP_ALGO_MFMA : WISP_ALGO_GEMV;
   return dtype == WISP_BF16 && mfma_supported(H, I) && T >= kMfmaMinTokens ? WISP_ALGO_MFMA
                                                                           : WISP_ALGO_GEMV;
 }
@@ -432,10 +437,17 @@ int experts(Layer& L, const void* x, int T, int K, const float* w, const int32_t
     ProfLaunch* p2 = prof_begin(L, 1);
     StageEvents ev = {{p13 ? p13->start : nullptr, p13 ? p13->stop : nullptr,
                        p2 ? p2->start : nullptr, p2 ? p2->stop : nullptr}};
-    int rc = experts_fp8(x, T, d.hidden, d.inter, K, w, slots, d.cap, d.scratch_w13,
-                         d.scratch_w13_stride, d.scratch_s13, d.scratch_s13_stride, d.scratch_w2,
-                         d.scratch_w2_stride, d.scratch_s2, d.scratch_s2_stride, d.block_n, act,
-                         out, st, (p13 && p2) ? &ev : nullptr);
+    const StageEvents* pe = (p13 && p2) ? &ev : nullptr;
+    int rc = algo == WISP_ALGO_MFMA
+                 ? experts_fp8_grouped(x, T, d.hidden, d.inter, K, w, slots, d.cap,
+                                       d.scratch_w13, d.scratch_w13_stride, d.scratch_s13,
+                                       d.scratch_s13_stride, d.scratch_w2, d.scratch_w2_stride,
+                                       d.scratch_s2, d.scratch_s2_stride, d.block_n, act, out,
+                                       ws->work, ws->work_bytes, st, pe)
+                 : experts_fp8(x, T, d.hidden, d.inter, K, w, slots, d.cap, d.scratch_w13,
+                               d.scratch_w13_stride, d.scratch_s13, d.scratch_s13_stride,
+                               d.scratch_w2, d.scratch_w2_stride, d.scratch_s2,
+                               d.scratch_s2_stride, d.block_n, act, out, st, pe);
     if (rc == WISP_OK && p13 && p2) p13->pending = p2->pending = true;
     return rc;
   }
@@ -459,8 +471,9 @@ int experts(Layer& L, const void* x, int T, int K, const float* w, const int32_t
 int choose_algo(const Layer& L, int algo, int T) {
   const wisp_layer_desc& d = L.d;
   if (algo == WISP_ALGO_AUTO) return auto_algo(d.dtype, d.hidden, d.inter, T);
-  if (algo == WISP_ALGO_MFMA && (d.dtype != WISP_BF16 || !mfma_supported(d.hidden, d.inter)))
-    return -1;  // block-FP8 experts have one kernel pair, selected as GEMV
+  if (algo == WISP_ALGO_MFMA && d.dtype == WISP_F32) return -1;
+  if (algo == WISP_ALGO_MFMA && d.dtype == WISP_BF16 && !mfma_supported(d.hidden, d.inter))
+    return -1;
   if (algo != WISP_ALGO_GEMV && algo != WISP_ALGO_MFMA) return -1;
   return algo;
 }

@@ -118,8 +118,9 @@ class _Workspace:
     """Per-layer device workspaces and the pinned decision record, grown on demand."""
 
     def __init__(self, device: torch.device, hidden: int, inter: int,
-                 dtype: torch.dtype) -> None:
+                 dtype: torch.dtype, fp8: bool = False) -> None:
         self.device, self.hidden, self.inter, self.dtype = device, hidden, inter, dtype
+        self.fp8 = fp8
         self.pairs = 0
         self.record_words = 0
         self.work_bytes = 0
@@ -143,9 +144,11 @@ class _Workspace:
         if words > self.record_words:
             self.record_words = max(words, 2 * self.record_words)
             self.record = torch.zeros(self.record_words, dtype=torch.int32, pin_memory=True)
-        # the bf16 MFMA path's per-slot pair lists and fp32 per-pair outputs
+        # the grouped (MFMA) paths' per-slot pair lists and per-pair outputs
         need = 0
-        if self.dtype == torch.bfloat16 and self.hidden > 0:
+        if self.fp8 and self.hidden > 0:
+            need = lib().wisp_moe_fp8_work_bytes(max(1, T), K, self.hidden, self.inter, nslots)
+        elif self.dtype == torch.bfloat16 and self.hidden > 0:
             need = lib().wisp_moe_work_bytes(max(1, T), K, self.hidden, nslots)
         if need > self.work_bytes:
             self.work_bytes = max(need, 2 * self.work_bytes)

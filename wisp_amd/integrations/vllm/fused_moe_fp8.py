@@ -178,7 +178,7 @@ class WispMoEStateFP8(WispMoEState):
         self._pf_record = None
         self._pf_words = 0
         self._pf_n = 0
-        self._ws = _Workspace(dev, self.hidden, I, torch.bfloat16)
+        self._ws = _Workspace(dev, self.hidden, I, torch.bfloat16, fp8=True)
         self._last_pairs = 0
         self._handle = C.c_void_p()
         self._desc = self._make_desc()
@@ -416,11 +416,14 @@ def route_and_experts_fp8(x, router_logits, top_k, renormalize, w13, w2, s13, s2
                                         topk_ids.data_ptr(), None, st), "route")
     act = torch.empty((max(1, T * top_k), I), dtype=torch.bfloat16, device=dev)
     out = torch.empty_like(x)
+    nbytes = lib().wisp_moe_fp8_work_bytes(max(1, T), top_k, H, I, E)
+    work = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     check(lib().wisp_moe_experts_fp8(
         x.data_ptr(), T, H, I, top_k, topk_w.data_ptr(), topk_ids.data_ptr(), E,
         w13.data_ptr(), w13.stride(0), s13.data_ptr(), s13.stride(0), w2.data_ptr(),
         w2.stride(0), s2.data_ptr(), s2.stride(0), int(block[0]), int(block[1]),
-        act.data_ptr(), out.data_ptr(), None, 0, _lib.WISP_ALGO_AUTO, st), "experts_fp8")
+        act.data_ptr(), out.data_ptr(), work.data_ptr(), nbytes, _lib.WISP_ALGO_AUTO, st),
+        "experts_fp8")
     return out
 
 
