@@ -27,6 +27,7 @@ default line above is the one the benchmark is quoted on):
   stack     48 Qwen3 layers, cap=24 each, bs=1 decode through the stack
   fp8       the default decode line on the Qwen3-30B-A3B-FP8 layer (e4m3fn
             weights with [128, 128] float32 block scales, w8a8)
+  fp8-prefill, fp8-batch32   the prefill and batch32 lines on that FP8 layer
 """
 from __future__ import annotations
 
@@ -39,6 +40,7 @@ import time
 
 HBM_PEAK_GBPS = 8000.0          # MI355X HBM3E, GB/s
 BF16_PEAK_TFLOPS = 2500.0       # dense bf16 MFMA
+FP8_PEAK_TFLOPS = 5000.0        # dense fp8 MFMA
 METRIC = "MoE decode tok/s, Qwen3-30B-A3B shape bs=1 cap=8; expert GEMM % HBM peak"
 
 
@@ -411,6 +413,81 @@ def cpu_baseline_fp8(routes, views, seconds: float, warm: int = 2) -> dict:
                       f"page-in); {cpu_name()}"}
 
 
+def _fp8_state_run(wl, cap: int, n_warm: int, n: int):
+    """``_state_run`` for a block-FP8 workload: ``n`` timed layer calls on a
+    fresh FP8 state with ``cap`` slots (cap = E: every expert stays resident
+    after its first call)."""
+    import torch
+
+    from wisp_amd.integrations.vllm.fused_moe_fp8 import WispMoEStateFP8
+    dev = torch.device("cuda", 0)
+    K = wl.shape.top_k
+    xs, lgs = wl.x.to(dev), wl.logits.to(dev)
+    out = torch.empty_like(xs[0])
+    st = WispMoEStateFP8(*wl.views(), cap, dev, 0)
+    r = _timed(lambda i: st.forward(xs[i % wl.steps], lgs[i % wl.steps], K, True, out=out),
+               n_warm, n, [st])
+    del st
+    torch.cuda.empty_cache()
+    return r
+
+
+def _fp8_gemm_report(agg: dict, wl, tokens_per_call: int, distinct_per_call: float) -> dict:
+    sh = wl.shape
+    calls = max(1, agg["calls"])
+    t = (agg["w13_ms"] + agg["w2_ms"]) / calls * 1e-3
+    flops = 2.0 * tokens_per_call * sh.top_k * 3 * sh.hidden * sh.inter
+    byts = distinct_per_call * wl.expert_bytes
+    return {"kernels": "fp8_grouped_w13_kernel + fp8_grouped_w2_kernel",
+            "avg_us_per_call": round(t * 1e6, 2),
+            "w13_us": round(agg["w13_ms"] / calls * 1e3, 2),
+            "w2_us": round(agg["w2_ms"] / calls * 1e3, 2),
+            "achieved_TFLOPs": round(flops / t / 1e12, 2) if t else None,
+            "frac_fp8_mfma_peak": round(flops / t / 1e12 / FP8_PEAK_TFLOPS, 4) if t else None,
+            "achieved_GBps": round(byts / t / 1e9, 1) if t else None,
+            "frac_hbm_peak": round(byts / t / 1e9 / HBM_PEAK_GBPS, 4) if t else None,
+            "bytes_per_call": int(byts), "flops_per_call": int(flops)}
+
+
+def bench_fp8_prefill(args) -> dict:
+    from wisp_amd import workloads as W
+    wl = W.fp8_layer(W.gaussian_logits("batch", seed=0, steps=3, tokens=512, weights=False),
+                     pin=True)
+    sh = wl.shape
+    pe, pa = _fp8_state_run(wl, sh.cap, 1, 2)
+    re_, ra = _fp8_state_run(wl, sh.experts, 3, 20)
+    dist = sum(_distinct(wl.logits[i], 8) for i in range(wl.steps)) / wl.steps
+    line = _line("MoE prefill tok/s, Qwen3-30B-A3B-FP8 shape, 512-token chunk, cap=32 paged",
+                 2 * 512 / pe, "tok/s", args, 2, pe,
+                 {"workload": "qwen3-fp8 moe layer, 512-token prefill chunk, router logits N(0,1)",
+                  "hidden": sh.hidden, "expert_intermediate": sh.inter, "experts": sh.experts,
+                  "top_k": sh.top_k, "cap": sh.cap, "tokens": 512, "weight_block": list(wl.block)},
+                 pagein=_pagein_report(pa),
+                 resident={"tok_per_s": round(20 * 512 / re_, 1),
+                           "expert_gemm": _fp8_gemm_report(ra, wl, 512, dist)})
+    line["dtype"] = "fp8_e4m3 (bf16 activations, f32 accumulate)"
+    return line
+
+
+def bench_fp8_batch32(args) -> dict:
+    from wisp_amd import workloads as W
+    wl = W.fp8_layer(W.batch_decode(steps=24, tokens=32, weights=False), pin=True)
+    sh = wl.shape
+    pe, pa = _fp8_state_run(wl, sh.cap, 2, 16)
+    re_, ra = _fp8_state_run(wl, sh.experts, 24, 128)
+    dist = sum(_distinct(wl.logits[i], 8) for i in range(wl.steps)) / wl.steps
+    line = _line("MoE batched decode tok/s, Qwen3-30B-A3B-FP8 shape, bs=32, cap=32 paged",
+                 16 * 32 / pe, "tok/s", args, 16, pe,
+                 {"workload": "qwen3-fp8 moe layer, bs=32 decode, router logits N(0,1)",
+                  "hidden": sh.hidden, "expert_intermediate": sh.inter, "experts": sh.experts,
+                  "top_k": sh.top_k, "cap": sh.cap, "batch": 32, "weight_block": list(wl.block)},
+                 pagein=_pagein_report(pa),
+                 resident={"tok_per_s": round(128 * 32 / re_, 1),
+                           "expert_gemm": _fp8_gemm_report(ra, wl, 32, dist)})
+    line["dtype"] = "fp8_e4m3 (bf16 activations, f32 accumulate)"
+    return line
+
+
 def bench_fp8(args) -> dict:
     """The default decode measurement on the block-FP8 twin of the Qwen3
     layer: same routing sequences, eight layer instances sharing one set of
@@ -495,7 +572,8 @@ def main() -> int:
                     help="time bound of the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", default="qwen3",
-                    choices=["qwen3", "prefill", "batch32", "mixtral", "stack", "fp8"])
+                    choices=["qwen3", "prefill", "batch32", "mixtral", "stack", "fp8",
+                             "fp8-prefill", "fp8-batch32"])
     ap.add_argument("--prefetch", action="store_true",
                     help="stack workload: cross-layer speculative prefetch with a co-occurrence "
                          "table learned online (WISP_PREFETCH=1, WISP_COOCCUR_ONLINE=1)")
@@ -507,7 +585,8 @@ def main() -> int:
 
     if args.workload != "qwen3":
         line = {"prefill": bench_prefill, "batch32": bench_batch32, "mixtral": bench_mixtral,
-                "stack": bench_stack, "fp8": bench_fp8}[args.workload](args)
+                "stack": bench_stack, "fp8": bench_fp8, "fp8-prefill": bench_fp8_prefill,
+                "fp8-batch32": bench_fp8_batch32}[args.workload](args)
         print(json.dumps(line), flush=True)
         return 0
 
