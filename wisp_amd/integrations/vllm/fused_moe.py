@@ -477,8 +477,14 @@ def num_experts_per_layer() -> int | None:
 
 
 def expert_bytes_per_cap() -> int:
-    """HBM bytes of one scratch slot summed over the registered layers."""
-    return sum(st._slab_elems * st._scratch.element_size() for st in _LAYER_STATES)
+    """HBM bytes one scratch slot holds (its w13 and w2), summed over the
+    registered layers: what changing the per-layer cap by one slot frees or
+    claims (reference 571-582)."""
+    total = 0
+    for st in _LAYER_STATES:
+        total += st.scratch_w13[0].numel() * st.scratch_w13.element_size()
+        total += st.scratch_w2[0].numel() * st.scratch_w2.element_size()
+    return total
 
 
 def snapshot_expert_stats(reset: bool = True) -> dict:
