@@ -257,7 +257,7 @@ def bench_prefill(args) -> dict:
                  pagein=_pagein_report(pa),
                  resident={"tok_per_s": round(20 * 512 / re_, 1),
                            "expert_gemm": _gemm_report(ra, sh, 512, dist,
-                                                       "mfma_w13_kernel + mfma_w2_kernel")},
+                                                       "mfma_w13_dma_kernel + mfma_w2_dma_kernel")},
                  cpu_baseline=cpu)
 
 
@@ -277,7 +277,7 @@ def bench_batch32(args) -> dict:
                  pagein=_pagein_report(pa),
                  resident={"tok_per_s": round(128 * 32 / re_, 1),
                            "expert_gemm": _gemm_report(ra, sh, 32, dist,
-                                                       "mfma_w13_kernel + mfma_w2_kernel")},
+                                                       "mfma_w13_dma_kernel + mfma_w2_dma_kernel")},
                  cpu_baseline=cpu)
 
 

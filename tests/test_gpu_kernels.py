@@ -203,6 +203,50 @@ def test_experts_mfma_bf16(T, H, I, E, K):
     assert rel_err(out, moe_forward(x, w, ids, w13, w2, act_round="bf16")) < 4e-3
 
 
+def _counted_case(seed, counts, H, I):
+    """K = 2 routing where expert e receives exactly counts[e] tokens: the
+    sorted expert labels are dealt to (token t, k = 0) for the first T labels
+    and (t, k = 1) for the rest, so no token meets an expert twice while every
+    count is at most T."""
+    labels = np.repeat(np.arange(len(counts)), counts)
+    T = len(labels) // 2
+    assert len(labels) == 2 * T and max(counts) <= T
+    ids = np.stack([labels[:T], labels[T:]], axis=1).astype(np.int64)
+    g = torch.Generator().manual_seed(seed)
+    E = len(counts)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    w13 = (torch.randn(E, 2 * I, H, generator=g) * 0.02).to(torch.bfloat16)
+    w2 = (torch.randn(E, H, I, generator=g) * 0.02).to(torch.bfloat16)
+    w = torch.rand(T, 2, generator=g).numpy().astype(np.float32) + 0.1
+    return x, w, ids, w13, w2
+
+
+# Slot sizes at every edge of the 16-token tiles and 64-token passes of the
+# prefill kernels (more than 128 tokens per call): empty, 1, 15/16/17,
+# 33, 48/49, 64/65 and a three-pass slot.
+@pytest.mark.parametrize("H,I", [(512, 256), (2048, 768)])
+def test_experts_mfma_prefill_slot_sizes(H, I):
+    counts = [0, 1, 15, 16, 17, 33, 48, 49, 64, 65, 130, 2]
+    x, w, ids, w13, w2 = _counted_case(H + I, counts, H, I)
+    assert x.shape[0] > 128
+    out = run_experts(*_dev_case(x, w, ids, w13, w2), algo=MFMA)
+    assert rel_err(out, moe_forward(x, w, ids, w13, w2)) < 1e-2
+    assert rel_err(out, moe_forward(x, w, ids, w13, w2, act_round="bf16")) < 4e-3
+
+
+def test_mfma_prefill_bytes_independent_of_grouping():
+    # a token's bytes are the same whether the call holds 300 tokens (LDS-
+    # staged prefill kernels), 150 or 40 (direct-load kernels)
+    x, w, ids, w13, w2 = _expert_case(31, 300, 1024, 512, 16, 8, torch.bfloat16)
+    xd, wd, idd, w13d, w2d = _dev_case(x, w, ids, w13, w2)
+    whole = run_experts(xd, wd, idd, w13d, w2d, algo=MFMA)
+    assert rel_err(whole, moe_forward(x, w, ids, w13, w2, act_round="bf16")) < 4e-3
+    for a, b in [(0, 150), (150, 300), (100, 140)]:
+        part = run_experts(xd[a:b].contiguous(), wd[a:b].contiguous(), idd[a:b].contiguous(),
+                           w13d, w2d, algo=MFMA)
+        assert torch.equal(part.view(torch.int16), whole[a:b].view(torch.int16)), (a, b)
+
+
 def test_experts_mfma_absent_slot_contributes_zero():
     x, w, ids, w13, w2 = _expert_case(6, 20, 512, 256, 8, 2, torch.bfloat16)
     slots = torch.tensor(ids, dtype=torch.int32)

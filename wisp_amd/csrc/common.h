@@ -66,6 +66,16 @@ inline void launch_timed(Kern kernel, dim3 grid, dim3 block, hipStream_t st, hip
     hipLaunchKernelGGL(kernel, grid, block, 0, st, args...);
 }
 
+// launch_timed with lds bytes of dynamic LDS per block.
+template <typename Kern, typename... Args>
+inline void launch_timed_lds(Kern kernel, dim3 grid, dim3 block, unsigned lds, hipStream_t st,
+                             hipEvent_t start, hipEvent_t stop, Args... args) {
+  if (start)
+    hipExtLaunchKernelGGL(kernel, grid, block, lds, st, start, stop, 0, args...);
+  else
+    hipLaunchKernelGGL(kernel, grid, block, lds, st, args...);
+}
+
 }  // namespace wisp
 
 #define WISP_HIP_TRY(expr)                               \

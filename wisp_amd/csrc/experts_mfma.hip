@@ -10,11 +10,13 @@
 //
 // Four launches:
 //   1. gather: per slot s, the ascending list of pairs routed to s and its
-//      length (one wave per slot, ballot compaction - stable, deterministic);
+//      length (block-wide ballot compaction - stable, deterministic);
 //   2. w13: block (i-panel of 64, slot s) streams the 64 gate rows and 64 up
 //      rows of the panel once per 64 tokens of s and multiplies them against
-//      those tokens, 16 per MFMA tile (v_mfma_f32_16x16x32_bf16), with the
-//      token fragments read from the L2-resident x rows; epilogue silu(g) * u;
+//      those tokens, 16 per MFMA tile (v_mfma_f32_16x16x32_bf16); epilogue
+//      silu(g) * u.  Up to 16 tokens per call the fragments are loaded straight
+//      into registers (the tokens from the L2-resident x rows); above that
+//      both operands are staged through LDS by asynchronous global->LDS copies;
 //   3. w2: block (h-panel of 64, slot s) likewise over act, writing fp32 y;
 //   4. combine: out[t] from y in routing order.
 // Each output element is one MFMA dot product chain over K in a fixed order,
@@ -37,8 +39,6 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kKAlign = 256;         // H and I must be multiples (up to 8 k-steps per iteration)
 constexpr int kPanel = 64;           // output columns per block: 4 waves x 16
-constexpr int kMaxMT = 4;            // 16-token tiles per pass (64 tokens); more tokens
-                                     // on a slot take further passes over its weights
 
 // Weight and token fragments alike use plain loads: here the nontemporal
 // hint made every variant slower (measured on MI355X at the Qwen3 shape: -8 %
@@ -69,22 +69,54 @@ struct WorkLayout {
 
 // ---------------------------------------------------------------------------
 // 1. gather: lists[s * P + j] = j-th pair (ascending) with slots[p] == s.
-// grid = nslots, block = one wave.
+// grid = nslots, block = 512 threads; each iteration covers 4096 pairs, 8
+// consecutive ones per thread, and places the matches by a block-wide
+// exclusive prefix of the per-thread counts (counts <= 8: four ballots per
+// wave for the bits, one LDS exchange across the eight waves).
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(64) void gather_kernel(const int32_t* __restrict__ slots, int P,
-                                                    int32_t* __restrict__ lists,
-                                                    int32_t* __restrict__ counts) {
-  const int s = blockIdx.x, lane = threadIdx.x;
+constexpr int kGatherPer = 8;
+constexpr int kGatherWaves = 8;
+
+__global__ __launch_bounds__(64 * kGatherWaves) void gather_kernel(
+    const int32_t* __restrict__ slots, int P, int32_t* __restrict__ lists,
+    int32_t* __restrict__ counts) {
+  __shared__ int wave_total[kGatherWaves];
+  const int s = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   int32_t* L = lists + (size_t)s * P;
-  int n = 0;
-  for (int base = 0; base < P; base += 64) {
-    const int p = base + lane;
-    const bool m = p < P && slots[p] == s;
-    const uint64_t b = __ballot(m);
-    if (m) L[n + __popcll(b & ((1ull << lane) - 1ull))] = p;
-    n += __popcll(b);
+  const uint64_t below = (1ull << lane) - 1ull;
+  int n = 0;  // matches before this iteration (block-uniform)
+  for (int base = 0; base < P; base += 64 * kGatherWaves * kGatherPer) {
+    const int p0 = base + tid * kGatherPer;
+    int v[kGatherPer];
+#pragma unroll
+    for (int q = 0; q < kGatherPer; ++q) v[q] = p0 + q < P ? slots[p0 + q] : -1;
+    unsigned hit = 0;
+#pragma unroll
+    for (int q = 0; q < kGatherPer; ++q) hit |= (unsigned)(v[q] == s) << q;
+    const int c = __popc(hit);
+    int pre = 0, tot = 0;
+#pragma unroll
+    for (int bit = 0; bit < 4; ++bit) {
+      const uint64_t m = __ballot((c >> bit) & 1);
+      pre += __popcll(m & below) << bit;
+      tot += __popcll(m) << bit;
+    }
+    if (lane == 0) wave_total[wave] = tot;
+    __syncthreads();
+    int off = n, all = 0;
+#pragma unroll
+    for (int w = 0; w < kGatherWaves; ++w) {
+      off += w < wave ? wave_total[w] : 0;
+      all += wave_total[w];
+    }
+    __syncthreads();  // wave_total is rewritten by the next iteration
+    int o = off + pre;
+#pragma unroll
+    for (int q = 0; q < kGatherPer; ++q)
+      if (hit >> q & 1u) L[o++] = p0 + q;
+    n += all;
   }
-  if (lane == 0) counts[s] = n;
+  if (tid == 0) counts[s] = n;
 }
 
 // Row pointers of this lane's A rows (row lane%16 of each 16-token tile of
@@ -237,156 +269,249 @@ __global__ __launch_bounds__(256) void mfma_w2_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Software-pipelined variants for slots with many tokens (prefill).  The
-// token tile of the pass (MT*16 rows) is staged through double-buffered LDS,
-// 32*U columns at a time and shared by the four waves; each wave keeps the
-// next chunk's weight fragments in flight in registers while it runs the
-// MFMAs of the current chunk.  One barrier per chunk, and it waits only for
-// LDS operations, so the weight loads stay in flight across it; the token
-// loads of a chunk are issued before its weight loads, so storing them to
-// LDS does not wait for the weights either.  Each thread's token rows are
-// resolved once per pass.  Measured on MI355X at the Qwen3 shape, resident
-// 512-token chunk: w13 231 -> 178 us and w2 136 -> 99 us against a block
-// barrier, weight-then-token issue order, per-chunk row lookups and
-// nontemporal weight loads.
+// LDS-staged panels for prefill: the weight panel and the token tile of each
+// C-column chunk are copied from global memory straight into LDS by the
+// asynchronous global->LDS loads (global_load_lds_dwordx4), S - 1 chunks
+// ahead, so neither operand passes through registers and each chunk's data
+// was requested S - 1 chunks before it is used.  Per block (four waves):
+//   weights: wave w's own rows (w13: 16 gate + 16 up, w2: 16), one slice per
+//            wave and stage, read only by that wave;
+//   tokens:  the 16 * NT rows of the NT tiles the pass fills (NT <= 4),
+//            shared by the waves, copy j of the tile issued by wave j % 4.
+// One copy instruction moves 1 KiB: 8 rows of 128 bytes.  Each LDS row holds
+// its 16-byte column blocks XOR-swizzled by the row (block cb at position
+// cb ^ (row & 7)), so the MFMA operand reads of 16 rows at one column block
+// spread over the banks.  Rows past the pass's last token copy a valid row;
+// their results are never stored.  Each wave waits for its own copies by
+// vmcnt (a constant per chunk), then one barrier per chunk: after it, every
+// wave's copies of the chunk have landed and every wave is done with the
+// stage the next copy overwrites.
+// What bounds these kernels: with the weights row-major, a chunk takes 128
+// bytes from each of 128 rows 4 KiB apart, and a pure read of the Qwen3 w13
+// tensor in that order runs at 4.7 TB/s on MI355X (4.5-5.1 TB/s for 128 B to
+// 1 KiB per row and 1-3 blocks per CU), against 6.2 TB/s for the same bytes
+// read as contiguous 512 KiB panels; w13 here runs at 4.7 TB/s.
 // ---------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void lds_void;
 
-// Block barrier that waits only for this wave's LDS operations.
+// Block barrier that waits only for this wave's LDS operations (its
+// global->LDS copies are waited for by vmcnt, explicitly, beforehand).
 __device__ inline void lds_barrier() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt/expcnt left at max
   __builtin_amdgcn_s_barrier();
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
-template <int MT, int U>
-struct PipeA {
-  static constexpr int kCols = 32 * U;
-  static constexpr int kLd = kCols + 8;                  // padded row (bf16)
-  static constexpr int kVecs = MT * 16 * kCols / 8;      // 16-byte vectors per chunk
-  static constexpr int kPer = (kVecs + 255) / 256;       // per thread
+
+constexpr int kDmaTokRows = 64;  // 4 MFMA tiles of 16 tokens
+
+// Chunk geometry for C bf16 columns per chunk.
+template <int C>
+struct DmaGeo {
+  static_assert(C == 64, "chunk width: 128-byte rows (8 rows per copy)");
+  static constexpr int kRowBytes = 2 * C;
+  static constexpr int kRowsPerCopy = 1024 / kRowBytes;
+  static constexpr int kLanesPerRow = kRowBytes / 16;
 };
 
-// Row pointers of this thread's share of the A tile: vector q of the thread
-// is row idx / kRowVecs, 8 columns at (idx % kRowVecs) * 8 of each chunk
-// (null past the pass's last row: loads as zero).
-template <int MT, int U, bool kTokenRows, int NPER>
-__device__ inline void pipe_rows(const uint16_t* (&rp)[NPER], const uint16_t* __restrict__ A,
-                                 int ld, int K, const int32_t* __restrict__ list, int m0,
-                                 int mrows) {
-  constexpr int kRowVecs = PipeA<MT, U>::kCols / 8;
+// Token copies per wave at most: 64 rows = 64 / rows-per-copy copies over 4
+// waves (2 for 64-column chunks).
+constexpr int kDmaMaxTokCopies = 2;
+
+// 16 bytes per lane from g into LDS at dst + 16 * lane.
+__device__ inline void dma16(const void* g, void* dst) {
+  __builtin_amdgcn_global_load_lds(g, (lds_void*)dst, 16, 0, 0);
+}
+
+// Waits until at most N of this wave's vector memory operations are
+// outstanding.
+template <int N>
+__device__ inline void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// Waits for the copies of the chunk that has `ahead` later chunks issued
+// behind it (each chunk is PER copy instructions per wave).
+template <int PER, int A>
+__device__ inline void wait_chunk(int ahead) {
+  if constexpr (A > 0) {
+    if (ahead >= A) {
+      wait_vm<A * PER>();
+      return;
+    }
+    wait_chunk<PER, A - 1>(ahead);
+  } else {
+    wait_vm<0>();
+  }
+}
+
+// Byte offset of column block cb of row r in a swizzled slice of C columns.
+template <int C>
+__device__ inline int swz(int r, int cb) {
+  return r * DmaGeo<C>::kRowBytes + ((cb ^ (r & 7)) << 4);
+}
+
+// NWR weight rows per wave (32 for w13: gate then up; 16 for w2).
+template <int NWR, int S, int C>
+struct DmaSmem {
+  static constexpr int kW = 4 * NWR * DmaGeo<C>::kRowBytes;       // weight slices of a stage
+  static constexpr int kA = kDmaTokRows * DmaGeo<C>::kRowBytes;   // token tile of a stage
+  static constexpr int kStage = kW + kA;
+  static constexpr int kBytes = S * kStage;
+};
+
+// One stage's copies for the chunk at column k0: this wave's weight rows and
+// its TCW token copies.  wrow[i] / arow[i] are the lane's source rows
+// (element pointers); the token copies of a wave are copies wave + 4i of the
+// tile, copy j covering tile rows [j * rows-per-copy, (j + 1) * rows-per-copy).
+template <int NWR, int C, int TCW>
+__device__ inline void dma_chunk(unsigned char* stage,
+                                 const uint16_t* const (&wrow)[NWR / DmaGeo<C>::kRowsPerCopy],
+                                 const uint16_t* const (&arow)[kDmaMaxTokCopies], int wave,
+                                 int lane, int k0) {
+  using G = DmaGeo<C>;
+  const int pos = lane % G::kLanesPerRow, sub = lane / G::kLanesPerRow;
 #pragma unroll
-  for (int q = 0; q < PipeA<MT, U>::kPer; ++q) {
-    const int idx = threadIdx.x + q * 256;
-    const int row = idx / kRowVecs, c = idx % kRowVecs;
-    rp[q] = nullptr;
-    if (idx < PipeA<MT, U>::kVecs && row < mrows) {
-      const int p = list[m0 + row];
-      rp[q] = A + (size_t)(kTokenRows ? p / K : p) * ld + c * 8;
+  for (int i = 0; i < NWR / G::kRowsPerCopy; ++i) {
+    const int r = i * G::kRowsPerCopy + sub;
+    dma16(wrow[i] + k0 + ((pos ^ (r & 7)) << 3),
+          stage + (wave * NWR + i * G::kRowsPerCopy) * G::kRowBytes);
+  }
+  unsigned char* at = stage + 4 * NWR * G::kRowBytes;
+#pragma unroll
+  for (int i = 0; i < TCW; ++i) {
+    const int r0 = (wave + 4 * i) * G::kRowsPerCopy;
+    dma16(arow[i] + k0 + ((pos ^ ((r0 + sub) & 7)) << 3), at + r0 * G::kRowBytes);
+  }
+}
+
+// The chunk loop of a pass: S-stage copy pipeline, MFMAs over the NT tiles.
+template <int NG, int S, int C, int NT, int TCW>
+__device__ inline void dma_loop(unsigned char* smem,
+                                const uint16_t* const (&wrow)[16 * NG / DmaGeo<C>::kRowsPerCopy],
+                                const uint16_t* const (&arow)[kDmaMaxTokCopies], int Kdim,
+                                f32x4 (&acc)[NG][4]) {
+  constexpr int NWR = 16 * NG;
+  using G = DmaGeo<C>;
+  using Sm = DmaSmem<NWR, S, C>;
+  constexpr int PER = NWR / G::kRowsPerCopy + TCW;  // copies per wave and chunk
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int n = Kdim / C;
+#pragma unroll
+  for (int c = 0; c < S - 1; ++c)
+    if (c < n) dma_chunk<NWR, C, TCW>(smem + c * Sm::kStage, wrow, arow, wave, lane, c * C);
+  for (int c = 0; c < n; ++c) {
+    wait_chunk<PER, S - 2>(min(S - 2, n - 1 - c));
+    lds_barrier();
+    if (c + S - 1 < n)
+      dma_chunk<NWR, C, TCW>(smem + ((c + S - 1) % S) * Sm::kStage, wrow, arow, wave, lane,
+                             (c + S - 1) * C);
+    const unsigned char* st = smem + (c % S) * Sm::kStage;
+    const unsigned char* ws = st + wave * NWR * G::kRowBytes;
+    const unsigned char* as = st + Sm::kW;
+#pragma unroll
+    for (int u = 0; u < C / 32; ++u) {
+      const int cb = u * 4 + (lane >> 4);
+      bf16x8 b[NG], a[NT];
+#pragma unroll
+      for (int g = 0; g < NG; ++g)
+        b[g] = *reinterpret_cast<const bf16x8*>(ws + swz<C>(g * 16 + (lane & 15), cb));
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+        a[t] = *reinterpret_cast<const bf16x8*>(as + swz<C>(t * 16 + (lane & 15), cb));
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int g = 0; g < NG; ++g)
+          acc[g][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[t], b[g], acc[g][t], 0, 0, 0);
     }
   }
 }
 
-// Loads this thread's share of the A chunk at column k0 into registers.
-template <int MT, int U, int NPER>
-__device__ inline void pipe_load_a(u32x4 (&r)[NPER], const uint16_t* const (&rp)[NPER], int k0) {
+// The pass's GEMM over Kdim columns for mrows tokens (list[m0 ..]):
+// acc[g][t] += A(token tile t) . W(row group g)^T for the NT = ceil(mrows /
+// 16) tiles the pass fills, NG row groups of 16 per wave.  Only those tiles'
+// rows are copied; rows past the last token repeat the last one.  A is the
+// token matrix (leading dimension ld); with kTokenRows, pair p reads row p / K.
+template <int NG, int S, int C, int NT, bool kTokenRows>
+__device__ inline void dma_gemm(unsigned char* smem,
+                                const uint16_t* const (&wrow)[16 * NG / DmaGeo<C>::kRowsPerCopy],
+                                const uint16_t* __restrict__ A, int ld, int K,
+                                const int32_t* __restrict__ list, int m0, int mrows, int Kdim,
+                                f32x4 (&acc)[NG][4]) {
+  using G = DmaGeo<C>;
+  constexpr int copies = 16 * NT / G::kRowsPerCopy;  // token copies of the tile, all waves
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const uint16_t* arow[kDmaMaxTokCopies];
 #pragma unroll
-  for (int q = 0; q < PipeA<MT, U>::kPer; ++q)
-    r[q] = rp[q] ? ld16(rp[q] + k0) : u32x4{0u, 0u, 0u, 0u};
-}
-
-template <int MT, int U, int NPER, int LD>
-__device__ inline void pipe_store_a(uint16_t (*As)[LD], const u32x4 (&r)[NPER]) {
-  constexpr int kRowVecs = PipeA<MT, U>::kCols / 8;
-#pragma unroll
-  for (int q = 0; q < PipeA<MT, U>::kPer; ++q) {
-    const int idx = threadIdx.x + q * 256;
-    if (idx < PipeA<MT, U>::kVecs)
-      *reinterpret_cast<u32x4*>(&As[idx / kRowVecs][(idx % kRowVecs) * 8]) = r[q];
+  for (int i = 0; i < kDmaMaxTokCopies; ++i) {
+    const int r = min((wave + 4 * i) * G::kRowsPerCopy + lane / G::kLanesPerRow, mrows - 1);
+    const int p = list[m0 + r];
+    arow[i] = A + (size_t)(kTokenRows ? p / K : p) * ld;
   }
+  wait_vm<0>();   // nothing but this pass's copies is outstanding below
+  lds_barrier();  // the previous pass's readers of every stage are done
+  // copies j = wave + 4i < copies: 0, 1 or 2 per wave
+  static_assert(copies <= 4 * kDmaMaxTokCopies, "token copies per wave");
+  const int tcw = (copies - wave + 3) / 4;
+  if (tcw <= 0)
+    dma_loop<NG, S, C, NT, 0>(smem, wrow, arow, Kdim, acc);
+  else if (tcw == 1)
+    dma_loop<NG, S, C, NT, 1>(smem, wrow, arow, Kdim, acc);
+  else
+    dma_loop<NG, S, C, NT, 2>(smem, wrow, arow, Kdim, acc);
 }
 
-// NB: the weight operand rows of one wave are W[row0 + lane%16]; NW such row
-// groups (NW = 2 for gate/up, 1 for w2) share the A tile.
-template <int MT, int U, int NW, bool kTokenRows, int LD>
-__device__ inline void pipe_gemm(const uint16_t* __restrict__ A, int ld_a, int K, int Kdim,
-                                 const int32_t* __restrict__ list, int m0, int mrows,
-                                 const uint16_t* const (&Wr)[NW], f32x4 (&acc)[NW][MT],
-                                 uint16_t (*As)[MT * 16][LD]) {
-  using PA = PipeA<MT, U>;
-  const int lane = threadIdx.x & 63;
-  const int kq = (lane >> 4) * 8;
-  const uint16_t* rp[PA::kPer];
-  pipe_rows<MT, U, kTokenRows>(rp, A, ld_a, K, list, m0, mrows);
-  u32x4 b[NW][U], bn[NW][U], ar[PA::kPer];
-  pipe_load_a<MT, U>(ar, rp, 0);
-#pragma unroll
-  for (int w = 0; w < NW; ++w)
-#pragma unroll
-    for (int u = 0; u < U; ++u) b[w][u] = ld16(Wr[w] + u * 32);
-  lds_barrier();  // the previous pass's readers of buffer 0 are done
-  pipe_store_a<MT, U>(As[0], ar);
-  lds_barrier();
-  int buf = 0;
-  for (int k0 = 0; k0 < Kdim; k0 += PA::kCols) {
-    const bool more = k0 + PA::kCols < Kdim;
-    if (more) {
-      pipe_load_a<MT, U>(ar, rp, k0 + PA::kCols);
-#pragma unroll
-      for (int w = 0; w < NW; ++w)
-#pragma unroll
-        for (int u = 0; u < U; ++u) bn[w][u] = ld16(Wr[w] + k0 + PA::kCols + u * 32);
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-#pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        if (t * 16 < mrows) {
-          const bf16x8 a =
-              *reinterpret_cast<const bf16x8*>(&As[buf][t * 16 + (lane & 15)][u * 32 + kq]);
-#pragma unroll
-          for (int w = 0; w < NW; ++w)
-            acc[w][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, as_bf16x8(b[w][u]), acc[w][t],
-                                                                0, 0, 0);
-        }
-      }
-    }
-    if (more) {
-      pipe_store_a<MT, U>(As[buf ^ 1], ar);
-      lds_barrier();
-      buf ^= 1;
-#pragma unroll
-      for (int w = 0; w < NW; ++w)
-#pragma unroll
-        for (int u = 0; u < U; ++u) b[w][u] = bn[w][u];
-    }
-  }
+template <int NG, int S, int C, bool kTokenRows>
+__device__ inline void dma_gemm_rows(
+    unsigned char* smem, const uint16_t* const (&wrow)[16 * NG / DmaGeo<C>::kRowsPerCopy],
+    const uint16_t* __restrict__ A, int ld, int K, const int32_t* __restrict__ list, int m0,
+    int mrows, int Kdim, f32x4 (&acc)[NG][4]) {
+  const int nt = (mrows + 15) >> 4;
+  if (nt == 1)
+    dma_gemm<NG, S, C, 1, kTokenRows>(smem, wrow, A, ld, K, list, m0, mrows, Kdim, acc);
+  else if (nt == 2)
+    dma_gemm<NG, S, C, 2, kTokenRows>(smem, wrow, A, ld, K, list, m0, mrows, Kdim, acc);
+  else if (nt == 3)
+    dma_gemm<NG, S, C, 3, kTokenRows>(smem, wrow, A, ld, K, list, m0, mrows, Kdim, acc);
+  else
+    dma_gemm<NG, S, C, 4, kTokenRows>(smem, wrow, A, ld, K, list, m0, mrows, Kdim, acc);
 }
 
-template <int MT, int U>
-__global__ __launch_bounds__(256) void mfma_w13_pipe_kernel(
+template <int S, int C>
+__global__ __launch_bounds__(256) void mfma_w13_dma_kernel(
     const uint16_t* __restrict__ x, int H, int I, int K, int P, const int32_t* __restrict__ lists,
     const int32_t* __restrict__ counts, const uint16_t* __restrict__ w13, size_t w13_stride,
     uint16_t* __restrict__ act) {
-  __shared__ __attribute__((aligned(16))) uint16_t As[2][MT * 16][PipeA<MT, U>::kLd];
+  using G = DmaGeo<C>;
+  extern __shared__ __attribute__((aligned(16))) unsigned char dsm[];
   const int s = blockIdx.y;
   const int M = counts[s];
   if (M == 0) return;
   const int32_t* list = lists + (size_t)s * P;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int i0 = blockIdx.x * kPanel + wave * 16;
-  const uint16_t* Wg = w13 + (size_t)s * w13_stride + (size_t)(i0 + (lane & 15)) * H +
-                       (lane >> 4) * 8;
-  const uint16_t* const Wr[2] = {Wg, Wg + (size_t)I * H};
-  for (int m0 = 0; m0 < M; m0 += MT * 16) {
-    const int mrows = min(M - m0, MT * 16);
-    f32x4 acc[2][MT];
+  const uint16_t* W = w13 + (size_t)s * w13_stride;
+  // this lane's weight copy rows: slice rows 0-15 gate, 16-31 up
+  const uint16_t* wrow[32 / G::kRowsPerCopy];
 #pragma unroll
-    for (int w = 0; w < 2; ++w)
+  for (int i = 0; i < 32 / G::kRowsPerCopy; ++i) {
+    const int r = i * G::kRowsPerCopy + lane / G::kLanesPerRow;
+    wrow[i] = W + (size_t)(r < 16 ? i0 + r : I + i0 + r - 16) * H;
+  }
+  for (int m0 = 0; m0 < M; m0 += kDmaTokRows) {
+    const int mrows = min(M - m0, kDmaTokRows);
+    f32x4 acc[2][4];
 #pragma unroll
-      for (int t = 0; t < MT; ++t) acc[w][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    pipe_gemm<MT, U, 2, true>(x, H, K, H, list, m0, mrows, Wr, acc, As);
+    for (int g = 0; g < 2; ++g)
 #pragma unroll
-    for (int t = 0; t < MT; ++t) {
+      for (int t = 0; t < 4; ++t) acc[g][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    dma_gemm_rows<2, S, C, true>(dsm, wrow, x, H, K, list, m0, mrows, H, acc);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int r = t * 16 + (lane >> 4) * 4 + q;
@@ -399,28 +524,32 @@ __global__ __launch_bounds__(256) void mfma_w13_pipe_kernel(
   }
 }
 
-template <int MT, int U>
-__global__ __launch_bounds__(256) void mfma_w2_pipe_kernel(
+template <int S, int C>
+__global__ __launch_bounds__(256) void mfma_w2_dma_kernel(
     const uint16_t* __restrict__ act, int H, int I, int P, const int32_t* __restrict__ lists,
     const int32_t* __restrict__ counts, const uint16_t* __restrict__ w2, size_t w2_stride,
     float* __restrict__ y) {
-  __shared__ __attribute__((aligned(16))) uint16_t As[2][MT * 16][PipeA<MT, U>::kLd];
+  using G = DmaGeo<C>;
+  extern __shared__ __attribute__((aligned(16))) unsigned char dsm[];
   const int s = blockIdx.y;
   const int M = counts[s];
   if (M == 0) return;
   const int32_t* list = lists + (size_t)s * P;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int h0 = blockIdx.x * kPanel + wave * 16;
-  const uint16_t* const Wr[1] = {w2 + (size_t)s * w2_stride + (size_t)(h0 + (lane & 15)) * I +
-                                 (lane >> 4) * 8};
-  for (int m0 = 0; m0 < M; m0 += MT * 16) {
-    const int mrows = min(M - m0, MT * 16);
-    f32x4 acc[1][MT];
+  const uint16_t* W = w2 + (size_t)s * w2_stride;
+  const uint16_t* wrow[16 / G::kRowsPerCopy];
 #pragma unroll
-    for (int t = 0; t < MT; ++t) acc[0][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    pipe_gemm<MT, U, 1, false>(act, I, 1, I, list, m0, mrows, Wr, acc, As);
+  for (int i = 0; i < 16 / G::kRowsPerCopy; ++i)
+    wrow[i] = W + (size_t)(h0 + i * G::kRowsPerCopy + lane / G::kLanesPerRow) * I;
+  for (int m0 = 0; m0 < M; m0 += kDmaTokRows) {
+    const int mrows = min(M - m0, kDmaTokRows);
+    f32x4 acc[1][4];
 #pragma unroll
-    for (int t = 0; t < MT; ++t) {
+    for (int t = 0; t < 4; ++t) acc[0][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    dma_gemm_rows<1, S, C, false>(dsm, wrow, act, I, 1, list, m0, mrows, I, acc);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int r = t * 16 + (lane >> 4) * 4 + q;
@@ -432,50 +561,115 @@ __global__ __launch_bounds__(256) void mfma_w2_pipe_kernel(
 
 // ---------------------------------------------------------------------------
 // 4. combine: out[t, h] = bf16(sum_k w[t,k] * y[(t,k), h]), k ascending,
-// skipping pairs without a slot.  grid = (ceil(H / 256), T).
+// skipping pairs without a slot (their y rows are never written: selected
+// out, not multiplied by zero).  8 columns per thread, every k's slot,
+// weight and y loads issued before the sums.  grid = (ceil(H / 2048), T).
 // ---------------------------------------------------------------------------
+constexpr int kCombineK = 16;  // top-k handled with all loads up front; more loop
+
+template <bool kVecStore>
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ y, int H, int K,
                                                      int nslots, const float* __restrict__ topk_w,
                                                      const int32_t* __restrict__ slots,
                                                      uint16_t* __restrict__ out) {
   const int t = blockIdx.y;
-  const int h = blockIdx.x * 256 + threadIdx.x;
+  const int h = (blockIdx.x * 256 + threadIdx.x) * 8;
   if (h >= H) return;
-  float acc = 0.f;
-  for (int k = 0; k < K; ++k) {
-    const int p = t * K + k;
-    const int s = slots[p];
-    if (s < 0 || s >= nslots) continue;
-    acc = fmaf(topk_w[p], y[(size_t)p * H + h], acc);
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int k0 = 0; k0 < K; k0 += kCombineK) {
+    const int kn = min(K - k0, kCombineK);
+    f32x4 lo[kCombineK], hi[kCombineK];
+    float w[kCombineK];
+    bool ok[kCombineK];
+#pragma unroll
+    for (int k = 0; k < kCombineK; ++k) {
+      if (k < kn) {
+        const int p = t * K + k0 + k;
+        const int sl = slots[p];
+        ok[k] = sl >= 0 && sl < nslots;
+        w[k] = topk_w[p];
+        const f32x4* yr = reinterpret_cast<const f32x4*>(y + (size_t)p * H + h);
+        lo[k] = yr[0];
+        hi[k] = yr[1];
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kCombineK; ++k) {
+      if (k < kn && ok[k]) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          acc[j] = fmaf(w[k], lo[k][j], acc[j]);
+          acc[4 + j] = fmaf(w[k], hi[k][j], acc[4 + j]);
+        }
+      }
+    }
   }
-  out[(size_t)t * H + h] = bf16_rne(acc);
+  uint16_t* o = out + (size_t)t * H + h;
+  if constexpr (kVecStore) {
+    u32x4 v;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      v[j] = (uint32_t)bf16_rne(acc[2 * j]) | ((uint32_t)bf16_rne(acc[2 * j + 1]) << 16);
+    *reinterpret_cast<u32x4*>(o) = v;
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = bf16_rne(acc[j]);
+  }
 }
 
-template <int MT, int U, bool kPipe>
+void launch_combine(const float* y, int T, int H, int K, int nslots, const float* topk_w,
+                    const int32_t* slots, uint16_t* out, hipStream_t st) {
+  const dim3 grid((H + 2047) / 2048, T);
+  if (((uintptr_t)out | ((size_t)H * 2)) % 16 == 0)
+    hipLaunchKernelGGL(combine_kernel<true>, grid, dim3(256), 0, st, y, H, K, nslots, topk_w,
+                       slots, out);
+  else
+    hipLaunchKernelGGL(combine_kernel<false>, grid, dim3(256), 0, st, y, H, K, nslots, topk_w,
+                       slots, out);
+}
+
+template <int MT, int U>
 void launch_gemms(const uint16_t* x, int H, int I, int K, int P, int nslots, const int32_t* lists,
                   const int32_t* counts, const uint16_t* w13, size_t w13_stride,
                   const uint16_t* w2, size_t w2_stride, uint16_t* act, float* y, hipStream_t st,
                   const StageEvents* ev) {
   hipEvent_t e0 = ev ? ev->ev[0] : nullptr, e1 = ev ? ev->ev[1] : nullptr;
   hipEvent_t e2 = ev ? ev->ev[2] : nullptr, e3 = ev ? ev->ev[3] : nullptr;
-  if (kPipe) {
-    launch_timed(mfma_w13_pipe_kernel<MT, U>, dim3(I / kPanel, nslots), dim3(256), st, e0, e1, x,
-                 H, I, K, P, lists, counts, w13, w13_stride, act);
-    launch_timed(mfma_w2_pipe_kernel<MT, U>, dim3(H / kPanel, nslots), dim3(256), st, e2, e3, act,
-                 H, I, P, lists, counts, w2, w2_stride, y);
-  } else {
-    launch_timed(mfma_w13_kernel<MT, U>, dim3(I / kPanel, nslots), dim3(256), st, e0, e1, x, H, I,
-                 K, P, lists, counts, w13, w13_stride, act);
-    launch_timed(mfma_w2_kernel<MT, U>, dim3(H / kPanel, nslots), dim3(256), st, e2, e3, act, H,
-                 I, P, lists, counts, w2, w2_stride, y);
-  }
+  launch_timed(mfma_w13_kernel<MT, U>, dim3(I / kPanel, nslots), dim3(256), st, e0, e1, x, H, I,
+               K, P, lists, counts, w13, w13_stride, act);
+  launch_timed(mfma_w2_kernel<MT, U>, dim3(H / kPanel, nslots), dim3(256), st, e2, e3, act, H, I,
+               P, lists, counts, w2, w2_stride, y);
+}
+
+template <int S13, int S2, int C>
+void launch_dma(const uint16_t* x, int H, int I, int K, int P, int nslots, const int32_t* lists,
+                const int32_t* counts, const uint16_t* w13, size_t w13_stride,
+                const uint16_t* w2, size_t w2_stride, uint16_t* act, float* y, hipStream_t st,
+                const StageEvents* ev) {
+  constexpr unsigned b13 = DmaSmem<32, S13, C>::kBytes, b2 = DmaSmem<16, S2, C>::kBytes;
+  static_assert(b13 <= 160 * 1024 && b2 <= 160 * 1024, "LDS per block");
+  static const bool attrs = [] {
+    (void)hipFuncSetAttribute((const void*)mfma_w13_dma_kernel<S13, C>,
+                        hipFuncAttributeMaxDynamicSharedMemorySize, b13);
+    (void)hipFuncSetAttribute((const void*)mfma_w2_dma_kernel<S2, C>,
+                        hipFuncAttributeMaxDynamicSharedMemorySize, b2);
+    return true;
+  }();
+  (void)attrs;
+  hipEvent_t e0 = ev ? ev->ev[0] : nullptr, e1 = ev ? ev->ev[1] : nullptr;
+  hipEvent_t e2 = ev ? ev->ev[2] : nullptr, e3 = ev ? ev->ev[3] : nullptr;
+  launch_timed_lds(mfma_w13_dma_kernel<S13, C>, dim3(I / kPanel, nslots), dim3(256), b13, st, e0,
+                   e1, x, H, I, K, P, lists, counts, w13, w13_stride, act);
+  launch_timed_lds(mfma_w2_dma_kernel<S2, C>, dim3(H / kPanel, nslots), dim3(256), b2, st, e2, e3,
+                   act, H, I, P, lists, counts, w2, w2_stride, y);
 }
 
 }  // namespace
 
 void launch_gather(const int32_t* slots, int P, int nslots, int32_t* lists, int32_t* counts,
                    hipStream_t st) {
-  hipLaunchKernelGGL(gather_kernel, dim3(nslots), dim3(64), 0, st, slots, P, lists, counts);
+  hipLaunchKernelGGL(gather_kernel, dim3(nslots), dim3(64 * kGatherWaves), 0, st, slots, P, lists,
+                     counts);
 }
 
 size_t mfma_work_bytes(int T, int K, int H, int nslots) {
@@ -508,28 +702,26 @@ int experts_mfma(const void* x, int T, int H, int I, int K, const float* topk_w,
   int32_t* lists = (int32_t*)((char*)work + W.lists);
   int32_t* counts = (int32_t*)((char*)work + W.counts);
   float* y = (float*)((char*)work + W.y);
-  hipLaunchKernelGGL(gather_kernel, dim3(nslots), dim3(64), 0, st, slots, P, lists, counts);
+  hipLaunchKernelGGL(gather_kernel, dim3(nslots), dim3(64 * kGatherWaves), 0, st, slots, P, lists,
+                     counts);
   // A slot holds a token at most once (a token's top-k experts are
   // distinct), so T bounds the rows of any slot.
   const uint16_t* xb = (const uint16_t*)x;
   const uint16_t* a13 = (const uint16_t*)w13;
   const uint16_t* a2 = (const uint16_t*)w2;
   uint16_t* ab = (uint16_t*)act;
-  // (tiles per pass, k-steps per iteration, pipelined), measured at the Qwen3
-  // shapes on MI355X: more tiles per pass cost registers (fewer waves in
-  // flight) but save passes over the weights once slots hold more than 32
-  // tokens, where staging the token tile in LDS also pays.
+  // Measured on MI355X at the Qwen3 shapes (resident layer, 128 experts):
+  // up to 16 tokens the direct-load kernels with one tile and eight k-steps
+  // per iteration; above, the LDS-staged kernels with three stages, which at
+  // 32 / 128 / 512 / 2048 tokens took 0.96 / 0.96 / 0.92 / 0.78 of the time
+  // of the register-pipelined and direct-load kernels they replace.
   if (T <= 16)
-    launch_gemms<1, 8, false>(xb, H, I, K, P, nslots, lists, counts, a13, w13_stride, a2,
-                              w2_stride, ab, y, st, ev);
-  else if (T <= 128)
-    launch_gemms<2, 4, false>(xb, H, I, K, P, nslots, lists, counts, a13, w13_stride, a2,
-                              w2_stride, ab, y, st, ev);
+    launch_gemms<1, 8>(xb, H, I, K, P, nslots, lists, counts, a13, w13_stride, a2, w2_stride, ab,
+                       y, st, ev);
   else
-    launch_gemms<kMaxMT, 2, true>(xb, H, I, K, P, nslots, lists, counts, a13, w13_stride, a2,
-                                  w2_stride, ab, y, st, ev);
-  hipLaunchKernelGGL(combine_kernel, dim3((H + 255) / 256, T), dim3(256), 0, st, y, H, K, nslots,
-                     topk_w, slots, (uint16_t*)out);
+    launch_dma<3, 3, 64>(xb, H, I, K, P, nslots, lists, counts, a13, w13_stride, a2, w2_stride,
+                         ab, y, st, ev);
+  launch_combine(y, T, H, K, nslots, topk_w, slots, (uint16_t*)out, st);
   WISP_HIP_TRY(hipGetLastError());
   return WISP_OK;
 }
