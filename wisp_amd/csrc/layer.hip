@@ -198,9 +198,16 @@ ProfLaunch* prof_begin(Layer& L, int kind) {
   ProfLaunch& p = L.prof[L.prof_next];
   L.prof_next = (L.prof_next + 1) % kProfRing;
   prof_harvest(L, p);
-  if (!p.start && (hipEventCreate(&p.start) != hipSuccess ||
-                   hipEventCreate(&p.stop) != hipSuccess))
+  if (!p.start && hipEventCreate(&p.start) != hipSuccess) {
+    p.start = nullptr;
+    (void)hipGetLastError();
     return nullptr;
+  }
+  if (!p.stop && hipEventCreate(&p.stop) != hipSuccess) {
+    p.stop = nullptr;
+    (void)hipGetLastError();
+    return nullptr;  // the slot keeps its start event and retries the stop next time
+  }
   p.kind = kind;
   p.counted = true;
   return &p;
@@ -363,6 +370,7 @@ void setup_kernel_pagein(Layer& L) {
     if (hipEventCreate(&L.pin[i].start) != hipSuccess ||
         hipEventCreate(&L.pin[i].stop) != hipSuccess) {
       (void)hipGetLastError();
+      (void)hipHostFree(h);
       return;  // the events made so far are released by wisp_layer_destroy
     }
   }
