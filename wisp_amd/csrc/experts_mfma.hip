@@ -40,6 +40,10 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kKAlign = 256;         // H and I must be multiples (up to 8 k-steps per iteration)
 constexpr int kPanel = 64;           // output columns per block: 4 waves x 16
+// The LDS-staged w2 kernel's blocks own 128 output rows (4 waves x 32): a
+// w2 row is only 12 chunks long at the Qwen3 shape, so per-block setup and
+// the token tile weigh more than in w13, and 32 rows per wave halve both.
+constexpr int kW2PanelsPer = 2;      // 64-row panels per LDS-staged w2 block
 
 // Weight and token fragments alike use plain loads: here the nontemporal
 // hint made every variant slower (measured on MI355X at the Qwen3 shape: -8 %
@@ -146,9 +150,10 @@ __device__ inline void a_rows(const uint16_t* (&ap)[MT], const uint16_t* __restr
 // around gives 5.9 TB/s.  The start depends only on the panel (blockIdx.x),
 // never on the slot, so an output's dot-product order is the same for any
 // slot placement or token grouping, and both kernel families below use it.
-__device__ inline int k_rotation(int Kdim) {
-  return (int)(blockIdx.x * (unsigned)(Kdim / 64) / gridDim.x) * 64;
+__device__ inline int k_rotation(int Kdim, unsigned panel, unsigned npanels) {
+  return (int)(panel * (unsigned)(Kdim / 64) / npanels) * 64;
 }
+__device__ inline int k_rotation(int Kdim) { return k_rotation(Kdim, blockIdx.x, gridDim.x); }
 
 // Column of k-step offset k (0 <= k < Kdim) in a loop rotated by rot columns.
 __device__ inline int k_col(int k, int rot, int Kdim) {
@@ -239,7 +244,8 @@ __global__ __launch_bounds__(256) void mfma_w13_kernel(
 
 // ---------------------------------------------------------------------------
 // 3. w2: y[p, h] = W2[s][h, :] . act[p, :].  grid = (H / 64, nslots); wave w
-// owns h in [blockIdx.x*64 + 16w, +16); same streaming scheme over act.
+// owns h in [blockIdx.x*64 + 16w, +16); same streaming scheme over act, with
+// the k rotation of the 128-row panel around its block.
 // ---------------------------------------------------------------------------
 template <int MT, int U>
 __global__ __launch_bounds__(256) void mfma_w2_kernel(
@@ -255,7 +261,8 @@ __global__ __launch_bounds__(256) void mfma_w2_kernel(
   const uint16_t* Wr = w2 + (size_t)s * w2_stride + (size_t)(h0 + (lane & 15)) * I +
                        (lane >> 4) * 8;
 
-  const int rot = k_rotation(I);
+  // the w2 rotation belongs to the 128-row panel the LDS-staged kernel uses
+  const int rot = k_rotation(I, blockIdx.x / kW2PanelsPer, gridDim.x / kW2PanelsPer);
   for (int m0 = 0; m0 < M; m0 += MT * 16) {
     const int mrows = min(M - m0, MT * 16);
     const uint16_t* ap[MT];
@@ -566,24 +573,31 @@ __global__ __launch_bounds__(256) void mfma_w2_dma_kernel(
   if (M == 0) return;
   const int32_t* list = lists + (size_t)s * P;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int h0 = blockIdx.x * kPanel + wave * 16;
+  constexpr int NG = kW2PanelsPer;  // row groups of 16 per wave
+  const int h0 = blockIdx.x * kPanel * NG + wave * 16 * NG;
   const uint16_t* W = w2 + (size_t)s * w2_stride;
-  const uint16_t* wrow[16 / G::kRowsPerCopy];
+  const uint16_t* wrow[16 * NG / G::kRowsPerCopy];
 #pragma unroll
-  for (int i = 0; i < 16 / G::kRowsPerCopy; ++i)
+  for (int i = 0; i < 16 * NG / G::kRowsPerCopy; ++i)
     wrow[i] = W + (size_t)(h0 + i * G::kRowsPerCopy + lane / G::kLanesPerRow) * I;
   for (int m0 = 0; m0 < M; m0 += kDmaTokRows) {
     const int mrows = min(M - m0, kDmaTokRows);
-    f32x4 acc[1][4];
+    f32x4 acc[NG][4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) acc[0][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    dma_gemm_rows<1, S, C, false>(dsm, wrow, act, I, 1, list, m0, mrows, I, acc);
+    for (int g = 0; g < NG; ++g)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) acc[g][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    dma_gemm_rows<NG, S, C, false>(dsm, wrow, act, I, 1, list, m0, mrows, I, acc);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int r = t * 16 + (lane >> 4) * 4 + q;
-        if (r < mrows) y[(size_t)list[m0 + r] * H + h0 + (lane & 15)] = acc[0][t][q];
+        if (r < mrows) {
+          float* yr = y + (size_t)list[m0 + r] * H + h0 + (lane & 15);
+#pragma unroll
+          for (int g = 0; g < NG; ++g) yr[g * 16] = acc[g][t][q];
+        }
       }
     }
   }
@@ -676,7 +690,8 @@ void launch_dma(const uint16_t* x, int H, int I, int K, int P, int nslots, const
                 const int32_t* counts, const uint16_t* w13, size_t w13_stride,
                 const uint16_t* w2, size_t w2_stride, uint16_t* act, float* y, hipStream_t st,
                 const StageEvents* ev) {
-  constexpr unsigned b13 = DmaSmem<32, S13, C>::kBytes, b2 = DmaSmem<16, S2, C>::kBytes;
+  constexpr unsigned b13 = DmaSmem<32, S13, C>::kBytes;
+  constexpr unsigned b2 = DmaSmem<16 * kW2PanelsPer, S2, C>::kBytes;
   static_assert(b13 <= 160 * 1024 && b2 <= 160 * 1024, "LDS per block");
   static const bool attrs = [] {
     (void)hipFuncSetAttribute((const void*)mfma_w13_dma_kernel<S13, C>,
@@ -690,8 +705,8 @@ void launch_dma(const uint16_t* x, int H, int I, int K, int P, int nslots, const
   hipEvent_t e2 = ev ? ev->ev[2] : nullptr, e3 = ev ? ev->ev[3] : nullptr;
   launch_timed_lds(mfma_w13_dma_kernel<S13, C>, dim3(I / kPanel, nslots), dim3(256), b13, st, e0,
                    e1, x, H, I, K, P, lists, counts, w13, w13_stride, act);
-  launch_timed_lds(mfma_w2_dma_kernel<S2, C>, dim3(H / kPanel, nslots), dim3(256), b2, st, e2, e3,
-                   act, H, I, P, lists, counts, w2, w2_stride, y);
+  launch_timed_lds(mfma_w2_dma_kernel<S2, C>, dim3(H / (kPanel * kW2PanelsPer), nslots),
+                   dim3(256), b2, st, e2, e3, act, H, I, P, lists, counts, w2, w2_stride, y);
 }
 
 }  // namespace
