@@ -1,0 +1,165 @@
+// Global->LDS chunk pipeline shared by the LDS-staged grouped GEMMs (bf16
+// and block-FP8).
+//
+// A block of four waves streams, chunk by chunk, 128 bytes of each of its
+// weight rows (NWR rows per wave, one slice per wave and stage, read only by
+// that wave) and 128 bytes of each row of the pass's token tile (up to 64
+// rows, shared by the waves, copy j issued by wave j % 4) straight into LDS
+// with the asynchronous global->LDS loads (global_load_lds_dwordx4), S - 1
+// chunks ahead of their use.  Neither operand passes through registers.
+// One copy instruction moves 1 KiB: 8 rows of 128 bytes.  Each LDS row holds
+// its 16-byte column blocks XOR-swizzled by the row (block cb at position
+// cb ^ (row & 7)), so MFMA operand reads of 16 rows at one column block
+// spread over the banks.  Token rows past the pass's last token copy a valid
+// row; their results are never stored.  Each wave waits for its own copies
+// by vmcnt (a constant per chunk), then one barrier per chunk: after it,
+// every wave's copies of the chunk have landed and every wave is done with
+// the stage the next copy overwrites.
+#pragma once
+
+#include "common.h"
+
+namespace wisp {
+namespace dma {
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+constexpr int kRowBytes = 128;     // bytes of one row in one chunk
+constexpr int kRowsPerCopy = 8;    // one 1 KiB copy: 8 rows x 128 bytes
+constexpr int kLanesPerRow = 8;    // 16 bytes per lane
+constexpr int kTokRows = 64;       // token tile: four MFMA tiles of 16
+constexpr int kMaxTokCopies = 2;   // 64 rows / 8 per copy / 4 waves
+
+// Block barrier that waits only for this wave's LDS operations (its
+// global->LDS copies are waited for by vmcnt, explicitly, beforehand).
+__device__ inline void lds_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt/expcnt left at max
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// 16 bytes per lane from g into LDS at dst + 16 * lane.
+__device__ inline void dma16(const void* g, void* dst) {
+  __builtin_amdgcn_global_load_lds(g, (lds_void*)dst, 16, 0, 0);
+}
+
+// Waits until at most N of this wave's vector memory operations are
+// outstanding.
+template <int N>
+__device__ inline void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// Waits for the copies of the chunk that has `ahead` later chunks issued
+// behind it (each chunk is PER copy instructions per wave).
+template <int PER, int A>
+__device__ inline void wait_chunk(int ahead) {
+  if constexpr (A > 0) {
+    if (ahead >= A) {
+      wait_vm<A * PER>();
+      return;
+    }
+    wait_chunk<PER, A - 1>(ahead);
+  } else {
+    wait_vm<0>();
+  }
+}
+
+// Byte offset of 16-byte column block cb of row r in a swizzled slice.
+__device__ inline int swz(int r, int cb) { return r * kRowBytes + ((cb ^ (r & 7)) << 4); }
+
+// 16 bytes of row r, column block cb, of a swizzled slice.
+__device__ inline uint4 ld_swz(const unsigned char* slice, int r, int cb) {
+  return *reinterpret_cast<const uint4*>(slice + swz(r, cb));
+}
+
+// LDS of one stage: the four waves' weight slices, then the token tile.
+template <int NWR, int S>
+struct Smem {
+  static constexpr int kW = 4 * NWR * kRowBytes;
+  static constexpr int kA = kTokRows * kRowBytes;
+  static constexpr int kStage = kW + kA;
+  static constexpr int kBytes = S * kStage;
+};
+
+// One stage's copies of the chunk that starts `off` bytes into every row:
+// this wave's NWR weight rows and its TCW token copies.  wrow[i] / arow[i]
+// are the lane's source rows (copy i covers rows [8i, 8i + 8) of the wave's
+// weights; token copy wave + 4i covers tile rows [8 (wave + 4i), +8)).
+template <int NWR, int TCW>
+__device__ inline void chunk_copies(unsigned char* stage,
+                                    const unsigned char* const (&wrow)[NWR / kRowsPerCopy],
+                                    const unsigned char* const (&arow)[kMaxTokCopies], int wave,
+                                    int lane, size_t off) {
+  const int pos = lane % kLanesPerRow, sub = lane / kLanesPerRow;
+#pragma unroll
+  for (int i = 0; i < NWR / kRowsPerCopy; ++i) {
+    const int r = i * kRowsPerCopy + sub;
+    dma16(wrow[i] + off + ((pos ^ (r & 7)) << 4),
+          stage + (wave * NWR + i * kRowsPerCopy) * kRowBytes);
+  }
+  unsigned char* at = stage + 4 * NWR * kRowBytes;
+#pragma unroll
+  for (int i = 0; i < TCW; ++i) {
+    const int r0 = (wave + 4 * i) * kRowsPerCopy;
+    dma16(arow[i] + off + ((pos ^ ((r0 + sub) & 7)) << 4), at + r0 * kRowBytes);
+  }
+}
+
+// The S-stage pipeline over n chunks; chunk c starts off(c) bytes into every
+// row.  compute(ws, as, c) runs once chunk c has landed, with ws this wave's
+// weight slice and as the token tile of its stage.
+template <int NWR, int S, int TCW, typename Off, typename F>
+__device__ inline void pipeline(unsigned char* smem,
+                                const unsigned char* const (&wrow)[NWR / kRowsPerCopy],
+                                const unsigned char* const (&arow)[kMaxTokCopies], int n, Off off,
+                                F&& compute) {
+  using Sm = Smem<NWR, S>;
+  constexpr int PER = NWR / kRowsPerCopy + TCW;  // copies per wave and chunk
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+  for (int c = 0; c < S - 1; ++c)
+    if (c < n) chunk_copies<NWR, TCW>(smem + c * Sm::kStage, wrow, arow, wave, lane, off(c));
+  for (int c = 0; c < n; ++c) {
+    wait_chunk<PER, S - 2>(min(S - 2, n - 1 - c));
+    lds_barrier();
+    if (c + S - 1 < n)
+      chunk_copies<NWR, TCW>(smem + ((c + S - 1) % S) * Sm::kStage, wrow, arow, wave, lane,
+                             off(c + S - 1));
+    const unsigned char* st = smem + (c % S) * Sm::kStage;
+    compute(st + wave * NWR * kRowBytes, st + Sm::kW, c);
+  }
+}
+
+// One pass for mrows tokens (NT = ceil(mrows / 16) tiles): the lane's token
+// source rows (row_of(r) for tile row r; rows past mrows repeat the last),
+// a drain of the previous pass (its copies and its readers of every stage),
+// then the pipeline with this wave's share of the tile's copies.
+template <int NWR, int S, int NT, typename RowOf, typename Off, typename F>
+__device__ inline void pass(unsigned char* smem,
+                            const unsigned char* const (&wrow)[NWR / kRowsPerCopy], int mrows,
+                            RowOf row_of, int n, Off off, F&& compute) {
+  constexpr int copies = 16 * NT / kRowsPerCopy;  // token copies of the tile, all waves
+  static_assert(copies <= 4 * kMaxTokCopies, "token copies per wave");
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const unsigned char* arow[kMaxTokCopies];
+#pragma unroll
+  for (int i = 0; i < kMaxTokCopies; ++i)
+    arow[i] = row_of(min((wave + 4 * i) * kRowsPerCopy + lane / kLanesPerRow, mrows - 1));
+  wait_vm<0>();   // nothing but this pass's copies is outstanding below
+  lds_barrier();  // the previous pass's readers of every stage are done
+  const int tcw = (copies - wave + 3) / 4;  // copies j = wave + 4i < copies: 0, 1 or 2
+  if (tcw <= 0)
+    pipeline<NWR, S, 0>(smem, wrow, arow, n, off, compute);
+  else if (tcw == 1)
+    pipeline<NWR, S, 1>(smem, wrow, arow, n, off, compute);
+  else
+    pipeline<NWR, S, 2>(smem, wrow, arow, n, off, compute);
+}
+
+}  // namespace dma
+}  // namespace wisp

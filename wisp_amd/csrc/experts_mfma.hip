@@ -29,7 +29,10 @@
 // chunk routes ~32 tokens to each expert, about 32 FLOP per weight byte: far
 // below the bf16 ridge (~315 FLOP/B), so these kernels are HBM-bound and are
 // built to stream each weight byte once per call.
+#include <type_traits>
+
 #include "common.h"
+#include "dma_pipeline.h"
 
 namespace wisp {
 namespace {
@@ -303,227 +306,73 @@ __global__ __launch_bounds__(256) void mfma_w2_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// LDS-staged panels for prefill: the weight panel and the token tile of each
-// C-column chunk are copied from global memory straight into LDS by the
-// asynchronous global->LDS loads (global_load_lds_dwordx4), S - 1 chunks
-// ahead, so neither operand passes through registers and each chunk's data
-// was requested S - 1 chunks before it is used.  Per block (four waves):
-//   weights: wave w's own rows (w13: 16 gate + 16 up, w2: 16), one slice per
-//            wave and stage, read only by that wave;
-//   tokens:  the 16 * NT rows of the NT tiles the pass fills (NT <= 4),
-//            shared by the waves, copy j of the tile issued by wave j % 4.
-// One copy instruction moves 1 KiB: 8 rows of 128 bytes.  Each LDS row holds
-// its 16-byte column blocks XOR-swizzled by the row (block cb at position
-// cb ^ (row & 7)), so the MFMA operand reads of 16 rows at one column block
-// spread over the banks.  Rows past the pass's last token copy a valid row;
-// their results are never stored.  Each wave waits for its own copies by
-// vmcnt (a constant per chunk), then one barrier per chunk: after it, every
-// wave's copies of the chunk have landed and every wave is done with the
-// stage the next copy overwrites.
-// What bounds these kernels: with the weights row-major, a chunk takes 128
-// bytes from each of 128 rows 4 KiB apart, and a pure read of the Qwen3 w13
-// tensor in that order runs at 4.7 TB/s on MI355X (4.5-5.1 TB/s for 128 B to
-// 1 KiB per row and 1-3 blocks per CU), against 6.2 TB/s for the same bytes
-// read as contiguous 512 KiB panels; w13 here runs at 4.7 TB/s.
+// LDS-staged kernels for calls of more than 16 tokens: the chunk pipeline of
+// dma_pipeline.h over 64-column (128-byte) chunks, two 32-column k-steps of
+// MFMA per chunk, the k rotation of the output panel.  w13 blocks own a
+// 64-row panel (each wave 16 gate and 16 up rows); w2 blocks own 128 rows
+// (32 per wave).
+// What bounds them: a pure read of the Qwen3 w13 tensor in this chunk order
+// and rotation runs at 5.9 TB/s on MI355X and w13 here at 5.3 TB/s of
+// weights; the w2 tensor reads at 6.2 TB/s and w2 here at 4.5 TB/s.
 // ---------------------------------------------------------------------------
-typedef __attribute__((address_space(3))) void lds_void;
-
-// Block barrier that waits only for this wave's LDS operations (its
-// global->LDS copies are waited for by vmcnt, explicitly, beforehand).
-__device__ inline void lds_barrier() {
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt/expcnt left at max
-  __builtin_amdgcn_s_barrier();
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
-constexpr int kDmaTokRows = 64;  // 4 MFMA tiles of 16 tokens
-
-// Chunk geometry for C bf16 columns per chunk.
-template <int C>
-struct DmaGeo {
-  static_assert(C == 64, "chunk width: 128-byte rows (8 rows per copy)");
-  static constexpr int kRowBytes = 2 * C;
-  static constexpr int kRowsPerCopy = 1024 / kRowBytes;
-  static constexpr int kLanesPerRow = kRowBytes / 16;
-};
-
-// Token copies per wave at most: 64 rows = 64 / rows-per-copy copies over 4
-// waves (2 for 64-column chunks).
-constexpr int kDmaMaxTokCopies = 2;
-
-// 16 bytes per lane from g into LDS at dst + 16 * lane.
-__device__ inline void dma16(const void* g, void* dst) {
-  __builtin_amdgcn_global_load_lds(g, (lds_void*)dst, 16, 0, 0);
-}
-
-// Waits until at most N of this wave's vector memory operations are
-// outstanding.
-template <int N>
-__device__ inline void wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
-// Waits for the copies of the chunk that has `ahead` later chunks issued
-// behind it (each chunk is PER copy instructions per wave).
-template <int PER, int A>
-__device__ inline void wait_chunk(int ahead) {
-  if constexpr (A > 0) {
-    if (ahead >= A) {
-      wait_vm<A * PER>();
-      return;
-    }
-    wait_chunk<PER, A - 1>(ahead);
-  } else {
-    wait_vm<0>();
-  }
-}
-
-// Byte offset of column block cb of row r in a swizzled slice of C columns.
-template <int C>
-__device__ inline int swz(int r, int cb) {
-  return r * DmaGeo<C>::kRowBytes + ((cb ^ (r & 7)) << 4);
-}
-
-// NWR weight rows per wave (32 for w13: gate then up; 16 for w2).
-template <int NWR, int S, int C>
-struct DmaSmem {
-  static constexpr int kW = 4 * NWR * DmaGeo<C>::kRowBytes;       // weight slices of a stage
-  static constexpr int kA = kDmaTokRows * DmaGeo<C>::kRowBytes;   // token tile of a stage
-  static constexpr int kStage = kW + kA;
-  static constexpr int kBytes = S * kStage;
-};
-
-// One stage's copies for the chunk at column k0: this wave's weight rows and
-// its TCW token copies.  wrow[i] / arow[i] are the lane's source rows
-// (element pointers); the token copies of a wave are copies wave + 4i of the
-// tile, copy j covering tile rows [j * rows-per-copy, (j + 1) * rows-per-copy).
-template <int NWR, int C, int TCW>
-__device__ inline void dma_chunk(unsigned char* stage,
-                                 const uint16_t* const (&wrow)[NWR / DmaGeo<C>::kRowsPerCopy],
-                                 const uint16_t* const (&arow)[kDmaMaxTokCopies], int wave,
-                                 int lane, int k0) {
-  using G = DmaGeo<C>;
-  const int pos = lane % G::kLanesPerRow, sub = lane / G::kLanesPerRow;
-#pragma unroll
-  for (int i = 0; i < NWR / G::kRowsPerCopy; ++i) {
-    const int r = i * G::kRowsPerCopy + sub;
-    dma16(wrow[i] + k0 + ((pos ^ (r & 7)) << 3),
-          stage + (wave * NWR + i * G::kRowsPerCopy) * G::kRowBytes);
-  }
-  unsigned char* at = stage + 4 * NWR * G::kRowBytes;
-#pragma unroll
-  for (int i = 0; i < TCW; ++i) {
-    const int r0 = (wave + 4 * i) * G::kRowsPerCopy;
-    dma16(arow[i] + k0 + ((pos ^ ((r0 + sub) & 7)) << 3), at + r0 * G::kRowBytes);
-  }
-}
-
-// The chunk loop of a pass: S-stage copy pipeline, MFMAs over the NT tiles.
-template <int NG, int S, int C, int NT, int TCW>
-__device__ inline void dma_loop(unsigned char* smem,
-                                const uint16_t* const (&wrow)[16 * NG / DmaGeo<C>::kRowsPerCopy],
-                                const uint16_t* const (&arow)[kDmaMaxTokCopies], int Kdim,
-                                f32x4 (&acc)[NG][4]) {
-  constexpr int NWR = 16 * NG;
-  using G = DmaGeo<C>;
-  using Sm = DmaSmem<NWR, S, C>;
-  constexpr int PER = NWR / G::kRowsPerCopy + TCW;  // copies per wave and chunk
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int n = Kdim / C;
-  const int rot = k_rotation(Kdim);  // chunk c reads columns k_col(c * C, rot, Kdim) + [0, C)
-#pragma unroll
-  for (int c = 0; c < S - 1; ++c)
-    if (c < n)
-      dma_chunk<NWR, C, TCW>(smem + c * Sm::kStage, wrow, arow, wave, lane,
-                             k_col(c * C, rot, Kdim));
-  for (int c = 0; c < n; ++c) {
-    wait_chunk<PER, S - 2>(min(S - 2, n - 1 - c));
-    lds_barrier();
-    if (c + S - 1 < n)
-      dma_chunk<NWR, C, TCW>(smem + ((c + S - 1) % S) * Sm::kStage, wrow, arow, wave, lane,
-                             k_col((c + S - 1) * C, rot, Kdim));
-    const unsigned char* st = smem + (c % S) * Sm::kStage;
-    const unsigned char* ws = st + wave * NWR * G::kRowBytes;
-    const unsigned char* as = st + Sm::kW;
-#pragma unroll
-    for (int u = 0; u < C / 32; ++u) {
-      const int cb = u * 4 + (lane >> 4);
-      bf16x8 b[NG], a[NT];
-#pragma unroll
-      for (int g = 0; g < NG; ++g)
-        b[g] = *reinterpret_cast<const bf16x8*>(ws + swz<C>(g * 16 + (lane & 15), cb));
-#pragma unroll
-      for (int t = 0; t < NT; ++t)
-        a[t] = *reinterpret_cast<const bf16x8*>(as + swz<C>(t * 16 + (lane & 15), cb));
-#pragma unroll
-      for (int t = 0; t < NT; ++t)
-#pragma unroll
-        for (int g = 0; g < NG; ++g)
-          acc[g][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[t], b[g], acc[g][t], 0, 0, 0);
-    }
-  }
-}
 
 // The pass's GEMM over Kdim columns for mrows tokens (list[m0 ..]):
 // acc[g][t] += A(token tile t) . W(row group g)^T for the NT = ceil(mrows /
-// 16) tiles the pass fills, NG row groups of 16 per wave.  Only those tiles'
-// rows are copied; rows past the last token repeat the last one.  A is the
-// token matrix (leading dimension ld); with kTokenRows, pair p reads row p / K.
-template <int NG, int S, int C, int NT, bool kTokenRows>
+// 16) tiles the pass fills, NG row groups of 16 per wave, the k loop starting
+// rot columns in.  A is the token matrix (leading dimension ld); with
+// kTokenRows, pair p reads row p / K.
+template <int NG, int S, bool kTokenRows>
 __device__ inline void dma_gemm(unsigned char* smem,
-                                const uint16_t* const (&wrow)[16 * NG / DmaGeo<C>::kRowsPerCopy],
+                                const unsigned char* const (&wrow)[16 * NG / dma::kRowsPerCopy],
                                 const uint16_t* __restrict__ A, int ld, int K,
                                 const int32_t* __restrict__ list, int m0, int mrows, int Kdim,
-                                f32x4 (&acc)[NG][4]) {
-  using G = DmaGeo<C>;
-  constexpr int copies = 16 * NT / G::kRowsPerCopy;  // token copies of the tile, all waves
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const uint16_t* arow[kDmaMaxTokCopies];
-#pragma unroll
-  for (int i = 0; i < kDmaMaxTokCopies; ++i) {
-    const int r = min((wave + 4 * i) * G::kRowsPerCopy + lane / G::kLanesPerRow, mrows - 1);
+                                int rot, f32x4 (&acc)[NG][4]) {
+  const int lane = threadIdx.x & 63;
+  auto row_of = [&](int r) {
     const int p = list[m0 + r];
-    arow[i] = A + (size_t)(kTokenRows ? p / K : p) * ld;
-  }
-  wait_vm<0>();   // nothing but this pass's copies is outstanding below
-  lds_barrier();  // the previous pass's readers of every stage are done
-  // copies j = wave + 4i < copies: 0, 1 or 2 per wave
-  static_assert(copies <= 4 * kDmaMaxTokCopies, "token copies per wave");
-  const int tcw = (copies - wave + 3) / 4;
-  if (tcw <= 0)
-    dma_loop<NG, S, C, NT, 0>(smem, wrow, arow, Kdim, acc);
-  else if (tcw == 1)
-    dma_loop<NG, S, C, NT, 1>(smem, wrow, arow, Kdim, acc);
-  else
-    dma_loop<NG, S, C, NT, 2>(smem, wrow, arow, Kdim, acc);
-}
-
-template <int NG, int S, int C, bool kTokenRows>
-__device__ inline void dma_gemm_rows(
-    unsigned char* smem, const uint16_t* const (&wrow)[16 * NG / DmaGeo<C>::kRowsPerCopy],
-    const uint16_t* __restrict__ A, int ld, int K, const int32_t* __restrict__ list, int m0,
-    int mrows, int Kdim, f32x4 (&acc)[NG][4]) {
+    return reinterpret_cast<const unsigned char*>(A + (size_t)(kTokenRows ? p / K : p) * ld);
+  };
+  auto off = [&](int c) { return (size_t)k_col(c * 64, rot, Kdim) * sizeof(uint16_t); };
+  auto run = [&](auto nt) {
+    constexpr int NT = decltype(nt)::value;
+    dma::pass<16 * NG, S, NT>(
+        smem, wrow, mrows, row_of, Kdim / 64, off,
+        [&](const unsigned char* ws, const unsigned char* as, int) {
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const int cb = u * 4 + (lane >> 4);
+            bf16x8 b[NG], a[NT];
+#pragma unroll
+            for (int g = 0; g < NG; ++g)
+              b[g] = *reinterpret_cast<const bf16x8*>(ws + dma::swz(g * 16 + (lane & 15), cb));
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+              a[t] = *reinterpret_cast<const bf16x8*>(as + dma::swz(t * 16 + (lane & 15), cb));
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+              for (int g = 0; g < NG; ++g)
+                acc[g][t] =
+                    __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[t], b[g], acc[g][t], 0, 0, 0);
+          }
+        });
+  };
   const int nt = (mrows + 15) >> 4;
   if (nt == 1)
-    dma_gemm<NG, S, C, 1, kTokenRows>(smem, wrow, A, ld, K, list, m0, mrows, Kdim, acc);
+    run(std::integral_constant<int, 1>{});
   else if (nt == 2)
-    dma_gemm<NG, S, C, 2, kTokenRows>(smem, wrow, A, ld, K, list, m0, mrows, Kdim, acc);
+    run(std::integral_constant<int, 2>{});
   else if (nt == 3)
-    dma_gemm<NG, S, C, 3, kTokenRows>(smem, wrow, A, ld, K, list, m0, mrows, Kdim, acc);
+    run(std::integral_constant<int, 3>{});
   else
-    dma_gemm<NG, S, C, 4, kTokenRows>(smem, wrow, A, ld, K, list, m0, mrows, Kdim, acc);
+    run(std::integral_constant<int, 4>{});
 }
 
-template <int S, int C>
+template <int S>
 __global__ __launch_bounds__(256) void mfma_w13_dma_kernel(
     const uint16_t* __restrict__ x, int H, int I, int K, int P, const int32_t* __restrict__ lists,
     const int32_t* __restrict__ counts, const uint16_t* __restrict__ w13, size_t w13_stride,
     uint16_t* __restrict__ act) {
-  using G = DmaGeo<C>;
   extern __shared__ __attribute__((aligned(16))) unsigned char dsm[];
   const int s = blockIdx.y;
   const int M = counts[s];
@@ -533,20 +382,22 @@ __global__ __launch_bounds__(256) void mfma_w13_dma_kernel(
   const int i0 = blockIdx.x * kPanel + wave * 16;
   const uint16_t* W = w13 + (size_t)s * w13_stride;
   // this lane's weight copy rows: slice rows 0-15 gate, 16-31 up
-  const uint16_t* wrow[32 / G::kRowsPerCopy];
+  const unsigned char* wrow[32 / dma::kRowsPerCopy];
 #pragma unroll
-  for (int i = 0; i < 32 / G::kRowsPerCopy; ++i) {
-    const int r = i * G::kRowsPerCopy + lane / G::kLanesPerRow;
-    wrow[i] = W + (size_t)(r < 16 ? i0 + r : I + i0 + r - 16) * H;
+  for (int i = 0; i < 32 / dma::kRowsPerCopy; ++i) {
+    const int r = i * dma::kRowsPerCopy + lane / dma::kLanesPerRow;
+    wrow[i] = reinterpret_cast<const unsigned char*>(
+        W + (size_t)(r < 16 ? i0 + r : I + i0 + r - 16) * H);
   }
-  for (int m0 = 0; m0 < M; m0 += kDmaTokRows) {
-    const int mrows = min(M - m0, kDmaTokRows);
+  const int rot = k_rotation(H);
+  for (int m0 = 0; m0 < M; m0 += dma::kTokRows) {
+    const int mrows = min(M - m0, dma::kTokRows);
     f32x4 acc[2][4];
 #pragma unroll
     for (int g = 0; g < 2; ++g)
 #pragma unroll
       for (int t = 0; t < 4; ++t) acc[g][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    dma_gemm_rows<2, S, C, true>(dsm, wrow, x, H, K, list, m0, mrows, H, acc);
+    dma_gemm<2, S, true>(dsm, wrow, x, H, K, list, m0, mrows, H, rot, acc);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
 #pragma unroll
@@ -561,12 +412,11 @@ __global__ __launch_bounds__(256) void mfma_w13_dma_kernel(
   }
 }
 
-template <int S, int C>
+template <int S>
 __global__ __launch_bounds__(256) void mfma_w2_dma_kernel(
     const uint16_t* __restrict__ act, int H, int I, int P, const int32_t* __restrict__ lists,
     const int32_t* __restrict__ counts, const uint16_t* __restrict__ w2, size_t w2_stride,
     float* __restrict__ y) {
-  using G = DmaGeo<C>;
   extern __shared__ __attribute__((aligned(16))) unsigned char dsm[];
   const int s = blockIdx.y;
   const int M = counts[s];
@@ -576,18 +426,20 @@ __global__ __launch_bounds__(256) void mfma_w2_dma_kernel(
   constexpr int NG = kW2PanelsPer;  // row groups of 16 per wave
   const int h0 = blockIdx.x * kPanel * NG + wave * 16 * NG;
   const uint16_t* W = w2 + (size_t)s * w2_stride;
-  const uint16_t* wrow[16 * NG / G::kRowsPerCopy];
+  const unsigned char* wrow[16 * NG / dma::kRowsPerCopy];
 #pragma unroll
-  for (int i = 0; i < 16 * NG / G::kRowsPerCopy; ++i)
-    wrow[i] = W + (size_t)(h0 + i * G::kRowsPerCopy + lane / G::kLanesPerRow) * I;
-  for (int m0 = 0; m0 < M; m0 += kDmaTokRows) {
-    const int mrows = min(M - m0, kDmaTokRows);
+  for (int i = 0; i < 16 * NG / dma::kRowsPerCopy; ++i)
+    wrow[i] = reinterpret_cast<const unsigned char*>(
+        W + (size_t)(h0 + i * dma::kRowsPerCopy + lane / dma::kLanesPerRow) * I);
+  const int rot = k_rotation(I);
+  for (int m0 = 0; m0 < M; m0 += dma::kTokRows) {
+    const int mrows = min(M - m0, dma::kTokRows);
     f32x4 acc[NG][4];
 #pragma unroll
     for (int g = 0; g < NG; ++g)
 #pragma unroll
       for (int t = 0; t < 4; ++t) acc[g][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    dma_gemm_rows<NG, S, C, false>(dsm, wrow, act, I, 1, list, m0, mrows, I, acc);
+    dma_gemm<NG, S, false>(dsm, wrow, act, I, 1, list, m0, mrows, I, rot, acc);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
 #pragma unroll
@@ -685,27 +537,27 @@ void launch_gemms(const uint16_t* x, int H, int I, int K, int P, int nslots, con
                P, lists, counts, w2, w2_stride, y);
 }
 
-template <int S13, int S2, int C>
+template <int S13, int S2>
 void launch_dma(const uint16_t* x, int H, int I, int K, int P, int nslots, const int32_t* lists,
                 const int32_t* counts, const uint16_t* w13, size_t w13_stride,
                 const uint16_t* w2, size_t w2_stride, uint16_t* act, float* y, hipStream_t st,
                 const StageEvents* ev) {
-  constexpr unsigned b13 = DmaSmem<32, S13, C>::kBytes;
-  constexpr unsigned b2 = DmaSmem<16 * kW2PanelsPer, S2, C>::kBytes;
+  constexpr unsigned b13 = dma::Smem<32, S13>::kBytes;
+  constexpr unsigned b2 = dma::Smem<16 * kW2PanelsPer, S2>::kBytes;
   static_assert(b13 <= 160 * 1024 && b2 <= 160 * 1024, "LDS per block");
   static const bool attrs = [] {
-    (void)hipFuncSetAttribute((const void*)mfma_w13_dma_kernel<S13, C>,
-                        hipFuncAttributeMaxDynamicSharedMemorySize, b13);
-    (void)hipFuncSetAttribute((const void*)mfma_w2_dma_kernel<S2, C>,
-                        hipFuncAttributeMaxDynamicSharedMemorySize, b2);
+    (void)hipFuncSetAttribute((const void*)mfma_w13_dma_kernel<S13>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, b13);
+    (void)hipFuncSetAttribute((const void*)mfma_w2_dma_kernel<S2>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, b2);
     return true;
   }();
   (void)attrs;
   hipEvent_t e0 = ev ? ev->ev[0] : nullptr, e1 = ev ? ev->ev[1] : nullptr;
   hipEvent_t e2 = ev ? ev->ev[2] : nullptr, e3 = ev ? ev->ev[3] : nullptr;
-  launch_timed_lds(mfma_w13_dma_kernel<S13, C>, dim3(I / kPanel, nslots), dim3(256), b13, st, e0,
+  launch_timed_lds(mfma_w13_dma_kernel<S13>, dim3(I / kPanel, nslots), dim3(256), b13, st, e0,
                    e1, x, H, I, K, P, lists, counts, w13, w13_stride, act);
-  launch_timed_lds(mfma_w2_dma_kernel<S2, C>, dim3(H / (kPanel * kW2PanelsPer), nslots),
+  launch_timed_lds(mfma_w2_dma_kernel<S2>, dim3(H / (kPanel * kW2PanelsPer), nslots),
                    dim3(256), b2, st, e2, e3, act, H, I, P, lists, counts, w2, w2_stride, y);
 }
 
@@ -764,8 +616,8 @@ int experts_mfma(const void* x, int T, int H, int I, int K, const float* topk_w,
     launch_gemms<1, 8>(xb, H, I, K, P, nslots, lists, counts, a13, w13_stride, a2, w2_stride, ab,
                        y, st, ev);
   else
-    launch_dma<3, 3, 64>(xb, H, I, K, P, nslots, lists, counts, a13, w13_stride, a2, w2_stride,
-                         ab, y, st, ev);
+    launch_dma<3, 3>(xb, H, I, K, P, nslots, lists, counts, a13, w13_stride, a2, w2_stride, ab,
+                     y, st, ev);
   launch_combine(y, T, H, K, nslots, topk_w, slots, (uint16_t*)out, st);
   WISP_HIP_TRY(hipGetLastError());
   return WISP_OK;
