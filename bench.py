@@ -438,7 +438,9 @@ def _fp8_gemm_report(agg: dict, wl, tokens_per_call: int, distinct_per_call: flo
     t = (agg["w13_ms"] + agg["w2_ms"]) / calls * 1e-3
     flops = 2.0 * tokens_per_call * sh.top_k * 3 * sh.hidden * sh.inter
     byts = distinct_per_call * wl.expert_bytes
-    return {"kernels": "fp8_grouped_w13_kernel + fp8_grouped_w2_kernel",
+    kernels = ("fp8_w13_dma_kernel + fp8_w2_dma_kernel" if tokens_per_call > 16
+               else "fp8_grouped_w13_kernel + fp8_grouped_w2_kernel")
+    return {"kernels": kernels,
             "avg_us_per_call": round(t * 1e6, 2),
             "w13_us": round(agg["w13_ms"] / calls * 1e3, 2),
             "w2_us": round(agg["w2_ms"] / calls * 1e3, 2),

@@ -197,6 +197,25 @@ def test_experts_fp8_grouped_match_oracle(T, H, I, E, K, block):
     assert _rel(out, want) < REL_TOL, _rel(out, want)
 
 
+def test_experts_fp8_grouped_bytes_equal_across_kernel_families():
+    """Above 16 tokens the grouped path runs the LDS-staged kernels, up to 16
+    the register-streaming ones; both take each output through the same
+    k-block steps, so one call over 48 tokens, two of 24 and chunks of 8 or
+    16 give the same bytes for every token."""
+    T, H, I, E, K, block = 48, 1024, 384, 12, 4, (64, 128)
+    _, w13, w2, s13, s2 = _experts(E, H, I, block, seed=21)
+    ids, tw = _routing(T, E, K, seed=22)
+    x = torch.randn((T, H), generator=torch.Generator().manual_seed(23)).to(torch.bfloat16)
+    mfma = _lib.WISP_ALGO_MFMA
+    full, full_act = _run_experts(x, ids, tw, w13, w2, s13, s2, block, algo=mfma)
+    for step in (24, 16, 8):
+        parts = [_run_experts(x[a:a + step], ids[a:a + step], tw[a:a + step], w13, w2, s13, s2,
+                              block, algo=mfma)[0] for a in range(0, T, step)]
+        assert torch.equal(torch.cat(parts).view(torch.int32), full.view(torch.int32)), step
+    want, want_act = F.moe_forward_fp8(x, tw, ids, w13, w2, s13, s2, block, return_act=True)
+    assert _rel(full_act, want_act) < REL_TOL and _rel(full, want) < REL_TOL
+
+
 def test_experts_fp8_decode_kernels_over_256_pairs():
     """The decode kernels' in-memory slot scan (launches of more than 256
     pairs) against the oracle."""

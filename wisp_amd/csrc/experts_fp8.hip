@@ -38,7 +38,10 @@
 // token's K act rows into LDS, waves take (pair, k-range) jobs over I, and
 // the block scales each pair by its routing weight, rounds to bf16 and sums
 // the K results in routing order.
+#include <type_traits>
+
 #include "common.h"
+#include "dma_pipeline.h"
 
 #pragma clang fp contract(off)  // keep vLLM's separate multiply and add roundings
 
@@ -687,6 +690,228 @@ __global__ __launch_bounds__(256) void fp8_grouped_w2_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// LDS-staged grouped path for calls of more than 16 tokens: the chunk
+// pipeline of dma_pipeline.h, one chunk per 128-column k-block (128 bytes of
+// e4m3fn per row), the weight rows and the token tile of each k-block copied
+// straight into LDS two k-blocks ahead.  The k-blocks run in ascending order
+// and every output takes exactly the grouped kernels' steps (same MFMA
+// operands and orientation, acc + (D * s_act) * s_w per k-block), so its
+// bytes equal theirs: paged calls, whose token groups may use either, match
+// resident calls.  Per pass the token scales of the tile's 64 rows are
+// staged in LDS beside the stages; the weight scales of a wave's row tiles
+// are staged once per block.
+//   fp8_w13_dma: grid (I / 64, nslots), wave w owns gate rows
+//     [64 bx + 16w, +16) and the matching up rows;
+//   fp8_w2_dma: grid (H / 128, nslots), wave w owns rows [128 bx + 32w, +32).
+// ---------------------------------------------------------------------------
+
+// A lane's fp8 MFMA operand from a swizzled LDS slice: row r, the 32 bytes
+// at 32 * grp of the k-block (column blocks 2 grp and 2 grp + 1).
+__device__ inline i32x8 lds_operand(const unsigned char* slice, int r, int grp) {
+  return join(*reinterpret_cast<const u32x4*>(slice + dma::swz(r, 2 * grp)),
+              *reinterpret_cast<const u32x4*>(slice + dma::swz(r, 2 * grp + 1)));
+}
+
+// Dynamic LDS of the LDS-staged kernels: the stages, the pass's token scales
+// [64][nkb], the four waves' weight scales [4][2][nkb].
+template <int S>
+inline size_t fp8_dma_lds(int nkb) {
+  return dma::Smem<32, S>::kBytes + (size_t)dma::kTokRows * nkb * sizeof(float) +
+         (size_t)4 * 2 * nkb * sizeof(float);
+}
+
+// Stages the pass's token scales: row r < 64 of the tile reads the scales of
+// tile row min(r, mrows - 1).  After a barrier, so the previous pass's
+// readers are done.
+template <typename RowOf>
+__device__ inline void stage_token_scales(float* xsl, const float* __restrict__ scales, int nkb,
+                                          int mrows, bool first, RowOf row_of) {
+  if (!first) dma::lds_barrier();
+  for (int q = threadIdx.x; q < dma::kTokRows * nkb; q += 256) {
+    const int r = q / nkb, kb = q - r * nkb;
+    xsl[q] = scales[(size_t)row_of(min(r, mrows - 1)) * nkb + kb];
+  }
+}
+
+template <int S>
+__global__ __launch_bounds__(256) void fp8_w13_dma_kernel(
+    const uint8_t* __restrict__ xq, const float* __restrict__ xs, int H, int I, int K, int P,
+    const int32_t* __restrict__ lists, const int32_t* __restrict__ counts,
+    const uint8_t* __restrict__ w13, size_t w13_stride, const float* __restrict__ s13,
+    size_t s13_stride, int block_n, uint16_t* __restrict__ act) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int s = blockIdx.y;
+  const int M = counts[s];
+  if (M == 0) return;
+  const int32_t* list = lists + (size_t)s * P;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int col = lane & 15, grp = lane >> 4;
+  const int i0 = blockIdx.x * 64 + wave * 16;
+  const int nkb = H / kKB;
+  float* xsl = reinterpret_cast<float*>(smem + dma::Smem<32, S>::kBytes);
+  float* wsl = xsl + dma::kTokRows * nkb + wave * 2 * nkb;  // this wave's gate, up scales
+  const uint8_t* W = w13 + (size_t)s * w13_stride;
+  const float* Sg = s13 + (size_t)s * s13_stride + (size_t)(i0 / block_n) * nkb;
+  const float* Su = s13 + (size_t)s * s13_stride + (size_t)((I + i0) / block_n) * nkb;
+  for (int q = lane; q < nkb; q += 64) {
+    wsl[q] = Sg[q];
+    wsl[nkb + q] = Su[q];
+  }
+  // this lane's weight copy rows: slice rows 0-15 gate, 16-31 up
+  const unsigned char* wrow[32 / dma::kRowsPerCopy];
+#pragma unroll
+  for (int i = 0; i < 32 / dma::kRowsPerCopy; ++i) {
+    const int r = i * dma::kRowsPerCopy + lane / dma::kLanesPerRow;
+    wrow[i] = W + (size_t)(r < 16 ? i0 + r : I + i0 + r - 16) * H;
+  }
+  auto off = [](int c) { return (size_t)c * kKB; };
+  for (int m0 = 0; m0 < M; m0 += dma::kTokRows) {
+    const int mrows = min(M - m0, dma::kTokRows);
+    auto tok_of = [&](int r) { return list[m0 + r] / K; };
+    stage_token_scales(xsl, xs, nkb, mrows, m0 == 0, tok_of);
+    auto row_of = [&](int r) { return xq + (size_t)tok_of(r) * H; };
+    f32x4 ag[4], au[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      ag[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+      au[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    auto run = [&](auto nt) {
+      constexpr int NT = decltype(nt)::value;
+      dma::pass<32, S, NT>(smem, wrow, mrows, row_of, nkb, off,
+                           [&](const unsigned char* ws, const unsigned char* as, int c) {
+                             const i32x8 wg = lds_operand(ws, col, grp);
+                             const i32x8 wu = lds_operand(ws, 16 + col, grp);
+                             const float sg = wsl[c], su = wsl[nkb + c];
+#pragma unroll
+                             for (int t = 0; t < NT; ++t) {
+                               const i32x8 b = lds_operand(as, t * 16 + col, grp);
+                               const float sx = xsl[(t * 16 + col) * nkb + c];
+                               const f32x4 dg = mfma_fp8(wg, b);
+                               const f32x4 du = mfma_fp8(wu, b);
+#pragma unroll
+                               for (int j = 0; j < 4; ++j) {
+                                 ag[t][j] = ag[t][j] + (dg[j] * sx) * sg;
+                                 au[t][j] = au[t][j] + (du[j] * sx) * su;
+                               }
+                             }
+                           });
+    };
+    const int nt = (mrows + 15) >> 4;
+    if (nt == 1)
+      run(std::integral_constant<int, 1>{});
+    else if (nt == 2)
+      run(std::integral_constant<int, 2>{});
+    else if (nt == 3)
+      run(std::integral_constant<int, 3>{});
+    else
+      run(std::integral_constant<int, 4>{});
+    // D[row][col]: weight row i0 + 4 * grp + j, token column col
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int r = t * 16 + col;
+      if (r < mrows) {
+        const int p = list[m0 + r];
+        uint16_t* arow = act + (size_t)p * I + i0 + grp * 4;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float hg = round_bf16(ag[t][j]), hu = round_bf16(au[t][j]);
+          arow[j] = bf16_rne(round_bf16(silu(hg)) * hu);
+        }
+      }
+    }
+  }
+}
+
+template <int S>
+__global__ __launch_bounds__(256) void fp8_w2_dma_kernel(
+    const uint8_t* __restrict__ aq, const float* __restrict__ as_, int H, int I, int P,
+    const int32_t* __restrict__ lists, const int32_t* __restrict__ counts,
+    const float* __restrict__ topk_w, const uint8_t* __restrict__ w2, size_t w2_stride,
+    const float* __restrict__ s2, size_t s2_stride, int block_n, uint16_t* __restrict__ y) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int s = blockIdx.y;
+  const int M = counts[s];
+  if (M == 0) return;
+  const int32_t* list = lists + (size_t)s * P;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int col = lane & 15, grp = lane >> 4;
+  const int h0 = blockIdx.x * 128 + wave * 32;
+  const int nkb = I / kKB;
+  float* asl = reinterpret_cast<float*>(smem + dma::Smem<32, S>::kBytes);
+  float* wsl = asl + dma::kTokRows * nkb + wave * 2 * nkb;  // scales of row groups 0, 1
+  const uint8_t* W = w2 + (size_t)s * w2_stride;
+  for (int q = lane; q < 2 * nkb; q += 64) {
+    const int g = q / nkb, kb = q - g * nkb;
+    wsl[q] = s2[(size_t)s * s2_stride + (size_t)((h0 + 16 * g) / block_n) * nkb + kb];
+  }
+  const unsigned char* wrow[32 / dma::kRowsPerCopy];
+#pragma unroll
+  for (int i = 0; i < 32 / dma::kRowsPerCopy; ++i)
+    wrow[i] = W + (size_t)(h0 + i * dma::kRowsPerCopy + lane / dma::kLanesPerRow) * I;
+  auto off = [](int c) { return (size_t)c * kKB; };
+  for (int m0 = 0; m0 < M; m0 += dma::kTokRows) {
+    const int mrows = min(M - m0, dma::kTokRows);
+    auto pair_of = [&](int r) { return list[m0 + r]; };
+    stage_token_scales(asl, as_, nkb, mrows, m0 == 0, pair_of);
+    auto row_of = [&](int r) { return aq + (size_t)pair_of(r) * I; };
+    f32x4 acc[2][4];
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) acc[g][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    auto run = [&](auto nt) {
+      constexpr int NT = decltype(nt)::value;
+      dma::pass<32, S, NT>(smem, wrow, mrows, row_of, nkb, off,
+                           [&](const unsigned char* ws, const unsigned char* ts, int c) {
+                             i32x8 a[2];
+                             float sw[2];
+#pragma unroll
+                             for (int g = 0; g < 2; ++g) {
+                               a[g] = lds_operand(ws, g * 16 + col, grp);
+                               sw[g] = wsl[g * nkb + c];
+                             }
+#pragma unroll
+                             for (int t = 0; t < NT; ++t) {
+                               const i32x8 b = lds_operand(ts, t * 16 + col, grp);
+                               const float sa = asl[(t * 16 + col) * nkb + c];
+#pragma unroll
+                               for (int g = 0; g < 2; ++g) {
+                                 const f32x4 d = mfma_fp8(a[g], b);
+#pragma unroll
+                                 for (int j = 0; j < 4; ++j)
+                                   acc[g][t][j] = acc[g][t][j] + (d[j] * sa) * sw[g];
+                               }
+                             }
+                           });
+    };
+    const int nt = (mrows + 15) >> 4;
+    if (nt == 1)
+      run(std::integral_constant<int, 1>{});
+    else if (nt == 2)
+      run(std::integral_constant<int, 2>{});
+    else if (nt == 3)
+      run(std::integral_constant<int, 3>{});
+    else
+      run(std::integral_constant<int, 4>{});
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int r = t * 16 + col;
+      if (r < mrows) {
+        const int p = list[m0 + r];
+        const float w = topk_w[p];
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+          uint16_t* yr = y + (size_t)p * H + h0 + 16 * g + grp * 4;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) yr[j] = bf16_rne(acc[g][t][j] * w);
+        }
+      }
+    }
+  }
+}
+
 // out[t, h] = moe_sum over k ascending of y[(t, k), h]: bf16 adds for K in
 // {2, 3, 4}, else one float32 sum rounded once.  grid = (ceil(H / 256), T).
 __global__ __launch_bounds__(256) void fp8_combine_kernel(const uint16_t* __restrict__ y, int H,
@@ -822,6 +1047,37 @@ const char* fp8_unsupported(int H, int I, int K, int block_n, int block_k) {
   return nullptr;
 }
 
+// The LDS-staged kernels with the activation quantisation between them.
+template <int S13, int S2>
+bool launch_grouped_dma(const uint8_t* xq, const float* xs, uint8_t* aq, float* as, int T, int H,
+                        int I, int K, int nslots, const int32_t* lists, const int32_t* counts,
+                        const float* topk_w, const uint8_t* w13, size_t w13_stride,
+                        const float* s13, size_t s13_stride, const uint8_t* w2, size_t w2_stride,
+                        const float* s2, size_t s2_stride, int block_n, uint16_t* act,
+                        uint16_t* y, hipStream_t st, const StageEvents* ev) {
+  const size_t l13 = fp8_dma_lds<S13>(H / kKB), l2 = fp8_dma_lds<S2>(I / kKB);
+  if (l13 > kMaxLds || l2 > kMaxLds || H % 128) return false;
+  static bool big13 = false, big2 = false;
+  if (allow_lds(&fp8_w13_dma_kernel<S13>, l13, &big13) != hipSuccess ||
+      allow_lds(&fp8_w2_dma_kernel<S2>, l2, &big2) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  const int P = T * K;
+  hipEvent_t e0 = ev ? ev->ev[0] : nullptr, e1 = ev ? ev->ev[1] : nullptr;
+  hipEvent_t e2 = ev ? ev->ev[2] : nullptr, e3 = ev ? ev->ev[3] : nullptr;
+  launch_timed_lds(fp8_w13_dma_kernel<S13>, dim3(I / 64, nslots), dim3(256), (unsigned)l13, st,
+                   e0, e1, xq, xs, H, I, K, P, lists, counts, w13, w13_stride, s13, s13_stride,
+                   block_n, act);
+  const long jobs = (long)P * (I / kKB);
+  hipLaunchKernelGGL(quant_groups_kernel<uint16_t>, dim3((unsigned)((jobs + 15) / 16)),
+                     dim3(256), 0, st, (const uint16_t*)act, P, I, aq, as);
+  launch_timed_lds(fp8_w2_dma_kernel<S2>, dim3(H / 128, nslots), dim3(256), (unsigned)l2, st, e2,
+                   e3, aq, as, H, I, P, lists, counts, topk_w, w2, w2_stride, s2, s2_stride,
+                   block_n, y);
+  return true;
+}
+
 template <int MT, int U>
 void launch_grouped(const uint8_t* xq, const float* xs, uint8_t* aq, float* as, int T, int H,
                     int I, int K, int nslots, const int32_t* lists, const int32_t* counts,
@@ -874,6 +1130,22 @@ int experts_fp8_grouped(const void* x, int T, int H, int I, int K, const float* 
   const uint8_t* a13 = (const uint8_t*)w13;
   const uint8_t* a2 = (const uint8_t*)w2;
   uint16_t* ab = (uint16_t*)act;
+  // above 16 tokens the LDS-staged kernels; they return false where their
+  // LDS would not fit
+  // Two stages: an fp8 row is half a bf16 row's bytes, so its k loop is
+  // short (16 and 6 chunks at the Qwen3 shape), and with 48 KiB of stages
+  // three blocks fit per CU and overlap each other's setup.  Measured on
+  // MI355X at the Qwen3-FP8 512-token chunk: 157 us, against 172 us with
+  // three stages.
+  if (T > 16 && launch_grouped_dma<2, 2>(xq, xs, aq, as, T, H, I, K, nslots, lists, counts,
+                                         topk_w, (const uint8_t*)w13, w13_stride, s13,
+                                         s13_stride, (const uint8_t*)w2, w2_stride, s2, s2_stride,
+                                         block_n, (uint16_t*)act, y, st, ev)) {
+    hipLaunchKernelGGL(fp8_combine_kernel, dim3((H + 255) / 256, T), dim3(256), 0, st, y, H, K,
+                       nslots, slots, (uint16_t*)out);
+    WISP_HIP_TRY(hipGetLastError());
+    return WISP_OK;
+  }
   // two k-blocks per iteration when both k extents allow it; 16-token tiles
   // per pass: a slot holds at most T tokens
   const bool u2 = (H / kKB) % 2 == 0 && (I / kKB) % 2 == 0;
