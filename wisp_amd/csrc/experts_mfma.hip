@@ -609,14 +609,14 @@ int experts_mfma(const void* x, int T, int H, int I, int K, const float* topk_w,
   uint16_t* ab = (uint16_t*)act;
   // Measured on MI355X at the Qwen3 shapes (resident layer, 128 experts):
   // up to 16 tokens the direct-load kernels with one tile and eight k-steps
-  // per iteration; above, the LDS-staged kernels with three stages, which at
-  // 32 / 128 / 512 / 2048 tokens took 0.96 / 0.96 / 0.92 / 0.78 of the time
-  // of the register-pipelined and direct-load kernels they replace.
+  // per iteration; above, the LDS-staged kernels, w13 with two copy stages
+  // (three blocks per CU: 241 against 244 us at 512 tokens) and w2 with
+  // three (its shorter rows gain nothing from a third block per CU).
   if (T <= 16)
     launch_gemms<1, 8>(xb, H, I, K, P, nslots, lists, counts, a13, w13_stride, a2, w2_stride, ab,
                        y, st, ev);
   else
-    launch_dma<3, 3>(xb, H, I, K, P, nslots, lists, counts, a13, w13_stride, a2, w2_stride, ab,
+    launch_dma<2, 3>(xb, H, I, K, P, nslots, lists, counts, a13, w13_stride, a2, w2_stride, ab,
                      y, st, ev);
   launch_combine(y, T, H, K, nslots, topk_w, slots, (uint16_t*)out, st);
   WISP_HIP_TRY(hipGetLastError());
