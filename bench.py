@@ -305,7 +305,7 @@ def bench_mixtral(args) -> dict:
                        "resident_tok_per_s": round(8 * 16 / re16, 1),
                        "resident_expert_gemm": _gemm_report(
                            ra16, sh, 16, sum(_distinct(wl16.logits[i], 2) for i in range(10)) / 10,
-                           "mfma_w13_kernel + mfma_w2_kernel")},
+                           "mfma_w13_dma_kernel + mfma_w2_dma_kernel")},
                  cpu_baseline=cpu)
 
 

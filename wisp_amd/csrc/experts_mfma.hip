@@ -14,10 +14,11 @@
 //   2. w13: block (i-panel of 64, slot s) streams the 64 gate rows and 64 up
 //      rows of the panel once per 64 tokens of s and multiplies them against
 //      those tokens, 16 per MFMA tile (v_mfma_f32_16x16x32_bf16); epilogue
-//      silu(g) * u.  Up to 16 tokens per call the fragments are loaded straight
-//      into registers (the tokens from the L2-resident x rows); above that
-//      both operands are staged through LDS by asynchronous global->LDS copies;
-//   3. w2: block (h-panel of 64, slot s) likewise over act, writing fp32 y;
+//      silu(g) * u.  Below 16 tokens per call the fragments are loaded
+//      straight into registers (the tokens from the L2-resident x rows); from
+//      16 both operands are staged through LDS by asynchronous global->LDS
+//      copies;
+//   3. w2: block (h-panel, slot s) likewise over act, writing fp32 y;
 //   4. combine: out[t] from y in routing order.
 // Each output element is one MFMA dot product chain over K in a fixed order
 // (ascending 32-column k-steps from a start column set by the output panel,
@@ -607,12 +608,14 @@ int experts_mfma(const void* x, int T, int H, int I, int K, const float* topk_w,
   const uint16_t* a13 = (const uint16_t*)w13;
   const uint16_t* a2 = (const uint16_t*)w2;
   uint16_t* ab = (uint16_t*)act;
-  // Measured on MI355X at the Qwen3 shapes (resident layer, 128 experts):
-  // up to 16 tokens the direct-load kernels with one tile and eight k-steps
-  // per iteration; above, the LDS-staged kernels, w13 with two copy stages
+  // Measured on MI355X (resident layers): below 16 tokens the direct-load
+  // kernels with one tile and eight k-steps per iteration (calls that small
+  // reach this path only as token groups of a larger paged call); from 16
+  // tokens the LDS-staged kernels (Qwen3 at 16 tokens 160 against 171 us,
+  // Mixtral-8x7B at 16 tokens 461 against 497 us), w13 with two copy stages
   // (three blocks per CU: 241 against 244 us at 512 tokens) and w2 with
   // three (its shorter rows gain nothing from a third block per CU).
-  if (T <= 16)
+  if (T < 16)
     launch_gemms<1, 8>(xb, H, I, K, P, nslots, lists, counts, a13, w13_stride, a2, w2_stride, ab,
                        y, st, ev);
   else
