@@ -235,8 +235,8 @@ def test_experts_mfma_prefill_slot_sizes(H, I):
 
 
 def test_mfma_prefill_bytes_independent_of_grouping():
-    # a token's bytes are the same whether the call holds 300 tokens (LDS-
-    # staged prefill kernels), 150 or 40 (direct-load kernels)
+    # a token's bytes are the same whether the call holds 300 tokens (several
+    # 64-token passes per slot), 150 or 40
     x, w, ids, w13, w2 = _expert_case(31, 300, 1024, 512, 16, 8, torch.bfloat16)
     xd, wd, idd, w13d, w2d = _dev_case(x, w, ids, w13, w2)
     whole = run_experts(xd, wd, idd, w13d, w2d, algo=MFMA)

@@ -14,11 +14,9 @@
 //   2. w13: block (i-panel of 64, slot s) streams the 64 gate rows and 64 up
 //      rows of the panel once per 64 tokens of s and multiplies them against
 //      those tokens, 16 per MFMA tile (v_mfma_f32_16x16x32_bf16); epilogue
-//      silu(g) * u.  Below 16 tokens per call the fragments are loaded
-//      straight into registers (the tokens from the L2-resident x rows); from
-//      16 both operands are staged through LDS by asynchronous global->LDS
-//      copies;
-//   3. w2: block (h-panel, slot s) likewise over act, writing fp32 y;
+//      silu(g) * u.  Both operands are staged through LDS by asynchronous
+//      global->LDS copies (dma_pipeline.h);
+//   3. w2: block (h-panel of 128, slot s) likewise over act, writing fp32 y;
 //   4. combine: out[t] from y in routing order.
 // Each output element is one MFMA dot product chain over K in a fixed order
 // (ascending 32-column k-steps from a start column set by the output panel,
@@ -42,18 +40,13 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kKAlign = 256;         // H and I must be multiples (up to 8 k-steps per iteration)
+constexpr int kKAlign = 256;         // H and I must be multiples
 constexpr int kPanel = 64;           // output columns per block: 4 waves x 16
 // The LDS-staged w2 kernel's blocks own 128 output rows (4 waves x 32): a
 // w2 row is only 12 chunks long at the Qwen3 shape, so per-block setup and
 // the token tile weigh more than in w13, and 32 rows per wave halve both.
 constexpr int kW2PanelsPer = 2;      // 64-row panels per LDS-staged w2 block
 
-// Weight and token fragments alike use plain loads: here the nontemporal
-// hint made every variant slower (measured on MI355X at the Qwen3 shape: -8 %
-// at 16 and 32 tokens, -4 % at 512), unlike the decode GEMV.
-__device__ inline u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
-__device__ inline bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
 __device__ inline uint16_t bf16_rne(float f) {
   uint32_t u = __float_as_uint(f);
@@ -128,24 +121,6 @@ __global__ __launch_bounds__(64 * kGatherWaves) void gather_kernel(
   if (tid == 0) counts[s] = n;
 }
 
-// Row pointers of this lane's A rows (row lane%16 of each 16-token tile of
-// the pass starting at m0), offset to the lane's 8 columns of a k-step; null
-// for rows past the slot's last token (they read as zero).
-template <int MT, bool kTokenRows>
-__device__ inline void a_rows(const uint16_t* (&ap)[MT], const uint16_t* __restrict__ A, int ld,
-                              int K, const int32_t* __restrict__ list, int m0, int mrows,
-                              int lane) {
-#pragma unroll
-  for (int t = 0; t < MT; ++t) {
-    const int r = t * 16 + (lane & 15);
-    ap[t] = nullptr;
-    if (r < mrows) {
-      const int p = list[m0 + r];
-      ap[t] = A + (size_t)(kTokenRows ? p / K : p) * ld + (lane >> 4) * 8;
-    }
-  }
-}
-
 // Where the k loop of an output panel starts.  Every block streams its rows
 // chunk by chunk; when all blocks start at column 0, the reads in flight share
 // their low address bits and crowd a few memory channels (a pure read of the
@@ -153,11 +128,10 @@ __device__ inline void a_rows(const uint16_t* (&ap)[MT], const uint16_t* __restr
 // at its own multiple of 64 columns, evenly spread over the row, and wrapping
 // around gives 5.9 TB/s.  The start depends only on the panel (blockIdx.x),
 // never on the slot, so an output's dot-product order is the same for any
-// slot placement or token grouping, and both kernel families below use it.
-__device__ inline int k_rotation(int Kdim, unsigned panel, unsigned npanels) {
-  return (int)(panel * (unsigned)(Kdim / 64) / npanels) * 64;
+// slot placement or token grouping.
+__device__ inline int k_rotation(int Kdim) {
+  return (int)(blockIdx.x * (unsigned)(Kdim / 64) / gridDim.x) * 64;
 }
-__device__ inline int k_rotation(int Kdim) { return k_rotation(Kdim, blockIdx.x, gridDim.x); }
 
 // Column of k-step offset k (0 <= k < Kdim) in a loop rotated by rot columns.
 __device__ inline int k_col(int k, int rot, int Kdim) {
@@ -165,153 +139,11 @@ __device__ inline int k_col(int k, int rot, int Kdim) {
   return c >= Kdim ? c - Kdim : c;
 }
 
-__device__ inline u32x4 ld16_or_zero(const uint16_t* p, int off) {
-  if (!p) return u32x4{0u, 0u, 0u, 0u};
-  return ld16(p + off);
-}
-
 // ---------------------------------------------------------------------------
-// 2. w13 + SiLU*mul.  grid = (I / 64, nslots); wave w owns i in
-// [blockIdx.x*64 + 16w, +16): gate rows i and up rows I + i.  Each wave
-// streams its 32 weight rows once per pass of up to MT*16 tokens, U k-steps
-// of 32 columns per iteration (16-byte loads per lane), and fetches the token
-// fragments of the same k-steps from x (small and shared: L2-resident).
-// No LDS, no barriers: waves are independent streams.
-// ---------------------------------------------------------------------------
-template <int MT, int U>
-__global__ __launch_bounds__(256) void mfma_w13_kernel(
-    const uint16_t* __restrict__ x, int H, int I, int K, int P, const int32_t* __restrict__ lists,
-    const int32_t* __restrict__ counts, const uint16_t* __restrict__ w13, size_t w13_stride,
-    uint16_t* __restrict__ act) {
-  const int s = blockIdx.y;
-  const int M = counts[s];
-  if (M == 0) return;
-  const int32_t* list = lists + (size_t)s * P;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int i0 = blockIdx.x * kPanel + wave * 16;
-  const uint16_t* Wg = w13 + (size_t)s * w13_stride + (size_t)(i0 + (lane & 15)) * H +
-                       (lane >> 4) * 8;
-  const uint16_t* Wu = Wg + (size_t)I * H;
-
-  const int rot = k_rotation(H);
-  for (int m0 = 0; m0 < M; m0 += MT * 16) {
-    const int mrows = min(M - m0, MT * 16);
-    const uint16_t* ap[MT];
-    a_rows<MT, true>(ap, x, H, K, list, m0, mrows, lane);
-    f32x4 ag[MT], au[MT];
-#pragma unroll
-    for (int t = 0; t < MT; ++t) {
-      ag[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-      au[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-    for (int k0 = 0; k0 < H; k0 += 32 * U) {
-      u32x4 bg[U], bu[U], a[U][MT];
-      int kc[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) kc[u] = k_col(k0 + u * 32, rot, H);
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        bg[u] = ld16(Wg + kc[u]);
-        bu[u] = ld16(Wu + kc[u]);
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u)
-#pragma unroll
-        for (int t = 0; t < MT; ++t) a[u][t] = ld16_or_zero(ap[t], kc[u]);
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-#pragma unroll
-        for (int t = 0; t < MT; ++t) {
-          if (t * 16 < mrows) {
-            ag[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a[u][t]), as_bf16x8(bg[u]),
-                                                            ag[t], 0, 0, 0);
-            au[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a[u][t]), as_bf16x8(bu[u]),
-                                                            au[t], 0, 0, 0);
-          }
-        }
-      }
-    }
-    // C[row][col]: row = 16t + 4*(lane/16) + q, col = lane % 16
-#pragma unroll
-    for (int t = 0; t < MT; ++t) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int r = t * 16 + (lane >> 4) * 4 + q;
-        if (r < mrows) {
-          const int p = list[m0 + r];
-          act[(size_t)p * I + i0 + (lane & 15)] = bf16_rne(silu(ag[t][q]) * au[t][q]);
-        }
-      }
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// 3. w2: y[p, h] = W2[s][h, :] . act[p, :].  grid = (H / 64, nslots); wave w
-// owns h in [blockIdx.x*64 + 16w, +16); same streaming scheme over act, with
-// the k rotation of the 128-row panel around its block.
-// ---------------------------------------------------------------------------
-template <int MT, int U>
-__global__ __launch_bounds__(256) void mfma_w2_kernel(
-    const uint16_t* __restrict__ act, int H, int I, int P, const int32_t* __restrict__ lists,
-    const int32_t* __restrict__ counts, const uint16_t* __restrict__ w2, size_t w2_stride,
-    float* __restrict__ y) {
-  const int s = blockIdx.y;
-  const int M = counts[s];
-  if (M == 0) return;
-  const int32_t* list = lists + (size_t)s * P;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int h0 = blockIdx.x * kPanel + wave * 16;
-  const uint16_t* Wr = w2 + (size_t)s * w2_stride + (size_t)(h0 + (lane & 15)) * I +
-                       (lane >> 4) * 8;
-
-  // the w2 rotation belongs to the 128-row panel the LDS-staged kernel uses
-  const int rot = k_rotation(I, blockIdx.x / kW2PanelsPer, gridDim.x / kW2PanelsPer);
-  for (int m0 = 0; m0 < M; m0 += MT * 16) {
-    const int mrows = min(M - m0, MT * 16);
-    const uint16_t* ap[MT];
-    a_rows<MT, false>(ap, act, I, 1, list, m0, mrows, lane);
-    f32x4 acc[MT];
-#pragma unroll
-    for (int t = 0; t < MT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int k0 = 0; k0 < I; k0 += 32 * U) {
-      u32x4 b[U], a[U][MT];
-      int kc[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) kc[u] = k_col(k0 + u * 32, rot, I);
-#pragma unroll
-      for (int u = 0; u < U; ++u) b[u] = ld16(Wr + kc[u]);
-#pragma unroll
-      for (int u = 0; u < U; ++u)
-#pragma unroll
-        for (int t = 0; t < MT; ++t) a[u][t] = ld16_or_zero(ap[t], kc[u]);
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-#pragma unroll
-        for (int t = 0; t < MT; ++t) {
-          if (t * 16 < mrows)
-            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a[u][t]), as_bf16x8(b[u]),
-                                                             acc[t], 0, 0, 0);
-        }
-      }
-    }
-#pragma unroll
-    for (int t = 0; t < MT; ++t) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int r = t * 16 + (lane >> 4) * 4 + q;
-        if (r < mrows) y[(size_t)list[m0 + r] * H + h0 + (lane & 15)] = acc[t][q];
-      }
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// LDS-staged kernels for calls of more than 16 tokens: the chunk pipeline of
-// dma_pipeline.h over 64-column (128-byte) chunks, two 32-column k-steps of
-// MFMA per chunk, the k rotation of the output panel.  w13 blocks own a
-// 64-row panel (each wave 16 gate and 16 up rows); w2 blocks own 128 rows
-// (32 per wave).
+// w13 and w2 kernels: the chunk pipeline of dma_pipeline.h over 64-column
+// (128-byte) chunks, two 32-column k-steps of MFMA per chunk, the k rotation
+// of the output panel.  w13 blocks own a 64-row panel (each wave 16 gate and
+// 16 up rows); w2 blocks own 128 rows (32 per wave).
 // What bounds them: a pure read of the Qwen3 w13 tensor in this chunk order
 // and rotation runs at 5.9 TB/s on MI355X and w13 here at 5.3 TB/s of
 // weights; the w2 tensor reads at 6.2 TB/s and w2 here at 4.5 TB/s.
@@ -525,19 +357,6 @@ void launch_combine(const float* y, int T, int H, int K, int nslots, const float
                        slots, out);
 }
 
-template <int MT, int U>
-void launch_gemms(const uint16_t* x, int H, int I, int K, int P, int nslots, const int32_t* lists,
-                  const int32_t* counts, const uint16_t* w13, size_t w13_stride,
-                  const uint16_t* w2, size_t w2_stride, uint16_t* act, float* y, hipStream_t st,
-                  const StageEvents* ev) {
-  hipEvent_t e0 = ev ? ev->ev[0] : nullptr, e1 = ev ? ev->ev[1] : nullptr;
-  hipEvent_t e2 = ev ? ev->ev[2] : nullptr, e3 = ev ? ev->ev[3] : nullptr;
-  launch_timed(mfma_w13_kernel<MT, U>, dim3(I / kPanel, nslots), dim3(256), st, e0, e1, x, H, I,
-               K, P, lists, counts, w13, w13_stride, act);
-  launch_timed(mfma_w2_kernel<MT, U>, dim3(H / kPanel, nslots), dim3(256), st, e2, e3, act, H, I,
-               P, lists, counts, w2, w2_stride, y);
-}
-
 template <int S13, int S2>
 void launch_dma(const uint16_t* x, int H, int I, int K, int P, int nslots, const int32_t* lists,
                 const int32_t* counts, const uint16_t* w13, size_t w13_stride,
@@ -608,19 +427,13 @@ int experts_mfma(const void* x, int T, int H, int I, int K, const float* topk_w,
   const uint16_t* a13 = (const uint16_t*)w13;
   const uint16_t* a2 = (const uint16_t*)w2;
   uint16_t* ab = (uint16_t*)act;
-  // Measured on MI355X (resident layers): below 16 tokens the direct-load
-  // kernels with one tile and eight k-steps per iteration (calls that small
-  // reach this path only as token groups of a larger paged call); from 16
-  // tokens the LDS-staged kernels (Qwen3 at 16 tokens 160 against 171 us,
-  // Mixtral-8x7B at 16 tokens 461 against 497 us), w13 with two copy stages
-  // (three blocks per CU: 241 against 244 us at 512 tokens) and w2 with
-  // three (its shorter rows gain nothing from a third block per CU).
-  if (T < 16)
-    launch_gemms<1, 8>(xb, H, I, K, P, nslots, lists, counts, a13, w13_stride, a2, w2_stride, ab,
-                       y, st, ev);
-  else
-    launch_dma<2, 3>(xb, H, I, K, P, nslots, lists, counts, a13, w13_stride, a2, w2_stride, ab,
-                     y, st, ev);
+  // w13 with two copy stages (three blocks per CU: 241 against 244 us at the
+  // Qwen3 512-token chunk), w2 with three (its shorter rows gain nothing from
+  // a third block per CU).  Measured on MI355X, these kernels also beat
+  // register-streaming ones at every call size, down to 4 tokens (71 against
+  // 109 us at the Qwen3 shape).
+  launch_dma<2, 3>(xb, H, I, K, P, nslots, lists, counts, a13, w13_stride, a2, w2_stride, ab, y,
+                   st, ev);
   launch_combine(y, T, H, K, nslots, topk_w, slots, (uint16_t*)out, st);
   WISP_HIP_TRY(hipGetLastError());
   return WISP_OK;

@@ -97,16 +97,19 @@ bool mfma_supported(int H, int I);
 
 // Calls of at least this many tokens run the bf16 experts on the MFMA grouped
 // GEMM; fewer run the GEMV kernels, which stream each routed expert once per
-// token and win while the tokens of a call share few experts (measured on
-// MI355X at the Qwen3 shape, uniform routing: equal at 16 tokens, MFMA 1.4x
-// faster at 32 and 8.8x at 512).
-constexpr int kMfmaMinTokens = 16;
+// token and win while the tokens of a call share few experts.  Measured on
+// MI355X at the Qwen3 shape with uniform routing (resident, us per call):
+// GEMV 136 / 158 / 178 and MFMA 141 / 147 / 153 at 12 / 14 / 16 tokens.
+constexpr int kMfmaMinTokens = 14;
+// The block-FP8 grouped path takes over from its decode kernels from here.
+constexpr int kFp8GroupedMinTokens = 16;
 
 // The automatic expert-kernel choice.  It depends only on the call's dtype,
 // shape and token count, never on the grouping or the slots, so paged and
 // resident runs of one batch use one kernel.
 int auto_algo(int dtype, int H, int I, int T) {
-  if (dtype == WISP_FP8_E4M3) return T >= kMfmaMinTokens ? WISP_ALGO_MFMA : WISP_ALGO_GEMV;
+  if (dtype == WISP_FP8_E4M3)
+    return T >= kFp8GroupedMinTokens ? WISP_ALGO_MFMA : WISP_ALGO_GEMV;
   return dtype == WISP_BF16 && mfma_supported(H, I) && T >= kMfmaMinTokens ? WISP_ALGO_MFMA
                                                                           : WISP_ALGO_GEMV;
 }
