@@ -284,7 +284,8 @@ int wisp_layer_prime_identity(void* handle, wisp_stream_t stream);
 
 /* Milliseconds the page-in copies of the layer calls since the last query
  * took (memcpy engine: from the first copy to the last; kernel engine: the
- * copy kernels' execution) and the bytes they moved; then reset both. */
+ * copy kernels' execution) and the bytes they moved; then reset both.  Only
+ * calls made while timing is on (wisp_layer_profile) are counted. */
 int wisp_layer_last_pagein(void* handle, float* ms, double* bytes);
 
 /* The page-in engine the layer uses (WISP_PAGEIN_*), or -1 for a bad handle. */
@@ -294,7 +295,9 @@ int wisp_layer_pagein_engine(void* handle);
  * w13+SiLU kernels and of the w2+combine kernels of all layer calls since the
  * last read, and the number of layer calls; then switch timing on
  * (enable != 0) or off.  A speculative w2 launch that found experts to load
- * and exited is not counted. */
+ * and exited is not counted.  The switch also covers the page-in timing of
+ * wisp_layer_last_pagein.  Timing is off by default: every timed launch
+ * carries dispatch-timestamp events, which lengthen the stream. */
 int wisp_layer_profile(void* handle, int enable, double* w13_ms, double* w2_ms,
                        int64_t* calls);
 

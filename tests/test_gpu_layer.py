@@ -35,8 +35,10 @@ def bits(t):
     return t.view(torch.int16) if t.dtype == torch.bfloat16 else t.view(torch.int32)
 
 
-def drive(wl, cap, steps, check_out_every=1, tol=None, act_round=None, algo=0):
+def drive(wl, cap, steps, check_out_every=1, tol=None, act_round=None, algo=0, timed=False):
     sts = states(wl, cap)
+    if timed:
+        sts["paged"].profile(True)
     ora = PagerOracle(wl.shape.experts, cap)
     w13, w2 = wl.views()
     K = wl.shape.top_k
@@ -78,10 +80,16 @@ def test_qwen3_bf16_layer_decode(monkeypatch, engine, streams):
     monkeypatch.setenv("WISP_PAGEIN_ENGINE", engine)
     monkeypatch.setenv("WISP_PAGEIN_STREAMS", streams)
     wl = W.qwen3_decode(steps=48, pin=True)
-    sts = drive(wl, 8, wl.steps, check_out_every=8, tol=1e-2)
+    sts = drive(wl, 8, wl.steps, check_out_every=8, tol=1e-2, timed=True)
     assert sts["paged"].pagein_engine == engine
     ms, nbytes = sts["paged"].pagein_stats()
     assert ms > 0 and nbytes == sts["paged"].stats_miss * wl.shape.expert_bytes
+    # timing off (the default): the same calls count nothing
+    sts["paged"].profile(False)
+    for t in range(4):
+        sts["paged"].forward(wl.x[t].to(DEV), wl.logits[t].to(DEV), wl.shape.top_k, True)
+    torch.cuda.synchronize()
+    assert sts["paged"].pagein_stats() == (0.0, 0.0)
 
 
 @pytest.mark.parametrize("engine,streams", [("kernel", "0"), ("memcpy", "0"), ("memcpy", "2")])

@@ -402,7 +402,8 @@ class WispMoEState:
                 "clock": bool(r[2])}
 
     def pagein_stats(self) -> tuple[float, float]:
-        """(milliseconds, bytes) of page-in copies since the last query."""
+        """(milliseconds, bytes) of page-in copies since the last query,
+        counting the calls made while timing is on (``profile(True)``)."""
         ms, nbytes = C.c_float(), C.c_double()
         check(lib().wisp_layer_last_pagein(self._handle, C.byref(ms), C.byref(nbytes)),
               "pagein_stats")
@@ -411,7 +412,9 @@ class WispMoEState:
     def profile(self, enable: bool = True) -> dict:
         """Read and reset the execution time (ms, dispatch timestamps) of the
         ``w13`` and ``w2`` expert kernels of all layer calls since the last
-        read and the number of ``calls``; then switch timing on or off."""
+        read and the number of ``calls``; then switch timing on or off.  The
+        switch covers ``pagein_stats`` too; timing is off by default, since
+        its events lengthen the stream."""
         a, b, n = C.c_double(), C.c_double(), C.c_int64()
         check(lib().wisp_layer_profile(self._handle, int(enable), C.byref(a), C.byref(b),
                                        C.byref(n)), "profile")
