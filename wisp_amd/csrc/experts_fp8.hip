@@ -85,7 +85,26 @@ __device__ inline uint16_t bf16_rne(float f) {
 
 __device__ inline float round_bf16(float f) { return bf16f(bf16_rne(f)); }
 
+// Four values as bf16 to the 8 consecutive, 8-byte aligned bytes at p, in
+// one store (an MFMA lane holds four consecutive output columns).
+__device__ inline void store_bf16x4(uint16_t* p, float a, float b, float c, float d) {
+  *reinterpret_cast<uint2*>(p) =
+      make_uint2((uint32_t)bf16_rne(a) | ((uint32_t)bf16_rne(b) << 16),
+                 (uint32_t)bf16_rne(c) | ((uint32_t)bf16_rne(d) << 16));
+}
+
 __device__ inline float silu(float g) { return g / (1.0f + expf(-g)); }
+
+// act = bf16(bf16(silu(bf16(g))) * bf16(u)) for four consecutive columns.
+__device__ inline void store_act4(uint16_t* p, const f32x4& g, const f32x4& u) {
+  float v[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float hg = round_bf16(g[j]), hu = round_bf16(u[j]);
+    v[j] = round_bf16(silu(hg)) * hu;
+  }
+  store_bf16x4(p, v[0], v[1], v[2], v[3]);
+}
 
 __device__ inline f32x4 mfma_fp8(const i32x8& a, const i32x8& b) {
   const f32x4 z = {0.f, 0.f, 0.f, 0.f};
@@ -366,12 +385,8 @@ __global__ __launch_bounds__(NW * 64) void fp8_w13_kernel(
           u[j] = u[j] + rr[64 * 4 + j];
         }
       }
-      uint16_t* arow = act + (size_t)mypair * I + i0 + grp * 4;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float hg = round_bf16(g[j]), hu = round_bf16(u[j]);
-        arow[j] = bf16_rne(round_bf16(silu(hg)) * hu);
-      }
+      store_act4(act + (size_t)mypair * I + i0 + grp * 4, f32x4{g[0], g[1], g[2], g[3]},
+                 f32x4{u[0], u[1], u[2], u[3]});
     }
     __syncthreads();  // red is rewritten by the next column set
   }
@@ -615,12 +630,7 @@ __global__ __launch_bounds__(256) void fp8_grouped_w13_kernel(
       const int r = t * 16 + col;
       if (r < mrows) {
         const int p = list[m0 + r];
-        uint16_t* arow = act + (size_t)p * I + i0 + grp * 4;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float hg = round_bf16(ag[t][j]), hu = round_bf16(au[t][j]);
-          arow[j] = bf16_rne(round_bf16(silu(hg)) * hu);
-        }
+        store_act4(act + (size_t)p * I + i0 + grp * 4, ag[t], au[t]);
       }
     }
   }
@@ -682,9 +692,8 @@ __global__ __launch_bounds__(256) void fp8_grouped_w2_kernel(
       if (r < mrows) {
         const int p = list[m0 + r];
         const float w = topk_w[p];
-        uint16_t* yr = y + (size_t)p * H + h0 + grp * 4;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) yr[j] = bf16_rne(acc[t][j] * w);
+        store_bf16x4(y + (size_t)p * H + h0 + grp * 4, acc[t][0] * w, acc[t][1] * w,
+                     acc[t][2] * w, acc[t][3] * w);
       }
     }
   }
@@ -768,6 +777,11 @@ __global__ __launch_bounds__(256) void fp8_w13_dma_kernel(
   auto off = [](int c) { return (size_t)c * kKB; };
   for (int m0 = 0; m0 < M; m0 += dma::kTokRows) {
     const int mrows = min(M - m0, dma::kTokRows);
+    // the pairs of this lane's output rows (tile t, row col), loaded with
+    // the token-scale staging's own list loads rather than after the k loop
+    int pr[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) pr[t] = list[m0 + min(t * 16 + col, mrows - 1)];
     auto tok_of = [&](int r) { return list[m0 + r] / K; };
     stage_token_scales(xsl, xs, nkb, mrows, m0 == 0, tok_of);
     auto row_of = [&](int r) { return xq + (size_t)tok_of(r) * H; };
@@ -812,13 +826,7 @@ __global__ __launch_bounds__(256) void fp8_w13_dma_kernel(
     for (int t = 0; t < 4; ++t) {
       const int r = t * 16 + col;
       if (r < mrows) {
-        const int p = list[m0 + r];
-        uint16_t* arow = act + (size_t)p * I + i0 + grp * 4;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float hg = round_bf16(ag[t][j]), hu = round_bf16(au[t][j]);
-          arow[j] = bf16_rne(round_bf16(silu(hg)) * hu);
-        }
+        store_act4(act + (size_t)pr[t] * I + i0 + grp * 4, ag[t], au[t]);
       }
     }
   }
@@ -853,8 +861,17 @@ __global__ __launch_bounds__(256) void fp8_w2_dma_kernel(
   auto off = [](int c) { return (size_t)c * kKB; };
   for (int m0 = 0; m0 < M; m0 += dma::kTokRows) {
     const int mrows = min(M - m0, dma::kTokRows);
+    // the pairs and routing weights of this lane's output rows (tile t, row
+    // col): the pairs load with the token-scale staging's list loads, the
+    // weights with the pass's token-row loads, not after the k loop
+    int pr[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) pr[t] = list[m0 + min(t * 16 + col, mrows - 1)];
     auto pair_of = [&](int r) { return list[m0 + r]; };
     stage_token_scales(asl, as_, nkb, mrows, m0 == 0, pair_of);
+    float pw[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) pw[t] = topk_w[pr[t]];
     auto row_of = [&](int r) { return aq + (size_t)pair_of(r) * I; };
     f32x4 acc[2][4];
 #pragma unroll
@@ -899,13 +916,10 @@ __global__ __launch_bounds__(256) void fp8_w2_dma_kernel(
     for (int t = 0; t < 4; ++t) {
       const int r = t * 16 + col;
       if (r < mrows) {
-        const int p = list[m0 + r];
-        const float w = topk_w[p];
 #pragma unroll
         for (int g = 0; g < 2; ++g) {
-          uint16_t* yr = y + (size_t)p * H + h0 + 16 * g + grp * 4;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) yr[j] = bf16_rne(acc[g][t][j] * w);
+          store_bf16x4(y + (size_t)pr[t] * H + h0 + 16 * g + grp * 4, acc[g][t][0] * pw[t],
+                       acc[g][t][1] * pw[t], acc[g][t][2] * pw[t], acc[g][t][3] * pw[t]);
         }
       }
     }

@@ -150,10 +150,12 @@ __device__ inline int k_col(int k, int rot, int Kdim) {
 // ---------------------------------------------------------------------------
 
 // The pass's GEMM over Kdim columns for mrows tokens (list[m0 ..]):
-// acc[g][t] += A(token tile t) . W(row group g)^T for the NT = ceil(mrows /
+// acc[g][t] += W(row group g) . A(token tile t)^T for the NT = ceil(mrows /
 // 16) tiles the pass fills, NG row groups of 16 per wave, the k loop starting
 // rot columns in.  A is the token matrix (leading dimension ld); with
-// kTokenRows, pair p reads row p / K.
+// kTokenRows, pair p reads row p / K.  With the weights as the MFMA's first
+// operand, lane l holds rows 4 (l / 16) + q, q < 4, of its group for token
+// column l % 16: four consecutive outputs of one token, stored at once.
 template <int NG, int S, bool kTokenRows>
 __device__ inline void dma_gemm(unsigned char* smem,
                                 const unsigned char* const (&wrow)[16 * NG / dma::kRowsPerCopy],
@@ -186,7 +188,7 @@ __device__ inline void dma_gemm(unsigned char* smem,
 #pragma unroll
               for (int g = 0; g < NG; ++g)
                 acc[g][t] =
-                    __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[t], b[g], acc[g][t], 0, 0, 0);
+                    __builtin_amdgcn_mfma_f32_16x16x32_bf16(b[g], a[t], acc[g][t], 0, 0, 0);
           }
         });
   };
@@ -199,6 +201,25 @@ __device__ inline void dma_gemm(unsigned char* smem,
     run(std::integral_constant<int, 3>{});
   else
     run(std::integral_constant<int, 4>{});
+}
+
+// The pairs of the token columns this lane stores after the pass (tile t,
+// column lane % 16; columns past mrows repeat the last), loaded before the
+// pass so that they travel with its own token-row loads instead of adding a
+// memory round trip after the k loop.
+__device__ inline void epilogue_pairs(const int32_t* __restrict__ list, int m0, int mrows,
+                                      int (&pr)[4]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) pr[t] = list[m0 + min(t * 16 + (lane & 15), mrows - 1)];
+}
+
+// bf16(silu(g) * u) of four consecutive columns, one 8-byte store at p.
+__device__ inline void store_act4(uint16_t* p, const f32x4& g, const f32x4& u) {
+  uint32_t h[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) h[q] = bf16_rne(silu(g[q]) * u[q]);
+  *reinterpret_cast<uint2*>(p) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
 }
 
 template <int S>
@@ -230,18 +251,13 @@ __global__ __launch_bounds__(256) void mfma_w13_dma_kernel(
     for (int g = 0; g < 2; ++g)
 #pragma unroll
       for (int t = 0; t < 4; ++t) acc[g][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    int pr[4];
+    epilogue_pairs(list, m0, mrows, pr);
     dma_gemm<2, S, true>(dsm, wrow, x, H, K, list, m0, mrows, H, rot, acc);
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int r = t * 16 + (lane >> 4) * 4 + q;
-        if (r < mrows) {
-          const int p = list[m0 + r];
-          act[(size_t)p * I + i0 + (lane & 15)] = bf16_rne(silu(acc[0][t][q]) * acc[1][t][q]);
-        }
-      }
-    }
+    for (int t = 0; t < 4; ++t)
+      if (t * 16 + (lane & 15) < mrows)
+        store_act4(act + (size_t)pr[t] * I + i0 + (lane >> 4) * 4, acc[0][t], acc[1][t]);
   }
 }
 
@@ -272,19 +288,16 @@ __global__ __launch_bounds__(256) void mfma_w2_dma_kernel(
     for (int g = 0; g < NG; ++g)
 #pragma unroll
       for (int t = 0; t < 4; ++t) acc[g][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    int pr[4];
+    epilogue_pairs(list, m0, mrows, pr);
     dma_gemm<NG, S, false>(dsm, wrow, act, I, 1, list, m0, mrows, I, rot, acc);
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
+    for (int t = 0; t < 4; ++t)
+      if (t * 16 + (lane & 15) < mrows) {
+        float* yr = y + (size_t)pr[t] * H + h0 + (lane >> 4) * 4;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int r = t * 16 + (lane >> 4) * 4 + q;
-        if (r < mrows) {
-          float* yr = y + (size_t)list[m0 + r] * H + h0 + (lane & 15);
-#pragma unroll
-          for (int g = 0; g < NG; ++g) yr[g * 16] = acc[g][t][q];
-        }
+        for (int g = 0; g < NG; ++g) *reinterpret_cast<f32x4*>(yr + g * 16) = acc[g][t];
       }
-    }
   }
 }
 
