@@ -233,10 +233,27 @@ __global__ __launch_bounds__(64) void pager_kernel(
   const RecordLayout L(T, K);
   const int P = T * K;
 
-  for (int e = lane; e < E; e += 64) sm.map[e] = map_g[e];
-  for (int s = lane; s < cap; s += 64) {
-    sm.s2e[s] = s2e_g[s];
-    sm.tick[s] = tick_g[s];
+  // With the router fused (the launcher picks VALS * 64 >= E) and cap within
+  // the same bound, the layer state is read into registers first and reaches
+  // LDS after routing, so its loads travel while the router loads and ranks
+  // the logits instead of before them.
+  const bool state_in_regs = logits && cap <= VALS * 64;
+  int map_r[VALS], s2e_r[VALS];
+  int64_t tick_r[VALS];
+  if (state_in_regs) {
+#pragma unroll
+    for (int v = 0; v < VALS; ++v) {
+      const int i = v * 64 + lane;
+      map_r[v] = i < E ? map_g[i] : -1;
+      s2e_r[v] = i < cap ? s2e_g[i] : -1;
+      tick_r[v] = i < cap ? tick_g[i] : 0;
+    }
+  } else {
+    for (int e = lane; e < E; e += 64) sm.map[e] = map_g[e];
+    for (int s = lane; s < cap; s += 64) {
+      sm.s2e[s] = s2e_g[s];
+      sm.tick[s] = tick_g[s];
+    }
   }
   int64_t clock = ctr_g[kClock];
   int64_t n_forward = ctr_g[kForward], n_miss = ctr_g[kMiss], n_evict = ctr_g[kEvict],
@@ -258,6 +275,17 @@ __global__ __launch_bounds__(64) void pager_kernel(
         w_out[t * K + lane] = w;
         id_out[t * K + lane] = id;
         fr.ids[t * K + lane] = id;
+      }
+    }
+    if (state_in_regs) {
+#pragma unroll
+      for (int v = 0; v < VALS; ++v) {
+        const int i = v * 64 + lane;
+        if (i < E) sm.map[i] = map_r[v];
+        if (i < cap) {
+          sm.s2e[i] = s2e_r[v];
+          sm.tick[i] = tick_r[v];
+        }
       }
     }
     wave_lds_sync();
