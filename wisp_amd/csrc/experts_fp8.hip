@@ -581,11 +581,14 @@ __global__ __launch_bounds__(256) void fp8_grouped_w13_kernel(
   const float* Su = s13 + (size_t)s * s13_stride + (size_t)((I + i0) / block_n) * nkb;
   for (int m0 = 0; m0 < M; m0 += MT * 16) {
     const int mrows = min(M - m0, MT * 16);
-    // the token of this lane's column in each tile (past the last row: a
-    // clamped copy, computed and not stored)
-    int tok[MT];
+    // the pair and token of this lane's column in each tile (past the last
+    // row: a clamped copy, computed and not stored)
+    int pr[MT], tok[MT];
 #pragma unroll
-    for (int t = 0; t < MT; ++t) tok[t] = list[m0 + min(t * 16 + col, mrows - 1)] / K;
+    for (int t = 0; t < MT; ++t) {
+      pr[t] = list[m0 + min(t * 16 + col, mrows - 1)];
+      tok[t] = pr[t] / K;
+    }
     f32x4 ag[MT], au[MT];
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
@@ -629,8 +632,7 @@ __global__ __launch_bounds__(256) void fp8_grouped_w13_kernel(
     for (int t = 0; t < MT; ++t) {
       const int r = t * 16 + col;
       if (r < mrows) {
-        const int p = list[m0 + r];
-        store_act4(act + (size_t)p * I + i0 + grp * 4, ag[t], au[t]);
+        store_act4(act + (size_t)pr[t] * I + i0 + grp * 4, ag[t], au[t]);
       }
     }
   }
@@ -655,8 +657,12 @@ __global__ __launch_bounds__(256) void fp8_grouped_w2_kernel(
   for (int m0 = 0; m0 < M; m0 += MT * 16) {
     const int mrows = min(M - m0, MT * 16);
     int pr[MT];
+    float pw[MT];
 #pragma unroll
-    for (int t = 0; t < MT; ++t) pr[t] = list[m0 + min(t * 16 + col, mrows - 1)];
+    for (int t = 0; t < MT; ++t) {
+      pr[t] = list[m0 + min(t * 16 + col, mrows - 1)];
+      pw[t] = topk_w[pr[t]];
+    }
     f32x4 acc[MT];
 #pragma unroll
     for (int t = 0; t < MT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -690,10 +696,8 @@ __global__ __launch_bounds__(256) void fp8_grouped_w2_kernel(
     for (int t = 0; t < MT; ++t) {
       const int r = t * 16 + col;
       if (r < mrows) {
-        const int p = list[m0 + r];
-        const float w = topk_w[p];
-        store_bf16x4(y + (size_t)p * H + h0 + grp * 4, acc[t][0] * w, acc[t][1] * w,
-                     acc[t][2] * w, acc[t][3] * w);
+        store_bf16x4(y + (size_t)pr[t] * H + h0 + grp * 4, acc[t][0] * pw[t],
+                     acc[t][1] * pw[t], acc[t][2] * pw[t], acc[t][3] * pw[t]);
       }
     }
   }
