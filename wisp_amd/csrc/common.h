@@ -42,6 +42,20 @@ __device__ inline void wave_lds_sync() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
+// float -> bfloat16 bits, round to nearest even (a NaN stays a quiet NaN).
+__device__ inline uint16_t bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// bfloat16 bits -> float.
+__device__ inline float bf16f(uint32_t b) { return __uint_as_float(b << 16); }
+
+// SiLU in float32 as vLLM's silu_and_mul computes it: g / (1 + exp(-g)).
+__device__ inline float silu(float g) { return g / (1.0f + expf(-g)); }
+
 // Optional kernel timing: {w13 start, w13 stop, w2 start, w2 stop}, recorded
 // by the dispatch itself (hipExtLaunchKernelGGL), so the elapsed time is the
 // kernel's own execution time.

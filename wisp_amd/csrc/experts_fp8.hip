@@ -74,15 +74,6 @@ constexpr int kKC = 4;           // k-blocks a w13 wave loads before it computes
 constexpr int kW2Waves = 8;
 constexpr size_t kMaxLds = 160 * 1024;
 
-__device__ inline float bf16f(uint32_t b) { return __uint_as_float(b << 16); }
-
-__device__ inline uint16_t bf16_rne(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
-
 __device__ inline float round_bf16(float f) { return bf16f(bf16_rne(f)); }
 
 // Four values as bf16 to the 8 consecutive, 8-byte aligned bytes at p, in
@@ -92,8 +83,6 @@ __device__ inline void store_bf16x4(uint16_t* p, float a, float b, float c, floa
       make_uint2((uint32_t)bf16_rne(a) | ((uint32_t)bf16_rne(b) << 16),
                  (uint32_t)bf16_rne(c) | ((uint32_t)bf16_rne(d) << 16));
 }
-
-__device__ inline float silu(float g) { return g / (1.0f + expf(-g)); }
 
 // act = bf16(bf16(silu(bf16(g))) * bf16(u)) for four consecutive columns.
 __device__ inline void store_act4(uint16_t* p, const f32x4& g, const f32x4& u) {

@@ -37,19 +37,12 @@ struct Vec<uint16_t> {  // bf16 bits
   }
 };
 
-__device__ inline uint16_t f32_to_bf16_rne(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
-
 template <typename T>
 __device__ inline void store_elem(T* p, float v);
 template <>
 __device__ inline void store_elem<float>(float* p, float v) { *p = v; }
 template <>
-__device__ inline void store_elem<uint16_t>(uint16_t* p, float v) { *p = f32_to_bf16_rne(v); }
+__device__ inline void store_elem<uint16_t>(uint16_t* p, float v) { *p = bf16_rne(v); }
 
 __device__ inline uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 
@@ -61,8 +54,6 @@ __device__ inline uint4 ld16_stream(const void* p) {
   const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
   return make_uint4(v.x, v.y, v.z, v.w);
 }
-
-__device__ inline float silu(float g) { return g / (1.0f + expf(-g)); }
 
 // ---------------------------------------------------------------------------
 // Kernel A: act = silu(gate) * up.  Block = 4 waves, each wave owns RW

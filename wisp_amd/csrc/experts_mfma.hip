@@ -47,16 +47,6 @@ constexpr int kPanel = 64;           // output columns per block: 4 waves x 16
 // the token tile weigh more than in w13, and 32 rows per wave halve both.
 constexpr int kW2PanelsPer = 2;      // 64-row panels per LDS-staged w2 block
 
-
-__device__ inline uint16_t bf16_rne(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
-
-__device__ inline float silu(float g) { return g / (1.0f + expf(-g)); }
-
 // Work buffer carve-up (bytes, each piece 256-byte aligned).
 struct WorkLayout {
   size_t lists, counts, y, total;
