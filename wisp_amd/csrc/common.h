@@ -6,6 +6,8 @@
 #include <stdint.h>
 #include <stddef.h>
 
+#include <atomic>
+
 #include "../../include/wisp_hip.h"
 
 #define WISP_HD __host__ __device__
@@ -69,6 +71,24 @@ struct StageEvents {
 // GEMM; the block-FP8 grouped path shares it.
 void launch_gather(const int32_t* slots, int P, int nslots, int32_t* lists, int32_t* counts,
                    hipStream_t st);
+
+// Raises `kernel`'s dynamic-LDS limit to `max_lds` when a launch needs more
+// than the default 64 KiB, once per device (bit d of *done marks device d;
+// safe when several host threads launch at once).
+template <typename Kern>
+inline hipError_t allow_lds(Kern kernel, size_t lds, size_t max_lds,
+                            std::atomic<uint64_t>* done) {
+  if (lds <= 64 * 1024) return hipSuccess;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  const uint64_t bit = 1ull << (dev & 63);
+  if (done->load(std::memory_order_acquire) & bit) return hipSuccess;
+  e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)max_lds);
+  if (e == hipSuccess) done->fetch_or(bit, std::memory_order_acq_rel);
+  return e;
+}
 
 // Launch with or without dispatch timestamps.
 template <typename Kern, typename... Args>

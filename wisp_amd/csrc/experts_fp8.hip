@@ -969,16 +969,6 @@ size_t w2_lds(int K, int I, int WP) {
 // over chunks of kKC k-blocks).
 int w13_waves(int H) { return H / kKB <= 4 * kKC ? 4 : 8; }
 
-// Allows a kernel more than the default 64 KiB of dynamic LDS (once).
-template <typename Kern>
-hipError_t allow_lds(Kern kernel, size_t lds, bool* done) {
-  if (lds <= 64 * 1024 || *done) return hipSuccess;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds);
-  if (e == hipSuccess) *done = true;
-  return e;
-}
-
 struct W13Args {
   const uint16_t* x;
   int H, I, K, P;
@@ -994,10 +984,10 @@ struct W13Args {
 
 template <int NW, int NCOL, bool BIG>
 hipError_t launch_w13(const W13Args& a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
-  static bool big_lds = false;
+  static std::atomic<uint64_t> big_lds{0};
   const auto kern = &fp8_w13_kernel<NW, NCOL, BIG>;
   const size_t lds = w13_lds(NW, NCOL);
-  hipError_t e = allow_lds(kern, lds, &big_lds);
+  hipError_t e = allow_lds(kern, lds, kMaxLds, &big_lds);
   if (e != hipSuccess) return e;
   const dim3 grid(a.I / 16, a.P), block(NW * 64);
   if (e0)
@@ -1025,10 +1015,10 @@ struct W2Args {
 
 template <int KC2, int QP>
 hipError_t launch_w2(const W2Args& a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
-  static bool big_lds = false;
+  static std::atomic<uint64_t> big_lds{0};
   const auto kern = &fp8_w2_kernel<kW2Waves, KC2, QP>;
   const size_t lds = w2_lds(a.K, a.I, a.WP);
-  hipError_t e = allow_lds(kern, lds, &big_lds);
+  hipError_t e = allow_lds(kern, lds, kMaxLds, &big_lds);
   if (e != hipSuccess) return e;
   const dim3 grid(a.H / 16, a.T), block(kW2Waves * 64);
   if (e0)
@@ -1064,9 +1054,9 @@ bool launch_grouped_dma(const uint8_t* xq, const float* xs, uint8_t* aq, float* 
                         uint16_t* y, hipStream_t st, const StageEvents* ev) {
   const size_t l13 = fp8_dma_lds<S13>(H / kKB), l2 = fp8_dma_lds<S2>(I / kKB);
   if (l13 > kMaxLds || l2 > kMaxLds || H % 128) return false;
-  static bool big13 = false, big2 = false;
-  if (allow_lds(&fp8_w13_dma_kernel<S13>, l13, &big13) != hipSuccess ||
-      allow_lds(&fp8_w2_dma_kernel<S2>, l2, &big2) != hipSuccess) {
+  static std::atomic<uint64_t> big13{0}, big2{0};
+  if (allow_lds(&fp8_w13_dma_kernel<S13>, l13, kMaxLds, &big13) != hipSuccess ||
+      allow_lds(&fp8_w2_dma_kernel<S2>, l2, kMaxLds, &big2) != hipSuccess) {
     (void)hipGetLastError();
     return false;
   }

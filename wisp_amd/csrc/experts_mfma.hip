@@ -361,27 +361,24 @@ void launch_combine(const float* y, int T, int H, int K, int nslots, const float
 }
 
 template <int S13, int S2>
-void launch_dma(const uint16_t* x, int H, int I, int K, int P, int nslots, const int32_t* lists,
-                const int32_t* counts, const uint16_t* w13, size_t w13_stride,
-                const uint16_t* w2, size_t w2_stride, uint16_t* act, float* y, hipStream_t st,
-                const StageEvents* ev) {
+hipError_t launch_dma(const uint16_t* x, int H, int I, int K, int P, int nslots,
+                      const int32_t* lists, const int32_t* counts, const uint16_t* w13,
+                      size_t w13_stride, const uint16_t* w2, size_t w2_stride, uint16_t* act,
+                      float* y, hipStream_t st, const StageEvents* ev) {
   constexpr unsigned b13 = dma::Smem<32, S13>::kBytes;
   constexpr unsigned b2 = dma::Smem<16 * kW2PanelsPer, S2>::kBytes;
   static_assert(b13 <= 160 * 1024 && b2 <= 160 * 1024, "LDS per block");
-  static const bool attrs = [] {
-    (void)hipFuncSetAttribute((const void*)mfma_w13_dma_kernel<S13>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, b13);
-    (void)hipFuncSetAttribute((const void*)mfma_w2_dma_kernel<S2>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, b2);
-    return true;
-  }();
-  (void)attrs;
+  static std::atomic<uint64_t> big13{0}, big2{0};
+  hipError_t e = allow_lds(&mfma_w13_dma_kernel<S13>, b13, b13, &big13);
+  if (e == hipSuccess) e = allow_lds(&mfma_w2_dma_kernel<S2>, b2, b2, &big2);
+  if (e != hipSuccess) return e;
   hipEvent_t e0 = ev ? ev->ev[0] : nullptr, e1 = ev ? ev->ev[1] : nullptr;
   hipEvent_t e2 = ev ? ev->ev[2] : nullptr, e3 = ev ? ev->ev[3] : nullptr;
   launch_timed_lds(mfma_w13_dma_kernel<S13>, dim3(I / kPanel, nslots), dim3(256), b13, st, e0,
                    e1, x, H, I, K, P, lists, counts, w13, w13_stride, act);
   launch_timed_lds(mfma_w2_dma_kernel<S2>, dim3(H / (kPanel * kW2PanelsPer), nslots),
                    dim3(256), b2, st, e2, e3, act, H, I, P, lists, counts, w2, w2_stride, y);
+  return hipSuccess;
 }
 
 }  // namespace
@@ -435,8 +432,8 @@ int experts_mfma(const void* x, int T, int H, int I, int K, const float* topk_w,
   // a third block per CU).  Measured on MI355X, these kernels also beat
   // register-streaming ones at every call size, down to 4 tokens (71 against
   // 109 us at the Qwen3 shape).
-  launch_dma<2, 3>(xb, H, I, K, P, nslots, lists, counts, a13, w13_stride, a2, w2_stride, ab, y,
-                   st, ev);
+  WISP_HIP_TRY((launch_dma<2, 3>(xb, H, I, K, P, nslots, lists, counts, a13, w13_stride, a2,
+                                 w2_stride, ab, y, st, ev)));
   launch_combine(y, T, H, K, nslots, topk_w, slots, (uint16_t*)out, st);
   WISP_HIP_TRY(hipGetLastError());
   return WISP_OK;
