@@ -153,7 +153,7 @@ def test_prefetch_noops():
 
 
 def test_prefetch_uses_set_iteration_order_for_slots():
-    # {9, 2}: 9 & 7 = 1 and 2 & 7 = 2 -> iterates 9 then 2 (SURVEY Appendix A example)
+    # {9, 2} in an 8-slot CPython table: 9 & 7 = 1 and 2 & 7 = 2, so it iterates 9 then 2
     p = _state(3, [-1, -1, -1], [0, 0, 0], 0, set())
     rec = p.prefetch_async(set([2, 9]))
     assert [e for e, _ in rec["loaded"]] == list({2, 9}) == [9, 2]
