@@ -164,6 +164,39 @@ def test_kernel_engine_needs_pinned_masters():
             _lib.lib().wisp_layer_destroy(h)
 
 
+def test_kernel_engine_with_masters_in_a_large_pinned_allocation():
+    """Masters at the end of one pinned allocation of more than 2 GiB (the
+    allocator rounds it up to 4 GiB, a size whose range attribute does not
+    read back on this runtime) still take the copy kernel; decisions match the
+    oracle and paged bytes equal resident bytes.  A range that crosses the
+    allocation's end is still refused."""
+    import ctypes as C
+    from wisp_amd import _lib
+    wl = W.toy(steps=8)
+    n = wl.slabs.numel() * wl.slabs.element_size()
+    big = torch.empty(9 << 28, dtype=torch.uint8, pin_memory=True)  # 2.25 GiB
+    off = (big.numel() - n) & ~255
+    slabs = big[off:off + n].view(wl.slabs.dtype).view(wl.slabs.shape)
+    slabs.copy_(wl.slabs)
+    wl.slabs = slabs
+    sts = drive(wl, 4, wl.steps, tol=1e-5)
+    st = sts["paged"]
+    assert st.pagein_engine == "kernel"
+    alloc_end = big.data_ptr() + (4 << 30)  # the rounded allocation
+    d = st._make_desc()
+    d.pagein_engine = _lib.WISP_PAGEIN_KERNEL
+    d.master_w13 = alloc_end - st._w13_elems * 4 // 2
+    d.master_w2 = d.master_w13 + st._w13_elems * 4
+    h = C.c_void_p()
+    _lib.check(_lib.lib().wisp_layer_create(C.byref(d), C.byref(h)), "create")
+    try:
+        assert _lib.lib().wisp_layer_pagein_engine(h) == _lib.WISP_PAGEIN_MEMCPY
+    finally:
+        _lib.lib().wisp_layer_destroy(h)
+    del sts, st
+    torch.cuda.synchronize()
+
+
 def test_prefill_chunk_layer_mfma():
     # 96-token chunk at the Qwen3 shape, cap 32 of 128 experts: the call is
     # split into greedy token groups and runs on the MFMA grouped GEMM

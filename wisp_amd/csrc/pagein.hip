@@ -85,7 +85,27 @@ const char* mapped_host_range(const void* base, size_t bytes) {
   }
   const char* b = (const char*)base;
   const char* lo = (const char*)start;
-  if (b < lo || bytes > size || (size_t)(b - lo) > size - bytes) return nullptr;
+  if (b < lo || bytes == 0) return nullptr;
+  if (bytes <= size && (size_t)(b - lo) <= size - bytes) return (const char*)dptr;
+  // The range-size attribute of a pinned host allocation of 4 GiB or more
+  // reads modulo 2^32 on this runtime (torch rounds a 2.1 GiB pinned request
+  // up to 4 GiB, which reads 0).  Then the last byte of the range must lie
+  // in the same allocation and map to the device at the same offset.
+  const hipDeviceptr_t last = (hipDeviceptr_t)(b + (bytes - 1));
+  unsigned int type_last = 0;
+  void* start_last = nullptr;
+  void* dptr_last = nullptr;
+  if (hipPointerGetAttribute(&type_last, HIP_POINTER_ATTRIBUTE_MEMORY_TYPE, last) != hipSuccess ||
+      type_last != hipMemoryTypeHost ||
+      hipPointerGetAttribute(&start_last, HIP_POINTER_ATTRIBUTE_RANGE_START_ADDR, last) !=
+          hipSuccess ||
+      hipPointerGetAttribute(&dptr_last, HIP_POINTER_ATTRIBUTE_DEVICE_POINTER, last) !=
+          hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  if (start_last != start || (const char*)dptr_last != (const char*)dptr + (bytes - 1))
+    return nullptr;
   return (const char*)dptr;
 }
 
