@@ -268,6 +268,32 @@ def test_fp8_state_decode_matches_oracle(monkeypatch, small_fp8, engine):
     assert ora.stats_miss > cap  # the trace pages
 
 
+def test_fp8_state_empty_calls_tick_the_clock(small_fp8):
+    """Zero-token calls between decode steps: empty output, the pager moves
+    as the reference's empty call does, and the next calls still match the
+    oracle and the resident layer's bytes."""
+    wl = small_fp8
+    E, K, cap = 32, wl.shape.top_k, 8
+    st, full = _fp8_state(wl, cap), _fp8_state(wl, E)
+    ora = PagerOracle(E, cap)
+    x0 = torch.empty((0, wl.shape.hidden), dtype=torch.bfloat16, device=DEV)
+    lg0 = torch.empty((0, E), dtype=torch.float32, device=DEV)
+    for t in range(8):
+        if t % 2:
+            out0 = st.forward(x0, lg0, K, True)
+            torch.cuda.synchronize()
+            assert tuple(out0.shape) == (0, wl.shape.hidden)
+            ora.forward([])
+        x, lg = wl.x[t].to(DEV), wl.logits[t].to(DEV)
+        out = st.forward(x, lg, K, True)
+        ref = full.forward(x, lg, K, True)
+        ora.forward(route(wl.logits[t], K)[1].tolist())
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), t
+        assert st.slot_to_expert == ora.slot_to_expert and st.lru_tick == ora.lru_tick, t
+        assert st.lru_clock == ora.lru_clock and st.stats_forward == ora.stats_forward, t
+
+
 def test_fp8_state_subbatches_like_the_reference(small_fp8):
     """A batch whose experts overflow cap runs as greedy token groups."""
     wl = small_fp8

@@ -197,6 +197,36 @@ def test_kernel_engine_with_masters_in_a_large_pinned_allocation():
     torch.cuda.synchronize()
 
 
+def test_empty_calls_tick_the_clock_like_the_reference():
+    """A zero-token call between decode steps returns an empty output and
+    moves the pager as the reference's empty ensure_resident does (the
+    clock and the call count tick); later calls keep matching the oracle and
+    the resident layer's bytes."""
+    wl = W.toy(steps=8, pin=True)
+    sh, K = wl.shape, wl.shape.top_k
+    sts = states(wl, 4)
+    paged, res = sts["paged"], sts["resident"]
+    ora = PagerOracle(sh.experts, 4)
+    x0 = torch.empty((0, sh.hidden), dtype=wl.x.dtype, device=DEV)
+    lg0 = torch.empty((0, sh.experts), dtype=torch.float32, device=DEV)
+    for t in range(wl.steps):
+        if t % 2:
+            out0 = paged.forward(x0, lg0, K, True)
+            torch.cuda.synchronize()
+            assert tuple(out0.shape) == (0, sh.hidden)
+            ora.forward([])
+        x, lg = wl.x[t].to(DEV), wl.logits[t].to(DEV)
+        out = paged.forward(x, lg, K, True)
+        ref = res.forward(x, lg, K, True)
+        torch.cuda.synchronize()
+        assert torch.equal(bits(out), bits(ref)), t
+        ora.forward(route(wl.logits[t], K)[1].tolist())
+        assert paged.slot_to_expert == ora.slot_to_expert, t
+        assert paged.lru_tick == ora.lru_tick and paged.lru_clock == ora.lru_clock, t
+    assert (paged.stats_forward, paged.stats_miss, paged.stats_evict, paged.stats_hits) == \
+        (ora.stats_forward, ora.stats_miss, ora.stats_evict, ora.stats_hits)
+
+
 def test_prefill_chunk_layer_mfma():
     # 96-token chunk at the Qwen3 shape, cap 32 of 128 experts: the call is
     # split into greedy token groups and runs on the MFMA grouped GEMM
