@@ -227,6 +227,17 @@ def test_empty_calls_tick_the_clock_like_the_reference():
         (ora.stats_forward, ora.stats_miss, ora.stats_evict, ora.stats_hits)
 
 
+@pytest.mark.parametrize("E,T", [(200, 1), (200, 8), (512, 1), (512, 4), (512, 8)])
+def test_wide_expert_counts_with_fused_routing(monkeypatch, E, T):
+    """Routing fused into the pager for E above 128 (4 and 8 logits per lane,
+    with the layer state read into registers before routing): decisions match
+    the oracle bit for bit and paged bytes equal resident bytes, one-group and
+    sub-batched (T * K above cap)."""
+    monkeypatch.setitem(W.SHAPES, "wide", W.LayerShape(256, 128, E, 8, 48, torch.bfloat16))
+    wl = W.gaussian_logits("wide", seed=E + T, steps=6, tokens=T, pin=True)
+    drive(wl, 48, wl.steps, tol=1e-2)
+
+
 def test_prefill_chunk_layer_mfma():
     # 96-token chunk at the Qwen3 shape, cap 32 of 128 experts: the call is
     # split into greedy token groups and runs on the MFMA grouped GEMM
