@@ -238,6 +238,16 @@ def test_wide_expert_counts_with_fused_routing(monkeypatch, E, T):
     drive(wl, 48, wl.steps, tol=1e-2)
 
 
+@pytest.mark.parametrize("T", [1, 3])
+def test_top_k_above_the_gemv_limit_takes_the_mfma_path(monkeypatch, T):
+    """20 routed experts per token (the decode GEMV pair handles up to 16):
+    the automatic choice runs the MFMA path even for a one-token call, with
+    decisions matching the oracle and paged bytes equal to resident bytes."""
+    monkeypatch.setitem(W.SHAPES, "topk20", W.LayerShape(512, 256, 64, 20, 24, torch.bfloat16))
+    wl = W.gaussian_logits("topk20", seed=T, steps=4, tokens=T, pin=True)
+    drive(wl, 24, wl.steps, tol=1e-2)
+
+
 def test_prefill_chunk_layer_mfma():
     # 96-token chunk at the Qwen3 shape, cap 32 of 128 experts: the call is
     # split into greedy token groups and runs on the MFMA grouped GEMM

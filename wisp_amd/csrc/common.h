@@ -22,6 +22,9 @@ constexpr int kMaxTopK = 64;
 constexpr int kMaxSetTable = 8 * kMaxExperts;
 // Calls of at most this many tokens are routed inside the pager kernel.
 constexpr int kFusedRouteTokens = 8;
+// Routed experts per token the decode GEMV pair handles (its w2 kernel runs
+// one wave per expert in one block and keeps their partial sums in LDS).
+constexpr int kGemvMaxTopK = 16;
 
 // Per-layer counters kept on the device, in this order.
 enum Counter : int {

@@ -59,7 +59,7 @@ int experts_fp8_grouped(const void* x, int T, int H, int I, int K, const float* 
                         const float* s2, size_t s2_stride, int block_n, void* act, void* out,
                         void* work, size_t work_bytes, hipStream_t st, const StageEvents* ev);
 size_t fp8_work_bytes(int T, int K, int H, int I, int nslots);
-int auto_algo(int dtype, int H, int I, int T);
+int auto_algo(int dtype, int H, int I, int T, int K);
 
 namespace {
 
@@ -1265,7 +1265,7 @@ extern "C" int wisp_moe_experts_fp8(const void* x, int T, int H, int I, int K,
     wisp_set_last_error(why, "wisp_moe_experts_fp8");
     return WISP_ERR_UNSUPPORTED;
   }
-  const int a = algo == WISP_ALGO_AUTO ? auto_algo(WISP_FP8_E4M3, H, I, T) : algo;
+  const int a = algo == WISP_ALGO_AUTO ? auto_algo(WISP_FP8_E4M3, H, I, T, K) : algo;
   if (a == WISP_ALGO_MFMA)
     return experts_fp8_grouped(x, T, H, I, K, topk_w, slots, nslots, w13, w13_stride, s13,
                                s13_stride, w2, w2_stride, s2, s2_stride, block_n, act, out, work,

@@ -150,7 +150,7 @@ __global__ __launch_bounds__(256) void w13_silu_kernel(const T* __restrict__ x, 
 // LDS by the waves at the start (0 for an absent slot).
 // grid = (ceil(H / (64 / LPR)), T).
 // ---------------------------------------------------------------------------
-constexpr int kMaxKw2 = 16;
+constexpr int kMaxKw2 = kGemvMaxTopK;
 
 template <typename T, int LPR, int CH, bool FULL>
 __global__ __launch_bounds__(1024) void w2_combine_kernel(const T* __restrict__ act, int H, int I,

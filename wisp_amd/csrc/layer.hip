@@ -105,13 +105,17 @@ constexpr int kMfmaMinTokens = 14;
 constexpr int kFp8GroupedMinTokens = 16;
 
 // The automatic expert-kernel choice.  It depends only on the call's dtype,
-// shape and token count, never on the grouping or the slots, so paged and
-// resident runs of one batch use one kernel.
-int auto_algo(int dtype, int H, int I, int T) {
+// shape, token count and top-k, never on the grouping or the slots, so paged
+// and resident runs of one batch use one kernel.  A bf16 call with more
+// routed experts per token than the GEMV pair handles takes the MFMA path,
+// whose combine has no such limit.
+int auto_algo(int dtype, int H, int I, int T, int K) {
   if (dtype == WISP_FP8_E4M3)
     return T >= kFp8GroupedMinTokens ? WISP_ALGO_MFMA : WISP_ALGO_GEMV;
-  return dtype == WISP_BF16 && mfma_supported(H, I) && T >= kMfmaMinTokens ? WISP_ALGO_MFMA
-                                                                          : WISP_ALGO_GEMV;
+  return dtype == WISP_BF16 && mfma_supported(H, I) &&
+                 (T >= kMfmaMinTokens || K > kGemvMaxTopK)
+             ? WISP_ALGO_MFMA
+             : WISP_ALGO_GEMV;
 }
 
 namespace {
@@ -486,9 +490,9 @@ int experts(Layer& L, const void* x, int T, int K, const float* w, const int32_t
 }
 
 // The expert algorithm of a layer call (-1: the request does not cover it).
-int choose_algo(const Layer& L, int algo, int T) {
+int choose_algo(const Layer& L, int algo, int T, int K) {
   const wisp_layer_desc& d = L.d;
-  if (algo == WISP_ALGO_AUTO) return auto_algo(d.dtype, d.hidden, d.inter, T);
+  if (algo == WISP_ALGO_AUTO) return auto_algo(d.dtype, d.hidden, d.inter, T, K);
   if (algo == WISP_ALGO_MFMA && d.dtype == WISP_F32) return -1;
   if (algo == WISP_ALGO_MFMA && d.dtype == WISP_BF16 && !mfma_supported(d.hidden, d.inter))
     return -1;
@@ -715,7 +719,7 @@ extern "C" int wisp_layer_forward(void* handle, const void* x, const void* logit
       return WISP_ERR_UNSUPPORTED;
     }
   }
-  const int a = choose_algo(*L, algo, T);
+  const int a = choose_algo(*L, algo, T, K);
   if (a < 0) {
     wisp_set_last_error("requested expert algorithm does not cover this call",
                         "wisp_layer_forward");
@@ -968,7 +972,7 @@ extern "C" int wisp_moe_experts(const void* x, int dtype, int T, int H, int I, i
     wisp_set_last_error("H, I and buffers must be 16-byte aligned", "wisp_moe_experts");
     return WISP_ERR_UNSUPPORTED;
   }
-  const int a = algo == WISP_ALGO_AUTO ? auto_algo(dtype, H, I, T) : algo;
+  const int a = algo == WISP_ALGO_AUTO ? auto_algo(dtype, H, I, T, K) : algo;
   if (a == WISP_ALGO_MFMA) {
     if (dtype != WISP_BF16) {
       wisp_set_last_error("the MFMA path computes in bf16 only", "wisp_moe_experts");
