@@ -248,6 +248,28 @@ def test_top_k_above_the_gemv_limit_takes_the_mfma_path(monkeypatch, T):
     drive(wl, 24, wl.steps, tol=1e-2)
 
 
+def test_forward_refuses_tensors_off_the_device_and_bad_out():
+    """Tensors in host memory would reach the kernels as raw pointers, and a
+    wrong out buffer would be overrun: both are refused before any launch."""
+    wl = W.toy(steps=2, pin=True)
+    sh, K = wl.shape, wl.shape.top_k
+    st = states(wl, 4, modes=("paged",))["paged"]
+    x, lg = wl.x[0].to(DEV), wl.logits[0].to(DEV)
+    with pytest.raises(ValueError, match="x is on"):
+        st.forward(wl.x[0], lg, K, True)
+    with pytest.raises(ValueError, match="router_logits is on"):
+        st.forward(x, wl.logits[0], K, True)
+    for bad in (torch.empty((2, sh.hidden), dtype=x.dtype, device=DEV),
+                torch.empty((1, sh.hidden), dtype=torch.bfloat16, device=DEV),
+                torch.empty((sh.hidden, 2), dtype=x.dtype, device=DEV)[:, :1].t(),
+                torch.empty((1, sh.hidden), dtype=x.dtype)):
+        with pytest.raises(ValueError, match="out"):
+            st.forward(x, lg, K, True, out=bad)
+    assert st.stats_forward == 0  # nothing reached the pager
+    good = torch.empty_like(x)
+    assert st.forward(x, lg, K, True, out=good).data_ptr() == good.data_ptr()
+
+
 def test_prefill_chunk_layer_mfma():
     # 96-token chunk at the Qwen3 shape, cap 32 of 128 experts: the call is
     # split into greedy token groups and runs on the MFMA grouped GEMM

@@ -47,6 +47,21 @@ _PATCHED_FLAG = "_wisp_patched"
 # ---------------------------------------------------------------------------
 
 
+
+def _require_device(t: torch.Tensor, dev: torch.device, name: str) -> None:
+    """The kernels take raw device pointers: a tensor elsewhere (host memory,
+    another GPU) would be read as device memory, so it is refused here."""
+    if t.device.type != dev.type or (dev.index is not None and t.device.index != dev.index):
+        raise ValueError(f"wisp: {name} is on {t.device}; the layer runs on {dev}")
+
+
+def _check_out(out: torch.Tensor, like: torch.Tensor) -> None:
+    """A caller's output buffer must be exactly what the kernels write: a
+    contiguous [T, H] tensor of the activations' dtype on their device."""
+    if out.shape != like.shape or out.dtype != like.dtype or not out.is_contiguous():
+        raise ValueError(f"wisp: out must be a contiguous {tuple(like.shape)} {like.dtype} tensor")
+    _require_device(out, like.device, "out")
+
 class _Mode:
     COPY = "copy"          # full-tensor copy per forward (correctness only)
     RESIDENT = "resident"  # every expert resident, identity map
@@ -344,6 +359,8 @@ class WispMoEState:
             raise ValueError(f"x must be [T, {self.hidden}] {self.dtype}")
         if router_logits.shape != (x.shape[0], self.num_experts):
             raise ValueError(f"router_logits must be [T, {self.num_experts}]")
+        _require_device(x, self.device, "x")
+        _require_device(router_logits, self.device, "router_logits")
         if router_logits.dtype not in _DTYPES:
             router_logits = router_logits.float()
         x = x.contiguous()
@@ -351,6 +368,8 @@ class WispMoEState:
         T = x.shape[0]
         if out is None:
             out = torch.empty_like(x)
+        else:
+            _check_out(out, x)
         ws = self._ws.ensure(T, top_k, self.cap_experts)
         rc = lib().wisp_layer_forward(self._handle, x.data_ptr(), router_logits.data_ptr(),
                                       _DTYPES[router_logits.dtype], T, int(top_k),
@@ -608,6 +627,8 @@ def _route_and_experts(x, router_logits, top_k, renormalize, w13, w2) -> torch.T
     E = w13.shape[0]
     I = w2.shape[2]
     dev = x.device
+    for t, name in ((router_logits, "router_logits"), (w13, "w13"), (w2, "w2")):
+        _require_device(t, dev, name)
     st = _lib.stream_handle()
     x = x.contiguous()
     logits = router_logits if router_logits.dtype in _DTYPES else router_logits.float()

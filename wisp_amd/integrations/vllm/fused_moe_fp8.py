@@ -44,8 +44,8 @@ import torch
 
 from ... import _lib
 from ..._lib import check, lib
-from .fused_moe import (WispMoEState, _Mode, _resolve_pagein_engine, _resolve_pagein_streams,
-                        _Workspace)
+from .fused_moe import (WispMoEState, _Mode, _require_device, _resolve_pagein_engine,
+                        _resolve_pagein_streams, _Workspace)
 
 logger = logging.getLogger("wisp_amd.integrations.vllm.fused_moe_fp8")
 
@@ -401,6 +401,9 @@ def route_and_experts_fp8(x, router_logits, top_k, renormalize, w13, w2, s13, s2
     E = w13.shape[0]
     I = w2.shape[2]
     dev = x.device
+    for t, name in ((router_logits, "router_logits"), (w13, "w13"), (w2, "w2"), (s13, "s13"),
+                    (s2, "s2")):
+        _require_device(t, dev, name)
     st = _lib.stream_handle()
     if x.dtype != torch.bfloat16:
         raise NotImplementedError("wisp.fp8: activations must be bfloat16")
