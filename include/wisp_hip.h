@@ -5,6 +5,13 @@
  * int status (WISP_OK = 0) and never allocates device memory: the caller
  * owns all buffers.  On failure wisp_last_error() returns a message.
  *
+ * Tensor pointers are device memory of the stream's device unless an entry
+ * point says otherwise (expert masters live in host memory, pinned for the
+ * copy-kernel engine; decision records may be pinned host memory).  The
+ * kernels read what they are given as device addresses, so host memory passed
+ * where device memory is expected is not detected here: the Python layer
+ * checks devices before it calls in.
+ *
  * Each function names the reference code it replaces; paths are relative to
  * the reference checkout (nokia-applied-research/WiSP).
  */
