@@ -63,10 +63,12 @@ def cpu_name() -> str:
     return "unknown"
 
 
-def cpu_baseline(routes, w13, w2, seconds: float, warm: int = 4) -> dict:
+def cpu_baseline(routes, w13, w2, seconds: float, warm: int = 8) -> dict:
     """Oracle routing + LRU pager + torch CPU SwiGLU experts over the decode
-    routing sequences (one pager per sequence, round-robin, as on the GPU),
-    until ``seconds`` of timed work; throughput = timed steps / timed time."""
+    routing sequences (one pager per sequence, round-robin, as on the GPU):
+    ``warm`` untimed steps, then steps timed one by one with
+    ``time.perf_counter`` until ``seconds`` of timed work; throughput = 1 /
+    the median step time."""
     import torch
 
     from oracle.moe import moe_forward_fast, route
@@ -76,23 +78,28 @@ def cpu_baseline(routes, w13, w2, seconds: float, warm: int = 4) -> dict:
     K = routes[0].shape.top_k
     pagers = [PagerOracle(wl.shape.experts, wl.shape.cap) for wl in routes]
     R, per = len(routes), routes[0].steps
-    n = timed = 0
+    n = 0
     spent = 0.0
+    times = []
     while spent < seconds and n < 64 * R * per:
         r, pos = n % R, (n // R) % per
         t0 = time.perf_counter()
         w, ids = route(routes[r].logits[pos], K)
         pagers[r].forward(ids.tolist())
         moe_forward_fast(routes[r].x[pos], w, ids, w13, w2)
+        dt = time.perf_counter() - t0
         if n >= warm:
-            spent += time.perf_counter() - t0
-            timed += 1
+            spent += dt
+            times.append(dt)
         n += 1
-    return {"value": round(timed / spent, 2), "unit": "tok/s", "cores": cores, "kind": "port",
-            "sample": f"{timed} bs=1 decode steps of the qwen3 layer after {warm} warm-up steps, "
-                      f"round-robin over {R} routing sequences with one pager each, time-bounded "
-                      f"to {seconds:.0f} s (oracle routing + LRU pager + torch CPU SwiGLU "
-                      f"experts on bf16 weights in host memory, so no page-in); {cpu_name()}"}
+    med = statistics.median(times)
+    return {"value": round(1.0 / med, 2), "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": f"median of {len(times)} bs=1 decode steps of the qwen3 layer "
+                      f"({med * 1e3:.3f} ms; mean {spent / len(times) * 1e3:.3f} ms) after {warm} "
+                      f"warm-up steps, round-robin over {R} routing sequences with one pager "
+                      f"each, time-bounded to {seconds:.0f} s (oracle routing + LRU pager + torch "
+                      f"CPU SwiGLU experts on bf16 weights in host memory, so no page-in); "
+                      f"{cpu_name()}"}
 
 
 def pmc_traffic(path: str, kernel: str):
@@ -241,7 +248,7 @@ def _state_run(wl, cap: int, mode: str, n_warm: int, n: int):
     resident with every expert primed."""
     import torch
 
-    from wisp_amd.integrations.vllm.fused_moe import WispMoEState
+    from wisp.integrations.vllm.fused_moe import WispMoEState
     dev = torch.device("cuda", 0)
     w13, w2 = wl.views()
     K = wl.shape.top_k
@@ -332,7 +339,7 @@ def bench_stack(args) -> dict:
     import torch
 
     from wisp_amd import workloads as W
-    from wisp_amd.integrations.vllm.fused_moe import WispMoEState
+    from wisp.integrations.vllm.fused_moe import WispMoEState
     sh = W.SHAPES["stack"]
     layers, tokens = 48, 512
     t_setup = time.perf_counter()
@@ -347,7 +354,7 @@ def bench_stack(args) -> dict:
     n_warm = 8
     after = None
     if args.prefetch:
-        from wisp_amd.integrations.vllm import fused_moe as fm
+        from wisp.integrations.vllm import fused_moe as fm
         os.environ["WISP_PREFETCH"] = "1"
         os.environ["WISP_COOCCUR_ONLINE"] = "1"
         os.environ.pop("WISP_COOCCUR_PATH", None)
@@ -436,7 +443,7 @@ def _fp8_state_run(wl, cap: int, n_warm: int, n: int):
     after its first call)."""
     import torch
 
-    from wisp_amd.integrations.vllm.fused_moe_fp8 import WispMoEStateFP8
+    from wisp.integrations.vllm.fused_moe_fp8 import WispMoEStateFP8
     dev = torch.device("cuda", 0)
     K = wl.shape.top_k
     xs, lgs = wl.x.to(dev), wl.logits.to(dev)
@@ -514,9 +521,10 @@ def bench_fp8(args) -> dict:
     import torch
 
     from wisp_amd import workloads as W
-    from wisp_amd.integrations.vllm.fused_moe_fp8 import WispMoEStateFP8
+    from wisp.integrations.vllm.fused_moe_fp8 import WispMoEStateFP8
     R = args.replicas
-    per = -(-(args.warmup + args.steps) // R)
+    n_warm = args.warmup * R  # `warmup` untimed calls per instance
+    per = -(-(n_warm + args.steps) // R)
     t_setup = time.perf_counter()
     routes = [W.qwen3_decode(seed=r, steps=per, weights=False) for r in range(R)]
     wl = W.fp8_layer(routes[0], pin=True)
@@ -533,7 +541,7 @@ def bench_fp8(args) -> dict:
         r, pos = i % R, i // R
         states[r].forward(xs[r, pos], lgs[r, pos], sh.top_k, True, out=outs[r])
 
-    elapsed, agg = _timed(call, args.warmup, args.steps, states)
+    elapsed, agg = _timed(call, n_warm, args.steps, states)
     _calibration_copy(dev)
     lay = wl.layout
     K = sh.top_k
@@ -585,7 +593,9 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2048,
                     help="timed layer calls (default: 8 instances x 256 decode steps)")
-    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--warmup", type=int, default=8,
+                    help="untimed calls per layer instance before the timed window (decode "
+                         "workloads); untimed calls in total for the others")
     ap.add_argument("--replicas", type=int, default=8)
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="time bound of the CPU baseline sample")
@@ -612,10 +622,13 @@ def main() -> int:
     import torch
 
     from wisp_amd import workloads as W
-    from wisp_amd.integrations.vllm.fused_moe import WispMoEState
+    from wisp.integrations.vllm.fused_moe import WispMoEState
 
     R = args.replicas
-    per = -(-(args.warmup + args.steps) // R)
+    # every instance takes `warmup` untimed calls (its cold fill among them)
+    # before the timed window, so the K timed calls see the steady state
+    n_warm = args.warmup * R
+    per = -(-(n_warm + args.steps) // R)
     t_setup = time.perf_counter()
     base = W.qwen3_decode(seed=0, steps=per, pin=True)
     sh = base.shape
@@ -639,12 +652,12 @@ def main() -> int:
     def run_steps() -> float:
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        for i in range(args.warmup, args.warmup + args.steps):
+        for i in range(n_warm, n_warm + args.steps):
             call(i)
         torch.cuda.synchronize()
         return time.perf_counter() - t0
 
-    for i in range(args.warmup):
+    for i in range(n_warm):
         call(i)
     torch.cuda.synchronize()
 
@@ -712,6 +725,7 @@ def main() -> int:
             "workload": "qwen3-30b-a3b moe layer decode, bs=1, cap=8, paged from pinned host",
             "hidden": sh.hidden, "expert_intermediate": sh.inter, "experts": sh.experts,
             "top_k": K, "cap": sh.cap, "batch": 1, "layer_instances": R,
+            "warmup_calls_per_instance": args.warmup,
             "routing": "zipf(1.1) bias + 0.6 reuse of previous top-8",
         },
         "roofline": {
@@ -743,6 +757,7 @@ def main() -> int:
             "link_GBps_256MiB_p50": round(link_big, 2),
             "frac_of_link": round(pin_gbps / link_best, 4) if link_best else None,
             "misses": miss, "hits": hits,
+            "misses_per_call": round(miss / max(1, args.steps), 3),
             "timing": "copy-kernel events over the second pass; misses and hits of the first",
         },
         "cpu_baseline": cpu,

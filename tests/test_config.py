@@ -5,7 +5,7 @@ import logging
 
 import pytest
 
-fm = importlib.import_module("wisp_amd.integrations.vllm.fused_moe")
+fm = importlib.import_module("wisp.integrations.vllm.fused_moe")
 
 
 @pytest.mark.parametrize("raw,want", [(None, "paged"), ("paged", "paged"), ("resident", "resident"),
@@ -38,7 +38,7 @@ def test_resolve_cap(monkeypatch, raw, E, want):
 
 
 def test_install_is_idempotent_and_refreshes_config(monkeypatch):
-    from wisp_amd.integrations.vllm import layer
+    from wisp.integrations.vllm import layer
     cls = layer.UnquantizedFusedMoEMethod
     orig = (cls.create_weights, cls.process_weights_after_loading, cls.forward_cuda)
     try:
@@ -55,7 +55,7 @@ def test_install_is_idempotent_and_refreshes_config(monkeypatch):
 
 
 def test_plugin_register_honours_disable(monkeypatch):
-    from wisp_amd.integrations.vllm import plugin
+    from wisp.integrations.vllm import plugin
     monkeypatch.setenv("WISP_PLUGIN_DISABLE", "1")
     plugin.register()
     assert not fm.is_installed()
@@ -63,7 +63,7 @@ def test_plugin_register_honours_disable(monkeypatch):
 
 def test_create_weights_rejects_bias():
     import torch
-    from wisp_amd.integrations.vllm.layer import FusedMoEConfig, UnquantizedFusedMoEMethod
+    from wisp.integrations.vllm.layer import FusedMoEConfig, UnquantizedFusedMoEMethod
     m = UnquantizedFusedMoEMethod(FusedMoEConfig(has_bias=True))
     with pytest.raises(NotImplementedError):
         fm._patched_create_weights(m, torch.nn.Module(), 4, 16, 8, torch.float32)
@@ -71,7 +71,7 @@ def test_create_weights_rejects_bias():
 
 def test_create_weights_allocates_host_slab():
     import torch
-    from wisp_amd.integrations.vllm.layer import UnquantizedFusedMoEMethod
+    from wisp.integrations.vllm.layer import UnquantizedFusedMoEMethod
     layer = torch.nn.Module()
     fm._patched_create_weights(UnquantizedFusedMoEMethod(), layer, 4, 16, 8, torch.bfloat16)
     assert layer.w13_weight.shape == (4, 16, 16) and layer.w2_weight.shape == (4, 16, 8)
@@ -91,7 +91,7 @@ def test_unsupported_call_arguments():
 
 # --- block-FP8 path (reference fused_moe_fp8.py:48-58, 362-390) -------------
 
-f8m = importlib.import_module("wisp_amd.integrations.vllm.fused_moe_fp8")
+f8m = importlib.import_module("wisp.integrations.vllm.fused_moe_fp8")
 
 
 @pytest.mark.parametrize("raw,E,want", [(None, 128, 24), (None, 8, 8), ("8", 128, 8),
@@ -126,7 +126,7 @@ def test_fp8_slab_layout_qwen3_shape():
 
 
 def test_install_fp8_patches_standin_once():
-    from wisp_amd.integrations.vllm import layer
+    from wisp.integrations.vllm import layer
     cls = layer.Fp8MoEMethod
     names = ("create_weights", "process_weights_after_loading", "apply")
     orig = {n: cls.__dict__[n] for n in names}
@@ -148,3 +148,27 @@ def test_install_fp8_patches_standin_once():
             setattr(cls, f8m._PATCHED_FLAG, True)
         elif hasattr(cls, f8m._PATCHED_FLAG):
             delattr(cls, f8m._PATCHED_FLAG)
+
+
+def test_reference_import_path_and_entry_point():
+    """Caller code written against the reference imports unchanged
+    (src/wisp/integrations/vllm/__init__.py:37-39), and the vLLM plug-in
+    entry point names the reference's module (pyproject.toml:35-36)."""
+    import configparser
+    import os
+    import re
+
+    from wisp.integrations.vllm import install_wisp_moe, is_installed
+    from wisp.integrations.vllm.fused_moe import WispMoEState
+    from wisp.integrations.vllm.plugin import register
+    assert callable(install_wisp_moe) and callable(is_installed) and callable(register)
+    assert WispMoEState.__module__ == "wisp.integrations.vllm.fused_moe"
+    assert fm.__all__ == ["install_wisp_moe", "is_installed", "WispMoEState"]
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    with open(os.path.join(root, "pyproject.toml")) as f:
+        text = f.read()
+    block = re.search(r'\[project\.entry-points\."vllm\.general_plugins"\]\s*\n([^\[]*)', text)
+    assert block, "no vllm.general_plugins entry point"
+    cp = configparser.ConfigParser()
+    cp.read_string("[ep]\n" + block.group(1))
+    assert cp["ep"]["wisp"].strip('"') == "wisp.integrations.vllm.plugin:register"

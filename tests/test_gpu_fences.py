@@ -21,7 +21,7 @@ from oracle.cooccur import CooccurOracle, prefetch_glue
 from oracle.moe import route
 from oracle.pager import PagerOracle
 from wisp_amd import workloads as W
-from wisp_amd.integrations.vllm import fused_moe as fm
+from wisp.integrations.vllm import fused_moe as fm
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")

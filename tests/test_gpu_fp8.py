@@ -14,8 +14,8 @@ from oracle.moe import route
 from oracle.pager import PagerOracle
 from wisp_amd import _lib
 from wisp_amd import workloads as W
-from wisp_amd.integrations.vllm import fused_moe_fp8 as f8m
-from wisp_amd.integrations.vllm.fused_moe_fp8 import WispMoEStateFP8, fp8_slab_masters
+from wisp.integrations.vllm import fused_moe_fp8 as f8m
+from wisp.integrations.vllm.fused_moe_fp8 import WispMoEStateFP8, fp8_slab_masters
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -359,7 +359,7 @@ def test_fp8_cap_clamp_above_num_experts(monkeypatch):
 
 
 def test_install_wisp_fp8_standin_layer_matches_resident():
-    from wisp_amd.integrations.vllm.layer import Fp8FusedMoE, Fp8MoEMethod
+    from wisp.integrations.vllm.layer import Fp8FusedMoE, Fp8MoEMethod
     E, H, I, K, block = 16, 512, 256, 4, (128, 128)
     _, w13, w2, s13, s2 = _experts(E, H, I, block, seed=13)
     g = torch.Generator().manual_seed(14)

@@ -10,7 +10,7 @@ import torch
 from tests._util import fixture_matches, load_golden
 from tests.test_gpu_kernels import DevPager, gpu_route
 from wisp_amd import workloads as W
-from wisp_amd.integrations.vllm.fused_moe import WispMoEState
+from wisp.integrations.vllm.fused_moe import WispMoEState
 
 pytestmark = pytest.mark.gpu
 

@@ -4,8 +4,8 @@ import pytest
 import torch
 
 from wisp_amd import workloads as W
-from wisp_amd.integrations.vllm import fused_moe as fm
-from wisp_amd.integrations.vllm import layer as L
+from wisp.integrations.vllm import fused_moe as fm
+from wisp.integrations.vllm import layer as L
 
 pytestmark = pytest.mark.gpu
 

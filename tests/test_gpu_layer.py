@@ -8,7 +8,7 @@ from oracle.moe import moe_forward, route
 from oracle.pager import PagerOracle
 from tests._util import oracle_trace_matches
 from wisp_amd import workloads as W
-from wisp_amd.integrations.vllm.fused_moe import WispMoEState
+from wisp.integrations.vllm.fused_moe import WispMoEState
 from wisp_amd.record import parse_record
 
 pytestmark = pytest.mark.gpu
@@ -80,7 +80,7 @@ def test_qwen3_bf16_layer_decode(monkeypatch, engine, streams):
     monkeypatch.setenv("WISP_PAGEIN_ENGINE", engine)
     monkeypatch.setenv("WISP_PAGEIN_STREAMS", streams)
     wl = W.qwen3_decode(steps=48, pin=True)
-    sts = drive(wl, 8, wl.steps, check_out_every=8, tol=1e-2, timed=True)
+    sts = drive(wl, 8, wl.steps, check_out_every=1, tol=1e-2, timed=True)
     assert sts["paged"].pagein_engine == engine
     ms, nbytes = sts["paged"].pagein_stats()
     assert ms > 0 and nbytes == sts["paged"].stats_miss * wl.shape.expert_bytes
@@ -275,6 +275,40 @@ def test_prefill_chunk_layer_mfma():
     # split into greedy token groups and runs on the MFMA grouped GEMM
     wl = W.batch_prefill(tokens=96, pin=True)
     drive(wl, 32, 1, tol=1e-2)
+
+
+def test_batched_config_at_full_size_against_the_fixture():
+    """The batched configuration at its real sizes on one layer state (Qwen3
+    shape, cap 32, router logits N(0,1)): the 512-token prefill chunk, then
+    bs=32 decode steps, the sequence of tests/golden/batch.json.gz.  Every
+    call's decisions, slot table and ticks equal the fixture's; every output
+    equals the resident layer's bytes and is within 1e-2 of the float64
+    oracle."""
+    from tests._util import fixture_matches, load_golden
+    g = load_golden("batch.json.gz")
+    pre = W.batch_prefill(pin=True)
+    dec = W.batch_decode(steps=8, weights=False)  # the fixture's draw; 3 steps run
+    calls = [(pre.x[0], pre.logits[0])] + [(dec.x[t], dec.logits[t]) for t in range(3)]
+    w13, w2 = pre.views()
+    K, E, cap = 8, pre.shape.experts, 32
+    paged = WispMoEState(w13, w2, cap, "paged", DEV, 0)
+    res = WispMoEState(w13, w2, E, "resident", DEV, 1)
+    res.prime_identity()
+    for i, (x, lg) in enumerate(calls):
+        print(f"call {i}: {x.shape[0]} tokens", flush=True)
+        xd, lgd = x.to(DEV), lg.to(DEV)
+        out = paged.forward(xd, lgd, K, True)
+        ref = res.forward(xd, lgd, K, True)
+        torch.cuda.synchronize()
+        assert torch.equal(bits(out), bits(ref)), i
+        _, ids_gpu = paged.last_topk
+        assert ids_gpu.cpu().tolist() == g["ids"][i]
+        rec = parse_record(paged.last_record.numpy(), x.shape[0], K)
+        fixture_matches(g["trace"][i], rec, paged.slot_to_expert, paged.lru_tick,
+                        paged.lru_clock)
+        w_ref, ids_ref = route(lg, K)
+        o = moe_forward(x, w_ref, ids_ref, w13, w2)
+        assert rel_err(out, o) < 1e-2, i
 
 
 @pytest.mark.parametrize("algo", [1, 2], ids=["gemv", "mfma"])

@@ -12,8 +12,8 @@ from oracle.cooccur import CooccurOracle, predict_layer as predict_oracle, prefe
 from oracle.moe import route
 from oracle.pager import PagerOracle
 from wisp_amd import workloads as W
-from wisp_amd.integrations.vllm import fused_moe as fm
-from wisp_amd.integrations.vllm.cooccur import CooccurTable, predict_layer
+from wisp.integrations.vllm import fused_moe as fm
+from wisp.integrations.vllm.cooccur import CooccurTable, predict_layer
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")

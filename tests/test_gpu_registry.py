@@ -10,7 +10,7 @@ import torch
 from oracle.moe import route
 from oracle.pager import PagerOracle
 from wisp_amd import workloads as W
-from wisp_amd.integrations.vllm import fused_moe as fm
+from wisp.integrations.vllm import fused_moe as fm
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")

@@ -5,7 +5,7 @@ import pytest
 import torch
 
 from oracle.pager import PagerOracle
-from wisp_amd.integrations.vllm.fused_moe import WispMoEState
+from wisp.integrations.vllm.fused_moe import WispMoEState
 
 pytestmark = pytest.mark.gpu
 

@@ -4,7 +4,7 @@ memory into a small HBM scratch (``WISP_MODE``, ``WISP_CAP_EXPERTS``).
 Same import surface as the reference's ``wisp.integrations.vllm``
 (``src/wisp/integrations/vllm/__init__.py:37-39``)::
 
-    from wisp_amd.integrations.vllm import install_wisp_moe
+    from wisp.integrations.vllm import install_wisp_moe
     install_wisp_moe()   # before the model is built
 """
 from .fused_moe import install_wisp_moe, is_installed

@@ -25,10 +25,10 @@ from typing import Iterable, Mapping, Union
 import numpy as np
 import torch
 
-from ... import _lib
-from ..._lib import check, lib
+from wisp_amd import _lib
+from wisp_amd._lib import check, lib
 
-logger = logging.getLogger("wisp_amd.integrations.vllm.cooccur")
+logger = logging.getLogger("wisp.integrations.vllm.cooccur")
 
 
 class CooccurTable:

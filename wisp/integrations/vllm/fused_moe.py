@@ -15,7 +15,7 @@ Mirrors ``src/wisp/integrations/vllm/fused_moe.py`` of the reference:
   ``process_weights_after_loading`` and ``forward_cuda`` of
   ``UnquantizedFusedMoEMethod`` (reference 660-1315).  When vLLM is not
   importable the patch targets the stand-in class of
-  ``wisp_amd.integrations.vllm.layer`` with the same methods.
+  ``wisp.integrations.vllm.layer`` with the same methods.
 
 Everything on the call path runs in ``libwisp_hip.so``: routing, the pager
 (state lives on the GPU; the host views above are read back on demand), the
@@ -34,10 +34,10 @@ from typing import Any, Callable
 
 import torch
 
-from ... import _lib
-from ..._lib import check, lib
+from wisp_amd import _lib
+from wisp_amd._lib import check, lib
 
-logger = logging.getLogger("wisp_amd.integrations.vllm.fused_moe")
+logger = logging.getLogger("wisp.integrations.vllm.fused_moe")
 
 _PATCHED_FLAG = "_wisp_patched"
 
@@ -144,9 +144,27 @@ class _Workspace:
         self.topk_w = self.topk_ids = self.slots = self.flags = self.loads = None
         self.act = self.record = None
 
+    def _retire(self) -> None:
+        """Wait for every queued kernel before a buffer is replaced.  The
+        pinned decision record is written by the pager kernel through its
+        device mapping, which torch's host allocator cannot see, so dropping
+        it while a queued pager still writes it could hand the block to the
+        next pinned allocation mid-write; the device buffers may be in use on
+        another stream than the one that allocated them.  Growth doubles, so
+        this happens a handful of times per layer."""
+        if self.record is not None or self.work is not None or self.pairs:
+            torch.cuda.synchronize(self.device)
+
     def ensure(self, T: int, K: int, nslots: int) -> "_lib.Workspace":
         pairs = max(1, T * K)
         words = lib().wisp_record_words(T, K)
+        need = 0
+        if self.fp8 and self.hidden > 0:
+            need = lib().wisp_moe_fp8_work_bytes(max(1, T), K, self.hidden, self.inter, nslots)
+        elif self.dtype == torch.bfloat16 and self.hidden > 0:
+            need = lib().wisp_moe_work_bytes(max(1, T), K, self.hidden, nslots)
+        if pairs > self.pairs or words > self.record_words or need > self.work_bytes:
+            self._retire()
         if pairs > self.pairs:
             self.pairs = max(pairs, 2 * self.pairs)
             dev = self.device
@@ -160,11 +178,6 @@ class _Workspace:
             self.record_words = max(words, 2 * self.record_words)
             self.record = torch.zeros(self.record_words, dtype=torch.int32, pin_memory=True)
         # the grouped (MFMA) paths' per-slot pair lists and per-pair outputs
-        need = 0
-        if self.fp8 and self.hidden > 0:
-            need = lib().wisp_moe_fp8_work_bytes(max(1, T), K, self.hidden, self.inter, nslots)
-        elif self.dtype == torch.bfloat16 and self.hidden > 0:
-            need = lib().wisp_moe_work_bytes(max(1, T), K, self.hidden, nslots)
         if need > self.work_bytes:
             self.work_bytes = max(need, 2 * self.work_bytes)
             self.work = torch.empty(self.work_bytes, dtype=torch.uint8, device=self.device)
@@ -397,6 +410,10 @@ class WispMoEState:
                   count_pred: bool) -> None:
         words = lib().wisp_prefetch_record_words(n)
         if self._pf_record is None or self._pf_words < words:
+            if self._pf_record is not None:
+                # the last prefetch's copies on the side stream may still
+                # read the old record
+                torch.cuda.synchronize(self.device)
             self._pf_words = max(words, lib().wisp_prefetch_record_words(self.num_experts))
             self._pf_record = torch.zeros(self._pf_words, dtype=torch.int32, device=self.device)
         self._pf_n = n

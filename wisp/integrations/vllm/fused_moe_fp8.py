@@ -14,7 +14,7 @@ Mirrors ``src/wisp/integrations/vllm/fused_moe_fp8.py`` of the reference:
 * ``install_wisp_fp8()`` / ``is_fp8_installed()`` (362-390), patching
   ``create_weights``, ``process_weights_after_loading`` and ``apply`` of
   ``Fp8MoEMethod`` (vLLM's when importable, else the stand-in of
-  ``wisp_amd.integrations.vllm.layer``).
+  ``wisp.integrations.vllm.layer``).
 
 Weights are float8_e4m3fn with float32 block scales
 ``s13 [E, 2*ceil(I/bn), ceil(H/bk)]`` / ``s2 [E, ceil(H/bn), ceil(I/bk)]``;
@@ -42,12 +42,12 @@ from typing import Any
 
 import torch
 
-from ... import _lib
-from ..._lib import check, lib
+from wisp_amd import _lib
+from wisp_amd._lib import check, lib
 from .fused_moe import (WispMoEState, _Mode, _require_device, _resolve_pagein_engine,
                         _resolve_pagein_streams, _Workspace)
 
-logger = logging.getLogger("wisp_amd.integrations.vllm.fused_moe_fp8")
+logger = logging.getLogger("wisp.integrations.vllm.fused_moe_fp8")
 
 _PATCHED_FLAG = "_wisp_fp8_patched"
 FP8 = torch.float8_e4m3fn

@@ -1,10 +1,11 @@
-"""wisp_amd - paged fused-MoE layer for AMD Instinct MI355X (gfx950).
+"""wisp_amd - the MI355X (gfx950) native side of the paged fused-MoE layer.
 
-Expert weights live in pinned host memory; a fixed HBM scratch of ``cap``
-slots per layer holds the experts the current tokens route to, managed by an
-LRU pager that runs on the GPU.  Routing, paging decisions, page-in and the
-expert GEMMs are HIP kernels in ``libwisp_hip.so`` (C ABI:
-``include/wisp_hip.h``).
+``csrc/`` holds the HIP kernels (routing, the GPU pager, page-in copy kernel,
+decode GEMV and MFMA grouped expert GEMMs, block-FP8 experts, cross-layer
+prefetch) and the C ABI declared in ``include/wisp_hip.h``; ``build`` compiles
+them into the in-tree ``libwisp_hip.so`` and ``_lib`` binds it with ctypes.
+The drop-in host layer that calls it lives under the reference's import path,
+``wisp.integrations.vllm``.
 """
 __version__ = "0.1.0"
 __all__ = ["__version__"]

@@ -295,6 +295,15 @@ int dispatch_w2(const T* act, int T_, int H, int I, int K, const float* w, const
 
 }  // namespace
 
+// Shapes the GEMV pair covers: the w13 kernel holds up to 8 chunks of 16
+// bytes of a row per lane (H up to 4096 bf16 / 2048 fp32 elements), and the
+// w2 kernel runs one wave per routed expert in a block of at most 16 waves.
+bool gemv_supported(int dtype, int H, int K) {
+  const int V = dtype == WISP_F32 ? 4 : 8;
+  const int ch = (H / V + 63) / 64;
+  return K >= 1 && K <= kMaxKw2 && ch >= 1 && ch <= 8;
+}
+
 int gemv_w13(const void* x, int dtype, int T_, int H, int I, int K, const int32_t* slots,
              const void* w13, size_t w13_stride, void* act, hipStream_t st,
              hipEvent_t ev_start, hipEvent_t ev_stop, const int32_t* pair_filter, int want) {

@@ -77,6 +77,7 @@ int experts_mfma(const void* x, int T, int H, int I, int K, const float* topk_w,
                  const void* w2, size_t w2_stride, void* act, void* out, void* work,
                  size_t work_bytes, hipStream_t st, const StageEvents* ev);
 size_t mfma_work_bytes(int T, int K, int H, int nslots);
+size_t fp8_work_bytes(int T, int K, int H, int I, int nslots);
 int experts_fp8(const void* x, int T, int H, int I, int K, const float* topk_w,
                 const int32_t* slots, int nslots, const void* w13, size_t w13_stride,
                 const float* s13, size_t s13_stride, const void* w2, size_t w2_stride,
@@ -94,6 +95,7 @@ int launch_prefetch(const int32_t* predicted, const int32_t* n_pred_ptr, int n_p
                     int32_t* rec, hipStream_t st);
 int prefetch_record_words(int max_pred);
 bool mfma_supported(int H, int I);
+bool gemv_supported(int dtype, int H, int K);
 
 // Calls of at least this many tokens run the bf16 experts on the MFMA grouped
 // GEMM; fewer run the GEMV kernels, which stream each routed expert once per
@@ -104,18 +106,19 @@ constexpr int kMfmaMinTokens = 14;
 // The block-FP8 grouped path takes over from its decode kernels from here.
 constexpr int kFp8GroupedMinTokens = 16;
 
-// The automatic expert-kernel choice.  It depends only on the call's dtype,
-// shape, token count and top-k, never on the grouping or the slots, so paged
-// and resident runs of one batch use one kernel.  A bf16 call with more
-// routed experts per token than the GEMV pair handles takes the MFMA path,
-// whose combine has no such limit.
+// The automatic expert-kernel choice, or -1 when no kernel family covers the
+// call.  It depends only on the call's dtype, shape, token count and top-k,
+// never on the grouping or the slots, so paged and resident runs of one batch
+// use one kernel.  A bf16 call the GEMV pair does not cover (more routed
+// experts per token than its w2 block holds, or rows longer than its w13
+// registers) takes the MFMA path whenever that covers the shape.
 int auto_algo(int dtype, int H, int I, int T, int K) {
   if (dtype == WISP_FP8_E4M3)
     return T >= kFp8GroupedMinTokens ? WISP_ALGO_MFMA : WISP_ALGO_GEMV;
-  return dtype == WISP_BF16 && mfma_supported(H, I) &&
-                 (T >= kMfmaMinTokens || K > kGemvMaxTopK)
-             ? WISP_ALGO_MFMA
-             : WISP_ALGO_GEMV;
+  const bool gemv = gemv_supported(dtype, H, K);
+  if (dtype == WISP_BF16 && mfma_supported(H, I) && (T >= kMfmaMinTokens || !gemv))
+    return WISP_ALGO_MFMA;
+  return gemv ? WISP_ALGO_GEMV : -1;
 }
 
 namespace {
@@ -490,23 +493,30 @@ int experts(Layer& L, const void* x, int T, int K, const float* w, const int32_t
 }
 
 // The expert algorithm of a layer call (-1: the request does not cover it).
+// Decided before the pager runs, so a call the kernels cannot compute fails
+// without touching the pager state.
 int choose_algo(const Layer& L, int algo, int T, int K) {
   const wisp_layer_desc& d = L.d;
   if (algo == WISP_ALGO_AUTO) return auto_algo(d.dtype, d.hidden, d.inter, T, K);
   if (algo == WISP_ALGO_MFMA && d.dtype == WISP_F32) return -1;
   if (algo == WISP_ALGO_MFMA && d.dtype == WISP_BF16 && !mfma_supported(d.hidden, d.inter))
     return -1;
+  if (algo == WISP_ALGO_GEMV && d.dtype != WISP_FP8_E4M3 && !gemv_supported(d.dtype, d.hidden, K))
+    return -1;
   if (algo != WISP_ALGO_GEMV && algo != WISP_ALGO_MFMA) return -1;
   return algo;
 }
 
 // Copies and expert kernels for groups [0, ngroups) of a decision record.
+// Every group's copies are issued even after a failed expert launch, so the
+// map the pager already wrote never points at a slot that was not filled.
 int run_groups(Layer& L, const int32_t* rec, const int32_t* loads, int T, int K, int ngroups,
                bool compute, const void* x, const float* topk_w, const int32_t* slots, void* act,
                void* out, int algo, const wisp_workspace* ws, hipStream_t st) {
   const RecordLayout RL(T, K);
   const size_t row = (size_t)L.d.hidden * act_size(L.d.dtype);
   int last_gemm = -1;
+  int failed = WISP_OK;
   for (int g = 0; g < ngroups; ++g) {
     const int32_t* G = rec + RL.group_base(g);
     const int t0 = G[0], t1 = G[1], ld_off = G[6], n_ld = G[7];
@@ -517,15 +527,29 @@ int run_groups(Layer& L, const int32_t* rec, const int32_t* loads, int T, int K,
                                 st);
       if (rc != WISP_OK) return rc;
     }
-    if (compute && t1 > t0) {
-      int rc = experts(L, (const char*)x + (size_t)t0 * row, t1 - t0, K, topk_w + (size_t)t0 * K,
-                       slots + (size_t)t0 * K, act, (char*)out + (size_t)t0 * row, algo, ws, st);
-      if (rc != WISP_OK) return rc;
+    if (compute && failed == WISP_OK && t1 > t0) {
+      failed = experts(L, (const char*)x + (size_t)t0 * row, t1 - t0, K,
+                       topk_w + (size_t)t0 * K, slots + (size_t)t0 * K, act,
+                       (char*)out + (size_t)t0 * row, algo, ws, st);
+      if (failed != WISP_OK) continue;
       WISP_HIP_TRY(hipEventRecord(L.ev_gemm[g % kEventRing], st));
       last_gemm = g;
     }
   }
-  return WISP_OK;
+  return failed;
+}
+
+// Whether the workspace's work buffer holds what algorithm `a` needs for a
+// call of T tokens (checked before the pager runs).
+bool work_ok(const Layer& L, int a, int T, int K, const wisp_workspace* ws) {
+  const wisp_layer_desc& d = L.d;
+  size_t need = 0;
+  if (a == WISP_ALGO_MFMA && d.dtype == WISP_BF16)
+    need = mfma_work_bytes(T, K, d.hidden, d.cap);
+  else if (a == WISP_ALGO_MFMA && d.dtype == WISP_FP8_E4M3)
+    need = fp8_work_bytes(T, K, d.hidden, d.inter, d.cap);
+  if (need == 0 || T == 0) return true;
+  return ws->work && ws->work_bytes >= need && ((uintptr_t)ws->work) % 256 == 0;
 }
 
 // Device view of the (pinned host) decision record; device memory passes
@@ -721,9 +745,14 @@ extern "C" int wisp_layer_forward(void* handle, const void* x, const void* logit
   }
   const int a = choose_algo(*L, algo, T, K);
   if (a < 0) {
-    wisp_set_last_error("requested expert algorithm does not cover this call",
-                        "wisp_layer_forward");
+    wisp_set_last_error("no expert kernel covers this call (shape, top_k or requested "
+                        "algorithm)", "wisp_layer_forward");
     return WISP_ERR_UNSUPPORTED;
+  }
+  if (!work_ok(*L, a, T, K, ws)) {
+    wisp_set_last_error("work buffer missing, misaligned or too small for the grouped path",
+                        "wisp_layer_forward");
+    return WISP_ERR_INVALID;
   }
   if (L->profile) L->prof_calls += 1;
 
@@ -762,11 +791,13 @@ extern "C" int wisp_layer_forward(void* handle, const void* x, const void* logit
 
   const bool speculate = a == WISP_ALGO_GEMV && one_group && !L->fp8;
   ProfLaunch* spec_w2 = nullptr;
+  int spec_rc = WISP_OK;
   if (speculate) {
-    rc = w13(*L, x, T, K, ws->slots, ws->act, st, ws->flags + 1, 0);
-    if (rc == WISP_OK)
-      rc = w2(*L, ws->act, T, K, ws->topk_w, ws->slots, out, st, ws->flags, &spec_w2);
-    if (rc != WISP_OK) return rc;
+    // a failed launch here still lets the copies below run (the map already
+    // names the slots they fill); its error is returned after them
+    spec_rc = w13(*L, x, T, K, ws->slots, ws->act, st, ws->flags + 1, 0);
+    if (spec_rc == WISP_OK)
+      spec_rc = w2(*L, ws->act, T, K, ws->topk_w, ws->slots, out, st, ws->flags, &spec_w2);
   }
 
   WISP_HIP_TRY(hipEventSynchronize(L->ev_decided));
@@ -781,10 +812,10 @@ extern "C" int wisp_layer_forward(void* handle, const void* x, const void* logit
     const RecordLayout RL(T, K);
     const int32_t* G = rec + RL.group_base(0);
     const int n_ld = rec[kRecGroupsDone] > 0 ? G[7] : 0;
-    if (n_ld == 0) return WISP_OK;  // the queued kernels computed everything
+    if (n_ld == 0) return spec_rc;  // the queued kernels computed everything
     if (spec_w2) spec_w2->counted = false;  // it found loads and exited
     rc = page_in(*L, rec + RL.loaded_base() + 2 * G[6], n_ld, nullptr, 0, st);
-    if (rc != WISP_OK) return rc;
+    if (rc != WISP_OK || spec_rc != WISP_OK) return rc != WISP_OK ? rc : spec_rc;
     rc = w13(*L, x, T, K, ws->slots, ws->act, st, ws->flags + 1, 1);
     if (rc == WISP_OK) rc = w2(*L, ws->act, T, K, ws->topk_w, ws->slots, out, st, nullptr, nullptr);
     return rc;
@@ -880,7 +911,12 @@ extern "C" int wisp_layer_prefetch(void* handle, const int32_t* predicted,
   const wisp_layer_desc& d = L->d;
   if (d.mode == WISP_MODE_RESIDENT || d.hidden < 1) return WISP_OK;  // nothing to page
   hipStream_t st = (hipStream_t)stream;
-  int rc = launch_prefetch(predicted, n_predicted, n, ordered, count_pred, last_ids, n_last,
+  // The previous prefetch's copies (side stream) still read their count and
+  // load list from the caller's record, which this call's decisions rewrite:
+  // order the decisions after those copies.
+  int rc = wait_prefetch(*L, st);
+  if (rc != WISP_OK) return rc;
+  rc = launch_prefetch(predicted, n_predicted, n, ordered, count_pred, last_ids, n_last,
                            d.num_experts, d.cap, n, d.expert_map, d.slot_to_expert, d.lru_tick,
                            d.counters, record, st);
   if (rc != WISP_OK) return rc;
@@ -973,6 +1009,10 @@ extern "C" int wisp_moe_experts(const void* x, int dtype, int T, int H, int I, i
     return WISP_ERR_UNSUPPORTED;
   }
   const int a = algo == WISP_ALGO_AUTO ? auto_algo(dtype, H, I, T, K) : algo;
+  if (a < 0 || (a == WISP_ALGO_GEMV && !gemv_supported(dtype, H, K))) {
+    wisp_set_last_error("no expert kernel covers this shape and top_k", "wisp_moe_experts");
+    return WISP_ERR_UNSUPPORTED;
+  }
   if (a == WISP_ALGO_MFMA) {
     if (dtype != WISP_BF16) {
       wisp_set_last_error("the MFMA path computes in bf16 only", "wisp_moe_experts");

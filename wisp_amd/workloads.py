@@ -258,7 +258,7 @@ class Fp8Workload:
 
     @property
     def layout(self):
-        from .integrations.vllm.fused_moe_fp8 import Fp8SlabLayout
+        from wisp.integrations.vllm.fused_moe_fp8 import Fp8SlabLayout
         return Fp8SlabLayout(self.shape.hidden, self.shape.inter, self.block)
 
     def views(self):
@@ -291,7 +291,7 @@ def fp8_layer(base: Workload, pin: bool = False, seed: int = 7, experts: int | N
               block=FP8_BLOCK) -> Fp8Workload:
     """The block-FP8 twin of a bf16 workload: same activations and router
     logits, weights drawn from their own seeded generator and quantised."""
-    from .integrations.vllm.fused_moe_fp8 import fp8_slab_masters
+    from wisp.integrations.vllm.fused_moe_fp8 import fp8_slab_masters
     sh = base.shape
     E = sh.experts if experts is None else experts
     buf, w13, w2, s13, s2 = fp8_slab_masters(E, sh.hidden, sh.inter, block, pin=pin)
