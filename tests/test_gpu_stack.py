@@ -54,7 +54,7 @@ def test_stack_48_layers_cap24_through_the_layer_call():
             assert torch.equal(bits(h), bits(hr)), (t, L)
             st = paged[L]
             _, ids = st.last_topk
-            assert ids.cpu().tolist() == [g["layers"][L]["ids"][t]], (t, L)
+            assert ids.cpu().tolist() == g["layers"][L]["ids"][t], (t, L)
             rec = parse_record(st.last_record.numpy(), 1, K)
             fixture_matches(g["layers"][L]["trace"][t], rec, st.slot_to_expert, st.lru_tick,
                             st.lru_clock)
