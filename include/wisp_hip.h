@@ -3,7 +3,8 @@
  *
  * Every entry point takes plain pointers, sizes and a hipStream_t, returns an
  * int status (WISP_OK = 0) and never allocates device memory: the caller
- * owns all buffers.  On failure wisp_last_error() returns a message.
+ * owns all buffers (wisp_moe_experts_noalloc instead works in a static device
+ * array of the library).  On failure wisp_last_error() returns a message.
  *
  * Tensor pointers are device memory of the stream's device unless an entry
  * point says otherwise (expert masters live in host memory, pinned for the
@@ -191,6 +192,27 @@ size_t wisp_moe_fp8_work_bytes(int T, int K, int H, int I, int nslots);
  *           the fp8_w8a8 block path at fused_moe_fp8.py:316-326). */
 int wisp_quant_fp8_groups(const void* x, int dtype, int rows, int cols, int group, uint8_t* q,
                           float* scales, wisp_stream_t stream);
+
+/* Bytes of the device array wisp_moe_experts_noalloc works in, per GPU. */
+#define WISP_NOALLOC_SCRATCH_BYTES (64u << 20)
+
+/* wisp_moe_experts without act and work arguments, allocating nothing.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (work captured into a HIP graph, serving loops or harnesses
+ * that forbid hipMalloc).  The act intermediate and the MFMA work buffer live
+ * in a static device array of the library, WISP_NOALLOC_SCRATCH_BYTES per
+ * GPU, held from the library's first use on that GPU until the process
+ * ends.  A call needing more than that (T*K*I act elements, 256-byte
+ * aligned, plus wisp_moe_work_bytes(T, K, H, nslots) on the MFMA path)
+ * returns WISP_ERR_INVALID before any launch.  Every call on one GPU shares
+ * that GPU's array, so calls that overlap on one GPU (on different streams
+ * without ordering between them) race: order them on one stream or with
+ * events.  Arguments, algorithms and results are those of wisp_moe_experts
+ * (bit-identical outputs). */
+int wisp_moe_experts_noalloc(const void* x, int dtype, int T, int H, int I, int K,
+                             const float* topk_w, const int32_t* slots, int nslots,
+                             const void* w13, size_t w13_stride, const void* w2,
+                             size_t w2_stride, void* out, int algo, wisp_stream_t stream);
 
 /* Bytes of the work buffer the MFMA expert path needs for T tokens x K over
  * nslots slots at hidden size H: per-slot pair lists and fp32 per-pair

@@ -29,6 +29,7 @@ WISP_ALGO_GEMV = 1
 WISP_ALGO_MFMA = 2
 WISP_PAGEIN_MEMCPY = 0
 WISP_PAGEIN_KERNEL = 1
+WISP_NOALLOC_SCRATCH_BYTES = 64 << 20
 
 # Decision-record header words (wisp_amd/csrc/pager_core.h).
 REC_STATUS, REC_GROUPS_DONE, REC_GROUPS_PLANNED, REC_FAIL_GROUP, REC_FAIL_UNIQUE, \
@@ -88,6 +89,8 @@ SIGNATURES = {
     "wisp_moe_experts": (_i32, [_vp, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _i32, _vp, _sz,
                                 _vp, _sz, _vp, _vp, _vp, _sz, _i32, _vp]),
     "wisp_moe_work_bytes": (_sz, [_i32, _i32, _i32, _i32]),
+    "wisp_moe_experts_noalloc": (_i32, [_vp, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _i32, _vp,
+                                        _sz, _vp, _sz, _vp, _i32, _vp]),
     "wisp_moe_experts_fp8": (_i32, [_vp, _i32, _i32, _i32, _i32, _vp, _vp, _i32, _vp, _sz, _vp,
                                     _sz, _vp, _sz, _vp, _sz, _i32, _i32, _vp, _vp, _vp, _sz, _i32,
                                     _vp]),

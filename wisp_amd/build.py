@@ -29,6 +29,7 @@ SOURCES = [
     "prefetch.hip",
     "layer.hip",
     "probes.hip",
+    "noalloc.hip",
 ]
 
 ARCH = "gfx950"
