@@ -271,13 +271,20 @@ typedef struct wisp_workspace {
   int32_t* topk_ids;             /* device [max_pairs]                   */
   int32_t* slots;                /* device [max_pairs]                   */
   int32_t* flags;                /* device [1 + max_pairs]: experts loaded
-                                    by the call, then per pair 1 if its
-                                    expert was loaded by this call        */
+                                    by the call, then per pair a word: its
+                                    slot in bits 0-15 (0xFFFF: none) and,
+                                    if this call loaded its expert, that
+                                    expert id + 1 in bits 16-30            */
   int32_t* loads;                /* device [2*max_pairs]: (expert, slot)
                                     pairs loaded by the call              */
   void* act;                     /* device [max_pairs*inter]             */
   int32_t* record;               /* pinned host [record_words]           */
   int record_words;
+  int32_t* record_dev;           /* device [record_words] or NULL: where
+                                    one-group calls on the copy-kernel
+                                    engine write their record instead
+                                    (read it back with
+                                    wisp_layer_sync_record)               */
   void* work;                    /* device, 256-byte aligned: MFMA path
                                     work buffer (wisp_moe_work_bytes with
                                     nslots = cap)                         */
@@ -302,6 +309,12 @@ int wisp_layer_forward(void* handle, const void* x, const void* logits, int logi
                        int T, int top_k, int renormalize, void* out, const wisp_workspace* ws,
                        int algo, wisp_stream_t stream);
 
+/* Wait for the device, then make the decision record of the layer's last
+ * call readable at ws->record (pinned host), copying it from ws->record_dev
+ * when the call wrote it there.  No reference counterpart (the reference
+ * pager runs on the host). */
+int wisp_layer_sync_record(void* handle, const wisp_workspace* ws);
+
 /* Make the experts in ids[n] resident as one call (no sub-batching).
  * Replaces: WispMoEState.ensure_resident (fused_moe.py:264-358). */
 int wisp_layer_ensure_resident(void* handle, const int32_t* ids, int n,
@@ -322,13 +335,16 @@ int wisp_layer_pagein_engine(void* handle);
 
 /* Read and reset the accumulated execution time (dispatch timestamps) of the
  * w13+SiLU kernels and of the w2+combine kernels of all layer calls since the
- * last read, and the number of layer calls; then switch timing on
- * (enable != 0) or off.  A speculative w2 launch that found experts to load
- * and exited is not counted.  The switch also covers the page-in timing of
- * wisp_layer_last_pagein.  Timing is off by default: every timed launch
- * carries dispatch-timestamp events, which lengthen the stream. */
+ * last read, the number of layer calls, and the number of calls whose w13
+ * time is in w13_ms; then switch timing on (enable != 0) or off.  A
+ * speculative w2 launch that found experts to load and exited is not counted.
+ * One-group GEMV calls on the copy-kernel engine run page-in and w13 as one
+ * launch: it counts as w13 time when it copied nothing, else as page-in time
+ * (wisp_layer_last_pagein).  The switch also covers the page-in timing.
+ * Timing is off by default: every timed launch carries dispatch-timestamp
+ * events, which lengthen the stream. */
 int wisp_layer_profile(void* handle, int enable, double* w13_ms, double* w2_ms,
-                       int64_t* calls);
+                       int64_t* calls, int64_t* w13_calls);
 
 /* ---- group 4: cross-layer speculative prefetch ------------------------ */
 

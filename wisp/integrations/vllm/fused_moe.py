@@ -142,7 +142,7 @@ class _Workspace:
         self.work = None
         self.struct = _lib.Workspace()
         self.topk_w = self.topk_ids = self.slots = self.flags = self.loads = None
-        self.act = self.record = None
+        self.act = self.record = self.record_dev = None
 
     def _retire(self) -> None:
         """Wait for every queued kernel before a buffer is replaced.  The
@@ -177,6 +177,8 @@ class _Workspace:
         if words > self.record_words:
             self.record_words = max(words, 2 * self.record_words)
             self.record = torch.zeros(self.record_words, dtype=torch.int32, pin_memory=True)
+            self.record_dev = torch.zeros(self.record_words, dtype=torch.int32,
+                                          device=self.device)
         # the grouped (MFMA) paths' per-slot pair lists and per-pair outputs
         if need > self.work_bytes:
             self.work_bytes = max(need, 2 * self.work_bytes)
@@ -187,6 +189,7 @@ class _Workspace:
         s.slots, s.act = self.slots.data_ptr(), self.act.data_ptr()
         s.flags, s.loads = self.flags.data_ptr(), self.loads.data_ptr()
         s.record, s.record_words = self.record.data_ptr(), self.record_words
+        s.record_dev = self.record_dev.data_ptr()
         s.work = self.work.data_ptr() if self.work is not None else None
         s.work_bytes = self.work_bytes
         return s
@@ -330,8 +333,10 @@ class WispMoEState:
     @property
     def last_record(self) -> torch.Tensor:
         """The pinned decision record of the last paged call (waits for the
-        device to finish the calls already queued)."""
-        torch.cuda.synchronize(self.device)
+        device to finish the calls already queued; decode calls on the
+        copy-kernel engine keep their record in device memory until asked)."""
+        check(lib().wisp_layer_sync_record(self._handle, C.byref(self._ws.struct)),
+              "last_record")
         return self._ws.record
 
     @property
@@ -448,13 +453,16 @@ class WispMoEState:
     def profile(self, enable: bool = True) -> dict:
         """Read and reset the execution time (ms, dispatch timestamps) of the
         ``w13`` and ``w2`` expert kernels of all layer calls since the last
-        read and the number of ``calls``; then switch timing on or off.  The
-        switch covers ``pagein_stats`` too; timing is off by default, since
-        its events lengthen the stream."""
-        a, b, n = C.c_double(), C.c_double(), C.c_int64()
+        read, the number of ``calls`` and of ``w13_calls`` (calls whose w13
+        time is in ``w13``: a decode call that pages experts in runs its w13
+        inside the page-in launch, which is timed as page-in); then switch
+        timing on or off.  The switch covers ``pagein_stats`` too; timing is
+        off by default, since its events lengthen the stream."""
+        a, b, n, n13 = C.c_double(), C.c_double(), C.c_int64(), C.c_int64()
         check(lib().wisp_layer_profile(self._handle, int(enable), C.byref(a), C.byref(b),
-                                       C.byref(n)), "profile")
-        return {"w13": float(a.value), "w2": float(b.value), "calls": int(n.value)}
+                                       C.byref(n), C.byref(n13)), "profile")
+        return {"w13": float(a.value), "w2": float(b.value), "calls": int(n.value),
+                "w13_calls": int(n13.value)}
 
     def resize_cap(self, new_cap: int) -> None:
         """Resize the scratch to ``new_cap`` slots at a drained barrier

@@ -68,7 +68,7 @@ class Workspace(C.Structure):
     _fields_ = [
         ("max_pairs", C.c_int), ("topk_w", _vp), ("topk_ids", _vp), ("slots", _vp),
         ("flags", _vp), ("loads", _vp), ("act", _vp), ("record", _vp),
-        ("record_words", C.c_int), ("work", _vp), ("work_bytes", _sz),
+        ("record_words", C.c_int), ("record_dev", _vp), ("work", _vp), ("work_bytes", _sz),
     ]
 
 
@@ -105,8 +105,9 @@ SIGNATURES = {
     "wisp_layer_prime_identity": (_i32, [_vp, _vp]),
     "wisp_layer_last_pagein": (_i32, [_vp, _f32p, C.POINTER(C.c_double)]),
     "wisp_layer_pagein_engine": (_i32, [_vp]),
+    "wisp_layer_sync_record": (_i32, [_vp, C.POINTER(Workspace)]),
     "wisp_layer_profile": (_i32, [_vp, _i32, C.POINTER(C.c_double), C.POINTER(C.c_double),
-                                  C.POINTER(C.c_int64)]),
+                                  C.POINTER(C.c_int64), C.POINTER(C.c_int64)]),
     "wisp_cooccur_observe_layer": (_i32, [C.POINTER(Cooccur), _i32, _vp, _i32, _i32, _vp]),
     "wisp_cooccur_predict": (_i32, [C.POINTER(Cooccur), _i32, _i32, _vp, _i32, _i32, _vp, _vp,
                                     _vp]),

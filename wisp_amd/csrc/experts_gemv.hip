@@ -12,16 +12,24 @@
 // never on the slot numbers, on cap or on the other tokens of the launch.
 // That is what makes paged output byte-identical to resident output.
 #include "common.h"
+#include "pagein.h"
+#include "pager_core.h"
 
 namespace wisp {
 namespace {
 
 template <typename T>
 struct Vec;
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
 template <>
 struct Vec<float> {
   static constexpr int N = 4;
   __device__ static inline void unpack(const uint4& u, float* f) {
+    f[0] = __uint_as_float(u.x); f[1] = __uint_as_float(u.y);
+    f[2] = __uint_as_float(u.z); f[3] = __uint_as_float(u.w);
+  }
+  __device__ static inline void unpack(const u32x4& u, float* f) {
     f[0] = __uint_as_float(u.x); f[1] = __uint_as_float(u.y);
     f[2] = __uint_as_float(u.z); f[3] = __uint_as_float(u.w);
   }
@@ -30,6 +38,12 @@ template <>
 struct Vec<uint16_t> {  // bf16 bits
   static constexpr int N = 8;
   __device__ static inline void unpack(const uint4& u, float* f) {
+    f[0] = __uint_as_float(u.x << 16); f[1] = __uint_as_float(u.x & 0xffff0000u);
+    f[2] = __uint_as_float(u.y << 16); f[3] = __uint_as_float(u.y & 0xffff0000u);
+    f[4] = __uint_as_float(u.z << 16); f[5] = __uint_as_float(u.z & 0xffff0000u);
+    f[6] = __uint_as_float(u.w << 16); f[7] = __uint_as_float(u.w & 0xffff0000u);
+  }
+  __device__ static inline void unpack(const u32x4& u, float* f) {
     f[0] = __uint_as_float(u.x << 16); f[1] = __uint_as_float(u.x & 0xffff0000u);
     f[2] = __uint_as_float(u.y << 16); f[3] = __uint_as_float(u.y & 0xffff0000u);
     f[4] = __uint_as_float(u.z << 16); f[5] = __uint_as_float(u.z & 0xffff0000u);
@@ -49,110 +63,261 @@ __device__ inline uint4 ld16(const void* p) { return *reinterpret_cast<const uin
 // Streaming load for weight rows: each byte is read once per launch, so the
 // nontemporal hint keeps the rows from displacing cached data (measured on
 // MI355X: w13 at the Qwen3 decode shape 9.2 us instead of 10.2 us).
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 __device__ inline uint4 ld16_stream(const void* p) {
   const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
 // ---------------------------------------------------------------------------
-// Kernel A: act = silu(gate) * up.  Block = 4 waves, each wave owns RW
-// consecutive i (gate row i and up row I + i) of one (token, k) pair; each
-// lane covers CH chunks of 16 bytes of a row (chunk c*64 + lane).
-// grid = (ceil(I / (4 * RW)), T * K).  One row pair per wave (RW = 1) gives
-// the most waves in flight, which is what a pure weight stream needs.  FULL:
-// a row is exactly CH chunks per lane, so the loads carry no bounds guard
-// (a guarded load sits in its own exec-masked block, which costs ~0.7 us per
-// launch at the Qwen3 shape by keeping the loads from issuing back to back).
+// Kernel A: act = silu(gate) * up.  Block = 4 waves, each wave owns one i
+// (gate row i and up row I + i) of one (token, k) pair; each lane covers CH
+// chunks of 16 bytes of a row (chunk c*64 + lane).  grid = (ceil(I / 4),
+// T * K).  One row pair per wave gives the most waves in flight, which is
+// what a pure weight stream needs.  FULL: a row is exactly CH chunks per lane,
+// so the loads carry no bounds guard (a guarded load sits in its own
+// exec-masked block, which costs ~0.7 us per launch at the Qwen3 shape by
+// keeping the loads from issuing back to back).
+//
+// The row loads and the dot products are shared with the fused page-in
+// kernel below, which computes the same act values from rows it copies.
 // ---------------------------------------------------------------------------
-template <typename T, int CH, int RW, bool FULL>
+template <typename T, int CH, bool FULL, bool STREAM>
+__device__ inline void load_row(const T* __restrict__ row, int nch, int lane, uint4 (&v)[CH]) {
+  constexpr int V = Vec<T>::N;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int ch = c * 64 + lane;
+    v[c] = (FULL || ch < nch) ? (STREAM ? ld16_stream(row + (size_t)ch * V)
+                                        : ld16(row + (size_t)ch * V))
+                              : make_uint4(0, 0, 0, 0);
+  }
+}
+
+// silu(gate . x) * (up . x) for the rows and x chunks a wave holds: fp32 FMA
+// over each lane's chunks in order, then a butterfly over the 64 lanes; every
+// lane returns the result.
+template <typename T, int CH, typename VW>
+__device__ inline float swiglu_rows(const VW (&wg)[CH], const VW (&wu)[CH],
+                                    const uint4 (&xv)[CH]) {
+  constexpr int V = Vec<T>::N;
+  float ag = 0.f, au = 0.f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    float xf[V], gf[V], uf[V];
+    Vec<T>::unpack(xv[c], xf);
+    Vec<T>::unpack(wg[c], gf);
+    Vec<T>::unpack(wu[c], uf);
+#pragma unroll
+    for (int q = 0; q < V; ++q) {
+      ag = fmaf(gf[q], xf[q], ag);
+      au = fmaf(uf[q], xf[q], au);
+    }
+  }
+  for (int off = 32; off > 0; off >>= 1) {
+    ag += __shfl_xor(ag, off);
+    au += __shfl_xor(au, off);
+  }
+  return silu(ag) * au;
+}
+
+// The same dot product one row at a time: this lane's FMA chain over its
+// chunks, then the butterfly.  Each of swiglu_rows' two accumulators follows
+// exactly this sequence, so silu(row_dot(gate)) * row_dot(up) equals
+// swiglu_rows bit for bit.
+template <typename T, int CH>
+__device__ inline float row_dot(const u32x4 (&w)[CH], const uint4 (&xv)[CH]) {
+  constexpr int V = Vec<T>::N;
+  float a = 0.f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    float xf[V], wf[V];
+    Vec<T>::unpack(xv[c], xf);
+    Vec<T>::unpack(w[c], wf);
+#pragma unroll
+    for (int q = 0; q < V; ++q) a = fmaf(wf[q], xf[q], a);
+  }
+  for (int off = 32; off > 0; off >>= 1) a += __shfl_xor(a, off);
+  return a;
+}
+
+// One wave: act[pair][i] of a pair whose expert sits in slot s, stored only
+// when `keep` (the loads and the arithmetic happen either way, so a caller
+// can load `keep` together with s instead of before it).
+template <typename T, int CH, bool FULL>
+__device__ inline void w13_wave(const T* __restrict__ x, int H, int I, int K, int pair, int i,
+                                int s, const T* __restrict__ w13, size_t w13_stride,
+                                T* __restrict__ act, int lane, bool keep = true) {
+  constexpr int V = Vec<T>::N;
+  T* arow = act + (size_t)pair * I;
+  if (s < 0) {
+    if (lane == 0 && keep) store_elem(arow + i, 0.f);
+    return;
+  }
+  const int nch = H / V;
+  const T* W = w13 + (size_t)s * w13_stride;
+  uint4 xv[CH], wg[CH], wu[CH];
+  load_row<T, CH, FULL, false>(x + (size_t)(pair / K) * H, nch, lane, xv);
+  load_row<T, CH, FULL, true>(W + (size_t)i * H, nch, lane, wg);
+  load_row<T, CH, FULL, true>(W + (size_t)(I + i) * H, nch, lane, wu);
+  const float v = swiglu_rows<T, CH, uint4>(wg, wu, xv);
+  if (lane == 0 && keep) store_elem(arow + i, v);
+}
+
+template <typename T, int CH, bool FULL>
 __global__ __launch_bounds__(256) void w13_silu_kernel(const T* __restrict__ x, int H, int I,
                                                         int K, const int32_t* __restrict__ slots,
                                                         const T* __restrict__ w13,
                                                         size_t w13_stride, T* __restrict__ act,
                                                         const int32_t* __restrict__ pair_filter,
                                                         int want) {
-  constexpr int V = Vec<T>::N;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int pair = blockIdx.y;
-  if (pair_filter && pair_filter[pair] != want) return;
-  const int t = pair / K;
-  const int i0 = (blockIdx.x * 4 + wave) * RW;
-  if (i0 >= I) return;
-  const int s = slots[pair];
-  T* arow = act + (size_t)pair * I;
-  if (s < 0) {
-    if (lane < RW && i0 + lane < I) store_elem(arow + i0 + lane, 0.f);
+  // the pager's per-pair words: run only the pairs whose expert this call
+  // loaded (want != 0) or only the others (want == 0)
+  if (pair_filter && (pair_word_loaded(pair_filter[pair]) >= 0) != (want != 0)) return;
+  const int i = blockIdx.x * 4 + wave;
+  if (i >= I) return;
+  w13_wave<T, CH, FULL>(x, H, I, K, pair, i, slots[pair], w13, w13_stride, act, lane);
+}
+
+// ---------------------------------------------------------------------------
+// Kernel A': page-in and w13 in one launch, for one-token calls on the
+// copy-kernel engine (a token's routed experts are distinct, so each expert
+// serves exactly one pair).
+//   * Blocks [0, kPageInBlocks) copy each expert the pager loaded from its
+//     pinned master into its slot, in load order: first its w13 rows, one
+//     row pair (gate i, up I + i) per wave and iteration, computing act[p][i]
+//     of the expert's pair p from the rows the wave holds (Kernel A's
+//     arithmetic on the same bytes, so the output equals a resident call's);
+//     then the rest of its bytes as a plain copy.  Streaming the experts in
+//     order keeps ~2 MiB of host reads in flight, which holds the host link
+//     at its copy rate (reading every loaded expert at once from all the
+//     w13 waves cost ~4 % of it).
+//   * Blocks from kPageInBlocks on are Kernel A's blocks in (i-block, pair)
+//     order, for the pairs whose expert was already resident.  A wave reads
+//     its pair's slot and loaded flag from one word the pager wrote
+//     (pair_word), so its row loads wait for a single load, as in Kernel A.
+// A call that loads nothing costs the w13 work plus 64 blocks that exit
+// after one load; one that loads experts runs the resident pairs' w13 under
+// the copies.
+// ---------------------------------------------------------------------------
+struct FusedW13Args {
+  const void* x;
+  int H, I, K;
+  const int32_t* words;  // the pager's flags + 1: pair_word(slot, loaded expert)
+  const void* w13;       // scratch base, slot s at + s * w13_stride elements
+  size_t w13_stride;
+  void* act;
+};
+
+template <typename T, int CH, bool FULL>
+__global__ __launch_bounds__(256) void pagein_w13_kernel(PageInArgs a, FusedW13Args f) {
+  constexpr int V = Vec<T>::N;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int H = f.H, I = f.I, nch = H / V;
+  if (blockIdx.x >= kPageInBlocks) {
+    const int nbx = (I + 3) / 4;
+    const int local = blockIdx.x - kPageInBlocks;
+    const int pair = local / nbx;
+    const int i = (local - pair * nbx) * 4 + wave;
+    if (i >= I) return;
+    const int32_t word = f.words[pair];
+    if (pair_word_loaded(word) >= 0) return;  // the copy blocks compute it
+    const int s = pair_word_slot(word);
+    w13_wave<T, CH, FULL>((const T*)f.x, H, I, f.K, pair, i, s < a.cap ? s : -1,
+                          (const T*)f.w13, f.w13_stride, (T*)f.act, lane);
     return;
   }
-  const int nch = H / V;
-  const T* W = w13 + (size_t)s * w13_stride;
-  const T* xr = x + (size_t)t * H;
-
-  uint4 wg[RW][CH], wu[RW][CH], xv[CH];
-#pragma unroll
-  for (int c = 0; c < CH; ++c) {
-    const int ch = c * 64 + lane;
-    xv[c] = (FULL || ch < nch) ? ld16(xr + (size_t)ch * V) : make_uint4(0, 0, 0, 0);
+  const int n = *a.count;
+  if (a.hist && blockIdx.x == 0 && threadIdx.x == 0) {
+    *a.hist = n;
+    __threadfence_system();
   }
+  if (n <= 0) return;
+  // lane p < K holds the expert pair p's word says was loaded (or -1)
+  const int mine = lane < f.K ? pair_word_loaded(f.words[lane]) : -1;
+  const PageInPlane& p0 = a.p[0];  // starts with the expert's w13 rows
+  const size_t row_bytes = (size_t)H * sizeof(T);
+  uint4 xv[CH];
+  load_row<T, CH, FULL, false>((const T*)f.x, nch, lane, xv);  // the call's one token
+  int jcur = -1, e = -1, s = -1, pair = -1;
+  for (int q = blockIdx.x * 4 + wave; q < n * I; q += kPageInBlocks * 4) {
+    const int j = q / I, i = q - j * I;
+    if (j != jcur) {
+      jcur = j;
+      e = a.loads[2 * j];
+      s = a.loads[2 * j + 1];
+      const uint64_t m = __ballot(mine == e);
+      pair = m ? __builtin_ctzll(m) : -1;
+    }
+    if (e < 0 || e >= a.num_experts || s < 0 || s >= a.cap) continue;
+    const u32x4* src_g = reinterpret_cast<const u32x4*>(p0.m + (size_t)e * p0.m_stride +
+                                                        (size_t)i * row_bytes);
+    const u32x4* src_u = reinterpret_cast<const u32x4*>(p0.m + (size_t)e * p0.m_stride +
+                                                        (size_t)(I + i) * row_bytes);
+    u32x4* dst_g = reinterpret_cast<u32x4*>(p0.d + (size_t)s * p0.d_stride + (size_t)i * row_bytes);
+    u32x4* dst_u = reinterpret_cast<u32x4*>(p0.d + (size_t)s * p0.d_stride +
+                                            (size_t)(I + i) * row_bytes);
+    // One row at a time, straight from the load registers to the slot and
+    // the dot product: 256 copy waves with 4 KiB each in flight keep the
+    // host link busy, and the registers stay within the w13 blocks' budget.
+    float dot[2];
 #pragma unroll
-  for (int r = 0; r < RW; ++r) {
-    const int i = min(i0 + r, I - 1);
+    for (int r = 0; r < 2; ++r) {
+      const u32x4* src = r ? src_u : src_g;
+      u32x4* dst = r ? dst_u : dst_g;
+      u32x4 w[CH];
 #pragma unroll
-    for (int c = 0; c < CH; ++c) {
-      const int ch = c * 64 + lane;
-      if (FULL || ch < nch) {
-        wg[r][c] = ld16_stream(W + (size_t)i * H + (size_t)ch * V);
-        wu[r][c] = ld16_stream(W + (size_t)(I + i) * H + (size_t)ch * V);
-      } else {
-        wg[r][c] = make_uint4(0, 0, 0, 0);
-        wu[r][c] = make_uint4(0, 0, 0, 0);
+      for (int c = 0; c < CH; ++c) {
+        const int ch = c * 64 + lane;
+        w[c] = (FULL || ch < nch) ? src[ch] : u32x4{0u, 0u, 0u, 0u};
       }
-    }
-  }
-  float ag[RW], au[RW];
 #pragma unroll
-  for (int r = 0; r < RW; ++r) { ag[r] = 0.f; au[r] = 0.f; }
-#pragma unroll
-  for (int c = 0; c < CH; ++c) {
-    float xf[V];
-    Vec<T>::unpack(xv[c], xf);
-#pragma unroll
-    for (int r = 0; r < RW; ++r) {
-      float gf[V], uf[V];
-      Vec<T>::unpack(wg[r][c], gf);
-      Vec<T>::unpack(wu[r][c], uf);
-#pragma unroll
-      for (int q = 0; q < V; ++q) {
-        ag[r] = fmaf(gf[q], xf[q], ag[r]);
-        au[r] = fmaf(uf[q], xf[q], au[r]);
+      for (int c = 0; c < CH; ++c) {
+        const int ch = c * 64 + lane;
+        if (FULL || ch < nch) __builtin_nontemporal_store(w[c], dst + ch);
       }
+      dot[r] = pair >= 0 ? row_dot<T, CH>(w, xv) : 0.f;
+    }
+    if (pair >= 0 && lane == 0) store_elem((T*)f.act + (size_t)pair * I + i, silu(dot[0]) * dot[1]);
+  }
+  // the rest of each loaded expert: plane 0 past its w13 rows, other planes
+  const size_t w13_bytes = 2 * (size_t)I * row_bytes;
+  for (int j = 0; j < n; ++j) {
+    const int ej = a.loads[2 * j], sj = a.loads[2 * j + 1];
+    if (ej < 0 || ej >= a.num_experts || sj < 0 || sj >= a.cap) continue;
+    copy_range(p0.m + (size_t)ej * p0.m_stride + w13_bytes,
+               p0.d + (size_t)sj * p0.d_stride + w13_bytes, p0.bytes - w13_bytes, blockIdx.x,
+               kPageInBlocks);
+    for (int q = 1; q < a.nplanes; ++q) {
+      const PageInPlane& pl = a.p[q];
+      copy_range(pl.m + (size_t)ej * pl.m_stride, pl.d + (size_t)sj * pl.d_stride, pl.bytes,
+                 blockIdx.x, kPageInBlocks);
     }
   }
-#pragma unroll
-  for (int r = 0; r < RW; ++r) {
-    for (int off = 32; off > 0; off >>= 1) {
-      ag[r] += __shfl_xor(ag[r], off);
-      au[r] += __shfl_xor(au[r], off);
-    }
-  }
-#pragma unroll
-  for (int r = 0; r < RW; ++r)
-    if (lane == r && i0 + r < I) store_elem(arow + i0 + r, silu(ag[r]) * au[r]);
 }
 
 // ---------------------------------------------------------------------------
 // Kernel B: out[t, h] = sum_k w[t,k] * dot(W2[s_k][h, :], act[t,k,:]).
 // Block = K waves, wave k computes the dot products of expert k for the
-// 64/LPR rows of this block (LPR lanes per row, CH chunks per lane, or a
-// runtime chunk loop when CH == 0); the partials meet in LDS and one lane
-// per row sums them in routing order, with the routing weights staged in
-// LDS by the waves at the start (0 for an absent slot).
-// grid = (ceil(H / (64 / LPR)), T).
+// (64/LPR)*RPH rows of this block: LPR lanes per row group, each group RPH
+// consecutive rows, CH chunks per lane (or a runtime chunk loop when
+// CH == 0).  A group loads its act chunks once for its RPH rows.  The
+// partials meet in LDS and one lane per row sums them in routing order, with
+// the routing weights staged in LDS by the waves at the start (0 for an
+// absent slot).  grid = (ceil(H / ((64 / LPR) * RPH)), T).
+//
+// Each row's arithmetic (chunk order, then the butterfly over the LPR lanes,
+// then the k-ordered sum) does not depend on RPH, so the row grouping is a
+// launch-shape choice only.  Measured on MI355X inside the Qwen3 bs=1 decode
+// step (dispatch events, the kernel following the w13 kernel): one row per
+// half-wave 5.89 us, two rows 5.78 us; non-temporal weight loads made both
+// slower (6.36 and 6.33 us), unlike in the w13 kernel, whose waves read whole
+// rows.  A pure read of the same 25 MB in this launch shape takes 5.1-5.3 us.
 // ---------------------------------------------------------------------------
 constexpr int kMaxKw2 = kGemvMaxTopK;
 
-template <typename T, int LPR, int CH, bool FULL>
+template <typename T, int LPR, int CH, int RPH, bool FULL>
 __global__ __launch_bounds__(1024) void w2_combine_kernel(const T* __restrict__ act, int H, int I,
                                                            int K, const float* __restrict__ topk_w,
                                                            const int32_t* __restrict__ slots,
@@ -161,59 +326,76 @@ __global__ __launch_bounds__(1024) void w2_combine_kernel(const T* __restrict__ 
                                                            T* __restrict__ out,
                                                            const int32_t* __restrict__ skip_if) {
   constexpr int V = Vec<T>::N;
-  constexpr int RPW = 64 / LPR;
-  __shared__ float part[kMaxKw2][RPW];
+  constexpr int RPB = 64 / LPR * RPH;  // rows per block
+  __shared__ float part[kMaxKw2][RPB];
   __shared__ float wk[kMaxKw2];
   if (skip_if && *skip_if != 0) return;
   const int k = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int sub = lane / LPR, l = lane % LPR;
   const int t = blockIdx.y;
-  const int h = blockIdx.x * RPW + sub;
+  const int h0 = blockIdx.x * RPB + sub * RPH;
   const int s = slots[t * K + k];
   if (lane == 0) wk[k] = s >= 0 ? topk_w[t * K + k] : 0.f;
   const int nch = I / V;
-  float d = 0.f;
-  if (s >= 0 && h < H) {
-    const T* wrow = w2 + (size_t)s * w2_stride + (size_t)h * I;
+  float d[RPH];
+#pragma unroll
+  for (int r = 0; r < RPH; ++r) d[r] = 0.f;
+  if (s >= 0 && h0 < H) {
+    const T* wbase = w2 + (size_t)s * w2_stride;
     const T* arow = act + ((size_t)t * K + k) * I;
     if (CH > 0) {
-      uint4 wv[CH > 0 ? CH : 1], av[CH > 0 ? CH : 1];
+      uint4 wv[RPH][CH > 0 ? CH : 1], av[CH > 0 ? CH : 1];
 #pragma unroll
-      for (int c = 0; c < CH; ++c) {
-        const int ch = c * LPR + l;
-        if (FULL || ch < nch) {
-          wv[c] = ld16(wrow + (size_t)ch * V);
-          av[c] = ld16(arow + (size_t)ch * V);
-        } else {
-          wv[c] = make_uint4(0, 0, 0, 0);
-          av[c] = make_uint4(0, 0, 0, 0);
+      for (int r = 0; r < RPH; ++r) {
+        const T* wrow = wbase + (size_t)min(h0 + r, H - 1) * I;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+          const int ch = c * LPR + l;
+          wv[r][c] = (FULL || ch < nch) ? ld16(wrow + (size_t)ch * V) : make_uint4(0, 0, 0, 0);
         }
       }
 #pragma unroll
       for (int c = 0; c < CH; ++c) {
-        float wf[V], af[V];
-        Vec<T>::unpack(wv[c], wf);
-        Vec<T>::unpack(av[c], af);
+        const int ch = c * LPR + l;
+        av[c] = (FULL || ch < nch) ? ld16(arow + (size_t)ch * V) : make_uint4(0, 0, 0, 0);
+      }
 #pragma unroll
-        for (int q = 0; q < V; ++q) d = fmaf(wf[q], af[q], d);
+      for (int r = 0; r < RPH; ++r) {
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+          float wf[V], af[V];
+          Vec<T>::unpack(wv[r][c], wf);
+          Vec<T>::unpack(av[c], af);
+#pragma unroll
+          for (int q = 0; q < V; ++q) d[r] = fmaf(wf[q], af[q], d[r]);
+        }
       }
     } else {
-#pragma unroll 4
-      for (int ch = l; ch < nch; ch += LPR) {
-        float wf[V], af[V];
-        Vec<T>::unpack(ld16(wrow + (size_t)ch * V), wf);
-        Vec<T>::unpack(ld16(arow + (size_t)ch * V), af);
 #pragma unroll
-        for (int q = 0; q < V; ++q) d = fmaf(wf[q], af[q], d);
+      for (int r = 0; r < RPH; ++r) {
+        const T* wrow = wbase + (size_t)min(h0 + r, H - 1) * I;
+#pragma unroll 4
+        for (int ch = l; ch < nch; ch += LPR) {
+          float wf[V], af[V];
+          Vec<T>::unpack(ld16(wrow + (size_t)ch * V), wf);
+          Vec<T>::unpack(ld16(arow + (size_t)ch * V), af);
+#pragma unroll
+          for (int q = 0; q < V; ++q) d[r] = fmaf(wf[q], af[q], d[r]);
+        }
       }
     }
   }
-  for (int off = LPR / 2; off > 0; off >>= 1) d += __shfl_xor(d, off);
-  if (l == 0) part[k][sub] = d;
+#pragma unroll
+  for (int r = 0; r < RPH; ++r)
+    for (int off = LPR / 2; off > 0; off >>= 1) d[r] += __shfl_xor(d[r], off);
+  if (l == 0) {
+#pragma unroll
+    for (int r = 0; r < RPH; ++r) part[k][sub * RPH + r] = d[r];
+  }
   __syncthreads();
-  if (threadIdx.x < RPW) {
+  if (threadIdx.x < RPB) {
     const int r = threadIdx.x;
-    const int hh = blockIdx.x * RPW + r;
+    const int hh = blockIdx.x * RPB + r;
     if (hh < H) {
       float acc = 0.f;
       for (int kk = 0; kk < K; ++kk) acc = fmaf(wk[kk], part[kk][r], acc);
@@ -235,44 +417,74 @@ struct LaunchCtl {
 template <typename T, int CH>
 void launch_w13(const T* x, int T_, int H, int I, int K, const int32_t* slots, const T* w13,
                 size_t w13_stride, T* act, hipStream_t st, const LaunchCtl& c) {
-  constexpr int RW = 1;
-  dim3 grid((I + 4 * RW - 1) / (4 * RW), T_ * K);
+  dim3 grid((I + 3) / 4, T_ * K);
   if (H == CH * 64 * Vec<T>::N)
-    launch_timed(w13_silu_kernel<T, CH, RW, true>, grid, dim3(256), st, c.start, c.stop, x, H, I,
-                 K, slots, w13, w13_stride, act, c.pair_filter, c.want);
+    launch_timed(w13_silu_kernel<T, CH, true>, grid, dim3(256), st, c.start, c.stop, x, H, I, K,
+                 slots, w13, w13_stride, act, c.pair_filter, c.want);
   else
-    launch_timed(w13_silu_kernel<T, CH, RW, false>, grid, dim3(256), st, c.start, c.stop, x, H, I,
-                 K, slots, w13, w13_stride, act, c.pair_filter, c.want);
+    launch_timed(w13_silu_kernel<T, CH, false>, grid, dim3(256), st, c.start, c.stop, x, H, I, K,
+                 slots, w13, w13_stride, act, c.pair_filter, c.want);
+}
+
+template <typename T, int CH>
+void launch_pagein_w13(const PageInArgs& a, const FusedW13Args& f, hipStream_t st,
+                       hipEvent_t ev_start, hipEvent_t ev_stop) {
+  const dim3 grid(kPageInBlocks + (f.I + 3) / 4 * f.K);
+  if (f.H == CH * 64 * Vec<T>::N)
+    launch_timed(pagein_w13_kernel<T, CH, true>, grid, dim3(256), st, ev_start, ev_stop, a, f);
+  else
+    launch_timed(pagein_w13_kernel<T, CH, false>, grid, dim3(256), st, ev_start, ev_stop, a, f);
+}
+
+// The per-lane chunk count of the w13 kernels for a row of H elements (0 when
+// a row is longer than 8 chunks per lane).
+template <typename T>
+int w13_chunks(int H) {
+  const int ch = (H / Vec<T>::N + 63) / 64;
+  return ch <= 4 ? ch : ch <= 6 ? 6 : ch <= 8 ? 8 : 0;
 }
 
 template <typename T>
 int dispatch_w13(const T* x, int T_, int H, int I, int K, const int32_t* slots, const T* w13,
                  size_t w13_stride, T* act, hipStream_t st, const LaunchCtl& c) {
-  const int nch = H / Vec<T>::N;
-  const int ch = (nch + 63) / 64;
-  switch (ch) {
+  switch (w13_chunks<T>(H)) {
     case 1: launch_w13<T, 1>(x, T_, H, I, K, slots, w13, w13_stride, act, st, c); break;
     case 2: launch_w13<T, 2>(x, T_, H, I, K, slots, w13, w13_stride, act, st, c); break;
     case 3: launch_w13<T, 3>(x, T_, H, I, K, slots, w13, w13_stride, act, st, c); break;
     case 4: launch_w13<T, 4>(x, T_, H, I, K, slots, w13, w13_stride, act, st, c); break;
-    case 5: case 6: launch_w13<T, 6>(x, T_, H, I, K, slots, w13, w13_stride, act, st, c); break;
-    case 7: case 8: launch_w13<T, 8>(x, T_, H, I, K, slots, w13, w13_stride, act, st, c); break;
+    case 6: launch_w13<T, 6>(x, T_, H, I, K, slots, w13, w13_stride, act, st, c); break;
+    case 8: launch_w13<T, 8>(x, T_, H, I, K, slots, w13, w13_stride, act, st, c); break;
     default: return WISP_ERR_UNSUPPORTED;
   }
   return WISP_OK;
 }
 
-template <typename T, int LPR, int CH>
+template <typename T>
+int dispatch_pagein_w13(const PageInArgs& a, const FusedW13Args& f, hipStream_t st,
+                        hipEvent_t ev_start, hipEvent_t ev_stop) {
+  switch (w13_chunks<T>(f.H)) {
+    case 1: launch_pagein_w13<T, 1>(a, f, st, ev_start, ev_stop); break;
+    case 2: launch_pagein_w13<T, 2>(a, f, st, ev_start, ev_stop); break;
+    case 3: launch_pagein_w13<T, 3>(a, f, st, ev_start, ev_stop); break;
+    case 4: launch_pagein_w13<T, 4>(a, f, st, ev_start, ev_stop); break;
+    case 6: launch_pagein_w13<T, 6>(a, f, st, ev_start, ev_stop); break;
+    case 8: launch_pagein_w13<T, 8>(a, f, st, ev_start, ev_stop); break;
+    default: return WISP_ERR_UNSUPPORTED;
+  }
+  return WISP_OK;
+}
+
+template <typename T, int LPR, int CH, int RPH = 1>
 void launch_w2(const T* act, int T_, int H, int I, int K, const float* w, const int32_t* slots,
                const T* w2, size_t w2_stride, T* out, hipStream_t st, const LaunchCtl& c) {
-  constexpr int RPW = 64 / LPR;
-  dim3 grid((H + RPW - 1) / RPW, T_);
+  constexpr int RPB = 64 / LPR * RPH;
+  dim3 grid((H + RPB - 1) / RPB, T_);
   if (CH > 0 && I == CH * LPR * Vec<T>::N)
-    launch_timed(w2_combine_kernel<T, LPR, CH, true>, grid, dim3(64 * K), st, c.start, c.stop, act,
-                 H, I, K, w, slots, w2, w2_stride, out, c.skip_if);
+    launch_timed(w2_combine_kernel<T, LPR, CH, RPH, true>, grid, dim3(64 * K), st, c.start,
+                 c.stop, act, H, I, K, w, slots, w2, w2_stride, out, c.skip_if);
   else
-    launch_timed(w2_combine_kernel<T, LPR, CH, false>, grid, dim3(64 * K), st, c.start, c.stop,
-                 act, H, I, K, w, slots, w2, w2_stride, out, c.skip_if);
+    launch_timed(w2_combine_kernel<T, LPR, CH, RPH, false>, grid, dim3(64 * K), st, c.start,
+                 c.stop, act, H, I, K, w, slots, w2, w2_stride, out, c.skip_if);
 }
 
 template <typename T>
@@ -280,12 +492,12 @@ int dispatch_w2(const T* act, int T_, int H, int I, int K, const float* w, const
                 const T* w2, size_t w2_stride, T* out, hipStream_t st, const LaunchCtl& c) {
   if (K > kMaxKw2) return WISP_ERR_UNSUPPORTED;
   const int nch = I / Vec<T>::N;
-  if (nch <= 32 * 4) {  // half a wave per row, up to 4 chunks per lane
+  if (nch <= 32 * 4) {  // half a wave per row group of two rows, up to 4 chunks per lane
     switch ((nch + 31) / 32) {
-      case 1: launch_w2<T, 32, 1>(act, T_, H, I, K, w, slots, w2, w2_stride, out, st, c); break;
-      case 2: launch_w2<T, 32, 2>(act, T_, H, I, K, w, slots, w2, w2_stride, out, st, c); break;
-      case 3: launch_w2<T, 32, 3>(act, T_, H, I, K, w, slots, w2, w2_stride, out, st, c); break;
-      default: launch_w2<T, 32, 4>(act, T_, H, I, K, w, slots, w2, w2_stride, out, st, c); break;
+      case 1: launch_w2<T, 32, 1, 2>(act, T_, H, I, K, w, slots, w2, w2_stride, out, st, c); break;
+      case 2: launch_w2<T, 32, 2, 2>(act, T_, H, I, K, w, slots, w2, w2_stride, out, st, c); break;
+      case 3: launch_w2<T, 32, 3, 2>(act, T_, H, I, K, w, slots, w2, w2_stride, out, st, c); break;
+      default: launch_w2<T, 32, 4, 2>(act, T_, H, I, K, w, slots, w2, w2_stride, out, st, c); break;
     }
   } else {
     launch_w2<T, 64, 0>(act, T_, H, I, K, w, slots, w2, w2_stride, out, st, c);
@@ -302,6 +514,28 @@ bool gemv_supported(int dtype, int H, int K) {
   const int V = dtype == WISP_F32 ? 4 : 8;
   const int ch = (H / V + 63) / 64;
   return K >= 1 && K <= kMaxKw2 && ch >= 1 && ch <= 8;
+}
+
+// The fused page-in + w13 launch (Kernel A'): `a` as for the copy kernel,
+// with a.count the pager's flags word; plane 0 of `a` must start with the
+// expert's w13 rows.
+int pagein_w13(const PageInArgs& a, const void* x, int dtype, int T_, int H, int I, int K,
+               const int32_t* flags, const void* w13, size_t w13_stride, void* act,
+               hipStream_t st, hipEvent_t ev_start, hipEvent_t ev_stop) {
+  if (T_ != 1) {
+    wisp_set_last_error("the fused page-in + w13 launch serves one-token calls",
+                        "page-in + w13 kernel");
+    return WISP_ERR_INVALID;
+  }
+  FusedW13Args f{x, H, I, K, flags + 1, w13, w13_stride, act};
+  const int rc = dtype == WISP_F32 ? dispatch_pagein_w13<float>(a, f, st, ev_start, ev_stop)
+                                   : dispatch_pagein_w13<uint16_t>(a, f, st, ev_start, ev_stop);
+  if (rc != WISP_OK) {
+    wisp_set_last_error("hidden size outside the GEMV kernels' coverage", "page-in + w13 kernel");
+    return rc;
+  }
+  WISP_HIP_TRY(hipGetLastError());
+  return WISP_OK;
 }
 
 int gemv_w13(const void* x, int dtype, int T_, int H, int I, int K, const int32_t* slots,

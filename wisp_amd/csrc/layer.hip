@@ -66,6 +66,9 @@ int launch_pager(const int32_t* ids, const void* logits, int logits_dtype, int r
 int gemv_w13(const void* x, int dtype, int T, int H, int I, int K, const int32_t* slots,
              const void* w13, size_t w13_stride, void* act, hipStream_t st,
              hipEvent_t ev_start, hipEvent_t ev_stop, const int32_t* pair_filter, int want);
+int pagein_w13(const PageInArgs& a, const void* x, int dtype, int T, int H, int I, int K,
+               const int32_t* flags, const void* w13, size_t w13_stride, void* act,
+               hipStream_t st, hipEvent_t ev_start, hipEvent_t ev_stop);
 int gemv_w2(const void* act, int dtype, int T, int H, int I, int K, const float* topk_w,
             const int32_t* slots, const void* w2, size_t w2_stride, void* out, hipStream_t st,
             hipEvent_t ev_start, hipEvent_t ev_stop, const int32_t* skip_if);
@@ -153,10 +156,12 @@ struct ProfLaunch {
 };
 
 // One copy-kernel launch: dispatch timestamps and the pinned word its first
-// block sets to the number of experts it copied.
+// block sets to the number of experts it copied.  A fused page-in + w13
+// launch that copied nothing is pure w13 work and is timed as such.
 struct PinLaunch {
   hipEvent_t start = nullptr, stop = nullptr;
   bool pending = false;
+  bool fused = false;
 };
 
 struct Layer {
@@ -168,10 +173,16 @@ struct Layer {
   size_t expert_bytes = 0;  // weight (and scale) bytes of one expert
   // kernel page-in (engine WISP_PAGEIN_KERNEL and eligible masters)
   bool kpin = false;
+  // the fused page-in + w13 launch applies (plane 0 starts with the whole
+  // w13 of an expert, in master and scratch alike)
+  bool fused_ok = false;
   int32_t* hist = nullptr;        // pinned host [kPinRing]
   int32_t* hist_dev = nullptr;
   int pin_next = 0;
   PinLaunch pin[kPinRing];
+  // where the last layer call's decision record went: the workspace's device
+  // copy (one-group calls on the copy-kernel engine) or its pinned record
+  bool rec_on_device = false;
   // cross-layer prefetch: copies on copy[0], fenced by events
   hipEvent_t ev_pf_decided = nullptr, ev_pf_done = nullptr;
   bool pf_pending = false;
@@ -190,6 +201,7 @@ struct Layer {
   ProfLaunch prof[kProfRing];
   double prof_ms[2] = {0, 0};
   int64_t prof_calls = 0;
+  int64_t prof_w13_calls = 0;  // calls whose w13 time is in prof_ms[0]
 };
 
 void prof_harvest(Layer& L, ProfLaunch& p) {
@@ -311,6 +323,9 @@ void harvest_pin(Layer& L, int i) {
     if (n > 0) {
       L.pin_ms_total += ms;
       L.pin_bytes_total += (double)n * (double)L.expert_bytes;
+    } else if (p.fused) {
+      L.prof_ms[0] += ms;
+      L.prof_w13_calls += 1;
     }
   }
   p.pending = false;
@@ -325,14 +340,25 @@ int wait_prefetch(Layer& L, hipStream_t st) {
   return WISP_OK;
 }
 
+// The w13 half of a fused page-in + w13 launch (one-token GEMV calls).
+struct FusedW13 {
+  const void* x;
+  int T, K;
+  const int32_t* flags;
+  void* act;
+};
+
 // Copy-kernel page-in on `st` of the (expert, slot) pairs at `loads` (device
 // memory); their number is *count (device) when count is non-null, else n.
-int page_in_kernel(Layer& L, const int32_t* loads, const int32_t* count, int n, hipStream_t st) {
+// With `fw`, the same launch also runs the call's w13 stage (Kernel A').
+int page_in_kernel(Layer& L, const int32_t* loads, const int32_t* count, int n, hipStream_t st,
+                   const FusedW13* fw = nullptr) {
   const wisp_layer_desc& d = L.d;
   const int i = L.pin_next;
   L.pin_next = (L.pin_next + 1) % kPinRing;
   harvest_pin(L, i);
   PinLaunch& p = L.pin[i];
+  p.fused = fw != nullptr;
   PageInArgs a;
   a.loads = loads;
   a.count = count;
@@ -344,12 +370,31 @@ int page_in_kernel(Layer& L, const int32_t* loads, const int32_t* count, int n, 
     const Plane& pl = L.planes[q];
     a.p[q] = {pl.dev, pl.m_stride, pl.d, pl.d_stride, pl.bytes};
   }
-  a.hist = L.hist_dev + i;
-  // dispatch-timestamp events only while timing is on: each timed launch
-  // costs the stream ~4.5 us (measured at the Qwen3 bs=1 decode step)
-  int rc = launch_pagein(a, st, L.profile ? p.start : nullptr, L.profile ? p.stop : nullptr);
+  // The pinned word that tells the timing how many experts a launch copied
+  // is written (with a system-scope fence, a host-link round trip inside the
+  // kernel) only while timing is on, like the dispatch-timestamp events: each
+  // timed launch costs the stream ~4.5 us (measured at the Qwen3 bs=1 decode
+  // step).
+  a.hist = L.profile ? L.hist_dev + i : nullptr;
+  int rc = fw ? pagein_w13(a, fw->x, d.dtype, fw->T, d.hidden, d.inter, fw->K, fw->flags,
+                           d.scratch_w13, d.scratch_w13_stride, fw->act, st,
+                           L.profile ? p.start : nullptr, L.profile ? p.stop : nullptr)
+              : launch_pagein(a, st, L.profile ? p.start : nullptr, L.profile ? p.stop : nullptr);
   if (rc == WISP_OK && L.profile) p.pending = true;
   return rc;
+}
+
+// Whether the fused page-in + w13 launch can serve this layer: a bf16 or
+// fp32 layer whose first page-in plane begins with the expert's w13 rows in
+// both the master and the scratch.
+void set_fused_ok(Layer& L) {
+  const wisp_layer_desc& d = L.d;
+  const Plane& p0 = L.planes[0];
+  const size_t w13_bytes = d.w13_elems * L.es;
+  L.fused_ok = L.kpin && !L.fp8 && L.nplanes >= 1 && p0.host == (const char*)d.master_w13 &&
+               p0.d == (char*)d.scratch_w13 && p0.bytes >= w13_bytes &&
+               p0.m_stride == d.master_w13_stride * L.es &&
+               p0.d_stride == d.scratch_w13_stride * L.es;
 }
 
 // Enables the copy kernel when every master range is pinned, device-mapped
@@ -391,6 +436,7 @@ void setup_kernel_pagein(Layer& L) {
   L.hist_dev = (int32_t*)hd;
   for (int q = 0; q < L.nplanes; ++q) L.planes[q].dev = dev[q];
   L.kpin = true;
+  set_fused_ok(L);
 }
 
 // Page-in of `n` pairs.  On the caller's stream the copies simply follow
@@ -434,6 +480,9 @@ int w13(Layer& L, const void* x, int T, int K, const int32_t* slots, void* act, 
         const int32_t* filter, int want) {
   const wisp_layer_desc& d = L.d;
   ProfLaunch* p = prof_begin(L, 0);
+  // a call's w13 may take two launches (pairs that hit, then loaded pairs);
+  // the first of them counts the call
+  if (p && !(filter && want == 1)) L.prof_w13_calls += 1;
   int rc = gemv_w13(x, d.dtype, T, d.hidden, d.inter, K, slots, d.scratch_w13,
                     d.scratch_w13_stride, act, st, p ? p->start : nullptr,
                     p ? p->stop : nullptr, filter, want);
@@ -460,6 +509,7 @@ int experts(Layer& L, const void* x, int T, int K, const float* w, const int32_t
   if (L.fp8) {
     ProfLaunch* p13 = prof_begin(L, 0);
     ProfLaunch* p2 = prof_begin(L, 1);
+    if (p13 && p2) L.prof_w13_calls += 1;
     StageEvents ev = {{p13 ? p13->start : nullptr, p13 ? p13->stop : nullptr,
                        p2 ? p2->start : nullptr, p2 ? p2->stop : nullptr}};
     const StageEvents* pe = (p13 && p2) ? &ev : nullptr;
@@ -479,6 +529,7 @@ int experts(Layer& L, const void* x, int T, int K, const float* w, const int32_t
   if (algo == WISP_ALGO_MFMA) {
     ProfLaunch* p13 = prof_begin(L, 0);
     ProfLaunch* p2 = prof_begin(L, 1);
+    if (p13 && p2) L.prof_w13_calls += 1;
     StageEvents ev = {{p13 ? p13->start : nullptr, p13 ? p13->stop : nullptr,
                        p2 ? p2->start : nullptr, p2 ? p2->stop : nullptr}};
     int rc = experts_mfma(x, T, d.hidden, d.inter, K, w, slots, d.cap, d.scratch_w13,
@@ -706,6 +757,7 @@ extern "C" int wisp_layer_set_scratch(void* handle, void* scratch_w13, void* scr
   L->d.cap = cap;
   L->d.slot_to_expert = slot_to_expert;
   L->d.lru_tick = lru_tick;
+  set_fused_ok(*L);
   return WISP_OK;
 }
 
@@ -756,6 +808,7 @@ extern "C" int wisp_layer_forward(void* handle, const void* x, const void* logit
   }
   if (L->profile) L->prof_calls += 1;
 
+  L->rec_on_device = false;
   if (d.mode == WISP_MODE_RESIDENT) {
     rc = wisp_route_topk_softmax(logits, logits_dtype, T, d.num_experts, K, renormalize,
                                  ws->topk_w, ws->topk_ids, d.counters + kForward, stream);
@@ -769,19 +822,32 @@ extern "C" int wisp_layer_forward(void* handle, const void* x, const void* logit
                                  ws->topk_w, ws->topk_ids, nullptr, stream);
     if (rc != WISP_OK) return rc;
   }
-  int32_t* rec_dev = record_device_ptr(ws->record);
+  // One group is certain when every routed pair could be distinct and still
+  // fit (the ids come from the router, so they are in range and the pager
+  // cannot fail): then the rest of the call goes in right behind the pager.
+  // On the copy-kernel engine such a call never reads its decision record on
+  // the host, so the pager writes it to device memory (stores to pinned host
+  // memory would hold the kernel's end for a host-link round trip);
+  // wisp_layer_sync_record brings it to the pinned record on demand.
+  const bool one_group = T > 0 && (int64_t)T * K <= d.cap;
+  const bool rec_dev_only = one_group && L->kpin && ws->record_dev;
+  int32_t* rec_dev = rec_dev_only ? ws->record_dev : record_device_ptr(ws->record);
+  L->rec_on_device = rec_dev_only;
   rc = launch_pager(ws->topk_ids, fuse_route ? logits : nullptr, logits_dtype, renormalize,
                     ws->topk_w, ws->topk_ids, T, K, d.num_experts, d.cap, 0, d.expert_map,
                     d.slot_to_expert, d.lru_tick, d.counters, ws->slots, ws->flags, ws->loads,
                     rec_dev, ws->record_words, st);
   if (rc != WISP_OK) return rc;
 
-  // One group is certain when every routed pair could be distinct and still
-  // fit (the ids come from the router, so they are in range and the pager
-  // cannot fail): then the rest of the call goes in right behind the pager.
   rc = wait_prefetch(*L, st);
   if (rc != WISP_OK) return rc;
-  const bool one_group = T > 0 && (int64_t)T * K <= d.cap;
+  if (T == 1 && one_group && L->kpin && a == WISP_ALGO_GEMV && L->fused_ok) {
+    // [route+pager] [page-in + w13] [w2]
+    const FusedW13 fw{x, T, K, ws->flags, ws->act};
+    rc = page_in_kernel(*L, ws->loads, ws->flags, 0, st, &fw);
+    if (rc != WISP_OK) return rc;
+    return w2(*L, ws->act, T, K, ws->topk_w, ws->slots, out, st, nullptr, nullptr);
+  }
   if (one_group && L->kpin) {
     rc = page_in_kernel(*L, ws->loads, ws->flags, 0, st);
     if (rc != WISP_OK) return rc;
@@ -838,6 +904,7 @@ extern "C" int wisp_layer_ensure_resident(void* handle, const int32_t* ids, int 
     return WISP_ERR_INVALID;
   hipStream_t st = (hipStream_t)stream;
   const wisp_layer_desc& d = L->d;
+  L->rec_on_device = false;
   int rc = launch_pager(ids, nullptr, WISP_F32, 0, nullptr, nullptr, n, 1, d.num_experts, d.cap,
                         1, d.expert_map, d.slot_to_expert, d.lru_tick, d.counters, nullptr,
                         nullptr, nullptr, record_device_ptr(ws->record), ws->record_words, st);
@@ -941,6 +1008,19 @@ extern "C" int wisp_layer_prefetch(void* handle, const int32_t* predicted,
   return WISP_OK;
 }
 
+extern "C" int wisp_layer_sync_record(void* handle, const wisp_workspace* ws) {
+  using namespace wisp;
+  Layer* L = (Layer*)handle;
+  if (!L || !ws || !ws->record || ws->record_words < 8) return WISP_ERR_INVALID;
+  WISP_HIP_TRY(hipDeviceSynchronize());
+  if (L->rec_on_device) {
+    if (!ws->record_dev) return WISP_ERR_INVALID;
+    WISP_HIP_TRY(hipMemcpy(ws->record, ws->record_dev, (size_t)ws->record_words * sizeof(int32_t),
+                           hipMemcpyDeviceToHost));
+  }
+  return WISP_OK;
+}
+
 extern "C" int wisp_layer_pagein_engine(void* handle) {
   Layer* L = (Layer*)handle;
   if (!L) return -1;
@@ -948,15 +1028,18 @@ extern "C" int wisp_layer_pagein_engine(void* handle) {
 }
 
 extern "C" int wisp_layer_profile(void* handle, int enable, double* w13_ms, double* w2_ms,
-                                  int64_t* calls) {
+                                  int64_t* calls, int64_t* w13_calls) {
   Layer* L = (Layer*)handle;
   if (!L) return WISP_ERR_INVALID;
   for (int i = 0; i < wisp::kProfRing; ++i) wisp::prof_harvest(*L, L->prof[i]);
+  for (int i = 0; i < wisp::kPinRing; ++i) wisp::harvest_pin(*L, i);
   if (w13_ms) *w13_ms = L->prof_ms[0];
   if (w2_ms) *w2_ms = L->prof_ms[1];
   if (calls) *calls = L->prof_calls;
+  if (w13_calls) *w13_calls = L->prof_w13_calls;
   L->prof_ms[0] = L->prof_ms[1] = 0;
   L->prof_calls = 0;
+  L->prof_w13_calls = 0;
   L->profile = enable != 0;
   return WISP_OK;
 }

@@ -17,33 +17,6 @@
 namespace wisp {
 namespace {
 
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-
-constexpr int kUnroll = 4;
-
-// Copies `bytes` (a multiple of 16) from src to dst, spread over `nblocks`
-// blocks of 256 threads; `blk` is this block's index among them.
-__device__ inline void copy_range(const char* __restrict__ src, char* __restrict__ dst,
-                                  size_t bytes, int blk, int nblocks) {
-  const u32x4* s = reinterpret_cast<const u32x4*>(src);
-  u32x4* d = reinterpret_cast<u32x4*>(dst);
-  const size_t n = bytes >> 4;
-  const size_t step = (size_t)nblocks * 256 * kUnroll;
-  for (size_t base = (size_t)blk * 256 * kUnroll + threadIdx.x; base < n; base += step) {
-    u32x4 v[kUnroll];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const size_t i = base + (size_t)u * 256;
-      if (i < n) v[u] = s[i];
-    }
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const size_t i = base + (size_t)u * 256;
-      if (i < n) __builtin_nontemporal_store(v[u], d + i);
-    }
-  }
-}
-
 __global__ __launch_bounds__(256) void pagein_kernel(PageInArgs a) {
   const int n = a.count ? *a.count : a.n;
   if (a.hist && blockIdx.x == 0 && threadIdx.x == 0) {

@@ -111,6 +111,21 @@ enum RecordHeader : int {
   kRecLoaded = 6,
 };
 
+// Per-pair word of the pager's flags array (flags[1 + p]): the pair's slot in
+// the low 16 bits (0xFFFF: none) and, when the call loaded the pair's expert,
+// that expert id + 1 in bits 16-30 (0 otherwise).  One load gives an expert
+// kernel the slot, whether it was just loaded, and from which master.
+WISP_HD inline int32_t pair_word(int slot, int loaded_expert) {
+  return (int32_t)(((uint32_t)slot & 0xFFFFu) |
+                   (loaded_expert >= 0 ? (uint32_t)(loaded_expert + 1) << 16 : 0u));
+}
+WISP_HD inline int pair_word_slot(int32_t w) {
+  const int s = (int)((uint32_t)w & 0xFFFFu);
+  return s == 0xFFFF ? -1 : s;
+}
+// The expert the call loaded for this pair, or -1.
+WISP_HD inline int pair_word_loaded(int32_t w) { return (int)((uint32_t)w >> 16) - 1; }
+
 // Device- or host-resident pager state for one layer.
 struct PagerView {
   int E, cap;
