@@ -201,17 +201,20 @@ __global__ __launch_bounds__(256) void w13_silu_kernel(const T* __restrict__ x, 
 // after one load; one that loads experts runs the resident pairs' w13 under
 // the copies.
 // ---------------------------------------------------------------------------
+// The w13 blocks' arguments come first in the kernel's argument segment (and
+// the page-in blocks' 200-byte PageInArgs after them), so the blocks that
+// stream weights find theirs at the front.
 struct FusedW13Args {
   const void* x;
-  int H, I, K;
   const int32_t* words;  // the pager's flags + 1: pair_word(slot, loaded expert)
   const void* w13;       // scratch base, slot s at + s * w13_stride elements
   size_t w13_stride;
   void* act;
+  int H, I, K, cap;
 };
 
 template <typename T, int CH, bool FULL>
-__global__ __launch_bounds__(256) void pagein_w13_kernel(PageInArgs a, FusedW13Args f) {
+__global__ __launch_bounds__(256) void pagein_w13_kernel(FusedW13Args f, PageInArgs a) {
   constexpr int V = Vec<T>::N;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int H = f.H, I = f.I, nch = H / V;
@@ -224,7 +227,7 @@ __global__ __launch_bounds__(256) void pagein_w13_kernel(PageInArgs a, FusedW13A
     const int32_t word = f.words[pair];
     if (pair_word_loaded(word) >= 0) return;  // the copy blocks compute it
     const int s = pair_word_slot(word);
-    w13_wave<T, CH, FULL>((const T*)f.x, H, I, f.K, pair, i, s < a.cap ? s : -1,
+    w13_wave<T, CH, FULL>((const T*)f.x, H, I, f.K, pair, i, s < f.cap ? s : -1,
                           (const T*)f.w13, f.w13_stride, (T*)f.act, lane);
     return;
   }
@@ -431,9 +434,9 @@ void launch_pagein_w13(const PageInArgs& a, const FusedW13Args& f, hipStream_t s
                        hipEvent_t ev_start, hipEvent_t ev_stop) {
   const dim3 grid(kPageInBlocks + (f.I + 3) / 4 * f.K);
   if (f.H == CH * 64 * Vec<T>::N)
-    launch_timed(pagein_w13_kernel<T, CH, true>, grid, dim3(256), st, ev_start, ev_stop, a, f);
+    launch_timed(pagein_w13_kernel<T, CH, true>, grid, dim3(256), st, ev_start, ev_stop, f, a);
   else
-    launch_timed(pagein_w13_kernel<T, CH, false>, grid, dim3(256), st, ev_start, ev_stop, a, f);
+    launch_timed(pagein_w13_kernel<T, CH, false>, grid, dim3(256), st, ev_start, ev_stop, f, a);
 }
 
 // The per-lane chunk count of the w13 kernels for a row of H elements (0 when
@@ -527,7 +530,7 @@ int pagein_w13(const PageInArgs& a, const void* x, int dtype, int T_, int H, int
                         "page-in + w13 kernel");
     return WISP_ERR_INVALID;
   }
-  FusedW13Args f{x, H, I, K, flags + 1, w13, w13_stride, act};
+  FusedW13Args f{x, flags + 1, w13, w13_stride, act, H, I, K, a.cap};
   const int rc = dtype == WISP_F32 ? dispatch_pagein_w13<float>(a, f, st, ev_start, ev_stop)
                                    : dispatch_pagein_w13<uint16_t>(a, f, st, ev_start, ev_stop);
   if (rc != WISP_OK) {

@@ -62,7 +62,7 @@ int launch_pager(const int32_t* ids, const void* logits, int logits_dtype, int r
                  float* topk_w, int32_t* topk_ids, int T, int K, int E, int cap,
                  int single_group, int32_t* map, int32_t* s2e, int64_t* tick, int64_t* ctr,
                  int32_t* slots, int32_t* flags, int32_t* loads, int32_t* rec, int rec_words,
-                 hipStream_t stream);
+                 hipStream_t stream, int32_t* rec_host);
 int gemv_w13(const void* x, int dtype, int T, int H, int I, int K, const int32_t* slots,
              const void* w13, size_t w13_stride, void* act, hipStream_t st,
              hipEvent_t ev_start, hipEvent_t ev_stop, const int32_t* pair_filter, int want);
@@ -829,14 +829,16 @@ extern "C" int wisp_layer_forward(void* handle, const void* x, const void* logit
   // the host, so the pager writes it to device memory (stores to pinned host
   // memory would hold the kernel's end for a host-link round trip);
   // wisp_layer_sync_record brings it to the pinned record on demand.
+  // Every other call mirrors the record to the pinned one at the pager's end.
   const bool one_group = T > 0 && (int64_t)T * K <= d.cap;
   const bool rec_dev_only = one_group && L->kpin && ws->record_dev;
-  int32_t* rec_dev = rec_dev_only ? ws->record_dev : record_device_ptr(ws->record);
+  int32_t* rec_dev = ws->record_dev ? ws->record_dev : record_device_ptr(ws->record);
+  int32_t* rec_host = ws->record_dev && !rec_dev_only ? record_device_ptr(ws->record) : nullptr;
   L->rec_on_device = rec_dev_only;
   rc = launch_pager(ws->topk_ids, fuse_route ? logits : nullptr, logits_dtype, renormalize,
                     ws->topk_w, ws->topk_ids, T, K, d.num_experts, d.cap, 0, d.expert_map,
                     d.slot_to_expert, d.lru_tick, d.counters, ws->slots, ws->flags, ws->loads,
-                    rec_dev, ws->record_words, st);
+                    rec_dev, ws->record_words, st, rec_host);
   if (rc != WISP_OK) return rc;
 
   rc = wait_prefetch(*L, st);
@@ -905,9 +907,11 @@ extern "C" int wisp_layer_ensure_resident(void* handle, const int32_t* ids, int 
   hipStream_t st = (hipStream_t)stream;
   const wisp_layer_desc& d = L->d;
   L->rec_on_device = false;
+  int32_t* rec_dev = ws->record_dev ? ws->record_dev : record_device_ptr(ws->record);
+  int32_t* rec_host = ws->record_dev ? record_device_ptr(ws->record) : nullptr;
   int rc = launch_pager(ids, nullptr, WISP_F32, 0, nullptr, nullptr, n, 1, d.num_experts, d.cap,
                         1, d.expert_map, d.slot_to_expert, d.lru_tick, d.counters, nullptr,
-                        nullptr, nullptr, record_device_ptr(ws->record), ws->record_words, st);
+                        nullptr, nullptr, rec_dev, ws->record_words, st, rec_host);
   if (rc != WISP_OK) return rc;
   WISP_HIP_TRY(hipEventRecord(L->ev_decided, st));
   WISP_HIP_TRY(hipEventSynchronize(L->ev_decided));

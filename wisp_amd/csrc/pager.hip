@@ -194,6 +194,7 @@ int pager_decide_host(PagerView st, const int32_t* ids, int T, int K, int single
 namespace {
 
 struct PagerSmem {
+  int32_t lru[kMaxExperts];  // occupied slots in (tick, slot) order
   int32_t map[kMaxExperts];
   int32_t s2e[kMaxExperts];
   int64_t tick[kMaxExperts];
@@ -235,19 +236,25 @@ __device__ inline int set_table_size(int n) {
 // loads (optional): the (expert, slot) pairs loaded, in the record's order;
 // and the decision record.
 //
-// Group planning (greedy first-fit in token order) of calls above
-// kFusedRouteTokens tokens runs on per-token expert bitmasks: each lane
-// builds the W-word mask of one token of a 64-token batch in registers, and
-// the scan over the batch keeps the open group's union in scalar registers
-// (readlane, OR, popcount per token), so a token costs a few scalar
-// instructions instead of LDS atomics and a wave sync.
+// The kernel is one wavefront, so its time is the length of its chain of
+// dependent steps (each LDS round trip, each hand-off between the scalar and
+// the vector unit); it is built to keep that chain short per token group:
+//   * group planning (greedy first-fit in token order) on per-token expert
+//     bitmasks: lane l holds the mask of token b + l and a prefix OR across
+//     the lanes gives every token's group union at once, so a group costs a
+//     few DPP steps instead of a step per token;
+//   * the needed and the missing experts of a group in one pass over E;
+//   * eviction candidates from an LRU list kept in (tick, slot) order across
+//     the groups of a call instead of a sort per group;
+//   * the CPython set order only where collisions can reorder it.
 template <typename TL, int VALS>
 __global__ __launch_bounds__(64) void pager_kernel(
     const int32_t* __restrict__ ids_in, const TL* __restrict__ logits, int renorm,
     float* __restrict__ w_out, int32_t* __restrict__ id_out, int T, int K, int E, int cap,
     int single_group, int32_t* __restrict__ map_g, int32_t* __restrict__ s2e_g,
     int64_t* __restrict__ tick_g, int64_t* __restrict__ ctr_g, int32_t* __restrict__ slots_g,
-    int32_t* __restrict__ flags_g, int32_t* __restrict__ loads_g, int32_t* __restrict__ rec) {
+    int32_t* __restrict__ flags_g, int32_t* __restrict__ loads_g, int32_t* __restrict__ rec,
+    int32_t* __restrict__ rec_host) {
   constexpr int W = 2 * VALS;  // 32-bit mask words per token: E <= 32 * W
   __shared__ PagerSmem sm;
   __shared__ FusedRouteSmem fr;
@@ -288,7 +295,10 @@ __global__ __launch_bounds__(64) void pager_kernel(
     if (flags_g) flags_g[1 + p] = pair_word(-1, -1);
   }
 
-  const int32_t* ids = ids_in;
+  // Routed ids: staged in LDS (read with LDS loads) when the call has at most
+  // kStagedPairs pairs or was routed here, else read from global memory.
+  const bool staged = logits != nullptr || P <= kStagedPairs;
+  auto id_at = [&](int p) -> int { return staged ? fr.ids[p] : ids_in[p]; };
   if (logits) {
     for (int t = 0; t < T; ++t) {
       float w;
@@ -312,22 +322,26 @@ __global__ __launch_bounds__(64) void pager_kernel(
       }
     }
     wave_lds_sync();
-    ids = fr.ids;
-  } else if (P <= kStagedPairs) {
+  } else if (staged) {
     for (int p = lane; p < P; p += 64) fr.ids[p] = ids_in[p];
     wave_lds_sync();
-    ids = fr.ids;
   }
 
   // Validate ids.
   bool bad = false;
-  for (int p = lane; p < P; p += 64) bad |= (ids[p] < 0 || ids[p] >= E);
+  for (int p = lane; p < P; p += 64) bad |= (id_at(p) < 0 || id_at(p) >= E);
   const bool any_bad = ballot(bad) != 0;
   // the planner's masks hold E <= 32 * W experts
   const bool masks_ok = E <= 32 * W;
 
   int status = WISP_OK, groups_done = 0, groups_planned = 0, fail_group = -1, fail_u = 0;
   int ev_total = 0, ld_total = 0;
+  // The LRU list (sm.lru), built from the state the first time a group must
+  // evict, then kept up to date after every group: a group gives the slots
+  // of its needed experts the new clock, larger than every other tick, so
+  // they move to the list's end in slot order and the rest keep their order.
+  // Eviction candidates are then the list filtered, with no sort per group.
+  int nlru = -1;
 
   if (any_bad || (!single_group && !masks_ok)) {
     status = WISP_ERR_INVALID;
@@ -338,60 +352,37 @@ __global__ __launch_bounds__(64) void pager_kernel(
     while (first || start < T) {
       first = false;
       // ---- plan one group: tokens [start, end) -----------------------
-      for (int w = lane; w < nwords; w += 64) sm.loaded[w] = 0u;
       int end = start;
-      if (single_group) {
-        for (int w = lane; w < nwords; w += 64) sm.need[w] = 0u;
+      if (single_group || T == 1) {
+        for (int w = lane; w < nwords; w += 64) {
+          sm.need[w] = 0u;
+          sm.loaded[w] = 0u;
+        }
         wave_lds_sync();
         for (int p = lane; p < P; p += 64) {
-          const int e = ids[p];
+          const int e = id_at(p);
           atomicOr(&sm.need[e >> 5], 1u << (e & 31));
         }
         end = T;
-      }
-      else if (T <= kFusedRouteTokens) {
-        // Few tokens: each one ORs its ids into the need bits (lanes < K)
-        // and counts the new ones with a ballot.  Measured at the Qwen3 bs=1
-        // decode shape this is 0.6 us faster than building token masks.
-        for (int w = lane; w < nwords; w += 64) sm.need[w] = 0u;
-        wave_lds_sync();
-        int cnt = 0;
-        while (end < T) {
-          bool fresh = false;
-          int e = 0;
-          if (lane < K) {
-            e = ids[end * K + lane];
-            const uint32_t old = atomicOr(&sm.need[e >> 5], 1u << (e & 31));
-            fresh = !(old & (1u << (e & 31)));
-          }
-          const int nnew = __popcll(ballot(fresh));
-          if (cnt + nnew <= cap || end == start) {
-            cnt += nnew;
-            ++end;
-          } else {
-            if (fresh) atomicAnd(&sm.need[e >> 5], ~(1u << (e & 31)));
-            break;
-          }
-        }
-      }
-      else {
+      } else {
+        // Greedy first-fit over 64 tokens at once: lane l holds the expert
+        // mask of token b + l, a prefix OR across the lanes gives the union
+        // of the group up to each token, and the first token whose union
+        // exceeds cap (unless it opens the group) ends it.
         uint32_t u[W];
 #pragma unroll
         for (int w = 0; w < W; ++w) u[w] = 0u;
-        bool closed = false;
-        for (int b = start; b < T && !closed; b += 64) {
-          // this lane's token: its expert mask
+        end = -1;
+        for (int b = start; b < T && end < 0; b += 64) {
           uint32_t m[W];
 #pragma unroll
           for (int w = 0; w < W; ++w) m[w] = 0u;
-          const int t = b + lane;
-          if (t < T) {
-            // eight ids per round, loaded before any is used, so their load
-            // latencies overlap
+          const int tl = b + lane;
+          if (tl < T) {
             for (int j0 = 0; j0 < K; j0 += 8) {
               int e8[8];
 #pragma unroll
-              for (int jj = 0; jj < 8; ++jj) e8[jj] = j0 + jj < K ? ids[t * K + j0 + jj] : -1;
+              for (int jj = 0; jj < 8; ++jj) e8[jj] = j0 + jj < K ? id_at(tl * K + j0 + jj) : -1;
 #pragma unroll
               for (int jj = 0; jj < 8; ++jj) {
                 const int e = e8[jj];
@@ -401,80 +392,74 @@ __global__ __launch_bounds__(64) void pager_kernel(
               }
             }
           }
-          const int nb = min(64, T - b);
-          for (int i = 0; i < nb; ++i) {
-            uint32_t v[W];
-            int c = 0;
+          int c = 0;
 #pragma unroll
-            for (int w = 0; w < W; ++w) {
-              v[w] = u[w] | (uint32_t)__builtin_amdgcn_readlane((int)m[w], i);
-              c += __popc(v[w]);
-            }
-            if (c <= cap || b + i == start) {
-#pragma unroll
-              for (int w = 0; w < W; ++w) u[w] = v[w];
-            } else {
-              closed = true;
-              end = b + i;
-              break;
-            }
+          for (int w = 0; w < W; ++w) {
+            m[w] = wave_prefix_or(m[w], lane) | u[w];
+            c += __popc(m[w]);
           }
-          if (!closed) end = b + nb;
+          const uint64_t over = ballot(tl < T && c > cap && tl != start);
+          const int last = over ? __builtin_ctzll(over) - 1 : min(63, T - 1 - b);
+          if (last >= 0) {
+#pragma unroll
+            for (int w = 0; w < W; ++w)
+              u[w] = (uint32_t)__builtin_amdgcn_readlane((int)m[w], last);
+          }
+          if (over) end = b + __builtin_ctzll(over);
         }
+        if (end < 0) end = T;
 #pragma unroll
         for (int w = 0; w < W; ++w)
-          if (lane == w && w < nwords) sm.need[w] = u[w];
+          if (lane == w && w < nwords) {
+            sm.need[w] = u[w];
+            sm.loaded[w] = 0u;
+          }
       }
       wave_lds_sync();
       const int g = groups_planned++;
       const int t0 = start, t1 = end;
       start = end;
 
-      // ---- sorted unique ids of the group ----------------------------
-      int U = 0;
+      // ---- needed experts (ascending) and the missing ones, one pass ----
+      int U = 0, nmiss = 0, kmax = -1;
       for (int base = 0; base < E; base += 64) {
         const int e = base + lane;
-        const bool in = e < E && ((sm.need[e >> 5] >> (e & 31)) & 1u);
-        const uint64_t bb = ballot(in);
+        const uint32_t needw = e < E ? sm.need[e >> 5] : 0u;
+        const int mp = e < E ? sm.map[e] : 0;
+        const bool in = (needw >> (e & 31)) & 1u;
+        const bool miss = in && mp < 0;
+        const uint64_t bb = ballot(in), mb = ballot(miss);
         if (in) sm.keys[U + popc_below(bb)] = e;
+        if (miss) sm.missing[nmiss + popc_below(mb)] = e;
         U += __popcll(bb);
+        nmiss += __popcll(mb);
+        if (bb) kmax = base + 63 - __builtin_clzll(bb);
       }
       wave_lds_sync();
-      // ---- CPython set iteration order of the ascending keys ----------
-      // It only decides which free slot each missing expert takes, so it is
-      // computed when two or more are missing; otherwise any order will do.
-      // When every key is below the set's table size the order is ascending.
-      int nmiss_any = 0;
-      for (int base = 0; base < U; base += 64) {
-        const int j = base + lane;
-        nmiss_any += __popcll(ballot(j < U && sm.map[sm.keys[j]] < 0));
-      }
-      const int32_t* ord = sm.keys;
-      if (nmiss_any >= 2 && U > 0 && sm.keys[U - 1] >= set_table_size(U)) {
+      // ---- the missing experts in CPython set order -------------------
+      // The order only decides which free slot each missing expert takes,
+      // so it matters when two or more are missing.  When every key is below
+      // the set's table size it is ascending, the order found above.
+      if (nmiss >= 2 && kmax >= set_table_size(U)) {
         if (U <= 64) {
           const int key = lane < U ? sm.keys[lane] : -1;
-          const int pos = set_positions_wave(key, U, lane);
+          const int pos = U <= 18 ? set_positions_small(key, U, lane)
+                                  : set_positions_wave(key, U, lane);
           if (lane < U) sm.order[pos] = key;
         } else if (lane == 0) {
           cpython_set_order(sm.keys, U, sm.order, sm.table, kMaxSetTable);
         }
-        ord = sm.order;
         wave_lds_sync();
-      }
-
-      // ---- missing experts, in set order -----------------------------
-      int nmiss = 0;
-      for (int base = 0; base < U; base += 64) {
-        const int j = base + lane;
-        int e = -1;
-        bool m = false;
-        if (j < U) {
-          e = ord[j];
-          m = sm.map[e] < 0;
+        int nm = 0;
+        for (int base = 0; base < U; base += 64) {
+          const int j = base + lane;
+          const int e = j < U ? sm.order[j] : 0;
+          const bool m = j < U && sm.map[e] < 0;
+          const uint64_t mb = ballot(m);
+          if (m) sm.missing[nm + popc_below(mb)] = e;
+          nm += __popcll(mb);
         }
-        const uint64_t mb = ballot(m);
-        if (m) sm.missing[nmiss + popc_below(mb)] = e;
-        nmiss += __popcll(mb);
+        wave_lds_sync();
       }
       const int hits = U - nmiss;
       n_hits += hits;
@@ -511,15 +496,53 @@ __global__ __launch_bounds__(64) void pager_kernel(
           break;
         }
         if (shortfall > 0) {
-          // Stable sort of the candidates by tick (ties keep slot order).
-          for (int i = lane; i < ncand; i += 64) {
-            const int64_t ti = sm.tick[sm.cand[i]];
-            int r = 0;
-            for (int j = 0; j < ncand; ++j) {
-              const int64_t tj = sm.tick[sm.cand[j]];
-              r += (tj < ti) || (tj == ti && j < i);
+          if (nlru < 0) {
+            // occupied slots ranked by (tick, slot): up to 64 slots each
+            // lane holds one tick and the others come by readlane; beyond
+            // that, from LDS
+            nlru = 0;
+            if (cap <= 64) {
+              const bool occ = lane < cap && sm.s2e[lane] >= 0;
+              const int64_t ti = occ ? sm.tick[lane] : 0;
+              const uint32_t tlo = (uint32_t)ti, thi = (uint32_t)((uint64_t)ti >> 32);
+              const uint64_t occ_bits = ballot(occ);
+              int r = 0;
+              for (int j = 0; j < cap; ++j) {
+                if (!((occ_bits >> j) & 1ull)) continue;
+                const uint64_t tj =
+                    ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)thi, j) << 32) |
+                    (uint32_t)__builtin_amdgcn_readlane((int)tlo, j);
+                r += ((int64_t)tj < ti) || ((int64_t)tj == ti && j < lane);
+              }
+              if (occ) sm.lru[r] = lane;
+              nlru = __popcll(occ_bits);
+            } else {
+              for (int s0 = lane; s0 < cap; s0 += 64) {
+                if (sm.s2e[s0] < 0) continue;
+                const int64_t ti = sm.tick[s0];
+                int r = 0;
+                for (int j = 0; j < cap; ++j) {
+                  if (sm.s2e[j] < 0) continue;
+                  const int64_t tj = sm.tick[j];
+                  r += (tj < ti) || (tj == ti && j < s0);
+                }
+                sm.lru[r] = s0;
+              }
+              for (int base = 0; base < cap; base += 64)
+                nlru += __popcll(ballot(base + lane < cap && sm.s2e[base + lane] >= 0));
             }
-            sm.sorted[r] = sm.cand[i];
+            wave_lds_sync();
+          }
+          // candidates in LRU order: the list without the needed experts
+          int nc = 0;
+          for (int base = 0; base < nlru; base += 64) {
+            const int j = base + lane;
+            const int sl = j < nlru ? sm.lru[j] : 0;
+            const int cur = j < nlru ? sm.s2e[sl] : 0;
+            const bool c = j < nlru && !(sm.need[cur >> 5] & (1u << (cur & 31)));
+            const uint64_t cb = ballot(c);
+            if (c) sm.sorted[nc + popc_below(cb)] = sl;
+            nc += __popcll(cb);
           }
           wave_lds_sync();
           for (int r = lane; r < shortfall; r += 64) {
@@ -563,8 +586,34 @@ __global__ __launch_bounds__(64) void pager_kernel(
       }
       for (int j = lane; j < U; j += 64) sm.tick[sm.map[sm.keys[j]]] = clock;
       wave_lds_sync();
+      if (nlru >= 0) {
+        // In place: the list's entries still occupied by an expert the
+        // group did not need, in list order (an entry moves only towards
+        // the front, after every lane has read its own), then the needed
+        // experts' slots ascending.
+        int n2 = 0;
+        for (int base = 0; base < nlru; base += 64) {
+          const int j = base + lane;
+          const int sl = j < nlru ? sm.lru[j] : 0;
+          const int cur = j < nlru ? sm.s2e[sl] : -1;
+          const bool keep = cur >= 0 && !(sm.need[cur >> 5] & (1u << (cur & 31)));
+          const uint64_t kb = ballot(keep);
+          if (keep) sm.lru[n2 + popc_below(kb)] = sl;
+          n2 += __popcll(kb);
+        }
+        for (int base = 0; base < cap; base += 64) {
+          const int sl = base + lane;
+          const int cur = sl < cap ? sm.s2e[sl] : -1;
+          const bool in = cur >= 0 && (sm.need[cur >> 5] & (1u << (cur & 31)));
+          const uint64_t ib = ballot(in);
+          if (in) sm.lru[n2 + popc_below(ib)] = sl;
+          n2 += __popcll(ib);
+        }
+        nlru = n2;
+        wave_lds_sync();
+      }
       for (int p = t0 * K + lane; p < t1 * K; p += 64) {
-        const int e = ids[p];
+        const int e = id_at(p);
         if (slots_g) slots_g[p] = sm.map[e];
         if (flags_g)
           flags_g[1 + p] = pair_word(sm.map[e], (sm.loaded[e >> 5] >> (e & 31)) & 1u ? e : -1);
@@ -595,6 +644,17 @@ __global__ __launch_bounds__(64) void pager_kernel(
     rec[7] = 0;
     rec[kRecStatus] = status;
   }
+  if (rec_host) {
+    // Mirror the words the call wrote into the host's record in a few
+    // coalesced passes, instead of one host-link write per decision.
+    __threadfence();
+    const int nhead = 8 + 8 * groups_planned;
+    for (int w = lane; w < nhead; w += 64) rec_host[w] = rec[w];
+    for (int w = lane; w < 2 * ev_total; w += 64)
+      rec_host[L.evicted_base() + w] = rec[L.evicted_base() + w];
+    for (int w = lane; w < 2 * ld_total; w += 64)
+      rec_host[L.loaded_base() + w] = rec[L.loaded_base() + w];
+  }
 }
 
 }  // namespace
@@ -603,7 +663,7 @@ int launch_pager(const int32_t* ids, const void* logits, int logits_dtype, int r
                  float* topk_w, int32_t* topk_ids, int T, int K, int E, int cap,
                  int single_group, int32_t* map, int32_t* s2e, int64_t* tick, int64_t* ctr,
                  int32_t* slots, int32_t* flags, int32_t* loads, int32_t* rec, int rec_words,
-                 hipStream_t stream) {
+                 hipStream_t stream, int32_t* rec_host) {
   RecordLayout L(T, K);
   if (T < 0 || K < 1 || K > kMaxTopK || E < 1 || E > kMaxExperts || cap < 1 || cap > kMaxExperts ||
       rec_words < L.words() || !map || !s2e || !tick || !ctr || !rec ||
@@ -618,11 +678,13 @@ int launch_pager(const int32_t* ids, const void* logits, int logits_dtype, int r
     if (logits && logits_dtype == WISP_BF16)
       hipLaunchKernelGGL((pager_kernel<uint16_t, V>), dim3(1), dim3(64), 0, stream, ids,
                          (const uint16_t*)logits, renorm, topk_w, topk_ids, T, K, E, cap,
-                         single_group, map, s2e, tick, ctr, slots, flags, loads, rec);
+                         single_group, map, s2e, tick, ctr, slots, flags, loads, rec,
+                         rec_host);
     else
       hipLaunchKernelGGL((pager_kernel<float, V>), dim3(1), dim3(64), 0, stream, ids,
                          (const float*)logits, renorm, topk_w, topk_ids, T, K, E, cap,
-                         single_group, map, s2e, tick, ctr, slots, flags, loads, rec);
+                         single_group, map, s2e, tick, ctr, slots, flags, loads, rec,
+                         rec_host);
   });
   WISP_HIP_TRY(hipGetLastError());
   return WISP_OK;
@@ -637,7 +699,8 @@ extern "C" int wisp_pager_decide(const int32_t* topk_ids, int T, int K, int E, i
                                  int record_words, wisp_stream_t stream) {
   return wisp::launch_pager(topk_ids, nullptr, WISP_F32, 0, nullptr, nullptr, T, K, E, cap,
                             single_group, expert_map, slot_to_expert, lru_tick, counters, slots,
-                            nullptr, nullptr, record, record_words, (hipStream_t)stream);
+                            nullptr, nullptr, record, record_words, (hipStream_t)stream,
+                            nullptr);
 }
 
 extern "C" int wisp_pager_decide_host(const int32_t* topk_ids, int T, int K, int E, int cap,

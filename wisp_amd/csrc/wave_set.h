@@ -14,6 +14,21 @@ __device__ inline int popc_below(uint64_t mask) {
 
 __device__ inline uint64_t ballot(bool p) { return __ballot(p); }
 
+// Inclusive prefix OR across the 64 lanes: OR of v over lanes 0..lane.
+// Four DPP row shifts inside each 16-lane row, then the row totals by
+// readlane.
+__device__ inline uint32_t wave_prefix_or(uint32_t v, int lane) {
+  v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xF, 0xF, false);  // row_shr:1
+  v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xF, 0xF, false);  // row_shr:2
+  v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, false);  // row_shr:4
+  v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xF, 0xF, false);  // row_shr:8
+  const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)v, 15);
+  const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)v, 31);
+  const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)v, 47);
+  const int row = lane >> 4;
+  return v | (row >= 1 ? r0 : 0u) | (row >= 2 ? r1 : 0u) | (row >= 3 ? r2 : 0u);
+}
+
 // Insert `key` into a CPython set table of mask+1 <= 128 slots whose
 // occupancy is the bitmask (lo, hi); returns the slot (same probe sequence as
 // set_insert_clean).  All operands are wave-uniform.
@@ -86,6 +101,62 @@ __device__ int set_positions_wave(int key, int U, int lane) {
   return __popcll(below_lo) + __popcll(below_hi);
 }
 
+// Slot of `key` inserted into a CPython set table of mask+1 <= 32 slots with
+// occupancy `occ` (scalar); marks it occupied.  Same probe sequence as
+// set_insert_clean: slot i, then i+1 .. i+9 when i + 9 <= mask, then the
+// perturbed step.
+__device__ inline int probe_insert32(uint32_t& occ, uint32_t mask, int key) {
+  uint32_t perturb = (uint32_t)key;
+  uint32_t i = (uint32_t)key & mask;
+  for (;;) {
+    const uint32_t win = i + 9 <= mask ? 0x3FFu : 1u;
+    const uint32_t free = ~(occ >> i) & win;
+    if (free) {
+      const uint32_t s = i + (uint32_t)__builtin_ctz(free);
+      occ |= 1u << s;
+      return (int)s;
+    }
+    perturb >>= 5;
+    i = (i * 5 + 1 + perturb) & mask;
+  }
+}
+
+// set_positions_wave for U <= 18 keys, whose table is 8 slots up to 4 keys
+// and 32 slots from the resize at the fifth: all bookkeeping in scalar
+// registers (occupancy words, each key's slot in a packed word), the lanes
+// touched only to hand each key its slot.  Key j is held by lane j and
+// inserted j-th.
+__device__ inline int set_positions_small(int key, int U, int lane) {
+  uint32_t occ = 0, mask = 7;
+  uint32_t slot8 = 0;  // 3-bit table-8 slot of keys 0..4
+  int myslot = -1;
+  const int n8 = U < 5 ? U : 5;
+  for (int j = 0; j < n8; ++j) {
+    const int kj = __builtin_amdgcn_readlane(key, j);
+    const int s = probe_insert32(occ, mask, kj);
+    slot8 |= (uint32_t)s << (3 * j);
+    if (lane == j) myslot = s;
+  }
+  if (U >= 5) {
+    // resize to 32 slots: the five keys again, in table-8 slot order
+    occ = 0;
+    mask = 31;
+    for (int sl = 0; sl < 8; ++sl) {
+      for (int j = 0; j < 5; ++j) {
+        if (((slot8 >> (3 * j)) & 7u) != (uint32_t)sl) continue;
+        const int s = probe_insert32(occ, mask, __builtin_amdgcn_readlane(key, j));
+        if (lane == j) myslot = s;
+      }
+    }
+    for (int j = 5; j < U; ++j) {
+      const int s = probe_insert32(occ, mask, __builtin_amdgcn_readlane(key, j));
+      if (lane == j) myslot = s;
+    }
+  }
+  if (lane >= U) return -1;
+  return __popc(occ & ((1u << myslot) - 1u));
+}
+
 // Writes to order[0..n) the CPython iteration order of a set built by
 // inserting keys[0..n) (distinct) in array order.  keys, order and table
 // (kMaxSetTable words) live in LDS; all lanes of the wave call it.
@@ -93,7 +164,7 @@ __device__ inline void set_order_wave(const int32_t* keys, int n, int32_t* order
                                       int lane) {
   if (n <= 64) {
     const int key = lane < n ? keys[lane] : -1;
-    const int pos = set_positions_wave(key, n, lane);
+    const int pos = n <= 18 ? set_positions_small(key, n, lane) : set_positions_wave(key, n, lane);
     if (lane < n) order[pos] = key;
   } else if (lane == 0) {
     cpython_set_order(keys, n, order, table, kMaxSetTable);
