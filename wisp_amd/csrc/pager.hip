@@ -216,6 +216,7 @@ constexpr int kStagedPairs = 4096;
 
 struct FusedRouteSmem {
   int32_t ids[kStagedPairs];
+  float w[kFusedRouteTokens * kMaxTopK];  // routing weights of a routed call
 };
 
 // Size of the table of a CPython set of n small ints built by insertion: 8
@@ -246,8 +247,13 @@ __device__ inline int set_table_size(int n) {
 //   * the needed and the missing experts of a group in one pass over E;
 //   * eviction candidates from an LRU list kept in (tick, slot) order across
 //     the groups of a call instead of a sort per group;
-//   * the CPython set order only where collisions can reorder it.
-template <typename TL, int VALS>
+//   * the CPython set order only where collisions can reorder it;
+//   * no global loads after the start when the ids are staged in LDS
+//     (STAGED, decided at launch): on CDNA a wait for a global load also
+//     waits for every global store before it (one counter covers both), so
+//     a load that could read LDS or global memory (a flat load) would hold
+//     every group behind the previous group's record and slot stores.
+template <typename TL, int VALS, bool STAGED>
 __global__ __launch_bounds__(64) void pager_kernel(
     const int32_t* __restrict__ ids_in, const TL* __restrict__ logits, int renorm,
     float* __restrict__ w_out, int32_t* __restrict__ id_out, int T, int K, int E, int cap,
@@ -288,25 +294,19 @@ __global__ __launch_bounds__(64) void pager_kernel(
   int64_t clock = ctr_g[kClock];
   int64_t n_forward = ctr_g[kForward], n_miss = ctr_g[kMiss], n_evict = ctr_g[kEvict],
           n_hits = ctr_g[kHits];
-  // Every pair starts as "not computed" (slot -1, not loaded); the same lane
-  // owns pair p for all later writes.
-  for (int p = lane; p < P; p += 64) {
-    if (slots_g) slots_g[p] = -1;
-    if (flags_g) flags_g[1 + p] = pair_word(-1, -1);
-  }
-
-  // Routed ids: staged in LDS (read with LDS loads) when the call has at most
-  // kStagedPairs pairs or was routed here, else read from global memory.
-  const bool staged = logits != nullptr || P <= kStagedPairs;
-  auto id_at = [&](int p) -> int { return staged ? fr.ids[p] : ids_in[p]; };
+  // Routed ids: staged in LDS when the call has at most kStagedPairs pairs
+  // or was routed here (STAGED), else read from global memory.
+  auto id_at = [&](int p) -> int {
+    if constexpr (STAGED) return fr.ids[p];
+    else return ids_in[p];
+  };
   if (logits) {
     for (int t = 0; t < T; ++t) {
       float w;
       int id;
       route_token_wave<TL, VALS>(logits + (size_t)t * E, E, K, renorm, lane, true, &w, &id);
       if (lane < K) {
-        w_out[t * K + lane] = w;
-        id_out[t * K + lane] = id;
+        fr.w[t * K + lane] = w;
         fr.ids[t * K + lane] = id;
       }
     }
@@ -322,9 +322,21 @@ __global__ __launch_bounds__(64) void pager_kernel(
       }
     }
     wave_lds_sync();
-  } else if (staged) {
+    // The first global stores come only now: a wait for the state's loads
+    // above would otherwise also wait for them.
+    for (int p = lane; p < P; p += 64) {
+      w_out[p] = fr.w[p];
+      id_out[p] = fr.ids[p];
+    }
+  } else if (STAGED) {
     for (int p = lane; p < P; p += 64) fr.ids[p] = ids_in[p];
     wave_lds_sync();
+  }
+  // Every pair starts as "not computed" (slot -1, not loaded); the same lane
+  // owns pair p for all later writes.
+  for (int p = lane; p < P; p += 64) {
+    if (slots_g) slots_g[p] = -1;
+    if (flags_g) flags_g[1 + p] = pair_word(-1, -1);
   }
 
   // Validate ids.
@@ -342,6 +354,12 @@ __global__ __launch_bounds__(64) void pager_kernel(
   // they move to the list's end in slot order and the rest keep their order.
   // Eviction candidates are then the list filtered, with no sort per group.
   int nlru = -1;
+  // The planner's window: lane l holds the expert mask of token wb + l; a
+  // group of a few tokens uses it without rebuilding it.
+  uint32_t wm[W];
+#pragma unroll
+  for (int w = 0; w < W; ++w) wm[w] = 0u;
+  int wb = -1;
 
   if (any_bad || (!single_group && !masks_ok)) {
     status = WISP_ERR_INVALID;
@@ -365,47 +383,54 @@ __global__ __launch_bounds__(64) void pager_kernel(
         }
         end = T;
       } else {
-        // Greedy first-fit over 64 tokens at once: lane l holds the expert
-        // mask of token b + l, a prefix OR across the lanes gives the union
-        // of the group up to each token, and the first token whose union
-        // exceeds cap (unless it opens the group) ends it.
+        // Greedy first-fit over the window: a prefix OR across the lanes
+        // (tokens before `b` masked out) gives the union of the group up to
+        // each token, and the first token whose union exceeds cap (unless it
+        // opens the group) ends it.
         uint32_t u[W];
 #pragma unroll
         for (int w = 0; w < W; ++w) u[w] = 0u;
         end = -1;
-        for (int b = start; b < T && end < 0; b += 64) {
-          uint32_t m[W];
+        for (int b = start; b < T && end < 0;) {
+          if (wb < 0 || b >= wb + 64) {
+            wb = b;
 #pragma unroll
-          for (int w = 0; w < W; ++w) m[w] = 0u;
-          const int tl = b + lane;
-          if (tl < T) {
-            for (int j0 = 0; j0 < K; j0 += 8) {
-              int e8[8];
+            for (int w = 0; w < W; ++w) wm[w] = 0u;
+            const int tw = wb + lane;
+            if (tw < T) {
+              for (int j0 = 0; j0 < K; j0 += 8) {
+                int e8[8];
 #pragma unroll
-              for (int jj = 0; jj < 8; ++jj) e8[jj] = j0 + jj < K ? id_at(tl * K + j0 + jj) : -1;
+                for (int jj = 0; jj < 8; ++jj)
+                  e8[jj] = j0 + jj < K ? id_at(tw * K + j0 + jj) : -1;
 #pragma unroll
-              for (int jj = 0; jj < 8; ++jj) {
-                const int e = e8[jj];
+                for (int jj = 0; jj < 8; ++jj) {
+                  const int e = e8[jj];
 #pragma unroll
-                for (int w = 0; w < W; ++w)
-                  m[w] |= (e >= 0 && (e >> 5) == w) ? 1u << (e & 31) : 0u;
+                  for (int w = 0; w < W; ++w)
+                    wm[w] |= (e >= 0 && (e >> 5) == w) ? 1u << (e & 31) : 0u;
+                }
               }
             }
           }
+          const int tl = wb + lane;
+          const bool live = tl >= b && tl < T;
+          uint32_t m[W];
           int c = 0;
 #pragma unroll
           for (int w = 0; w < W; ++w) {
-            m[w] = wave_prefix_or(m[w], lane) | u[w];
+            m[w] = wave_prefix_or(live ? wm[w] : 0u, lane) | u[w];
             c += __popc(m[w]);
           }
-          const uint64_t over = ballot(tl < T && c > cap && tl != start);
-          const int last = over ? __builtin_ctzll(over) - 1 : min(63, T - 1 - b);
+          const uint64_t over = ballot(live && c > cap && tl != start);
+          const int last = over ? __builtin_ctzll(over) - 1 : min(63, T - 1 - wb);
           if (last >= 0) {
 #pragma unroll
             for (int w = 0; w < W; ++w)
               u[w] = (uint32_t)__builtin_amdgcn_readlane((int)m[w], last);
           }
-          if (over) end = b + __builtin_ctzll(over);
+          if (over) end = wb + __builtin_ctzll(over);
+          b = wb + 64;
         }
         if (end < 0) end = T;
 #pragma unroll
@@ -473,6 +498,7 @@ __global__ __launch_bounds__(64) void pager_kernel(
       if (nmiss > 0) {
         // ---- free slots and eviction candidates, ascending slot --------
         int nfree = 0, ncand = 0;
+        uint64_t cand_bits = 0;  // the candidate slots when cap <= 64
         for (int base = 0; base < cap; base += 64) {
           const int s = base + lane;
           bool f = false, c = false;
@@ -486,6 +512,7 @@ __global__ __launch_bounds__(64) void pager_kernel(
           if (c) sm.cand[ncand + popc_below(cbits)] = s;
           nfree += __popcll(fbits);
           ncand += __popcll(cbits);
+          cand_bits = cbits;
         }
         wave_lds_sync();
         const int shortfall = nmiss - nfree;
@@ -534,15 +561,22 @@ __global__ __launch_bounds__(64) void pager_kernel(
             wave_lds_sync();
           }
           // candidates in LRU order: the list without the needed experts
-          int nc = 0;
-          for (int base = 0; base < nlru; base += 64) {
-            const int j = base + lane;
-            const int sl = j < nlru ? sm.lru[j] : 0;
-            const int cur = j < nlru ? sm.s2e[sl] : 0;
-            const bool c = j < nlru && !(sm.need[cur >> 5] & (1u << (cur & 31)));
+          if (cap <= 64) {
+            const int sl = lane < nlru ? sm.lru[lane] : 0;
+            const bool c = lane < nlru && ((cand_bits >> sl) & 1ull);
             const uint64_t cb = ballot(c);
-            if (c) sm.sorted[nc + popc_below(cb)] = sl;
-            nc += __popcll(cb);
+            if (c) sm.sorted[popc_below(cb)] = sl;
+          } else {
+            int nc = 0;
+            for (int base = 0; base < nlru; base += 64) {
+              const int j = base + lane;
+              const int sl = j < nlru ? sm.lru[j] : 0;
+              const int cur = j < nlru ? sm.s2e[sl] : 0;
+              const bool c = j < nlru && !(sm.need[cur >> 5] & (1u << (cur & 31)));
+              const uint64_t cb = ballot(c);
+              if (c) sm.sorted[nc + popc_below(cb)] = sl;
+              nc += __popcll(cb);
+            }
           }
           wave_lds_sync();
           for (int r = lane; r < shortfall; r += 64) {
@@ -586,7 +620,24 @@ __global__ __launch_bounds__(64) void pager_kernel(
       }
       for (int j = lane; j < U; j += 64) sm.tick[sm.map[sm.keys[j]]] = clock;
       wave_lds_sync();
-      if (nlru >= 0) {
+      if (nlru >= 0 && cap <= 64) {
+        // The same update with one lane per slot: each lane reads its slot's
+        // expert and need bit, and entry j learns its slot's from lane
+        // lru[j] by a lane permute instead of two more LDS round trips.
+        const int sl = lane < nlru ? sm.lru[lane] : 0;
+        const int cs = lane < cap ? sm.s2e[lane] : -1;
+        const bool ins = cs >= 0 && ((sm.need[cs >> 5] >> (cs & 31)) & 1u);
+        const int state = (cs >= 0 ? 1 : 0) | (ins ? 2 : 0);
+        // every lane joins the permute: a lane a permute reads must be active
+        const int st_sl = __shfl(state, sl);
+        const bool keep = lane < nlru && st_sl == 1;  // occupied, not needed
+        const uint64_t kb = ballot(keep), ib = ballot(ins);
+        const int nk = __popcll(kb);
+        if (keep) sm.lru[popc_below(kb)] = sl;
+        if (ins) sm.lru[nk + popc_below(ib)] = lane;
+        nlru = nk + __popcll(ib);
+        wave_lds_sync();
+      } else if (nlru >= 0) {
         // In place: the list's entries still occupied by an expert the
         // group did not need, in list order (an entry moves only towards
         // the front, after every lane has read its own), then the needed
@@ -673,18 +724,32 @@ int launch_pager(const int32_t* ids, const void* logits, int logits_dtype, int r
     wisp_set_last_error("invalid pager arguments", "wisp_pager_decide");
     return WISP_ERR_INVALID;
   }
+  const bool staged = logits != nullptr || (int64_t)T * K <= kStagedPairs;
+  // A call with its ids in LDS issues no global load after its start, so
+  // nothing in it waits for its record stores: it writes the host record
+  // directly.  Otherwise it writes the device record and copies it to the
+  // host record at its end (a read of device memory there would wait for
+  // every host store before it).
+  if (staged && rec_host) {
+    rec = rec_host;
+    rec_host = nullptr;
+  }
   with_route_vals(E, [&](auto vals) {
     constexpr int V = decltype(vals)::value;
     if (logits && logits_dtype == WISP_BF16)
-      hipLaunchKernelGGL((pager_kernel<uint16_t, V>), dim3(1), dim3(64), 0, stream, ids,
+      hipLaunchKernelGGL((pager_kernel<uint16_t, V, true>), dim3(1), dim3(64), 0, stream, ids,
                          (const uint16_t*)logits, renorm, topk_w, topk_ids, T, K, E, cap,
                          single_group, map, s2e, tick, ctr, slots, flags, loads, rec,
                          rec_host);
-    else
-      hipLaunchKernelGGL((pager_kernel<float, V>), dim3(1), dim3(64), 0, stream, ids,
+    else if (staged)
+      hipLaunchKernelGGL((pager_kernel<float, V, true>), dim3(1), dim3(64), 0, stream, ids,
                          (const float*)logits, renorm, topk_w, topk_ids, T, K, E, cap,
                          single_group, map, s2e, tick, ctr, slots, flags, loads, rec,
                          rec_host);
+    else
+      hipLaunchKernelGGL((pager_kernel<float, V, false>), dim3(1), dim3(64), 0, stream, ids,
+                         nullptr, renorm, topk_w, topk_ids, T, K, E, cap, single_group, map, s2e,
+                         tick, ctr, slots, flags, loads, rec, rec_host);
   });
   WISP_HIP_TRY(hipGetLastError());
   return WISP_OK;
