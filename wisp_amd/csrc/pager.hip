@@ -195,6 +195,7 @@ namespace {
 
 struct PagerSmem {
   int32_t lru[kMaxExperts];  // occupied slots in (tick, slot) order
+  int32_t lru_pos[64];       // slot -> its place in lru (register path)
   int32_t map[kMaxExperts];
   int32_t s2e[kMaxExperts];
   int64_t tick[kMaxExperts];
@@ -269,11 +270,18 @@ __global__ __launch_bounds__(64) void pager_kernel(
   const RecordLayout L(T, K);
   const int P = T * K;
 
-  // With the router fused (the launcher picks VALS * 64 >= E) and cap within
-  // the same bound, the layer state is read into registers first and reaches
-  // LDS after routing, so its loads travel while the router loads and ranks
-  // the logits instead of before them.
-  const bool state_in_regs = logits && cap <= VALS * 64;
+  // The register path (E <= 128, cap <= 64): the layer state lives in
+  // registers for the whole call, one lane per slot (expert, tick, place in
+  // the LRU list) and per expert (slot), and a group's needed experts in
+  // scalar registers, so a group's decisions are lane arithmetic, ballots and
+  // lane permutes instead of chains of LDS round trips.
+  constexpr bool kRegsPath = VALS <= 2;
+  const bool regs = kRegsPath && cap <= 64;
+  // Otherwise, with the router fused (the launcher picks VALS * 64 >= E) and
+  // cap within the same bound, the layer state is read into registers first
+  // and reaches LDS after routing, so its loads travel while the router loads
+  // and ranks the logits instead of before them.
+  const bool state_in_regs = regs || (logits && cap <= VALS * 64);
   int map_r[VALS], s2e_r[VALS];
   int64_t tick_r[VALS];
   if (state_in_regs) {
@@ -310,7 +318,7 @@ __global__ __launch_bounds__(64) void pager_kernel(
         fr.ids[t * K + lane] = id;
       }
     }
-    if (state_in_regs) {
+    if (state_in_regs && !regs) {
 #pragma unroll
       for (int v = 0; v < VALS; ++v) {
         const int i = v * 64 + lane;
@@ -354,12 +362,82 @@ __global__ __launch_bounds__(64) void pager_kernel(
   // they move to the list's end in slot order and the rest keep their order.
   // Eviction candidates are then the list filtered, with no sort per group.
   int nlru = -1;
-  // The planner's window: lane l holds the expert mask of token wb + l; a
-  // group of a few tokens uses it without rebuilding it.
+  int lru_r = 0, lru_pos_r = 0;  // register path: entry `lane` of the list, slot `lane`'s place
+  // The planner's window: lane l holds the expert mask of token wb + l.
   uint32_t wm[W];
 #pragma unroll
   for (int w = 0; w < W; ++w) wm[w] = 0u;
   int wb = -1;
+  auto load_window = [&](int b) {
+    wb = b;
+#pragma unroll
+    for (int w = 0; w < W; ++w) wm[w] = 0u;
+    const int tw = wb + lane;
+    if (tw < T) {
+      for (int j0 = 0; j0 < K; j0 += 8) {
+        int e8[8];
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) e8[jj] = j0 + jj < K ? id_at(tw * K + j0 + jj) : -1;
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+          const int e = e8[jj];
+#pragma unroll
+          for (int w = 0; w < W; ++w) wm[w] |= (e >= 0 && (e >> 5) == w) ? 1u << (e & 31) : 0u;
+        }
+      }
+    }
+  };
+  // The window's scan: lane l finds where a group that starts at token
+  // wb + l ends (the first later token whose union with the group exceeds
+  // cap; gend = offset from wb, kOpenEnd when that lies past the window) and
+  // that group's union gu, reading the next tokens' masks by lane permute.
+  // Each group of a call then costs a few readlanes.
+  constexpr int kOpenEnd = 65;
+  int gend = kOpenEnd;
+  uint32_t gu[W];
+#pragma unroll
+  for (int w = 0; w < W; ++w) gu[w] = 0u;
+  int sw = -1;  // the window the scan describes (-1: none)
+  auto scan_window = [&](int b) {
+    load_window(b);
+    const int lim = min(64, T - wb);  // tokens in the window
+    const int closed = wb + lim == T ? lim : kOpenEnd;  // a group running to the window's end
+#pragma unroll
+    for (int w = 0; w < W; ++w) gu[w] = wm[w];
+    bool done = lane >= lim;
+    int endl = lim;
+    for (int d = 1; d < 64; ++d) {
+      if (ballot(!done) == 0) break;
+      uint32_t nx[W];
+#pragma unroll
+      for (int w = 0; w < W; ++w)  // every lane joins the permute
+        nx[w] = (uint32_t)__shfl((int)wm[w], (lane + d) & 63);
+      if (!done) {
+        if (lane + d >= lim) {
+          done = true;
+          endl = closed;
+        } else {
+          uint32_t na[W];
+          int c = 0;
+#pragma unroll
+          for (int w = 0; w < W; ++w) {
+            na[w] = gu[w] | nx[w];
+            c += __popc(na[w]);
+          }
+          if (c > cap) {
+            done = true;
+            endl = lane + d;
+          } else {
+#pragma unroll
+            for (int w = 0; w < W; ++w) gu[w] = na[w];
+          }
+        }
+      }
+    }
+    if (!done) endl = closed;
+    gend = endl;
+    sw = wb;
+  };
 
   if (any_bad || (!single_group && !masks_ok)) {
     status = WISP_ERR_INVALID;
@@ -371,6 +449,7 @@ __global__ __launch_bounds__(64) void pager_kernel(
       first = false;
       // ---- plan one group: tokens [start, end) -----------------------
       int end = start;
+      uint32_t u[W];  // the group's needed experts (wave-uniform)
       if (single_group || T == 1) {
         for (int w = lane; w < nwords; w += 64) {
           sm.need[w] = 0u;
@@ -382,37 +461,31 @@ __global__ __launch_bounds__(64) void pager_kernel(
           atomicOr(&sm.need[e >> 5], 1u << (e & 31));
         }
         end = T;
+        wave_lds_sync();
+#pragma unroll
+        for (int w = 0; w < W; ++w)
+          u[w] = w < nwords ? (uint32_t)__builtin_amdgcn_readfirstlane((int)sm.need[w]) : 0u;
       } else {
-        // Greedy first-fit over the window: a prefix OR across the lanes
-        // (tokens before `b` masked out) gives the union of the group up to
-        // each token, and the first token whose union exceeds cap (unless it
-        // opens the group) ends it.
-        uint32_t u[W];
+        // Greedy first-fit in token order: the group that starts at `start`
+        // from the window scan (scanning a window that starts there when the
+        // current one does not cover it).
+        int l = start - sw;
+        const bool covered = sw >= 0 && l >= 0 && l < 64;
+        int eo = covered ? __builtin_amdgcn_readlane(gend, l) : kOpenEnd;
+        if (eo == kOpenEnd && !(covered && l == 0)) {
+          scan_window(start);
+          l = 0;
+          eo = __builtin_amdgcn_readlane(gend, 0);
+        }
 #pragma unroll
-        for (int w = 0; w < W; ++w) u[w] = 0u;
-        end = -1;
-        for (int b = start; b < T && end < 0;) {
-          if (wb < 0 || b >= wb + 64) {
-            wb = b;
-#pragma unroll
-            for (int w = 0; w < W; ++w) wm[w] = 0u;
-            const int tw = wb + lane;
-            if (tw < T) {
-              for (int j0 = 0; j0 < K; j0 += 8) {
-                int e8[8];
-#pragma unroll
-                for (int jj = 0; jj < 8; ++jj)
-                  e8[jj] = j0 + jj < K ? id_at(tw * K + j0 + jj) : -1;
-#pragma unroll
-                for (int jj = 0; jj < 8; ++jj) {
-                  const int e = e8[jj];
-#pragma unroll
-                  for (int w = 0; w < W; ++w)
-                    wm[w] |= (e >= 0 && (e >> 5) == w) ? 1u << (e & 31) : 0u;
-                }
-              }
-            }
-          }
+        for (int w = 0; w < W; ++w) u[w] = (uint32_t)__builtin_amdgcn_readlane((int)gu[w], l);
+        end = eo == kOpenEnd ? -1 : sw + eo;
+        // A group longer than the window (it starts the window): extend it
+        // window by window with a prefix OR across the lanes (tokens before
+        // `b` masked out), up to the first token whose union exceeds cap.
+        for (int b = sw + 64; b < T && end < 0;) {
+          if (b >= wb + 64) load_window(b);
+          sw = -1;  // wm no longer holds the scanned window
           const int tl = wb + lane;
           const bool live = tl >= b && tl < T;
           uint32_t m[W];
@@ -422,7 +495,7 @@ __global__ __launch_bounds__(64) void pager_kernel(
             m[w] = wave_prefix_or(live ? wm[w] : 0u, lane) | u[w];
             c += __popc(m[w]);
           }
-          const uint64_t over = ballot(live && c > cap && tl != start);
+          const uint64_t over = ballot(live && c > cap);
           const int last = over ? __builtin_ctzll(over) - 1 : min(63, T - 1 - wb);
           if (last >= 0) {
 #pragma unroll
@@ -444,6 +517,196 @@ __global__ __launch_bounds__(64) void pager_kernel(
       const int g = groups_planned++;
       const int t0 = start, t1 = end;
       start = end;
+
+      if (regs) {
+        // need bit of expert e (0 <= e < E) from the scalar mask words
+        auto need_of = [&](int e) -> bool {
+          uint32_t w = u[0];
+#pragma unroll
+          for (int k = 1; k < W; ++k) w = (e >> 5) == k ? u[k] : w;
+          return (w >> (e & 31)) & 1u;
+        };
+        // ---- needed and missing experts, ascending ----------------------
+        uint64_t mb[VALS];
+        int U = 0, nmiss = 0, kmax = -1;
+#pragma unroll
+        for (int v = 0; v < VALS; ++v) {
+          const int e = v * 64 + lane;
+          const uint32_t needw = lane < 32 ? u[2 * v] : u[2 * v + 1];
+          const bool in = e < E && ((needw >> (lane & 31)) & 1u);
+          const bool miss = in && map_r[v] < 0;
+          const uint64_t bb = ballot(in);
+          mb[v] = ballot(miss);
+          if (in) sm.keys[U + popc_below(bb)] = e;
+          if (miss) sm.missing[nmiss + popc_below(mb[v])] = e;
+          U += __popcll(bb);
+          nmiss += __popcll(mb[v]);
+          if (bb) kmax = v * 64 + 63 - __builtin_clzll(bb);
+        }
+        auto missed = [&](int e) -> bool {
+          const uint64_t m = (VALS > 1 && (e >> 6) == 1) ? mb[VALS - 1] : mb[0];
+          return (m >> (e & 63)) & 1ull;
+        };
+        wave_lds_sync();
+        // ---- the missing experts in CPython set order -------------------
+        // (a group with more needed experts than cap fails below, and its
+        // order decides nothing)
+        if (nmiss >= 2 && U <= cap && kmax >= set_table_size(U)) {
+          const int key = lane < U ? sm.keys[lane] : -1;
+          const int pos = U <= 18 ? set_positions_small(key, U, lane)
+                                  : set_positions_wave(key, U, lane);
+          if (lane < U) sm.order[pos] = key;
+          wave_lds_sync();
+          const int e = lane < U ? sm.order[lane] : 0;
+          const bool m = lane < U && missed(e);
+          const uint64_t b = ballot(m);
+          if (m) sm.missing[popc_below(b)] = e;
+          wave_lds_sync();
+        }
+        const int hits = U - nmiss;
+        n_hits += hits;
+        const int gb = L.group_base(g);
+        if (lane == 0) {
+          rec[gb + 0] = t0; rec[gb + 1] = t1; rec[gb + 2] = U; rec[gb + 3] = hits;
+          rec[gb + 4] = ev_total; rec[gb + 5] = 0; rec[gb + 6] = ld_total; rec[gb + 7] = 0;
+        }
+        if (nmiss > 0) {
+          // ---- slot lanes: free slots and eviction candidates -----------
+          const int cs = s2e_r[0];  // -1 on lanes >= cap
+          const bool occ = cs >= 0;
+          const bool cand = occ && !need_of(occ ? cs : 0);
+          const uint64_t fbits = ballot(lane < cap && !occ), cbits = ballot(cand);
+          const int nfree = __popcll(fbits), ncand = __popcll(cbits);
+          const int shortfall = nmiss - nfree;
+          if (shortfall > ncand) {
+            status = WISP_ERR_SUBBATCH;
+            fail_group = g;
+            fail_u = U;
+            break;
+          }
+          uint64_t evb = 0;  // evicted slots
+          int q = 0;         // this slot's place among the victims
+          if (shortfall > 0) {
+            if (nlru < 0) {
+              // occupied slots ranked by (tick, slot), ticks by readlane
+              const int64_t ti = occ ? tick_r[0] : 0;
+              const uint32_t tlo = (uint32_t)ti, thi = (uint32_t)((uint64_t)ti >> 32);
+              const uint64_t occ_bits = ballot(occ);
+              int r = 0;
+              for (int j = 0; j < cap; ++j) {
+                if (!((occ_bits >> j) & 1ull)) continue;
+                const uint64_t tj =
+                    ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)thi, j) << 32) |
+                    (uint32_t)__builtin_amdgcn_readlane((int)tlo, j);
+                r += ((int64_t)tj < ti) || ((int64_t)tj == ti && j < lane);
+              }
+              if (occ) sm.lru[r] = lane;
+              lru_pos_r = r;
+              nlru = __popcll(occ_bits);
+              wave_lds_sync();
+              lru_r = lane < nlru ? sm.lru[lane] : 0;
+            }
+            // candidates in LRU order: entry j's slot is a candidate; a
+            // candidate slot's place among them is the candidates ahead of
+            // its entry; the first `shortfall` are evicted
+            const uint64_t cb = ballot(lane < nlru && ((cbits >> lru_r) & 1ull));
+            q = cand ? __popcll(cb & ((1ull << lru_pos_r) - 1ull)) : 0;
+            const bool ev = cand && q < shortfall;
+            evb = ballot(ev);
+            if (ev) {
+              const int o = L.evicted_base() + 2 * (ev_total + q);
+              rec[o] = cs;
+              rec[o + 1] = lane;
+            }
+            n_evict += shortfall;
+            ev_total += shortfall;
+            if (lane == 0) rec[gb + 5] = shortfall;
+          }
+          // evicted experts leave the map
+#pragma unroll
+          for (int v = 0; v < VALS; ++v)
+            if (map_r[v] >= 0 && ((evb >> map_r[v]) & 1ull)) map_r[v] = -1;
+          clock += 1;
+          // The free list is the free slots ascending, then the evicted ones
+          // in victim order; missing expert j takes entry nfree_all - 1 - j.
+          const int sf = shortfall > 0 ? shortfall : 0;
+          const int nfree_all = nfree + sf;
+          int j = -1;
+          if (lane < cap && !occ)
+            j = nfree_all - 1 - __popcll(fbits & ((1ull << lane) - 1ull));
+          else if ((evb >> lane) & 1ull)
+            j = sf - 1 - q;
+          const bool takes = j >= 0 && j < nmiss;
+          if (takes) {
+            const int e = sm.missing[j];
+            s2e_r[0] = e;
+            tick_r[0] = clock;
+            sm.map[e] = lane;  // for the expert lanes below
+            const int o = L.loaded_base() + 2 * (ld_total + j);
+            rec[o] = e;
+            rec[o + 1] = lane;
+            if (loads_g) {
+              loads_g[2 * (ld_total + j)] = e;
+              loads_g[2 * (ld_total + j) + 1] = lane;
+            }
+          } else if ((evb >> lane) & 1ull) {
+            s2e_r[0] = -1;  // (every victim's slot is taken)
+          }
+          wave_lds_sync();
+#pragma unroll
+          for (int v = 0; v < VALS; ++v)
+            if ((mb[v] >> lane) & 1ull) map_r[v] = sm.map[v * 64 + lane];
+          n_miss += nmiss;
+          ld_total += nmiss;
+          if (lane == 0) rec[gb + 7] = nmiss;
+        } else {
+          clock += 1;
+        }
+        // ---- slot lanes: ticks of the needed experts, the LRU list ------
+        const int cs2 = s2e_r[0];
+        const bool ins = cs2 >= 0 && need_of(cs2 >= 0 ? cs2 : 0);
+        if (ins) tick_r[0] = clock;
+        if (nlru >= 0) {
+          // entries still occupied by an expert the group did not need, in
+          // list order, then the needed experts' slots ascending
+          const int state = (cs2 >= 0 ? 1 : 0) | (ins ? 2 : 0);
+          const int st_entry = __shfl(state, lru_r);  // every lane joins the permute
+          const bool keep = lane < nlru && st_entry == 1;
+          const uint64_t kb = ballot(keep), ib = ballot(ins);
+          const int nk = __popcll(kb);
+          if (keep) {
+            sm.lru[popc_below(kb)] = lru_r;
+            sm.lru_pos[lru_r] = popc_below(kb);
+          }
+          if (ins) {
+            sm.lru[nk + popc_below(ib)] = lane;
+            sm.lru_pos[lane] = nk + popc_below(ib);
+          }
+          nlru = nk + __popcll(ib);
+          wave_lds_sync();
+          lru_r = lane < nlru ? sm.lru[lane] : 0;
+          lru_pos_r = lane < cap ? sm.lru_pos[lane] : 0;
+        }
+        // ---- the group's pairs: slot and loaded flag --------------------
+        for (int base = t0 * K; base < t1 * K; base += 64) {
+          const int p = base + lane;
+          const bool valid = p < t1 * K;
+          const int e = valid ? id_at(p) : 0;
+          const int src = e & 63;
+          int sl = __shfl(map_r[0], src);
+          if (VALS > 1) {
+            const int s1 = __shfl(map_r[VALS - 1], src);
+            if ((e >> 6) == 1) sl = s1;
+          }
+          if (valid) {
+            if (slots_g) slots_g[p] = sl;
+            if (flags_g) flags_g[1 + p] = pair_word(sl, missed(e) ? e : -1);
+          }
+        }
+        groups_done = g + 1;
+        wave_lds_sync();
+        continue;
+      }
 
       // ---- needed experts (ascending) and the missing ones, one pass ----
       int U = 0, nmiss = 0, kmax = -1;
@@ -674,10 +937,20 @@ __global__ __launch_bounds__(64) void pager_kernel(
     }
   }
 
-  for (int e = lane; e < E; e += 64) map_g[e] = sm.map[e];
-  for (int s = lane; s < cap; s += 64) {
-    s2e_g[s] = sm.s2e[s];
-    tick_g[s] = sm.tick[s];
+  if (regs) {
+#pragma unroll
+    for (int v = 0; v < VALS; ++v)
+      if (v * 64 + lane < E) map_g[v * 64 + lane] = map_r[v];
+    if (lane < cap) {
+      s2e_g[lane] = s2e_r[0];
+      tick_g[lane] = tick_r[0];
+    }
+  } else {
+    for (int e = lane; e < E; e += 64) map_g[e] = sm.map[e];
+    for (int s = lane; s < cap; s += 64) {
+      s2e_g[s] = sm.s2e[s];
+      tick_g[s] = sm.tick[s];
+    }
   }
   if (lane == 0) {
     ctr_g[kClock] = clock;
