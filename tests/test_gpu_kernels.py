@@ -79,7 +79,11 @@ class DevPager:
 @pytest.mark.parametrize("E,K,cap,tmax", [(8, 2, 4, 3), (16, 2, 4, 4), (128, 8, 8, 1),
                                            (128, 8, 24, 6), (128, 8, 32, 64), (8, 2, 2, 16),
                                            (512, 8, 64, 8), (100, 3, 7, 5), (256, 8, 100, 20),
-                                           (512, 16, 300, 40)])
+                                           (512, 16, 300, 40),
+                                           # the register path's edges: every lane a slot,
+                                           # E <= 64 (one mask word pair), odd E and cap
+                                           (128, 8, 64, 24), (64, 4, 64, 40), (100, 7, 63, 30),
+                                           (128, 8, 65, 24)])
 def test_gpu_pager_matches_oracle(E, K, cap, tmax):
     rng = np.random.default_rng(E * 7 + cap)
     ora, dp = PagerOracle(E, cap), DevPager(E, cap)

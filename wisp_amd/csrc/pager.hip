@@ -242,10 +242,14 @@ __device__ inline int set_table_size(int n) {
 // dependent steps (each LDS round trip, each hand-off between the scalar and
 // the vector unit); it is built to keep that chain short per token group:
 //   * group planning (greedy first-fit in token order) on per-token expert
-//     bitmasks: lane l holds the mask of token b + l and a prefix OR across
-//     the lanes gives every token's group union at once, so a group costs a
-//     few DPP steps instead of a step per token;
-//   * the needed and the missing experts of a group in one pass over E;
+//     bitmasks: lane l holds the mask of token b + l of a 64-token window,
+//     and one scan per window finds, for every lane at once, where a group
+//     starting at its token ends and that group's union, so a group costs a
+//     few readlanes;
+//   * for E <= 128 and cap <= 64, the layer state in registers (a lane per
+//     slot and per expert) and each group's decisions as lane arithmetic,
+//     ballots and lane permutes; otherwise staged in LDS, with the needed
+//     and the missing experts of a group in one pass over E;
 //   * eviction candidates from an LRU list kept in (tick, slot) order across
 //     the groups of a call instead of a sort per group;
 //   * the CPython set order only where collisions can reorder it;
