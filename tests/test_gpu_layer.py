@@ -72,6 +72,13 @@ def test_toy_fp32_layer_all_steps():
     drive(wl, 4, wl.steps, tol=1e-5)
 
 
+def test_toy_fp32_layer_cap_equals_top_k():
+    # cap == top_k: every one-token call fills every slot, so the decode
+    # kernels lay their waves out by slot (a miss on most calls here)
+    wl = W.toy(pin=True)
+    drive(wl, wl.shape.top_k, wl.steps, tol=1e-5)
+
+
 @pytest.mark.parametrize("engine,streams", [("kernel", "0"), ("memcpy", "0"), ("memcpy", "1"),
                                             ("memcpy", "2")])
 def test_qwen3_bf16_layer_decode(monkeypatch, engine, streams):

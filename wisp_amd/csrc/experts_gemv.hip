@@ -60,6 +60,13 @@ __device__ inline void store_elem<uint16_t>(uint16_t* p, float v) { *p = bf16_rn
 
 __device__ inline uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 
+// A word loaded before the loads that follow it in the source: the compiler
+// neither sinks nor reorders a relaxed atomic load (plain loads of
+// restrict-qualified data it may move below later loads).
+__device__ inline int32_t load_first(const int32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
 // Streaming load for weight rows: each byte is read once per launch, so the
 // nontemporal hint keeps the rows from displacing cached data (measured on
 // MI355X: w13 at the Qwen3 decode shape 9.2 us instead of 10.2 us).
@@ -320,7 +327,56 @@ __global__ __launch_bounds__(256) void pagein_w13_kernel(FusedW13Args f, PageInA
 // ---------------------------------------------------------------------------
 constexpr int kMaxKw2 = kGemvMaxTopK;
 
+// The RPH weight rows from h0 of one expert (rows past H read row H - 1 and
+// are dropped), CH chunks per lane of an LPR-lane row group.
 template <typename T, int LPR, int CH, int RPH, bool FULL>
+__device__ inline void w2_load_rows(const T* __restrict__ wbase, int h0, int H, int I, int l,
+                                    uint4 (&wv)[RPH][CH]) {
+  constexpr int V = Vec<T>::N;
+  const int nch = I / V;
+#pragma unroll
+  for (int r = 0; r < RPH; ++r) {
+    const T* wrow = wbase + (size_t)min(h0 + r, H - 1) * I;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int ch = c * LPR + l;
+      wv[r][c] = (FULL || ch < nch) ? ld16(wrow + (size_t)ch * V) : make_uint4(0, 0, 0, 0);
+    }
+  }
+}
+
+// This lane's part of the RPH dot products of the rows in wv with one act
+// row: the FMA chain over its chunks in order.
+template <typename T, int LPR, int CH, int RPH, bool FULL>
+__device__ inline void w2_dots(const uint4 (&wv)[RPH][CH], const T* __restrict__ arow, int I,
+                               int l, float (&d)[RPH]) {
+  constexpr int V = Vec<T>::N;
+  const int nch = I / V;
+  uint4 av[CH];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int ch = c * LPR + l;
+    av[c] = (FULL || ch < nch) ? ld16(arow + (size_t)ch * V) : make_uint4(0, 0, 0, 0);
+  }
+#pragma unroll
+  for (int r = 0; r < RPH; ++r) {
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      float wf[V], af[V];
+      Vec<T>::unpack(wv[r][c], wf);
+      Vec<T>::unpack(av[c], af);
+#pragma unroll
+      for (int q = 0; q < V; ++q) d[r] = fmaf(wf[q], af[q], d[r]);
+    }
+  }
+}
+
+// SLOTS (one token whose top-k equals cap, CH > 0): wave k streams slot k
+// instead of pair k's slot.  It issues its row loads right after the pairs'
+// slots and weights, without waiting for them, then finds the pair the slot
+// serves and dots its rows with that pair's act row.  Each row's arithmetic
+// is the same as with one wave per pair, so the output bytes are too.
+template <typename T, int LPR, int CH, int RPH, bool FULL, bool SLOTS>
 __global__ __launch_bounds__(1024) void w2_combine_kernel(const T* __restrict__ act, int H, int I,
                                                            int K, const float* __restrict__ topk_w,
                                                            const int32_t* __restrict__ slots,
@@ -330,6 +386,7 @@ __global__ __launch_bounds__(1024) void w2_combine_kernel(const T* __restrict__ 
                                                            const int32_t* __restrict__ skip_if) {
   constexpr int V = Vec<T>::N;
   constexpr int RPB = 64 / LPR * RPH;  // rows per block
+  constexpr int CHA = CH > 0 ? CH : 1;
   __shared__ float part[kMaxKw2][RPB];
   __shared__ float wk[kMaxKw2];
   if (skip_if && *skip_if != 0) return;
@@ -337,53 +394,56 @@ __global__ __launch_bounds__(1024) void w2_combine_kernel(const T* __restrict__ 
   const int sub = lane / LPR, l = lane % LPR;
   const int t = blockIdx.y;
   const int h0 = blockIdx.x * RPB + sub * RPH;
-  const int s = slots[t * K + k];
-  if (lane == 0) wk[k] = s >= 0 ? topk_w[t * K + k] : 0.f;
-  const int nch = I / V;
   float d[RPH];
 #pragma unroll
   for (int r = 0; r < RPH; ++r) d[r] = 0.f;
-  if (s >= 0 && h0 < H) {
-    const T* wbase = w2 + (size_t)s * w2_stride;
-    const T* arow = act + ((size_t)t * K + k) * I;
-    if (CH > 0) {
-      uint4 wv[RPH][CH > 0 ? CH : 1], av[CH > 0 ? CH : 1];
+  int p = k;  // the pair whose dot products this wave computes (-1: none)
+  if (SLOTS) {
+    // lane j < K: pair j's slot and routing weight
+    // (both loaded ahead of the rows, so that waiting for them does not wait
+    // for the rows: loads complete in order)
+    const int jl = min(lane, K - 1);
+    const int sj = load_first(slots + t * K + jl);
+    const float wj = __int_as_float(load_first((const int32_t*)topk_w + t * K + jl));
+    uint4 wv[RPH][CHA];
+    w2_load_rows<T, LPR, CHA, RPH, FULL>(w2 + (size_t)k * w2_stride, h0, H, I, l, wv);
+    // nothing that waits for sj or wj may be scheduled above the row loads
+    __builtin_amdgcn_sched_barrier(0);
+    const uint64_t mine = __ballot(lane < K && sj == k);
+    p = mine ? __builtin_ctzll(mine) : -1;
+    const int sk = __shfl(sj, k);
+    const float wsk = __shfl(wj, k);
+    // unconditional (a wave whose slot serves no pair dots with pair 0's act
+    // and drops the result): rows used under a branch would be loaded there
+    w2_dots<T, LPR, CHA, RPH, FULL>(wv, act + ((size_t)t * K + (p < 0 ? 0 : p)) * I, I, l, d);
+    if (lane == 0) wk[k] = sk >= 0 ? wsk : 0.f;
+    if (sk < 0 && l == 0) {  // pair k reads no expert: its partials are 0
 #pragma unroll
-      for (int r = 0; r < RPH; ++r) {
-        const T* wrow = wbase + (size_t)min(h0 + r, H - 1) * I;
+      for (int r = 0; r < RPH; ++r) part[k][sub * RPH + r] = 0.f;
+    }
+  } else {
+    const int s = slots[t * K + k];
+    if (lane == 0) wk[k] = s >= 0 ? topk_w[t * K + k] : 0.f;
+    if (s >= 0 && h0 < H) {
+      const T* wbase = w2 + (size_t)s * w2_stride;
+      const T* arow = act + ((size_t)t * K + k) * I;
+      if (CH > 0) {
+        uint4 wv[RPH][CHA];
+        w2_load_rows<T, LPR, CHA, RPH, FULL>(wbase, h0, H, I, l, wv);
+        w2_dots<T, LPR, CHA, RPH, FULL>(wv, arow, I, l, d);
+      } else {
+        const int nch = I / V;
 #pragma unroll
-        for (int c = 0; c < CH; ++c) {
-          const int ch = c * LPR + l;
-          wv[r][c] = (FULL || ch < nch) ? ld16(wrow + (size_t)ch * V) : make_uint4(0, 0, 0, 0);
-        }
-      }
-#pragma unroll
-      for (int c = 0; c < CH; ++c) {
-        const int ch = c * LPR + l;
-        av[c] = (FULL || ch < nch) ? ld16(arow + (size_t)ch * V) : make_uint4(0, 0, 0, 0);
-      }
-#pragma unroll
-      for (int r = 0; r < RPH; ++r) {
-#pragma unroll
-        for (int c = 0; c < CH; ++c) {
-          float wf[V], af[V];
-          Vec<T>::unpack(wv[r][c], wf);
-          Vec<T>::unpack(av[c], af);
-#pragma unroll
-          for (int q = 0; q < V; ++q) d[r] = fmaf(wf[q], af[q], d[r]);
-        }
-      }
-    } else {
-#pragma unroll
-      for (int r = 0; r < RPH; ++r) {
-        const T* wrow = wbase + (size_t)min(h0 + r, H - 1) * I;
+        for (int r = 0; r < RPH; ++r) {
+          const T* wrow = wbase + (size_t)min(h0 + r, H - 1) * I;
 #pragma unroll 4
-        for (int ch = l; ch < nch; ch += LPR) {
-          float wf[V], af[V];
-          Vec<T>::unpack(ld16(wrow + (size_t)ch * V), wf);
-          Vec<T>::unpack(ld16(arow + (size_t)ch * V), af);
+          for (int ch = l; ch < nch; ch += LPR) {
+            float wf[V], af[V];
+            Vec<T>::unpack(ld16(wrow + (size_t)ch * V), wf);
+            Vec<T>::unpack(ld16(arow + (size_t)ch * V), af);
 #pragma unroll
-          for (int q = 0; q < V; ++q) d[r] = fmaf(wf[q], af[q], d[r]);
+            for (int q = 0; q < V; ++q) d[r] = fmaf(wf[q], af[q], d[r]);
+          }
         }
       }
     }
@@ -391,9 +451,9 @@ __global__ __launch_bounds__(1024) void w2_combine_kernel(const T* __restrict__ 
 #pragma unroll
   for (int r = 0; r < RPH; ++r)
     for (int off = LPR / 2; off > 0; off >>= 1) d[r] += __shfl_xor(d[r], off);
-  if (l == 0) {
+  if (l == 0 && p >= 0) {
 #pragma unroll
-    for (int r = 0; r < RPH; ++r) part[k][sub * RPH + r] = d[r];
+    for (int r = 0; r < RPH; ++r) part[p][sub * RPH + r] = d[r];
   }
   __syncthreads();
   if (threadIdx.x < RPB) {
@@ -409,12 +469,14 @@ __global__ __launch_bounds__(1024) void w2_combine_kernel(const T* __restrict__ 
 
 // Optional controls of a launch: kernel timing events, the pair filter of
 // the w13 kernel (run only pairs with pair_filter[p] == want) and the skip
-// word of the w2 kernel (exit when *skip_if != 0).
+// word of the w2 kernel (exit when *skip_if != 0), and the w2 kernel's
+// one-wave-per-slot layout (a one-token call whose top-k equals cap).
 struct LaunchCtl {
   hipEvent_t start = nullptr, stop = nullptr;
   const int32_t* pair_filter = nullptr;
   int want = 0;
   const int32_t* skip_if = nullptr;
+  bool slots = false;
 };
 
 template <typename T, int CH>
@@ -482,12 +544,21 @@ void launch_w2(const T* act, int T_, int H, int I, int K, const float* w, const 
                const T* w2, size_t w2_stride, T* out, hipStream_t st, const LaunchCtl& c) {
   constexpr int RPB = 64 / LPR * RPH;
   dim3 grid((H + RPB - 1) / RPB, T_);
-  if (CH > 0 && I == CH * LPR * Vec<T>::N)
-    launch_timed(w2_combine_kernel<T, LPR, CH, RPH, true>, grid, dim3(64 * K), st, c.start,
-                 c.stop, act, H, I, K, w, slots, w2, w2_stride, out, c.skip_if);
-  else
-    launch_timed(w2_combine_kernel<T, LPR, CH, RPH, false>, grid, dim3(64 * K), st, c.start,
-                 c.stop, act, H, I, K, w, slots, w2, w2_stride, out, c.skip_if);
+  const bool full = CH > 0 && I == CH * LPR * Vec<T>::N;
+  if (CH > 0 && c.slots) {
+    if (full)
+      launch_timed(w2_combine_kernel<T, LPR, CH, RPH, true, true>, grid, dim3(64 * K), st,
+                   c.start, c.stop, act, H, I, K, w, slots, w2, w2_stride, out, c.skip_if);
+    else
+      launch_timed(w2_combine_kernel<T, LPR, CH, RPH, false, true>, grid, dim3(64 * K), st,
+                   c.start, c.stop, act, H, I, K, w, slots, w2, w2_stride, out, c.skip_if);
+  } else if (full) {
+    launch_timed(w2_combine_kernel<T, LPR, CH, RPH, true, false>, grid, dim3(64 * K), st,
+                 c.start, c.stop, act, H, I, K, w, slots, w2, w2_stride, out, c.skip_if);
+  } else {
+    launch_timed(w2_combine_kernel<T, LPR, CH, RPH, false, false>, grid, dim3(64 * K), st,
+                 c.start, c.stop, act, H, I, K, w, slots, w2, w2_stride, out, c.skip_if);
+  }
 }
 
 template <typename T>
@@ -563,14 +634,17 @@ int gemv_w13(const void* x, int dtype, int T_, int H, int I, int K, const int32_
   return WISP_OK;
 }
 
+// With `cap` > 0, a one-token call whose top-k equals cap uses every slot
+// and runs the w2 kernel one wave per slot (cap 0: one wave per pair).
 int gemv_w2(const void* act, int dtype, int T_, int H, int I, int K, const float* topk_w,
             const int32_t* slots, const void* w2, size_t w2_stride, void* out, hipStream_t st,
-            hipEvent_t ev_start, hipEvent_t ev_stop, const int32_t* skip_if) {
+            hipEvent_t ev_start, hipEvent_t ev_stop, const int32_t* skip_if, int cap) {
   if (T_ == 0) return WISP_OK;
   LaunchCtl c;
   c.start = ev_start;
   c.stop = ev_stop;
   c.skip_if = skip_if;
+  c.slots = T_ == 1 && K == cap;
   const int rc = dtype == WISP_F32
       ? dispatch_w2<float>((const float*)act, T_, H, I, K, topk_w, slots, (const float*)w2,
                            w2_stride, (float*)out, st, c)
@@ -591,7 +665,7 @@ int experts_gemv(const void* x, int dtype, int T_, int H, int I, int K, const fl
                     ev ? ev->ev[0] : nullptr, ev ? ev->ev[1] : nullptr, nullptr, 0);
   if (rc != WISP_OK) return rc;
   return gemv_w2(act, dtype, T_, H, I, K, topk_w, slots, w2, w2_stride, out, st,
-                 ev ? ev->ev[2] : nullptr, ev ? ev->ev[3] : nullptr, nullptr);
+                 ev ? ev->ev[2] : nullptr, ev ? ev->ev[3] : nullptr, nullptr, 0);
 }
 
 }  // namespace wisp

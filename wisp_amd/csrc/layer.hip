@@ -71,7 +71,7 @@ int pagein_w13(const PageInArgs& a, const void* x, int dtype, int T, int H, int 
                hipStream_t st, hipEvent_t ev_start, hipEvent_t ev_stop);
 int gemv_w2(const void* act, int dtype, int T, int H, int I, int K, const float* topk_w,
             const int32_t* slots, const void* w2, size_t w2_stride, void* out, hipStream_t st,
-            hipEvent_t ev_start, hipEvent_t ev_stop, const int32_t* skip_if);
+            hipEvent_t ev_start, hipEvent_t ev_stop, const int32_t* skip_if, int cap);
 int experts_gemv(const void* x, int dtype, int T, int H, int I, int K, const float* topk_w,
                  const int32_t* slots, const void* w13, size_t w13_stride, const void* w2,
                  size_t w2_stride, void* act, void* out, hipStream_t st, const StageEvents* ev);
@@ -494,9 +494,11 @@ int w2(Layer& L, const void* act, int T, int K, const float* w, const int32_t* s
        hipStream_t st, const int32_t* skip_if, ProfLaunch** launched) {
   const wisp_layer_desc& d = L.d;
   ProfLaunch* p = prof_begin(L, 1);
+  // the slots come from the pager, so a one-token call with K == cap fills
+  // every slot and the w2 kernel may run one wave per slot
   int rc = gemv_w2(act, d.dtype, T, d.hidden, d.inter, K, w, slots, d.scratch_w2,
                    d.scratch_w2_stride, out, st, p ? p->start : nullptr, p ? p->stop : nullptr,
-                   skip_if);
+                   skip_if, d.cap);
   if (p && rc == WISP_OK) p->pending = true;
   if (launched) *launched = p;
   return rc;
