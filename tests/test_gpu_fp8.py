@@ -159,6 +159,30 @@ def test_experts_fp8_absent_slot_and_slot_placement(algo):
     assert _rel(got, want) < REL_TOL
 
 
+def test_experts_fp8_one_token_absent_slots():
+    """One-token calls run their own w13 kernel: a slot of -1 or past the
+    scratch contributes nothing there too, with the act rows of those pairs
+    zero, and the other pairs keep the bytes of the full call."""
+    T, H, I, E, K, block = 1, 1024, 384, 10, 5, (128, 128)
+    _, w13, w2, s13, s2 = _experts(E, H, I, block, seed=11)
+    ids, tw = _routing(T, E, K, seed=12)
+    x = torch.randn((T, H), generator=torch.Generator().manual_seed(13)).to(torch.bfloat16)
+    full, full_act = _run_experts(x, ids, tw, w13, w2, s13, s2, block)
+    sl = ids.copy()
+    sl[0, 1] = -1
+    sl[0, 3] = E + 2  # past the nslots = E slots of the scratch
+    got, act = _run_experts(x, ids, tw, w13, w2, s13, s2, block, slots=sl)
+    assert torch.count_nonzero(act[0, 1]) == 0 and torch.count_nonzero(act[0, 3]) == 0
+    for k in (0, 2, 4):
+        assert torch.equal(act[0, k].view(torch.int32), full_act[0, k].view(torch.int32)), k
+    ext = list(range(E)) + [0]
+    emap = np.concatenate([np.zeros(E, np.int32), [-1]])
+    absent = (sl < 0) | (sl >= E)
+    want = F.moe_forward_fp8(x, tw, np.where(absent, E, ids), _rows(w13, ext), _rows(w2, ext),
+                             _rows(s13, ext), _rows(s2, ext), block, expert_map=emap)
+    assert _rel(got, want) < REL_TOL
+
+
 @pytest.mark.parametrize("algo", ALGOS)
 def test_experts_fp8_batching_is_byte_invariant(algo):
     """A token's output does not depend on the other tokens of the launch

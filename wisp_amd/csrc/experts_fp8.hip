@@ -51,7 +51,7 @@ int experts_fp8(const void* x, int T, int H, int I, int K, const float* topk_w,
                 const int32_t* slots, int nslots, const void* w13, size_t w13_stride,
                 const float* s13, size_t s13_stride, const void* w2, size_t w2_stride,
                 const float* s2, size_t s2_stride, int block_n, void* act, void* out,
-                hipStream_t st, const StageEvents* ev);
+                hipStream_t st, const StageEvents* ev, bool pager_slots);
 const char* fp8_unsupported(int H, int I, int K, int block_n, int block_k);
 int experts_fp8_grouped(const void* x, int T, int H, int I, int K, const float* topk_w,
                         const int32_t* slots, int nslots, const void* w13, size_t w13_stride,
@@ -379,6 +379,137 @@ __global__ __launch_bounds__(NW * 64) void fp8_w13_kernel(
     }
     __syncthreads();  // red is rewritten by the next column set
   }
+}
+
+// A word loaded before the loads that follow it in the source: the compiler
+// neither sinks nor reorders a relaxed atomic load (plain loads of
+// restrict-qualified data it may move below later loads).
+__device__ inline int32_t load_first(const int32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// ---------------------------------------------------------------------------
+// w13 + silu_and_mul for a one-token call.  A token's routed experts are
+// distinct, so every block computes its own pair (no search for other pairs
+// of its slot), and the token's activation loads go out first, with no wait
+// before them.  SLOTS (the call fills every slot: top-k == cap and the slots
+// come from the pager): blockIdx.y is a slot, whose weight and scale loads go
+// out before the slot table is read; the table then names the pair to store
+// (slot 0's blocks store zeros for pairs that name no slot of the scratch).
+// Per output the steps are fp8_w13_kernel's with one MFMA column, so act is
+// the same bit for bit.  Dynamic LDS: w13_lds(NW, 1).
+// ---------------------------------------------------------------------------
+template <int NW, bool SLOTS>
+__global__ __launch_bounds__(NW * 64) void fp8_w13_one_kernel(
+    const uint16_t* __restrict__ x, int H, int I, int K, const int32_t* __restrict__ slots,
+    int nslots, const uint8_t* __restrict__ w13, size_t w13_stride, const float* __restrict__ s13,
+    size_t s13_stride, int block_n, uint16_t* __restrict__ act) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  float* red = reinterpret_cast<float*>(smem);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int col = lane & 15, grp = lane >> 4;
+  const int i0 = blockIdx.x * 16;
+  const int nkb = H / kKB;
+  const int per = (nkb + NW - 1) / NW;
+  const int kb0 = min(nkb, wave * per), kb1 = min(nkb, kb0 + per);
+  float* xs = reinterpret_cast<float*>(smem + NW * 2 * 64 * 4 * sizeof(float) +
+                                       (size_t)wave * kKC * (4 + kKB));
+  uint8_t* xq = reinterpret_cast<uint8_t*>(xs + kKC);
+
+  // the first chunk's activation loads, ahead of everything else (a wave
+  // without k-blocks loads the last one and drops it)
+  const int kbx = min(kb0 + min(grp, max(min(kKC, kb1 - kb0), 1) - 1), nkb - 1);
+  u32x4 xv = *reinterpret_cast<const u32x4*>(x + (size_t)kbx * kKB + col * 8);
+  int s, sl = -1;
+  bool absent = false;  // this block's pair reads no expert: it stores zeros
+  if (SLOTS) {
+    s = blockIdx.y;
+    sl = load_first(slots + min(lane, K - 1));  // lane j < K: pair j's slot
+  } else {
+    s = slots[blockIdx.y];
+    absent = s < 0 || s >= nslots;
+    if (absent) s = 0;  // loads from slot 0, dropped (no branch around them)
+  }
+  const uint8_t* W = w13 + (size_t)s * w13_stride;
+  const float* Sg = s13 + (size_t)s * s13_stride + (size_t)(i0 / block_n) * nkb;
+  const float* Su = s13 + (size_t)s * s13_stride + (size_t)((I + i0) / block_n) * nkb;
+  const uint8_t* rowg = W + (size_t)(i0 + col) * H + grp * 32;
+  const uint8_t* rowu = W + (size_t)(I + i0 + col) * H + grp * 32;
+
+  f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
+  for (int kc = kb0; kc < kb1; kc += kKC) {
+    const int nk = min(kKC, kb1 - kc);
+    if (kc != kb0)
+      xv = *reinterpret_cast<const u32x4*>(x + (size_t)(kc + min(grp, nk - 1)) * kKB + col * 8);
+    i32x8 wg[kKC], wu[kKC];
+    float sg[kKC], su[kKC];
+#pragma unroll
+    for (int kbi = 0; kbi < kKC; ++kbi) {
+      const int kb = kc + min(kbi, nk - 1);
+      wg[kbi] = ld32(rowg + (size_t)kb * kKB);
+      wu[kbi] = ld32(rowu + (size_t)kb * kKB);
+      sg[kbi] = Sg[kb];
+      su[kbi] = Su[kb];
+    }
+    {
+      float v[8];
+      unpack_bf16x8(xv, v);
+      uint32_t q[2];
+      const float sc = quant8(v, q);
+      if (grp < nk) {
+        *reinterpret_cast<uint2*>(xq + (size_t)grp * kKB + col * 8) = make_uint2(q[0], q[1]);
+        if (col == 0) xs[grp] = sc;
+      }
+    }
+    wave_lds_sync();
+#pragma unroll
+    for (int kbi = 0; kbi < kKC; ++kbi) {
+      if (kbi < nk) {
+        const i32x8 b = col == 0 ? lds32(xq + (size_t)kbi * kKB + grp * 32) : zero8();
+        const float sa = col == 0 ? xs[kbi] : 0.f;
+        const f32x4 dg = mfma_fp8(wg[kbi], b);
+        const f32x4 du = mfma_fp8(wu[kbi], b);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          ag[j] = ag[j] + (dg[j] * sa) * sg[kbi];
+          au[j] = au[j] + (du[j] * sa) * su[kbi];
+        }
+      }
+    }
+    wave_lds_sync();  // the slice is rewritten by the next chunk
+  }
+  float* rw = red + ((size_t)wave * 2 * 64 + lane) * 4;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    rw[j] = ag[j];
+    rw[64 * 4 + j] = au[j];
+  }
+  int p = blockIdx.y;
+  uint64_t none = 0;  // SLOTS: pairs whose slot lies outside the scratch
+  if (SLOTS) {
+    const uint64_t mine = __ballot(lane < K && sl == s);
+    p = mine ? __builtin_ctzll(mine) : -1;
+    none = s == 0 ? __ballot(lane < K && (sl < 0 || sl >= nslots)) : 0;
+  }
+  const int zp = absent ? p : -1;  // stored as zeros below
+  if (absent) p = -1;
+  __syncthreads();
+  if (wave == 0 && col == 0 && p >= 0) {
+    float g[4] = {0.f, 0.f, 0.f, 0.f}, u[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int w = 0; w < NW; ++w) {
+      const float* rr = red + ((size_t)w * 2 * 64 + lane) * 4;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        g[j] = g[j] + rr[j];
+        u[j] = u[j] + rr[64 * 4 + j];
+      }
+    }
+    store_act4(act + (size_t)p * I + i0 + grp * 4, f32x4{g[0], g[1], g[2], g[3]},
+               f32x4{u[0], u[1], u[2], u[3]});
+  }
+  for (; none; none &= none - 1)
+    if (threadIdx.x < 16) act[(size_t)__builtin_ctzll(none) * I + i0 + threadIdx.x] = 0;
+  if (zp >= 0 && threadIdx.x < 16) act[(size_t)zp * I + i0 + threadIdx.x] = 0;
 }
 
 // ---------------------------------------------------------------------------
@@ -999,6 +1130,25 @@ hipError_t launch_w13(const W13Args& a, hipStream_t st, hipEvent_t e0, hipEvent_
   return hipGetLastError();
 }
 
+// The one-token w13 kernel: one block per (16-row tile, pair), or per
+// (tile, slot) with SLOTS.
+template <int NW, bool SLOTS>
+hipError_t launch_w13_one(const W13Args& a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
+  static std::atomic<uint64_t> big_lds{0};
+  const auto kern = &fp8_w13_one_kernel<NW, SLOTS>;
+  const size_t lds = w13_lds(NW, 1);
+  hipError_t e = allow_lds(kern, lds, kMaxLds, &big_lds);
+  if (e != hipSuccess) return e;
+  const dim3 grid(a.I / 16, SLOTS ? a.nslots : a.P), block(NW * 64);
+  if (e0)
+    hipExtLaunchKernelGGL(kern, grid, block, lds, st, e0, e1, 0, a.x, a.H, a.I, a.K, a.slots,
+                          a.nslots, a.w13, a.w13_stride, a.s13, a.s13_stride, a.block_n, a.act);
+  else
+    hipLaunchKernelGGL(kern, grid, block, lds, st, a.x, a.H, a.I, a.K, a.slots, a.nslots, a.w13,
+                       a.w13_stride, a.s13, a.s13_stride, a.block_n, a.act);
+  return hipGetLastError();
+}
+
 struct W2Args {
   const uint16_t* act;
   int H, I, K, T;
@@ -1168,16 +1318,20 @@ int experts_fp8_grouped(const void* x, int T, int H, int I, int K, const float* 
   return WISP_OK;
 }
 
+// pager_slots: the slots come from the pager, so a token's pairs name
+// distinct slots of the scratch, and a one-token call with K == nslots
+// fills every slot (the w13 kernel then lays its blocks out by slot).
 int experts_fp8(const void* x, int T, int H, int I, int K, const float* topk_w,
                 const int32_t* slots, int nslots, const void* w13, size_t w13_stride,
                 const float* s13, size_t s13_stride, const void* w2, size_t w2_stride,
                 const float* s2, size_t s2_stride, int block_n, void* act, void* out,
-                hipStream_t st, const StageEvents* ev) {
+                hipStream_t st, const StageEvents* ev, bool pager_slots) {
   if (T == 0) return WISP_OK;
   const int P = T * K;
   const W13Args a13 = {(const uint16_t*)x, H, I, K, P, slots, nslots, (const uint8_t*)w13,
                        w13_stride, s13, s13_stride, block_n, (uint16_t*)act};
   hipEvent_t e0 = ev ? ev->ev[0] : nullptr, e1 = ev ? ev->ev[1] : nullptr;
+  const bool by_slot = T == 1 && pager_slots && K == nslots;
   // MFMA columns per pass: a decode token needs one; pairs sharing a slot
   // are at most T (a token's experts are distinct)
   const int ncol = T == 1 ? 1 : T <= 4 ? 4 : 16;
@@ -1185,11 +1339,11 @@ int experts_fp8(const void* x, int T, int H, int I, int K, const float* topk_w,
   using L13 = hipError_t (*)(const W13Args&, hipStream_t, hipEvent_t, hipEvent_t);
   L13 l13;
   if (w13_waves(H) == 4)
-    l13 = ncol == 1 ? &launch_w13<4, 1, false>
+    l13 = ncol == 1 ? (by_slot ? &launch_w13_one<4, true> : &launch_w13_one<4, false>)
         : ncol == 4 ? &launch_w13<4, 4, false>
         : big ? &launch_w13<4, 16, true> : &launch_w13<4, 16, false>;
   else
-    l13 = ncol == 1 ? &launch_w13<8, 1, false>
+    l13 = ncol == 1 ? (by_slot ? &launch_w13_one<8, true> : &launch_w13_one<8, false>)
         : ncol == 4 ? &launch_w13<8, 4, false>
         : big ? &launch_w13<8, 16, true> : &launch_w13<8, 16, false>;
   WISP_HIP_TRY(l13(a13, st, e0, e1));
@@ -1271,7 +1425,8 @@ extern "C" int wisp_moe_experts_fp8(const void* x, int T, int H, int I, int K,
                                s13_stride, w2, w2_stride, s2, s2_stride, block_n, act, out, work,
                                work_bytes, (hipStream_t)stream, nullptr);
   return experts_fp8(x, T, H, I, K, topk_w, slots, nslots, w13, w13_stride, s13, s13_stride, w2,
-                     w2_stride, s2, s2_stride, block_n, act, out, (hipStream_t)stream, nullptr);
+                     w2_stride, s2, s2_stride, block_n, act, out, (hipStream_t)stream, nullptr,
+                     false);
 }
 
 extern "C" size_t wisp_moe_fp8_work_bytes(int T, int K, int H, int I, int nslots) {

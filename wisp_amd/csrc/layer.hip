@@ -85,7 +85,7 @@ int experts_fp8(const void* x, int T, int H, int I, int K, const float* topk_w,
                 const int32_t* slots, int nslots, const void* w13, size_t w13_stride,
                 const float* s13, size_t s13_stride, const void* w2, size_t w2_stride,
                 const float* s2, size_t s2_stride, int block_n, void* act, void* out,
-                hipStream_t st, const StageEvents* ev);
+                hipStream_t st, const StageEvents* ev, bool pager_slots);
 const char* fp8_unsupported(int H, int I, int K, int block_n, int block_k);
 int experts_fp8_grouped(const void* x, int T, int H, int I, int K, const float* topk_w,
                         const int32_t* slots, int nslots, const void* w13, size_t w13_stride,
@@ -533,7 +533,7 @@ int experts(Layer& L, const void* x, int T, int K, const float* w, const int32_t
                  : experts_fp8(x, T, d.hidden, d.inter, K, w, slots, d.cap, d.scratch_w13,
                                d.scratch_w13_stride, d.scratch_s13, d.scratch_s13_stride,
                                d.scratch_w2, d.scratch_w2_stride, d.scratch_s2,
-                               d.scratch_s2_stride, d.block_n, act, out, st, pe);
+                               d.scratch_s2_stride, d.block_n, act, out, st, pe, true);
     if (rc == WISP_OK && p13 && p2) p13->pending = p2->pending = true;
     return rc;
   }
