@@ -47,12 +47,48 @@ __device__ inline void wave_lds_sync() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
+// v of the lane that DPP control kCtrl names (all rows and banks enabled).
+template <int kCtrl>
+__device__ inline float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), kCtrl, 0xF, 0xF, false));
+}
+
+// v of lane `lane` (wave-uniform), through a scalar register.
+__device__ inline float readlane_f32(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// Max over each 16-lane row of the wave, in every lane of the row: xor 1,
+// xor 2, half-row mirror, row mirror.  Register-only (DPP), where a lane
+// shuffle goes through the LDS crossbar; max is exact and commutative, so
+// the order of the steps does not change the result.
+__device__ inline float row16_max_f32(float v) {
+  v = fmaxf(v, dpp_f32<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_f32<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp_f32<0x141>(v));  // row_half_mirror
+  v = fmaxf(v, dpp_f32<0x140>(v));  // row_mirror
+  return v;
+}
+
+// Block barrier for LDS data only: this wave's LDS accesses complete, then
+// every wave meets.  __syncthreads() also waits for the wave's outstanding
+// global loads (on CDNA its fence waits for the whole vector memory
+// counter), so a block that has weight loads in flight while it stages data
+// in LDS would wait for the weights at the barrier.
+__device__ inline void block_lds_sync() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt/expcnt left at max
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // float -> bfloat16 bits, round to nearest even (a NaN stays a quiet NaN).
+// Branch-free: both results are formed and one is selected.
 __device__ inline uint16_t bf16_rne(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t r = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  const bool nan = (u & 0x7fffffffu) > 0x7f800000u;
+  return (uint16_t)(nan ? ((u >> 16) | 0x40u) : r);
 }
 
 // bfloat16 bits -> float.

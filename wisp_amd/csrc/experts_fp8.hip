@@ -129,12 +129,8 @@ __device__ inline i32x8 zero8() {
   return r;
 }
 
-// Max over the 16 lanes of this lane's quarter-wave.
-__device__ inline float quarter_max(float v) {
-#pragma unroll
-  for (int o = 8; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  return v;
-}
+// Max over the 16 lanes of this lane's quarter-wave (one DPP row).
+__device__ inline float quarter_max(float v) { return row16_max_f32(v); }
 
 // Quantises one 128-value group held 8 values per lane by the 16 lanes of a
 // quarter-wave (per_token_group_quant_fp8): returns the scale and the 8 codes
@@ -222,7 +218,7 @@ __device__ inline int slot_of(const int32_t* __restrict__ slots, const int (&v)[
     int r = -1;
 #pragma unroll
     for (int c = 0; c < kPairRegs; ++c)
-      if (p / 64 == c) r = __shfl(v[c], p % 64);
+      if (p / 64 == c) r = __builtin_amdgcn_readlane(v[c], p % 64);
     return r;
   }
 }
@@ -313,7 +309,7 @@ __global__ __launch_bounds__(NW * 64) void fp8_w13_kernel(
       u32x4 xv[NCOL];
 #pragma unroll
       for (int c = 0; c < NCOL; ++c) {
-        const int tok = __shfl(mytok, min(c, npc - 1));
+        const int tok = __builtin_amdgcn_readlane(mytok, min(c, npc - 1));
         xv[c] = *reinterpret_cast<const u32x4*>(x + (size_t)tok * H +
                                                 (size_t)(kc + min(grp, nk - 1)) * kKB + col * 8);
       }
@@ -397,9 +393,11 @@ __device__ inline int32_t load_first(const int32_t* p) {
 // out before the slot table is read; the table then names the pair to store
 // (slot 0's blocks store zeros for pairs that name no slot of the scratch).
 // Per output the steps are fp8_w13_kernel's with one MFMA column, so act is
-// the same bit for bit.  Dynamic LDS: w13_lds(NW, 1).
+// the same bit for bit.  Each of the NW waves takes KC k-blocks of H per
+// chunk.  Dynamic LDS: red [NW][2][64][4] f32, then per wave xs [KC] f32 and
+// xq [KC][kKB] codes.
 // ---------------------------------------------------------------------------
-template <int NW, bool SLOTS>
+template <int NW, int KC, bool SLOTS>
 __global__ __launch_bounds__(NW * 64) void fp8_w13_one_kernel(
     const uint16_t* __restrict__ x, int H, int I, int K, const int32_t* __restrict__ slots,
     int nslots, const uint8_t* __restrict__ w13, size_t w13_stride, const float* __restrict__ s13,
@@ -413,12 +411,12 @@ __global__ __launch_bounds__(NW * 64) void fp8_w13_one_kernel(
   const int per = (nkb + NW - 1) / NW;
   const int kb0 = min(nkb, wave * per), kb1 = min(nkb, kb0 + per);
   float* xs = reinterpret_cast<float*>(smem + NW * 2 * 64 * 4 * sizeof(float) +
-                                       (size_t)wave * kKC * (4 + kKB));
-  uint8_t* xq = reinterpret_cast<uint8_t*>(xs + kKC);
+                                       (size_t)wave * KC * (4 + kKB));
+  uint8_t* xq = reinterpret_cast<uint8_t*>(xs + KC);
 
   // the first chunk's activation loads, ahead of everything else (a wave
   // without k-blocks loads the last one and drops it)
-  const int kbx = min(kb0 + min(grp, max(min(kKC, kb1 - kb0), 1) - 1), nkb - 1);
+  const int kbx = min(kb0 + min(grp, max(min(KC, kb1 - kb0), 1) - 1), nkb - 1);
   u32x4 xv = *reinterpret_cast<const u32x4*>(x + (size_t)kbx * kKB + col * 8);
   int s, sl = -1;
   bool absent = false;  // this block's pair reads no expert: it stores zeros
@@ -437,14 +435,14 @@ __global__ __launch_bounds__(NW * 64) void fp8_w13_one_kernel(
   const uint8_t* rowu = W + (size_t)(I + i0 + col) * H + grp * 32;
 
   f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
-  for (int kc = kb0; kc < kb1; kc += kKC) {
-    const int nk = min(kKC, kb1 - kc);
+  for (int kc = kb0; kc < kb1; kc += KC) {
+    const int nk = min(KC, kb1 - kc);
     if (kc != kb0)
       xv = *reinterpret_cast<const u32x4*>(x + (size_t)(kc + min(grp, nk - 1)) * kKB + col * 8);
-    i32x8 wg[kKC], wu[kKC];
-    float sg[kKC], su[kKC];
+    i32x8 wg[KC], wu[KC];
+    float sg[KC], su[KC];
 #pragma unroll
-    for (int kbi = 0; kbi < kKC; ++kbi) {
+    for (int kbi = 0; kbi < KC; ++kbi) {
       const int kb = kc + min(kbi, nk - 1);
       wg[kbi] = ld32(rowg + (size_t)kb * kKB);
       wu[kbi] = ld32(rowu + (size_t)kb * kKB);
@@ -462,17 +460,30 @@ __global__ __launch_bounds__(NW * 64) void fp8_w13_one_kernel(
       }
     }
     wave_lds_sync();
+    // every lane reads its group's column-0 operand (the other columns'
+    // results are never used, and one column's result does not depend on
+    // the others), so the reads and MFMAs of the chunk are independent;
+    // only the scaled sums run in k-block order
+    i32x8 b[KC];
+    float sa[KC];
 #pragma unroll
-    for (int kbi = 0; kbi < kKC; ++kbi) {
+    for (int kbi = 0; kbi < KC; ++kbi) {
+      b[kbi] = lds32(xq + (size_t)min(kbi, nk - 1) * kKB + grp * 32);
+      sa[kbi] = xs[min(kbi, nk - 1)];
+    }
+    f32x4 dg[KC], du[KC];
+#pragma unroll
+    for (int kbi = 0; kbi < KC; ++kbi) {
+      dg[kbi] = mfma_fp8(wg[kbi], b[kbi]);
+      du[kbi] = mfma_fp8(wu[kbi], b[kbi]);
+    }
+#pragma unroll
+    for (int kbi = 0; kbi < KC; ++kbi) {
       if (kbi < nk) {
-        const i32x8 b = col == 0 ? lds32(xq + (size_t)kbi * kKB + grp * 32) : zero8();
-        const float sa = col == 0 ? xs[kbi] : 0.f;
-        const f32x4 dg = mfma_fp8(wg[kbi], b);
-        const f32x4 du = mfma_fp8(wu[kbi], b);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          ag[j] = ag[j] + (dg[j] * sa) * sg[kbi];
-          au[j] = au[j] + (du[j] * sa) * su[kbi];
+          ag[j] = ag[j] + (dg[kbi][j] * sa[kbi]) * sg[kbi];
+          au[j] = au[j] + (du[kbi][j] * sa[kbi]) * su[kbi];
         }
       }
     }
@@ -493,7 +504,7 @@ __global__ __launch_bounds__(NW * 64) void fp8_w13_one_kernel(
   }
   const int zp = absent ? p : -1;  // stored as zeros below
   if (absent) p = -1;
-  __syncthreads();
+  block_lds_sync();
   if (wave == 0 && col == 0 && p >= 0) {
     float g[4] = {0.f, 0.f, 0.f, 0.f}, u[4] = {0.f, 0.f, 0.f, 0.f};
     for (int w = 0; w < NW; ++w) {
@@ -586,7 +597,7 @@ __global__ __launch_bounds__(NW * 64) void fp8_w2_kernel(
   // under a branch would make the wait before the quantisation below count
   // them too.
   const int j0 = wave;
-  const int s0 = j0 < njob ? __shfl(sk, min(j0, njob - 1) / WP) : -1;
+  const int s0 = j0 < njob ? __builtin_amdgcn_readlane(sk, min(j0, njob - 1) / WP) : -1;
   const int kbs0 = min(nkb, (j0 % WP) * per);
   const int kbe0 = min(nkb, kbs0 + per);
   {
@@ -608,11 +619,11 @@ __global__ __launch_bounds__(NW * 64) void fp8_w2_kernel(
     load_round(g0);
     quant_round(g0);
   }
-  __syncthreads();
+  block_lds_sync();  // the first job's weights stay in flight
 
   for (int j = wave; j < njob; j += NW) {
     const int k = j / WP;
-    const int s = j == j0 ? s0 : __shfl(sk, k);
+    const int s = j == j0 ? s0 : __builtin_amdgcn_readlane(sk, k);
     const int kbs = j == j0 ? kbs0 : min(nkb, (j % WP) * per);
     const int kbe = j == j0 ? kbe0 : min(nkb, kbs + per);
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -650,22 +661,153 @@ __global__ __launch_bounds__(NW * 64) void fp8_w2_kernel(
     }
   }
   __syncthreads();
-  if (wave == 0) {  // every lane runs the loop (shuffles); lanes < 16 store
+  if (wave == 0) {  // lanes < 16 store
+    // pair k's slot and weight come through scalar registers and every
+    // job wrote its partials, so the k steps' LDS reads do not wait on each
+    // other; only the sum runs in routing order
     const int r = lane & 15;
     const bool bf16_adds = K >= 2 && K <= 4;
     float sum = 0.f;
-    for (int k = 0; k < K; ++k) {
-      const int s = __shfl(sk, k);
-      const float w = __shfl(wk, k);
-      float y = 0.f;
-      if (s >= 0) {
-        float v = 0.f;
-        for (int q = 0; q < WP; ++q) v = v + part[((size_t)k * WP + q) * 16 + r];
-        y = round_bf16(v * w);
+    for (int k0 = 0; k0 < K; k0 += 8) {
+      float v[8];
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+        const int k = min(k0 + kk, K - 1);
+        v[kk] = 0.f;
+        for (int q = 0; q < WP; ++q) v[kk] = v[kk] + part[((size_t)k * WP + q) * 16 + r];
       }
-      sum = bf16_adds ? round_bf16(sum + y) : sum + y;
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+        const int k = k0 + kk;
+        if (k < K) {
+          const int s = __builtin_amdgcn_readlane(sk, k);
+          const float y = s >= 0 ? round_bf16(v[kk] * readlane_f32(wk, k)) : 0.f;
+          sum = bf16_adds ? round_bf16(sum + y) : sum + y;
+        }
+      }
     }
     if (lane < 16) out[(size_t)t * H + h0 + r] = bf16_rne(sum);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// w2 + routing weight + moe_sum for a one-token call with K <= 16 and
+// KB = I / 128 <= 8 k-blocks.  Block = K waves over one 16-row tile of H;
+// wave w quantises pair w's act into LDS and streams one expert's tile: pair
+// w's slot, or slot w with SLOTS (the call fills every slot: top-k == cap,
+// slots from the pager), whose loads then go out before the slot table
+// arrives.  Everything a wave needs after the LDS barrier is read at once
+// and its KB MFMAs are independent; only the scaled sums run in k-block
+// order.  Per output the steps are fp8_w2_kernel's with one job per pair, so
+// the bytes are the same.  Dynamic LDS: aq [K][I] codes, as [K][KB] f32,
+// part [K][16] f32.
+// ---------------------------------------------------------------------------
+template <int KB, bool SLOTS>
+__global__ __launch_bounds__(1024) void fp8_w2_one_kernel(
+    const uint16_t* __restrict__ act, int H, int I, int K, const float* __restrict__ topk_w,
+    const int32_t* __restrict__ slots, int nslots, const uint8_t* __restrict__ w2,
+    size_t w2_stride, const float* __restrict__ s2, size_t s2_stride, int block_n,
+    uint16_t* __restrict__ out) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int col = lane & 15, grp = lane >> 4;
+  const int h0 = blockIdx.x * 16;
+  uint8_t* aq = smem;
+  float* as = reinterpret_cast<float*>(smem + (size_t)K * I);
+  float* part = as + (size_t)K * KB;
+
+  // lane j < K: pair j's slot and routing weight (a slot outside the
+  // scratch contributes zero)
+  const int jl = min(lane, K - 1);
+  int sj = load_first(slots + jl);
+  const float wj = __int_as_float(load_first((const int32_t*)topk_w + jl));
+  // pair `wave`'s act: quarter-wave g quantises k-blocks g and g + 4
+  u32x4 av[2];
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int kb = min(grp + 4 * it, KB - 1);
+    av[it] = *reinterpret_cast<const u32x4*>(act + (size_t)wave * I + (size_t)kb * kKB + col * 8);
+  }
+  // the tile this wave streams: slot `wave`, or pair `wave`'s slot
+  if (sj >= nslots) sj = -1;
+  const int s = SLOTS ? wave : __builtin_amdgcn_readlane(sj, wave);
+  const int sl = s >= 0 ? s : 0;  // an absent pair reads slot 0 and drops it
+  const uint8_t* row = w2 + (size_t)sl * w2_stride + (size_t)(h0 + col) * I + grp * 32;
+  const float* S = s2 + (size_t)sl * s2_stride + (size_t)(h0 / block_n) * KB;
+  i32x8 a[KB];
+  float sw[KB];
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb) {
+    a[kb] = ld32(row + (size_t)kb * kKB);
+    sw[kb] = S[kb];
+  }
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    float v[8];
+    unpack_bf16x8(av[it], v);
+    uint32_t q[2];
+    const float sc = quant8(v, q);
+    const int kb = grp + 4 * it;
+    if (kb < KB) {
+      *reinterpret_cast<uint2*>(aq + (size_t)wave * I + (size_t)kb * kKB + col * 8) =
+          make_uint2(q[0], q[1]);
+      if (col == 0) as[wave * KB + kb] = sc;
+    }
+  }
+  block_lds_sync();  // the tile's loads stay in flight
+  // the pair this wave's tile serves (-1: none)
+  int p = wave;
+  if (SLOTS) {
+    const uint64_t m = __ballot(lane < K && sj == s);
+    p = m ? __builtin_ctzll(m) : -1;
+  } else if (s < 0) {
+    p = -1;
+  }
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  if (p >= 0) {
+    // every lane reads its group's column-0 operand (the other columns'
+    // results are never used, and one column's result does not depend on
+    // the others)
+    i32x8 b[KB];
+    float sa[KB];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      b[kb] = lds32(aq + (size_t)p * I + (size_t)kb * kKB + grp * 32);
+      sa[kb] = as[p * KB + kb];
+    }
+    f32x4 d[KB];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) d[kb] = mfma_fp8(a[kb], b[kb]);
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc[q] = acc[q] + (d[kb][q] * sa[kb]) * sw[kb];
+  }
+  if (col == 0 && p >= 0) {  // an absent pair's partials are never read
+    float* pr = part + (size_t)p * 16 + grp * 4;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) pr[q] = acc[q];
+  }
+  block_lds_sync();
+  if (wave == 0) {  // lanes < 16 store
+    const int r = lane & 15;
+    const bool bf16_adds = K >= 2 && K <= 4;
+    float sum = 0.f;
+    for (int k0 = 0; k0 < K; k0 += 8) {
+      float v[8];
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) v[kk] = 0.f + part[(size_t)min(k0 + kk, K - 1) * 16 + r];
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+        const int k = k0 + kk;
+        if (k < K) {
+          const float y = __builtin_amdgcn_readlane(sj, k) >= 0
+                              ? round_bf16(v[kk] * readlane_f32(wj, k)) : 0.f;
+          sum = bf16_adds ? round_bf16(sum + y) : sum + y;
+        }
+      }
+    }
+    if (lane < 16) out[(size_t)h0 + r] = bf16_rne(sum);
   }
 }
 
@@ -1132,11 +1274,11 @@ hipError_t launch_w13(const W13Args& a, hipStream_t st, hipEvent_t e0, hipEvent_
 
 // The one-token w13 kernel: one block per (16-row tile, pair), or per
 // (tile, slot) with SLOTS.
-template <int NW, bool SLOTS>
+template <int NW, int KC, bool SLOTS>
 hipError_t launch_w13_one(const W13Args& a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
   static std::atomic<uint64_t> big_lds{0};
-  const auto kern = &fp8_w13_one_kernel<NW, SLOTS>;
-  const size_t lds = w13_lds(NW, 1);
+  const auto kern = &fp8_w13_one_kernel<NW, KC, SLOTS>;
+  const size_t lds = (size_t)NW * 2 * 64 * 4 * sizeof(float) + (size_t)NW * KC * (4 + kKB);
   hipError_t e = allow_lds(kern, lds, kMaxLds, &big_lds);
   if (e != hipSuccess) return e;
   const dim3 grid(a.I / 16, SLOTS ? a.nslots : a.P), block(NW * 64);
@@ -1179,6 +1321,42 @@ hipError_t launch_w2(const W2Args& a, hipStream_t st, hipEvent_t e0, hipEvent_t 
     hipLaunchKernelGGL(kern, grid, block, lds, st, a.act, a.H, a.I, a.K, a.topk_w, a.slots,
                        a.nslots, a.w2, a.w2_stride, a.s2, a.s2_stride, a.block_n, a.WP, a.out);
   return hipGetLastError();
+}
+
+// The one-token w2 kernel for I = KB * 128.
+template <int KB, bool SLOTS>
+hipError_t launch_w2_one(const W2Args& a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
+  static std::atomic<uint64_t> big_lds{0};
+  const auto kern = &fp8_w2_one_kernel<KB, SLOTS>;
+  const size_t lds = (size_t)a.K * a.I + (size_t)a.K * KB * 4 + (size_t)a.K * 16 * 4;
+  hipError_t e = allow_lds(kern, lds, kMaxLds, &big_lds);
+  if (e != hipSuccess) return e;
+  const dim3 grid(a.H / 16), block(a.K * 64);
+  if (e0)
+    hipExtLaunchKernelGGL(kern, grid, block, lds, st, e0, e1, 0, a.act, a.H, a.I, a.K, a.topk_w,
+                          a.slots, a.nslots, a.w2, a.w2_stride, a.s2, a.s2_stride, a.block_n,
+                          a.out);
+  else
+    hipLaunchKernelGGL(kern, grid, block, lds, st, a.act, a.H, a.I, a.K, a.topk_w, a.slots,
+                       a.nslots, a.w2, a.w2_stride, a.s2, a.s2_stride, a.block_n, a.out);
+  return hipGetLastError();
+}
+
+using L2 = hipError_t (*)(const W2Args&, hipStream_t, hipEvent_t, hipEvent_t);
+
+template <bool SLOTS>
+L2 pick_w2_one(int kb) {
+  switch (kb) {
+    case 1: return &launch_w2_one<1, SLOTS>;
+    case 2: return &launch_w2_one<2, SLOTS>;
+    case 3: return &launch_w2_one<3, SLOTS>;
+    case 4: return &launch_w2_one<4, SLOTS>;
+    case 5: return &launch_w2_one<5, SLOTS>;
+    case 6: return &launch_w2_one<6, SLOTS>;
+    case 7: return &launch_w2_one<7, SLOTS>;
+    case 8: return &launch_w2_one<8, SLOTS>;
+    default: return nullptr;
+  }
 }
 
 }  // namespace
@@ -1320,7 +1498,7 @@ int experts_fp8_grouped(const void* x, int T, int H, int I, int K, const float* 
 
 // pager_slots: the slots come from the pager, so a token's pairs name
 // distinct slots of the scratch, and a one-token call with K == nslots
-// fills every slot (the w13 kernel then lays its blocks out by slot).
+// fills every slot (the one-token kernels then lay their work out by slot).
 int experts_fp8(const void* x, int T, int H, int I, int K, const float* topk_w,
                 const int32_t* slots, int nslots, const void* w13, size_t w13_stride,
                 const float* s13, size_t s13_stride, const void* w2, size_t w2_stride,
@@ -1338,13 +1516,19 @@ int experts_fp8(const void* x, int T, int H, int I, int K, const float* topk_w,
   const bool big = P > kPairRegs * 64;
   using L13 = hipError_t (*)(const W13Args&, hipStream_t, hipEvent_t, hipEvent_t);
   L13 l13;
-  if (w13_waves(H) == 4)
-    l13 = ncol == 1 ? (by_slot ? &launch_w13_one<4, true> : &launch_w13_one<4, false>)
-        : ncol == 4 ? &launch_w13<4, 4, false>
+  // one-token kernel: eight waves of two k-blocks each up to H = 2048
+  // (measured at the Qwen3-FP8 decode shape: 7.48 us, against 7.61 us for
+  // four waves of four and 7.77 us for sixteen waves of one), of four above
+  if (ncol == 1)
+    l13 = H / kKB <= 16 ? (by_slot ? &launch_w13_one<8, 2, true>
+                                   : &launch_w13_one<8, 2, false>)
+                        : (by_slot ? &launch_w13_one<8, kKC, true>
+                                   : &launch_w13_one<8, kKC, false>);
+  else if (w13_waves(H) == 4)
+    l13 = ncol == 4 ? &launch_w13<4, 4, false>
         : big ? &launch_w13<4, 16, true> : &launch_w13<4, 16, false>;
   else
-    l13 = ncol == 1 ? (by_slot ? &launch_w13_one<8, true> : &launch_w13_one<8, false>)
-        : ncol == 4 ? &launch_w13<8, 4, false>
+    l13 = ncol == 4 ? &launch_w13<8, 4, false>
         : big ? &launch_w13<8, 16, true> : &launch_w13<8, 16, false>;
   WISP_HIP_TRY(l13(a13, st, e0, e1));
 
@@ -1357,14 +1541,17 @@ int experts_fp8(const void* x, int T, int H, int I, int K, const float* topk_w,
                      w2_stride, s2, s2_stride, block_n, WP, (uint16_t*)out};
   // quantisation passes a wave needs (4 groups each), capped at 4 per round
   const int passes = (K * (I / kKB) + kW2Waves * 4 - 1) / (kW2Waves * 4);
-  using L2 = hipError_t (*)(const W2Args&, hipStream_t, hipEvent_t, hipEvent_t);
-  L2 l2;
-  if (passes <= 1)
-    l2 = kc2 == 4 ? &launch_w2<4, 1> : kc2 == 6 ? &launch_w2<6, 1> : &launch_w2<8, 1>;
-  else if (passes <= 2)
-    l2 = kc2 == 4 ? &launch_w2<4, 2> : kc2 == 6 ? &launch_w2<6, 2> : &launch_w2<8, 2>;
-  else
-    l2 = kc2 == 4 ? &launch_w2<4, 4> : kc2 == 6 ? &launch_w2<6, 4> : &launch_w2<8, 4>;
+  L2 l2 = nullptr;
+  if (T == 1 && K <= 16)  // one wave per pair or slot
+    l2 = by_slot ? pick_w2_one<true>(I / kKB) : pick_w2_one<false>(I / kKB);
+  if (!l2) {
+    if (passes <= 1)
+      l2 = kc2 == 4 ? &launch_w2<4, 1> : kc2 == 6 ? &launch_w2<6, 1> : &launch_w2<8, 1>;
+    else if (passes <= 2)
+      l2 = kc2 == 4 ? &launch_w2<4, 2> : kc2 == 6 ? &launch_w2<6, 2> : &launch_w2<8, 2>;
+    else
+      l2 = kc2 == 4 ? &launch_w2<4, 4> : kc2 == 6 ? &launch_w2<6, 4> : &launch_w2<8, 4>;
+  }
   WISP_HIP_TRY(l2(a2, st, ev ? ev->ev[2] : nullptr, ev ? ev->ev[3] : nullptr));
   return WISP_OK;
 }

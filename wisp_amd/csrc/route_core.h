@@ -49,15 +49,6 @@ __device__ inline float load_logit<uint16_t>(const uint16_t* p) {
   return __uint_as_float((uint32_t)(*p) << 16);
 }
 
-template <int kCtrl>
-__device__ inline float dpp_f32(float v) {
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), kCtrl, 0xF, 0xF, false));
-}
-
-__device__ inline float readlane_f32(float v, int lane) {
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
-}
-
 // Sum over the 64 lanes, same bits in every lane.
 __device__ inline float wave_sum_f32(float v) {
   v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
