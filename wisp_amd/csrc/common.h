@@ -82,6 +82,34 @@ __device__ inline void block_lds_sync() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
+// Sum over each 16-lane row, the same bits in every lane of the row (after
+// each step both partners hold the same bits, since IEEE add is
+// commutative).  Register-only (DPP).
+__device__ inline float row16_sum_f32(float v) {
+  v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f32<0x141>(v);  // row_half_mirror
+  v += dpp_f32<0x140>(v);  // row_mirror
+  return v;
+}
+
+// Sum over the 64 lanes, the same bits in every lane: the four row sums
+// combined in a fixed order through scalar registers.
+__device__ inline float wave_sum_f32(float v) {
+  v = row16_sum_f32(v);
+  return ((readlane_f32(v, 0) + readlane_f32(v, 16)) + readlane_f32(v, 32)) +
+         readlane_f32(v, 48);
+}
+
+// Sum over each 32-lane half of the wave, the same bits in every lane of
+// the half.
+__device__ inline float half_sum_f32(float v) {
+  v = row16_sum_f32(v);
+  const float lo = readlane_f32(v, 0) + readlane_f32(v, 16);
+  const float hi = readlane_f32(v, 32) + readlane_f32(v, 48);
+  return (__lane_id() < 32) ? lo : hi;
+}
+
 // float -> bfloat16 bits, round to nearest even (a NaN stays a quiet NaN).
 // Branch-free: both results are formed and one is selected.
 __device__ inline uint16_t bf16_rne(float f) {

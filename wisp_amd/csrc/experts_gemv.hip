@@ -7,7 +7,7 @@
 //   out[t]   = sum_{k=0..K-1} w[t,k] * (W2[s] act[t,k])     (k ascending)
 //
 // Both kernels stream weight rows with 16-byte loads, one wavefront (or half
-// of one) per row, and reduce in a fixed butterfly order, so the bytes of
+// of one) per row, and reduce in a fixed order, so the bytes of
 // out[t] depend only on x[t], the routing of token t and the weights read -
 // never on the slot numbers, on cap or on the other tokens of the launch.
 // That is what makes paged output byte-identical to resident output.
@@ -101,8 +101,8 @@ __device__ inline void load_row(const T* __restrict__ row, int nch, int lane, ui
 }
 
 // silu(gate . x) * (up . x) for the rows and x chunks a wave holds: fp32 FMA
-// over each lane's chunks in order, then a butterfly over the 64 lanes; every
-// lane returns the result.
+// over each lane's chunks in order, then wave_sum_f32 over the 64 lanes (DPP
+// row sums, then the four rows in order); every lane returns the result.
 template <typename T, int CH, typename VW>
 __device__ inline float swiglu_rows(const VW (&wg)[CH], const VW (&wu)[CH],
                                     const uint4 (&xv)[CH]) {
@@ -120,15 +120,11 @@ __device__ inline float swiglu_rows(const VW (&wg)[CH], const VW (&wu)[CH],
       au = fmaf(uf[q], xf[q], au);
     }
   }
-  for (int off = 32; off > 0; off >>= 1) {
-    ag += __shfl_xor(ag, off);
-    au += __shfl_xor(au, off);
-  }
-  return silu(ag) * au;
+  return silu(wave_sum_f32(ag)) * wave_sum_f32(au);
 }
 
 // The same dot product one row at a time: this lane's FMA chain over its
-// chunks, then the butterfly.  Each of swiglu_rows' two accumulators follows
+// chunks, then wave_sum_f32.  Each of swiglu_rows' two accumulators follows
 // exactly this sequence, so silu(row_dot(gate)) * row_dot(up) equals
 // swiglu_rows bit for bit.
 template <typename T, int CH>
@@ -143,8 +139,7 @@ __device__ inline float row_dot(const u32x4 (&w)[CH], const uint4 (&xv)[CH]) {
 #pragma unroll
     for (int q = 0; q < V; ++q) a = fmaf(wf[q], xf[q], a);
   }
-  for (int off = 32; off > 0; off >>= 1) a += __shfl_xor(a, off);
-  return a;
+  return wave_sum_f32(a);
 }
 
 // One wave: act[pair][i] of a pair whose expert sits in slot s, stored only
@@ -317,7 +312,7 @@ __global__ __launch_bounds__(256) void pagein_w13_kernel(FusedW13Args f, PageInA
 // the routing weights staged in LDS by the waves at the start (0 for an
 // absent slot).  grid = (ceil(H / ((64 / LPR) * RPH)), T).
 //
-// Each row's arithmetic (chunk order, then the butterfly over the LPR lanes,
+// Each row's arithmetic (chunk order, then the sum over the LPR lanes,
 // then the k-ordered sum) does not depend on RPH, so the row grouping is a
 // launch-shape choice only.  Measured on MI355X inside the Qwen3 bs=1 decode
 // step (dispatch events, the kernel following the w13 kernel): one row per
@@ -384,6 +379,7 @@ __global__ __launch_bounds__(1024) void w2_combine_kernel(const T* __restrict__ 
                                                            size_t w2_stride,
                                                            T* __restrict__ out,
                                                            const int32_t* __restrict__ skip_if) {
+  static_assert(LPR == 32 || LPR == 64, "a row spans half a wave or a whole wave");
   constexpr int V = Vec<T>::N;
   constexpr int RPB = 64 / LPR * RPH;  // rows per block
   constexpr int CHA = CH > 0 ? CH : 1;
@@ -449,8 +445,7 @@ __global__ __launch_bounds__(1024) void w2_combine_kernel(const T* __restrict__ 
     }
   }
 #pragma unroll
-  for (int r = 0; r < RPH; ++r)
-    for (int off = LPR / 2; off > 0; off >>= 1) d[r] += __shfl_xor(d[r], off);
+  for (int r = 0; r < RPH; ++r) d[r] = LPR == 64 ? wave_sum_f32(d[r]) : half_sum_f32(d[r]);
   if (l == 0 && p >= 0) {
 #pragma unroll
     for (int r = 0; r < RPH; ++r) part[p][sub * RPH + r] = d[r];

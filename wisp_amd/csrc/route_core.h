@@ -49,16 +49,6 @@ __device__ inline float load_logit<uint16_t>(const uint16_t* p) {
   return __uint_as_float((uint32_t)(*p) << 16);
 }
 
-// Sum over the 64 lanes, same bits in every lane.
-__device__ inline float wave_sum_f32(float v) {
-  v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
-  v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
-  v += dpp_f32<0x141>(v);  // row_half_mirror
-  v += dpp_f32<0x140>(v);  // row_mirror
-  return ((readlane_f32(v, 0) + readlane_f32(v, 16)) + readlane_f32(v, 32)) +
-         readlane_f32(v, 48);
-}
-
 // Max over the 64 lanes, same bits in every lane.
 __device__ inline float wave_max_f32(float v) {
   v = fmaxf(v, dpp_f32<0xB1>(v));
