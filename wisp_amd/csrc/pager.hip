@@ -288,13 +288,27 @@ __global__ __launch_bounds__(64) void pager_kernel(
   const bool state_in_regs = regs || (logits && cap <= VALS * 64);
   int map_r[VALS], s2e_r[VALS];
   int64_t tick_r[VALS];
+  // Register path: loads at clamped positions, with no branch around them,
+  // masked (mask_state) only after the router has issued its logit loads, so
+  // that both travel together.
+  auto mask_state = [&]() {
+#pragma unroll
+    for (int v = 0; v < VALS; ++v) {
+      const int i = v * 64 + lane;
+      if (i >= E) map_r[v] = -1;
+      if (i >= cap) {
+        s2e_r[v] = -1;
+        tick_r[v] = 0;
+      }
+    }
+  };
   if (state_in_regs) {
 #pragma unroll
     for (int v = 0; v < VALS; ++v) {
       const int i = v * 64 + lane;
-      map_r[v] = i < E ? map_g[i] : -1;
-      s2e_r[v] = i < cap ? s2e_g[i] : -1;
-      tick_r[v] = i < cap ? tick_g[i] : 0;
+      map_r[v] = map_g[min(i, E - 1)];
+      s2e_r[v] = s2e_g[min(i, cap - 1)];
+      tick_r[v] = tick_g[min(i, cap - 1)];
     }
   } else {
     for (int e = lane; e < E; e += 64) sm.map[e] = map_g[e];
@@ -322,6 +336,7 @@ __global__ __launch_bounds__(64) void pager_kernel(
         fr.ids[t * K + lane] = id;
       }
     }
+    if (state_in_regs) mask_state();
     if (state_in_regs && !regs) {
 #pragma unroll
       for (int v = 0; v < VALS; ++v) {
@@ -344,6 +359,7 @@ __global__ __launch_bounds__(64) void pager_kernel(
     for (int p = lane; p < P; p += 64) fr.ids[p] = ids_in[p];
     wave_lds_sync();
   }
+  if (!logits && state_in_regs) mask_state();
   // Every pair starts as "not computed" (slot -1, not loaded); the same lane
   // owns pair p for all later writes.
   for (int p = lane; p < P; p += 64) {

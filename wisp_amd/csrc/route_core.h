@@ -83,19 +83,20 @@ __device__ inline void route_token_wave(const TL* __restrict__ logits_row, int E
                                         int* id_out) {
   (void)RouteVals<VALS>();
   const int per = min((E + 63) >> 6, VALS);
+  // every lane loads all its logits at clamped positions (the row is valid
+  // even for an inactive token), with no branch around the loads: a load
+  // under a branch waited for everything before it, one logit at a time
+  float raw[VALS];
+#pragma unroll
+  for (int j = 0; j < VALS; ++j) raw[j] = load_logit(logits_row + min(j * 64 + lane, E - 1));
   float v[VALS];
   uint32_t taken = 0;  // bit j: entry j of this lane is not eligible
 #pragma unroll
   for (int j = 0; j < VALS; ++j) {
-    const int e = j * 64 + lane;
-    float x = -INFINITY;
-    if (active && j < per && e < E) {
-      x = load_logit(logits_row + e);
-      if (x != x) x = -INFINITY;
-    } else {
-      taken |= 1u << j;
-    }
-    v[j] = x;
+    const bool ok = active && j < per && j * 64 + lane < E;
+    const float x = raw[j];
+    v[j] = ok && x == x ? x : -INFINITY;
+    if (!ok) taken |= 1u << j;
   }
   *w_out = 0.f;
   *id_out = -1;
