@@ -30,6 +30,8 @@
 // built to stream each weight byte once per call.
 #include <type_traits>
 
+#include <algorithm>
+
 #include "common.h"
 #include "dma_pipeline.h"
 
@@ -45,7 +47,10 @@ constexpr int kPanel = 64;           // output columns per block: 4 waves x 16
 // The LDS-staged w2 kernel's blocks own 128 output rows (4 waves x 32): a
 // w2 row is only 12 chunks long at the Qwen3 shape, so per-block setup and
 // the token tile weigh more than in w13, and 32 rows per wave halve both.
+// Calls with enough (slot, panel) work for two rounds of blocks use 256 rows
+// per block (two copy stages, two blocks per CU).
 constexpr int kW2PanelsPer = 2;      // 64-row panels per LDS-staged w2 block
+constexpr int kW2PanelsBig = 4;
 
 // Work buffer carve-up (bytes, each piece 256-byte aligned).
 struct WorkLayout {
@@ -121,6 +126,16 @@ __global__ __launch_bounds__(64 * kGatherWaves) void gather_kernel(
 // slot placement or token grouping.
 __device__ inline int k_rotation(int Kdim) {
   return (int)(blockIdx.x * (unsigned)(Kdim / 64) / gridDim.x) * 64;
+}
+
+// The w2 kernel's rotation: by the block's 256-row group of H (NG 64-row
+// panels per block, NG = 2 or 4), so that blocks of 128 and of 256 rows give
+// every output row the same k order and the same bytes.
+template <int NG>
+__device__ inline int k_rotation_w2(int Kdim) {
+  static_assert(NG == 2 || NG == 4, "64-row panels per w2 block");
+  const unsigned group = blockIdx.x * NG / 4, groups = gridDim.x * NG / 4;
+  return (int)(group * (unsigned)(Kdim / 64) / groups) * 64;
 }
 
 // Column of k-step offset k (0 <= k < Kdim) in a loop rotated by rot columns.
@@ -251,7 +266,7 @@ __global__ __launch_bounds__(256) void mfma_w13_dma_kernel(
   }
 }
 
-template <int S>
+template <int S, int NG>
 __global__ __launch_bounds__(256) void mfma_w2_dma_kernel(
     const uint16_t* __restrict__ act, int H, int I, int P, const int32_t* __restrict__ lists,
     const int32_t* __restrict__ counts, const uint16_t* __restrict__ w2, size_t w2_stride,
@@ -262,7 +277,7 @@ __global__ __launch_bounds__(256) void mfma_w2_dma_kernel(
   if (M == 0) return;
   const int32_t* list = lists + (size_t)s * P;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  constexpr int NG = kW2PanelsPer;  // row groups of 16 per wave
+  // NG row groups of 16 per wave
   const int h0 = blockIdx.x * kPanel * NG + wave * 16 * NG;
   const uint16_t* W = w2 + (size_t)s * w2_stride;
   const unsigned char* wrow[16 * NG / dma::kRowsPerCopy];
@@ -270,7 +285,7 @@ __global__ __launch_bounds__(256) void mfma_w2_dma_kernel(
   for (int i = 0; i < 16 * NG / dma::kRowsPerCopy; ++i)
     wrow[i] = reinterpret_cast<const unsigned char*>(
         W + (size_t)(h0 + i * dma::kRowsPerCopy + lane / dma::kLanesPerRow) * I);
-  const int rot = k_rotation(I);
+  const int rot = k_rotation_w2<NG>(I);
   for (int m0 = 0; m0 < M; m0 += dma::kTokRows) {
     const int mrows = min(M - m0, dma::kTokRows);
     f32x4 acc[NG][4];
@@ -360,25 +375,44 @@ void launch_combine(const float* y, int T, int H, int K, int nslots, const float
                        slots, out);
 }
 
-template <int S13, int S2>
+template <int S2, int NG>
+hipError_t launch_w2_dma(const uint16_t* act, int H, int I, int P, int nslots,
+                         const int32_t* lists, const int32_t* counts, const uint16_t* w2,
+                         size_t w2_stride, float* y, hipStream_t st, hipEvent_t e2,
+                         hipEvent_t e3) {
+  constexpr unsigned b2 = dma::Smem<16 * NG, S2>::kBytes;
+  static_assert(b2 <= 160 * 1024, "LDS per block");
+  static std::atomic<uint64_t> big2{0};
+  hipError_t e = allow_lds(&mfma_w2_dma_kernel<S2, NG>, b2, b2, &big2);
+  if (e != hipSuccess) return e;
+  launch_timed_lds(mfma_w2_dma_kernel<S2, NG>, dim3(H / (kPanel * NG), nslots), dim3(256), b2,
+                   st, e2, e3, act, H, I, P, lists, counts, w2, w2_stride, y);
+  return hipSuccess;
+}
+
+template <int S13>
 hipError_t launch_dma(const uint16_t* x, int H, int I, int K, int P, int nslots,
                       const int32_t* lists, const int32_t* counts, const uint16_t* w13,
                       size_t w13_stride, const uint16_t* w2, size_t w2_stride, uint16_t* act,
                       float* y, hipStream_t st, const StageEvents* ev) {
   constexpr unsigned b13 = dma::Smem<32, S13>::kBytes;
-  constexpr unsigned b2 = dma::Smem<16 * kW2PanelsPer, S2>::kBytes;
-  static_assert(b13 <= 160 * 1024 && b2 <= 160 * 1024, "LDS per block");
-  static std::atomic<uint64_t> big13{0}, big2{0};
+  static_assert(b13 <= 160 * 1024, "LDS per block");
+  static std::atomic<uint64_t> big13{0};
   hipError_t e = allow_lds(&mfma_w13_dma_kernel<S13>, b13, b13, &big13);
-  if (e == hipSuccess) e = allow_lds(&mfma_w2_dma_kernel<S2>, b2, b2, &big2);
   if (e != hipSuccess) return e;
   hipEvent_t e0 = ev ? ev->ev[0] : nullptr, e1 = ev ? ev->ev[1] : nullptr;
   hipEvent_t e2 = ev ? ev->ev[2] : nullptr, e3 = ev ? ev->ev[3] : nullptr;
   launch_timed_lds(mfma_w13_dma_kernel<S13>, dim3(I / kPanel, nslots), dim3(256), b13, st, e0,
                    e1, x, H, I, K, P, lists, counts, w13, w13_stride, act);
-  launch_timed_lds(mfma_w2_dma_kernel<S2>, dim3(H / (kPanel * kW2PanelsPer), nslots),
-                   dim3(256), b2, st, e2, e3, act, H, I, P, lists, counts, w2, w2_stride, y);
-  return hipSuccess;
+  // 256-row w2 blocks (two stages) when the call's slots could give two
+  // blocks per CU of them; else 128-row blocks (three stages).  Measured at
+  // the Qwen3 512-token chunk: 83 against 89 us; the smaller blocks keep
+  // calls with few slots (Mixtral, paged token groups) spread over the GPU.
+  const int64_t busy = (int64_t)std::min(P, nslots) * (H / (kPanel * kW2PanelsBig));
+  return busy >= 512 ? launch_w2_dma<2, kW2PanelsBig>(act, H, I, P, nslots, lists, counts, w2,
+                                                      w2_stride, y, st, e2, e3)
+                     : launch_w2_dma<3, kW2PanelsPer>(act, H, I, P, nslots, lists, counts, w2,
+                                                      w2_stride, y, st, e2, e3);
 }
 
 }  // namespace
@@ -432,8 +466,8 @@ int experts_mfma(const void* x, int T, int H, int I, int K, const float* topk_w,
   // a third block per CU).  Measured on MI355X, these kernels also beat
   // register-streaming ones at every call size, down to 4 tokens (71 against
   // 109 us at the Qwen3 shape).
-  WISP_HIP_TRY((launch_dma<2, 3>(xb, H, I, K, P, nslots, lists, counts, a13, w13_stride, a2,
-                                 w2_stride, ab, y, st, ev)));
+  WISP_HIP_TRY((launch_dma<2>(xb, H, I, K, P, nslots, lists, counts, a13, w13_stride, a2,
+                              w2_stride, ab, y, st, ev)));
   launch_combine(y, T, H, K, nslots, topk_w, slots, (uint16_t*)out, st);
   WISP_HIP_TRY(hipGetLastError());
   return WISP_OK;
