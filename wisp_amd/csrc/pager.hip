@@ -470,7 +470,14 @@ __global__ __launch_bounds__(64) void pager_kernel(
       // ---- plan one group: tokens [start, end) -----------------------
       int end = start;
       uint32_t u[W];  // the group's needed experts (wave-uniform)
-      if (single_group || T == 1) {
+      if (regs && (single_group || T == 1) && P <= 64) {
+        // one pair per lane: the needed set by wave ORs of the pairs' bits
+        const int e = lane < P ? id_at(lane) : -1;
+#pragma unroll
+        for (int w = 0; w < W; ++w)
+          u[w] = wave_or(e >= 0 && (e >> 5) == w ? 1u << (e & 31) : 0u);
+        end = T;
+      } else if (single_group || T == 1) {
         for (int w = lane; w < nwords; w += 64) {
           sm.need[w] = 0u;
           sm.loaded[w] = 0u;
@@ -526,14 +533,18 @@ __global__ __launch_bounds__(64) void pager_kernel(
           b = wb + 64;
         }
         if (end < 0) end = T;
+        // (the register path keeps the needed set in u and the loaded
+        // experts in ballots)
+        if (!regs) {
 #pragma unroll
-        for (int w = 0; w < W; ++w)
-          if (lane == w && w < nwords) {
-            sm.need[w] = u[w];
-            sm.loaded[w] = 0u;
-          }
+          for (int w = 0; w < W; ++w)
+            if (lane == w && w < nwords) {
+              sm.need[w] = u[w];
+              sm.loaded[w] = 0u;
+            }
+        }
       }
-      wave_lds_sync();
+      if (!regs) wave_lds_sync();
       const int g = groups_planned++;
       const int t0 = start, t1 = end;
       start = end;
@@ -608,17 +619,28 @@ __global__ __launch_bounds__(64) void pager_kernel(
           int q = 0;         // this slot's place among the victims
           if (shortfall > 0) {
             if (nlru < 0) {
-              // occupied slots ranked by (tick, slot), ticks by readlane
+              // occupied slots ranked by (tick, slot), the other slots' keys
+              // by readlane: as one 32-bit key (2^25 - 1 - age) << 6 | slot
+              // when every occupied tick lies within 2^25 ticks below the
+              // clock, else as 64-bit ticks
               const int64_t ti = occ ? tick_r[0] : 0;
-              const uint32_t tlo = (uint32_t)ti, thi = (uint32_t)((uint64_t)ti >> 32);
               const uint64_t occ_bits = ballot(occ);
+              const int64_t age = clock - ti;
+              const bool near = !occ || (age >= 0 && age < (1 << 25));
               int r = 0;
-              for (int j = 0; j < cap; ++j) {
-                if (!((occ_bits >> j) & 1ull)) continue;
-                const uint64_t tj =
-                    ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)thi, j) << 32) |
-                    (uint32_t)__builtin_amdgcn_readlane((int)tlo, j);
-                r += ((int64_t)tj < ti) || ((int64_t)tj == ti && j < lane);
+              if (ballot(!near) == 0) {
+                const uint32_t key = ((uint32_t)((1 << 25) - 1 - (int)age) << 6) | (uint32_t)lane;
+                for (uint64_t b = occ_bits; b; b &= b - 1ull)
+                  r += (uint32_t)__builtin_amdgcn_readlane((int)key, __builtin_ctzll(b)) < key;
+              } else {
+                const uint32_t tlo = (uint32_t)ti, thi = (uint32_t)((uint64_t)ti >> 32);
+                for (uint64_t b = occ_bits; b; b &= b - 1ull) {
+                  const int j = __builtin_ctzll(b);
+                  const uint64_t tj =
+                      ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)thi, j) << 32) |
+                      (uint32_t)__builtin_amdgcn_readlane((int)tlo, j);
+                  r += ((int64_t)tj < ti) || ((int64_t)tj == ti && j < lane);
+                }
               }
               if (occ) sm.lru[r] = lane;
               lru_pos_r = r;

@@ -29,6 +29,19 @@ __device__ inline uint32_t wave_prefix_or(uint32_t v, int lane) {
   return v | (row >= 1 ? r0 : 0u) | (row >= 2 ? r1 : 0u) | (row >= 3 ? r2 : 0u);
 }
 
+// OR of v over the 64 lanes (wave-uniform): the row prefix ORs of
+// wave_prefix_or, then the four row totals by readlane.
+__device__ inline uint32_t wave_or(uint32_t v) {
+  v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xF, 0xF, false);  // row_shr:1
+  v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xF, 0xF, false);  // row_shr:2
+  v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, false);  // row_shr:4
+  v |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xF, 0xF, false);  // row_shr:8
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 15) |
+         (uint32_t)__builtin_amdgcn_readlane((int)v, 31) |
+         (uint32_t)__builtin_amdgcn_readlane((int)v, 47) |
+         (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
 // Insert `key` into a CPython set table of mask+1 <= 128 slots whose
 // occupancy is the bitmask (lo, hi); returns the slot (same probe sequence as
 // set_insert_clean).  All operands are wave-uniform.
@@ -122,38 +135,48 @@ __device__ inline int probe_insert32(uint32_t& occ, uint32_t mask, int key) {
 }
 
 // set_positions_wave for U <= 18 keys, whose table is 8 slots up to 4 keys
-// and 32 slots from the resize at the fifth: all bookkeeping in scalar
-// registers (occupancy words, each key's slot in a packed word), the lanes
-// touched only to hand each key its slot.  Key j is held by lane j and
+// and 32 slots from the resize at the fifth.  Key j is held by lane j and
 // inserted j-th.
+//   * When no two keys share a home slot (key & mask of the final table),
+//     no insertion probes, whatever the order: every key sits at its home
+//     slot, and the order is the home slots ascending.
+//   * Otherwise the insertions run in scalar registers (occupancy words, the
+//     8-slot table's key per slot in a packed word, so the resize re-inserts
+//     its keys by walking the occupied slots), the lanes touched only to hand
+//     each key its slot.
 __device__ inline int set_positions_small(int key, int U, int lane) {
+  const bool mine = lane < U;
+  const uint32_t home_mask = U < 5 ? 7u : 31u;
+  const uint32_t home = mine ? 1u << ((uint32_t)key & home_mask) : 0u;
+  const uint32_t homes = wave_or(home);
+  if (__popc(homes) == U) return mine ? __popc(homes & (home - 1u)) : -1;
   uint32_t occ = 0, mask = 7;
-  uint32_t slot8 = 0;  // 3-bit table-8 slot of keys 0..4
+  uint32_t key_at = 0;  // 8-slot table: index of the key in slot s, 4 bits per slot
   int myslot = -1;
   const int n8 = U < 5 ? U : 5;
   for (int j = 0; j < n8; ++j) {
-    const int kj = __builtin_amdgcn_readlane(key, j);
-    const int s = probe_insert32(occ, mask, kj);
-    slot8 |= (uint32_t)s << (3 * j);
+    const int s = probe_insert32(occ, mask, __builtin_amdgcn_readlane(key, j));
+    key_at |= (uint32_t)j << (4 * s);
     if (lane == j) myslot = s;
   }
   if (U >= 5) {
-    // resize to 32 slots: the five keys again, in table-8 slot order
+    // resize to 32 slots: the five keys again, in 8-slot table order
+    uint32_t left = occ;
     occ = 0;
     mask = 31;
-    for (int sl = 0; sl < 8; ++sl) {
-      for (int j = 0; j < 5; ++j) {
-        if (((slot8 >> (3 * j)) & 7u) != (uint32_t)sl) continue;
-        const int s = probe_insert32(occ, mask, __builtin_amdgcn_readlane(key, j));
-        if (lane == j) myslot = s;
-      }
+    while (left) {
+      const int sl = __builtin_ctz(left);
+      left &= left - 1u;
+      const int j = (int)((key_at >> (4 * sl)) & 15u);
+      const int s = probe_insert32(occ, mask, __builtin_amdgcn_readlane(key, j));
+      if (lane == j) myslot = s;
     }
     for (int j = 5; j < U; ++j) {
       const int s = probe_insert32(occ, mask, __builtin_amdgcn_readlane(key, j));
       if (lane == j) myslot = s;
     }
   }
-  if (lane >= U) return -1;
+  if (!mine) return -1;
   return __popc(occ & ((1u << myslot) - 1u));
 }
 
