@@ -265,11 +265,16 @@ def small_fp8():
     return W.fp8_layer(base, pin=True, experts=32)
 
 
-@pytest.mark.parametrize("engine", ["kernel", "memcpy"])
-def test_fp8_state_decode_matches_oracle(monkeypatch, small_fp8, engine):
+@pytest.mark.parametrize("engine,cap", [("kernel", 8), ("memcpy", 8), ("kernel", 12)])
+def test_fp8_state_decode_matches_oracle(monkeypatch, small_fp8, engine, cap):
+    """Decode steps through cap slots: decisions equal the oracle's, outputs
+    the bytes of a cap=E state and, sampled, the oracle's within tolerance.
+    On the copy-kernel engine one launch pages in and runs w13: loaded
+    experts computed by the copy blocks from the codes they copy, the others
+    by w13 blocks laid out by slot (cap == top-k) or by pair (cap 12)."""
     monkeypatch.setenv("WISP_PAGEIN_ENGINE", engine)
     wl = small_fp8
-    E, K, cap = 32, wl.shape.top_k, 8
+    E, K = 32, wl.shape.top_k
     st = _fp8_state(wl, cap)
     assert st.pagein_engine == engine
     full = _fp8_state(wl, E)

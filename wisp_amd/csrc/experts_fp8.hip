@@ -42,6 +42,8 @@
 
 #include "common.h"
 #include "dma_pipeline.h"
+#include "pagein.h"
+#include "pager_core.h"
 
 #pragma clang fp contract(off)  // keep vLLM's separate multiply and add roundings
 
@@ -60,6 +62,15 @@ int experts_fp8_grouped(const void* x, int T, int H, int I, int K, const float* 
                         void* work, size_t work_bytes, hipStream_t st, const StageEvents* ev);
 size_t fp8_work_bytes(int T, int K, int H, int I, int nslots);
 int auto_algo(int dtype, int H, int I, int T, int K);
+int experts_fp8_w2(const void* act, int T, int H, int I, int K, const float* topk_w,
+                   const int32_t* slots, int nslots, const void* w2, size_t w2_stride,
+                   const float* s2, size_t s2_stride, int block_n, void* out, hipStream_t st,
+                   hipEvent_t e0, hipEvent_t e1, bool pager_slots);
+int pagein_fp8_w13(const PageInArgs& a, const void* x, int H, int I, int K,
+                   const int32_t* slots, const int32_t* flags, int nslots, const void* w13,
+                   size_t w13_stride, const float* s13, size_t s13_stride, int block_n,
+                   size_t s13_off, void* act, hipStream_t st, hipEvent_t e0, hipEvent_t e1,
+                   bool pager_slots);
 
 namespace {
 
@@ -120,6 +131,14 @@ __device__ inline i32x8 ld32(const uint8_t* p) {
 
 __device__ inline i32x8 lds32(const uint8_t* p) {
   return join(*reinterpret_cast<const u32x4*>(p), *reinterpret_cast<const u32x4*>(p + 16));
+}
+
+// 32 bytes to p (16-byte aligned) by two non-temporal 16-byte stores.
+__device__ inline void st32_nt(uint8_t* p, const i32x8& v) {
+  const u32x4 lo = {(uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]};
+  const u32x4 hi = {(uint32_t)v[4], (uint32_t)v[5], (uint32_t)v[6], (uint32_t)v[7]};
+  __builtin_nontemporal_store(lo, reinterpret_cast<u32x4*>(p));
+  __builtin_nontemporal_store(hi, reinterpret_cast<u32x4*>(p + 16));
 }
 
 __device__ inline i32x8 zero8() {
@@ -377,6 +396,33 @@ __global__ __launch_bounds__(NW * 64) void fp8_w13_kernel(
   }
 }
 
+// The NW waves' partial sums of this lane's four gate and four up outputs
+// (red [NW][2][64][4] f32), added in wave order to zero, read four waves at
+// a time: all eight at once would hold 64 registers (one 512-thread block per
+// CU), one at a time would make eight LDS round trips.
+template <int NW>
+__device__ inline void sum_partials(const float* red, int lane, f32x4& g, f32x4& u) {
+  g = f32x4{0.f, 0.f, 0.f, 0.f};
+  u = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+  for (int w0 = 0; w0 < NW; w0 += 4) {
+    f32x4 pg[4], pu[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int w = min(w0 + i, NW - 1);
+      pg[i] = *reinterpret_cast<const f32x4*>(red + ((size_t)w * 2 * 64 + lane) * 4);
+      pu[i] = *reinterpret_cast<const f32x4*>(red + ((size_t)w * 2 * 64 + 64 + lane) * 4);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (w0 + i < NW) {
+        g = g + pg[i];
+        u = u + pu[i];
+      }
+    }
+  }
+}
+
 // A word loaded before the loads that follow it in the source: the compiler
 // neither sinks nor reorders a relaxed atomic load (plain loads of
 // restrict-qualified data it may move below later loads).
@@ -397,16 +443,22 @@ __device__ inline int32_t load_first(const int32_t* p) {
 // chunk.  Dynamic LDS: red [NW][2][64][4] f32, then per wave xs [KC] f32 and
 // xq [KC][kKB] codes.
 // ---------------------------------------------------------------------------
+// The block of 16-row tile `tile` and pair (or, with SLOTS, slot) `by`.
+// With `words` (the pager's per-pair words; a fused page-in launch), a pair
+// whose expert this call loaded is left to the copy blocks, which compute it
+// from the bytes they copy.
 template <int NW, int KC, bool SLOTS>
-__global__ __launch_bounds__(NW * 64) void fp8_w13_one_kernel(
-    const uint16_t* __restrict__ x, int H, int I, int K, const int32_t* __restrict__ slots,
-    int nslots, const uint8_t* __restrict__ w13, size_t w13_stride, const float* __restrict__ s13,
-    size_t s13_stride, int block_n, uint16_t* __restrict__ act) {
-  extern __shared__ __align__(16) unsigned char smem[];
+__device__ inline void w13_one_block(const uint16_t* __restrict__ x, int H, int I, int K,
+                                     const int32_t* __restrict__ slots, int nslots,
+                                     const uint8_t* __restrict__ w13, size_t w13_stride,
+                                     const float* __restrict__ s13, size_t s13_stride,
+                                     int block_n, uint16_t* __restrict__ act,
+                                     unsigned char* smem, int tile, int by,
+                                     const int32_t* __restrict__ words) {
   float* red = reinterpret_cast<float*>(smem);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int col = lane & 15, grp = lane >> 4;
-  const int i0 = blockIdx.x * 16;
+  const int i0 = tile * 16;
   const int nkb = H / kKB;
   const int per = (nkb + NW - 1) / NW;
   const int kb0 = min(nkb, wave * per), kb1 = min(nkb, kb0 + per);
@@ -418,13 +470,15 @@ __global__ __launch_bounds__(NW * 64) void fp8_w13_one_kernel(
   // without k-blocks loads the last one and drops it)
   const int kbx = min(kb0 + min(grp, max(min(KC, kb1 - kb0), 1) - 1), nkb - 1);
   u32x4 xv = *reinterpret_cast<const u32x4*>(x + (size_t)kbx * kKB + col * 8);
-  int s, sl = -1;
+  int s, sl = -1, wd = -1;
   bool absent = false;  // this block's pair reads no expert: it stores zeros
   if (SLOTS) {
-    s = blockIdx.y;
+    s = by;
     sl = load_first(slots + min(lane, K - 1));  // lane j < K: pair j's slot
+    if (words) wd = load_first(words + min(lane, K - 1));
   } else {
-    s = slots[blockIdx.y];
+    if (words && pair_word_loaded(words[by]) >= 0) return;
+    s = slots[by];
     absent = s < 0 || s >= nslots;
     if (absent) s = 0;  // loads from slot 0, dropped (no branch around them)
   }
@@ -495,32 +549,229 @@ __global__ __launch_bounds__(NW * 64) void fp8_w13_one_kernel(
     rw[j] = ag[j];
     rw[64 * 4 + j] = au[j];
   }
-  int p = blockIdx.y;
+  int p = by;
   uint64_t none = 0;  // SLOTS: pairs whose slot lies outside the scratch
   if (SLOTS) {
     const uint64_t mine = __ballot(lane < K && sl == s);
     p = mine ? __builtin_ctzll(mine) : -1;
     none = s == 0 ? __ballot(lane < K && (sl < 0 || sl >= nslots)) : 0;
+    if (words && __ballot(lane < K && sl == s && pair_word_loaded(wd) >= 0)) p = -1;
   }
   const int zp = absent ? p : -1;  // stored as zeros below
   if (absent) p = -1;
   block_lds_sync();
   if (wave == 0 && col == 0 && p >= 0) {
-    float g[4] = {0.f, 0.f, 0.f, 0.f}, u[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int w = 0; w < NW; ++w) {
-      const float* rr = red + ((size_t)w * 2 * 64 + lane) * 4;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        g[j] = g[j] + rr[j];
-        u[j] = u[j] + rr[64 * 4 + j];
-      }
-    }
-    store_act4(act + (size_t)p * I + i0 + grp * 4, f32x4{g[0], g[1], g[2], g[3]},
-               f32x4{u[0], u[1], u[2], u[3]});
+    f32x4 g, u;
+    sum_partials<NW>(red, lane, g, u);
+    store_act4(act + (size_t)p * I + i0 + grp * 4, g, u);
   }
   for (; none; none &= none - 1)
     if (threadIdx.x < 16) act[(size_t)__builtin_ctzll(none) * I + i0 + threadIdx.x] = 0;
   if (zp >= 0 && threadIdx.x < 16) act[(size_t)zp * I + i0 + threadIdx.x] = 0;
+}
+
+template <int NW, int KC, bool SLOTS>
+__global__ __launch_bounds__(NW * 64) void fp8_w13_one_kernel(
+    const uint16_t* __restrict__ x, int H, int I, int K, const int32_t* __restrict__ slots,
+    int nslots, const uint8_t* __restrict__ w13, size_t w13_stride, const float* __restrict__ s13,
+    size_t s13_stride, int block_n, uint16_t* __restrict__ act) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  w13_one_block<NW, KC, SLOTS>(x, H, I, K, slots, nslots, w13, w13_stride, s13, s13_stride,
+                               block_n, act, smem, blockIdx.x, blockIdx.y, nullptr);
+}
+
+// ---------------------------------------------------------------------------
+// Page-in and w13 in one launch for one-token calls on the copy-kernel
+// engine, the block-FP8 twin of the bf16 page-in + w13 launch (one slab per
+// expert, [w13 | w2 | s13 | s2], in master and scratch alike).
+//   * Blocks [0, kFp8CopyBlocks) copy each expert the pager loaded: its w13
+//     rows in 16-row tiles (gate rows i0 .. i0 + 15 and the matching up
+//     rows), each tile from the pinned master into the slot, computing the
+//     tile's act of the expert's pair from the codes the block holds with
+//     w13_one_block's steps (the same k-block ranges per wave, k-blocks in
+//     ascending order within a wave, the waves' partial sums in wave order),
+//     so the output equals a resident call's; then the rest of the slab as
+//     a plain copy.  The token is quantised once per block, into LDS.
+//   * Blocks from kFp8CopyBlocks on are w13_one_block's for the pairs whose
+//     expert was already resident (grid order: tile fastest, then pair or
+//     slot).
+// Dynamic LDS: the larger of w13_one_block's and the copy blocks' (red
+// [NW][2][64][4] f32, then xq [nkb][kKB] codes and xs [nkb] f32).
+// ---------------------------------------------------------------------------
+// Copy blocks of the fused launch (512 threads each; 4 MiB of host reads in
+// flight).  32 blocks measured 1 % slower page-in.
+constexpr int kFp8CopyBlocks = 64;
+
+struct Fp8FusedArgs {
+  const uint16_t* x;
+  const int32_t* slots;  // the call's per-pair slots
+  const int32_t* words;  // the pager's per-pair words: pair_word(slot, loaded expert)
+  const uint8_t* w13;    // scratch, slot s at + s * w13_stride bytes
+  size_t w13_stride;
+  const float* s13;
+  size_t s13_stride;     // floats
+  uint16_t* act;
+  size_t s13_off;        // byte offset of the w13 scales in an expert's slab
+  int H, I, K, nslots, block_n;
+};
+
+// Copy blocks of the fused launch, for NW * PER == H / kKB (every wave PER
+// k-blocks).  A tile's 32 rows (16 gate, 16 up) are read over the host link
+// as whole PER * 128-byte row segments, 16 bytes a lane (requests of 1 KiB
+// per instruction, where the MFMA layout, 16 rows x 32 bytes per
+// instruction, would cut them into 64-byte pieces and cost ~15 % of the
+// link); each wave stores its segments to the slot and, one k-block and one
+// of gate and up at a time, puts them in its own 2 KiB of LDS (its slot of
+// red, free until the tile's partial sums), whence it reads its MFMA
+// operands.
+template <int NW, int PER>
+__device__ inline void fp8_copy_w13_blocks(const Fp8FusedArgs& f, const PageInArgs& a,
+                                           unsigned char* smem, int cb) {
+  constexpr int SEG = PER * kKB;     // bytes of a row a wave holds
+  constexpr int LPR = SEG / 16;      // lanes per row segment
+  constexpr int RPI = 64 / LPR;      // rows per load instruction
+  constexpr int NI = 32 / RPI;       // load instructions per tile
+  const int n = *a.count;
+  if (a.hist && cb == 0 && threadIdx.x == 0) {
+    *a.hist = n;
+    __threadfence_system();
+  }
+  if (n <= 0) return;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int col = lane & 15, grp = lane >> 4;
+  const int H = f.H, I = f.I, nkb = H / kKB, ntile = I / 16;
+  float* red = reinterpret_cast<float*>(smem);
+  uint8_t* xq = reinterpret_cast<uint8_t*>(red + NW * 2 * 64 * 4);
+  float* xs = reinterpret_cast<float*>(xq + (size_t)nkb * kKB);
+  uint8_t* ws = reinterpret_cast<uint8_t*>(red + (size_t)wave * 2 * 64 * 4);  // 16 rows x kKB
+  // lane p < K holds the expert pair p's word says was loaded (or -1)
+  const int mine = lane < f.K ? pair_word_loaded(f.words[lane]) : -1;
+  // the token's k-blocks, one per 16-lane row
+  for (int base = wave * 4; base < nkb; base += NW * 4) {
+    const int kb = base + grp;
+    float v[8];
+    unpack_bf16x8(*reinterpret_cast<const u32x4*>(f.x + (size_t)min(kb, nkb - 1) * kKB + col * 8),
+                  v);
+    uint32_t q[2];
+    const float sc = quant8(v, q);
+    if (kb < nkb) {
+      *reinterpret_cast<uint2*>(xq + (size_t)kb * kKB + col * 8) = make_uint2(q[0], q[1]);
+      if (col == 0) xs[kb] = sc;
+    }
+  }
+  block_lds_sync();
+  const int kb0 = wave * PER;  // this wave's k-blocks: kb0 .. kb0 + PER - 1
+  const int seg_row = lane / LPR, seg_cb = lane % LPR;  // a load's row and 16-byte block
+  const PageInPlane& p0 = a.p[0];
+  for (int q = cb; q < n * ntile; q += kFp8CopyBlocks) {
+    const int j = q / ntile, tile = q - j * ntile;
+    const int e = a.loads[2 * j], s = a.loads[2 * j + 1];
+    if (e < 0 || e >= a.num_experts || s < 0 || s >= a.cap) continue;
+    const uint64_t m = __ballot(mine == e);
+    const int pair = m ? __builtin_ctzll(m) : -1;
+    const int i0 = tile * 16;
+    const uint8_t* src = reinterpret_cast<const uint8_t*>(p0.m) + (size_t)e * p0.m_stride;
+    uint8_t* dst = reinterpret_cast<uint8_t*>(p0.d) + (size_t)s * p0.d_stride;
+    const float* S = reinterpret_cast<const float*>(src + f.s13_off);
+    float sg[PER], su[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      sg[k] = S[(size_t)(i0 / f.block_n) * nkb + kb0 + k];
+      su[k] = S[(size_t)((I + i0) / f.block_n) * nkb + kb0 + k];
+    }
+    u32x4 v[NI];
+    size_t off[NI];
+#pragma unroll
+    for (int ii = 0; ii < NI; ++ii) {
+      const int rr = ii * RPI + seg_row;  // tile row: 0-15 gate, 16-31 up
+      off[ii] = (size_t)(rr < 16 ? i0 + rr : I + i0 + rr - 16) * H + (size_t)kb0 * kKB +
+                seg_cb * 16;
+      v[ii] = *reinterpret_cast<const u32x4*>(src + off[ii]);
+    }
+#pragma unroll
+    for (int ii = 0; ii < NI; ++ii)
+      __builtin_nontemporal_store(v[ii], reinterpret_cast<u32x4*>(dst + off[ii]));
+    f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
+    // LDS row r (0-15) of a staged k-block: its 8 16-byte blocks at
+    // (block ^ (r & 7))
+    auto at = [&](int r, int cb) { return ws + r * kKB + ((cb ^ (r & 7)) << 4); };
+    // rows [16 h, 16 h + 16) of the tile (h 0: gate, 1: up), blocks
+    // 8k .. 8k + 7 of their segments; the wave's own LDS, so its reads of
+    // the previous staging come first in order
+    auto stage = [&](int h, int k) {
+#pragma unroll
+      for (int ii = 0; ii < NI; ++ii) {
+        const int rr = ii * RPI + seg_row;
+        if ((rr >> 4) == h && (seg_cb >> 3) == k)
+          *reinterpret_cast<u32x4*>(at(rr & 15, seg_cb & 7)) = v[ii];
+      }
+      wave_lds_sync();
+    };
+    const int cb = grp * 2;  // the lane's 32 bytes of a k-block
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      stage(0, k);
+      const i32x8 wg = join(*reinterpret_cast<const u32x4*>(at(col, cb)),
+                            *reinterpret_cast<const u32x4*>(at(col, cb + 1)));
+      stage(1, k);
+      const i32x8 wu = join(*reinterpret_cast<const u32x4*>(at(col, cb)),
+                            *reinterpret_cast<const u32x4*>(at(col, cb + 1)));
+      const int kb = kb0 + k;
+      const i32x8 b = lds32(xq + (size_t)kb * kKB + grp * 32);
+      const float sa = xs[kb];
+      const f32x4 dg = mfma_fp8(wg, b);
+      const f32x4 du = mfma_fp8(wu, b);
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        ag[jj] = ag[jj] + (dg[jj] * sa) * sg[k];
+        au[jj] = au[jj] + (du[jj] * sa) * su[k];
+      }
+    }
+    float* rw = red + ((size_t)wave * 2 * 64 + lane) * 4;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      rw[jj] = ag[jj];
+      rw[64 * 4 + jj] = au[jj];
+    }
+    block_lds_sync();
+    if (wave == 0 && col == 0 && pair >= 0) {
+      f32x4 g, u;
+      sum_partials<NW>(red, lane, g, u);
+      store_act4(f.act + (size_t)pair * I + i0 + grp * 4, g, u);
+    }
+    block_lds_sync();  // red and the segments are rewritten by the next tile
+  }
+  // the rest of each loaded expert's slab (w2 and the scales), other planes
+  const size_t w13_bytes = (size_t)2 * I * H;
+  for (int j = 0; j < n; ++j) {
+    const int ej = a.loads[2 * j], sj = a.loads[2 * j + 1];
+    if (ej < 0 || ej >= a.num_experts || sj < 0 || sj >= a.cap) continue;
+    copy_range<NW * 64>(p0.m + (size_t)ej * p0.m_stride + w13_bytes,
+                        p0.d + (size_t)sj * p0.d_stride + w13_bytes, p0.bytes - w13_bytes,
+                        cb, kFp8CopyBlocks);
+    for (int qq = 1; qq < a.nplanes; ++qq) {
+      const PageInPlane& pl = a.p[qq];
+      copy_range<NW * 64>(pl.m + (size_t)ej * pl.m_stride, pl.d + (size_t)sj * pl.d_stride,
+                          pl.bytes, cb, kFp8CopyBlocks);
+    }
+  }
+}
+
+// w13 blocks of KC k-blocks per wave chunk; copy blocks of PER k-blocks per
+// wave (NW * PER == H / kKB).
+template <int NW, int KC, int PER, bool SLOTS>
+__global__ __launch_bounds__(NW * 64) void pagein_fp8_w13_kernel(Fp8FusedArgs f, PageInArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  if (blockIdx.x >= kFp8CopyBlocks) {
+    const int ntile = f.I / 16;
+    const int local = blockIdx.x - kFp8CopyBlocks;
+    const int by = local / ntile;
+    w13_one_block<NW, KC, SLOTS>(f.x, f.H, f.I, f.K, f.slots, f.nslots, f.w13, f.w13_stride,
+                                 f.s13, f.s13_stride, f.block_n, f.act, smem,
+                                 local - by * ntile, by, f.words);
+    return;
+  }
+  fp8_copy_w13_blocks<NW, PER>(f, a, smem, blockIdx.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -1531,7 +1782,18 @@ int experts_fp8(const void* x, int T, int H, int I, int K, const float* topk_w,
     l13 = ncol == 4 ? &launch_w13<8, 4, false>
         : big ? &launch_w13<8, 16, true> : &launch_w13<8, 16, false>;
   WISP_HIP_TRY(l13(a13, st, e0, e1));
+  return experts_fp8_w2(act, T, H, I, K, topk_w, slots, nslots, w2, w2_stride, s2, s2_stride,
+                        block_n, out, st, ev ? ev->ev[2] : nullptr, ev ? ev->ev[3] : nullptr,
+                        pager_slots);
+}
 
+// The w2 stage of experts_fp8 (routing weights and moe_sum fused).
+int experts_fp8_w2(const void* act, int T, int H, int I, int K, const float* topk_w,
+                   const int32_t* slots, int nslots, const void* w2, size_t w2_stride,
+                   const float* s2, size_t s2_stride, int block_n, void* out, hipStream_t st,
+                   hipEvent_t e0, hipEvent_t e1, bool pager_slots) {
+  if (T == 0) return WISP_OK;
+  const bool by_slot = T == 1 && pager_slots && K == nslots;
   // waves per pair: split I's k-blocks when there are fewer pairs than waves
   int WP = K >= kW2Waves ? 1 : kW2Waves / K;
   while (WP > 1 && w2_lds(K, I, WP) > kMaxLds) WP >>= 1;
@@ -1552,7 +1814,58 @@ int experts_fp8(const void* x, int T, int H, int I, int K, const float* topk_w,
     else
       l2 = kc2 == 4 ? &launch_w2<4, 4> : kc2 == 6 ? &launch_w2<6, 4> : &launch_w2<8, 4>;
   }
-  WISP_HIP_TRY(l2(a2, st, ev ? ev->ev[2] : nullptr, ev ? ev->ev[3] : nullptr));
+  WISP_HIP_TRY(l2(a2, st, e0, e1));
+  return WISP_OK;
+}
+
+namespace {
+
+template <int NW, int KC, int PER, bool SLOTS>
+hipError_t launch_pagein_fp8_w13(const Fp8FusedArgs& f, const PageInArgs& a, hipStream_t st,
+                                 hipEvent_t e0, hipEvent_t e1) {
+  static std::atomic<uint64_t> big_lds{0};
+  const auto kern = &pagein_fp8_w13_kernel<NW, KC, PER, SLOTS>;
+  const int nkb = f.H / kKB;
+  const size_t red = (size_t)NW * 2 * 64 * 4 * sizeof(float);
+  const size_t lds = red + std::max((size_t)NW * KC * (4 + kKB), (size_t)nkb * (4 + kKB));
+  hipError_t e = allow_lds(kern, lds, kMaxLds, &big_lds);
+  if (e != hipSuccess) return e;
+  const dim3 grid(kFp8CopyBlocks + f.I / 16 * (SLOTS ? f.nslots : f.K)), block(NW * 64);
+  if (e0)
+    hipExtLaunchKernelGGL(kern, grid, block, lds, st, e0, e1, 0, f, a);
+  else
+    hipLaunchKernelGGL(kern, grid, block, lds, st, f, a);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+// Whether pagein_fp8_w13 serves a layer of hidden size H (its copy blocks
+// give every wave H / kKB / 8 whole k-blocks).
+bool fp8_fused_supported(int H) { return H == 16 * kKB || H == 8 * kKB; }
+
+// Page-in of the experts the pager loaded (a.count = flags) and the w13
+// stage of a one-token call in one launch; the layer's masters and scratch
+// hold one [w13 | w2 | s13 | s2] slab per expert (plane 0), the w13 scales
+// at byte s13_off of it.
+int pagein_fp8_w13(const PageInArgs& a, const void* x, int H, int I, int K,
+                   const int32_t* slots, const int32_t* flags, int nslots, const void* w13,
+                   size_t w13_stride, const float* s13, size_t s13_stride, int block_n,
+                   size_t s13_off, void* act, hipStream_t st, hipEvent_t e0, hipEvent_t e1,
+                   bool pager_slots) {
+  const Fp8FusedArgs f = {(const uint16_t*)x, slots, flags + 1, (const uint8_t*)w13, w13_stride,
+                          s13, s13_stride, (uint16_t*)act, s13_off, H, I, K, nslots, block_n};
+  const bool by_slot = pager_slots && K == nslots;
+  hipError_t e;
+  if (H == 16 * kKB)
+    e = by_slot ? launch_pagein_fp8_w13<8, 2, 2, true>(f, a, st, e0, e1)
+                : launch_pagein_fp8_w13<8, 2, 2, false>(f, a, st, e0, e1);
+  else if (H == 8 * kKB)
+    e = by_slot ? launch_pagein_fp8_w13<8, 2, 1, true>(f, a, st, e0, e1)
+                : launch_pagein_fp8_w13<8, 2, 1, false>(f, a, st, e0, e1);
+  else
+    return WISP_ERR_UNSUPPORTED;
+  WISP_HIP_TRY(e);
   return WISP_OK;
 }
 

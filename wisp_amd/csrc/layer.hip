@@ -86,6 +86,16 @@ int experts_fp8(const void* x, int T, int H, int I, int K, const float* topk_w,
                 const float* s13, size_t s13_stride, const void* w2, size_t w2_stride,
                 const float* s2, size_t s2_stride, int block_n, void* act, void* out,
                 hipStream_t st, const StageEvents* ev, bool pager_slots);
+int experts_fp8_w2(const void* act, int T, int H, int I, int K, const float* topk_w,
+                   const int32_t* slots, int nslots, const void* w2, size_t w2_stride,
+                   const float* s2, size_t s2_stride, int block_n, void* out, hipStream_t st,
+                   hipEvent_t e0, hipEvent_t e1, bool pager_slots);
+int pagein_fp8_w13(const PageInArgs& a, const void* x, int H, int I, int K,
+                   const int32_t* slots, const int32_t* flags, int nslots, const void* w13,
+                   size_t w13_stride, const float* s13, size_t s13_stride, int block_n,
+                   size_t s13_off, void* act, hipStream_t st, hipEvent_t e0, hipEvent_t e1,
+                   bool pager_slots);
+bool fp8_fused_supported(int H);
 const char* fp8_unsupported(int H, int I, int K, int block_n, int block_k);
 int experts_fp8_grouped(const void* x, int T, int H, int I, int K, const float* topk_w,
                         const int32_t* slots, int nslots, const void* w13, size_t w13_stride,
@@ -174,8 +184,11 @@ struct Layer {
   // kernel page-in (engine WISP_PAGEIN_KERNEL and eligible masters)
   bool kpin = false;
   // the fused page-in + w13 launch applies (plane 0 starts with the whole
-  // w13 of an expert, in master and scratch alike)
+  // w13 of an expert, in master and scratch alike; for block-FP8 experts
+  // the plane is the whole [w13 | w2 | s13 | s2] slab, the w13 scales at
+  // byte s13_off of it)
   bool fused_ok = false;
+  size_t s13_off = 0;
   int32_t* hist = nullptr;        // pinned host [kPinRing]
   int32_t* hist_dev = nullptr;
   int pin_next = 0;
@@ -355,6 +368,7 @@ struct FusedW13 {
   int T, K;
   const int32_t* flags;
   void* act;
+  const int32_t* slots;
 };
 
 // Copy-kernel page-in on `st` of the (expert, slot) pairs at `loads` (device
@@ -385,25 +399,44 @@ int page_in_kernel(Layer& L, const int32_t* loads, const int32_t* count, int n, 
   // timed launch costs the stream ~4.5 us (measured at the Qwen3 bs=1 decode
   // step).
   a.hist = L.profile ? L.hist_dev + i : nullptr;
-  int rc = fw ? pagein_w13(a, fw->x, d.dtype, fw->T, d.hidden, d.inter, fw->K, fw->flags,
-                           d.scratch_w13, d.scratch_w13_stride, fw->act, st,
-                           L.profile ? p.start : nullptr, L.profile ? p.stop : nullptr)
-              : launch_pagein(a, st, L.profile ? p.start : nullptr, L.profile ? p.stop : nullptr);
+  hipEvent_t e0 = L.profile ? p.start : nullptr, e1 = L.profile ? p.stop : nullptr;
+  int rc;
+  if (fw && L.fp8)
+    rc = pagein_fp8_w13(a, fw->x, d.hidden, d.inter, fw->K, fw->slots, fw->flags, d.cap,
+                        d.scratch_w13, d.scratch_w13_stride, d.scratch_s13, d.scratch_s13_stride,
+                        d.block_n, L.s13_off, fw->act, st, e0, e1, true);
+  else if (fw)
+    rc = pagein_w13(a, fw->x, d.dtype, fw->T, d.hidden, d.inter, fw->K, fw->flags, d.scratch_w13,
+                    d.scratch_w13_stride, fw->act, st, e0, e1);
+  else
+    rc = launch_pagein(a, st, e0, e1);
   if (rc == WISP_OK && L.profile) p.pending = true;
   return rc;
 }
 
 // Whether the fused page-in + w13 launch can serve this layer: a bf16 or
 // fp32 layer whose first page-in plane begins with the expert's w13 rows in
-// both the master and the scratch.
+// both the master and the scratch; a block-FP8 layer whose one plane is the
+// expert's whole slab, with its w13 scales at the same offset in master and
+// scratch.
 void set_fused_ok(Layer& L) {
   const wisp_layer_desc& d = L.d;
   const Plane& p0 = L.planes[0];
   const size_t w13_bytes = d.w13_elems * L.es;
-  L.fused_ok = L.kpin && !L.fp8 && L.nplanes >= 1 && p0.host == (const char*)d.master_w13 &&
+  L.fused_ok = L.kpin && L.nplanes >= 1 && p0.host == (const char*)d.master_w13 &&
                p0.d == (char*)d.scratch_w13 && p0.bytes >= w13_bytes &&
                p0.m_stride == d.master_w13_stride * L.es &&
                p0.d_stride == d.scratch_w13_stride * L.es;
+  L.s13_off = 0;
+  if (L.fused_ok && L.fp8) {
+    const ptrdiff_t om = (const char*)d.master_s13 - (const char*)d.master_w13;
+    const ptrdiff_t od = (const char*)d.scratch_s13 - (const char*)d.scratch_w13;
+    L.fused_ok = fp8_fused_supported(d.hidden) && L.nplanes == 1 && om == od &&
+                 om >= (ptrdiff_t)w13_bytes && om % 4 == 0 &&
+                 (size_t)om + d.s13_elems * 4 <= p0.bytes &&
+                 d.master_s13_stride * 4 == p0.m_stride && d.scratch_s13_stride * 4 == p0.d_stride;
+    if (L.fused_ok) L.s13_off = (size_t)om;
+  }
 }
 
 // Enables the copy kernel when every master range is pinned, device-mapped
@@ -502,12 +535,17 @@ int w13(Layer& L, const void* x, int T, int K, const int32_t* slots, void* act, 
 int w2(Layer& L, const void* act, int T, int K, const float* w, const int32_t* slots, void* out,
        hipStream_t st, const int32_t* skip_if, ProfLaunch** launched) {
   const wisp_layer_desc& d = L.d;
+  if (L.fp8 && skip_if) return WISP_ERR_INVALID;  // no speculative block-FP8 launches
   ProfLaunch* p = prof_begin(L, 1);
   // the slots come from the pager, so a one-token call with K == cap fills
   // every slot and the w2 kernel may run one wave per slot
-  int rc = gemv_w2(act, d.dtype, T, d.hidden, d.inter, K, w, slots, d.scratch_w2,
-                   d.scratch_w2_stride, out, st, p ? p->start : nullptr, p ? p->stop : nullptr,
-                   skip_if, d.cap);
+  int rc = L.fp8 ? experts_fp8_w2(act, T, d.hidden, d.inter, K, w, slots, d.cap, d.scratch_w2,
+                                  d.scratch_w2_stride, d.scratch_s2, d.scratch_s2_stride,
+                                  d.block_n, out, st, p ? p->start : nullptr,
+                                  p ? p->stop : nullptr, true)
+                 : gemv_w2(act, d.dtype, T, d.hidden, d.inter, K, w, slots, d.scratch_w2,
+                           d.scratch_w2_stride, out, st, p ? p->start : nullptr,
+                           p ? p->stop : nullptr, skip_if, d.cap);
   if (p && rc == WISP_OK) p->pending = true;
   if (launched) *launched = p;
   return rc;
@@ -856,7 +894,7 @@ extern "C" int wisp_layer_forward(void* handle, const void* x, const void* logit
   if (rc != WISP_OK) return rc;
   if (T == 1 && one_group && L->kpin && a == WISP_ALGO_GEMV && L->fused_ok) {
     // [route+pager] [page-in + w13] [w2]
-    const FusedW13 fw{x, T, K, ws->flags, ws->act};
+    const FusedW13 fw{x, T, K, ws->flags, ws->act, ws->slots};
     rc = page_in_kernel(*L, ws->loads, ws->flags, 0, st, &fw);
     if (rc != WISP_OK) return rc;
     return w2(*L, ws->act, T, K, ws->topk_w, ws->slots, out, st, nullptr, nullptr);

@@ -41,25 +41,27 @@ int launch_pagein(const PageInArgs& a, hipStream_t st, hipEvent_t ev_start, hipE
 constexpr int kPageInUnroll = 4;
 
 // Copies `bytes` (a multiple of 16) from src to dst, spread over `nblocks`
-// blocks of 256 threads; `blk` is this block's index among them.  Each
-// thread keeps kPageInUnroll 16-byte loads in flight (64 blocks: 1 MiB).
+// blocks of NT threads; `blk` is this block's index among them.  Each
+// thread keeps kPageInUnroll 16-byte loads in flight (64 blocks of 256
+// threads: 1 MiB).
+template <int NT = 256>
 __device__ inline void copy_range(const char* __restrict__ src, char* __restrict__ dst,
                                   size_t bytes, int blk, int nblocks) {
   typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
   const u32x4* s = reinterpret_cast<const u32x4*>(src);
   u32x4* d = reinterpret_cast<u32x4*>(dst);
   const size_t n = bytes >> 4;
-  const size_t step = (size_t)nblocks * 256 * kPageInUnroll;
-  for (size_t base = (size_t)blk * 256 * kPageInUnroll + threadIdx.x; base < n; base += step) {
+  const size_t step = (size_t)nblocks * NT * kPageInUnroll;
+  for (size_t base = (size_t)blk * NT * kPageInUnroll + threadIdx.x; base < n; base += step) {
     u32x4 v[kPageInUnroll];
 #pragma unroll
     for (int u = 0; u < kPageInUnroll; ++u) {
-      const size_t i = base + (size_t)u * 256;
+      const size_t i = base + (size_t)u * NT;
       if (i < n) v[u] = s[i];
     }
 #pragma unroll
     for (int u = 0; u < kPageInUnroll; ++u) {
-      const size_t i = base + (size_t)u * 256;
+      const size_t i = base + (size_t)u * NT;
       if (i < n) __builtin_nontemporal_store(v[u], d + i);
     }
   }
