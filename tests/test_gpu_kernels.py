@@ -140,8 +140,10 @@ def _expert_case(seed, T, H, I, E, K, dtype):
     return x, w, ids, w13, w2
 
 
+# the last case's w2 rows (256 chunks of 16 bytes) take the looping w2 kernel
 @pytest.mark.parametrize("T,H,I,E,K", [(1, 512, 256, 16, 2), (3, 512, 256, 16, 2),
-                                        (1, 256, 64, 8, 2), (2, 1024, 384, 12, 4)])
+                                        (1, 256, 64, 8, 2), (2, 1024, 384, 12, 4),
+                                        (2, 256, 1024, 4, 2)])
 def test_experts_gemv_fp32(T, H, I, E, K):
     x, w, ids, w13, w2 = _expert_case(T * 100 + H, T, H, I, E, K, torch.float32)
     ref = moe_forward(x, w, ids, w13, w2)
@@ -150,8 +152,13 @@ def test_experts_gemv_fp32(T, H, I, E, K):
     assert rel_err(out, ref) < 1e-5
 
 
+# w2 rows past 128 chunks of 16 bytes take the looping w2 kernel (I 3072,
+# 4608, 8192 and Mixtral's 14336, top-2 and top-8)
 @pytest.mark.parametrize("T,H,I,E,K", [(1, 2048, 768, 16, 8), (2, 2048, 768, 12, 8),
-                                        (1, 4096, 1024, 4, 2), (1, 1024, 512, 8, 2)])
+                                        (1, 4096, 1024, 4, 2), (1, 1024, 512, 8, 2),
+                                        (1, 1024, 3072, 4, 2), (2, 512, 4608, 4, 2),
+                                        (1, 256, 14336, 3, 2), (1, 256, 8192, 8, 8),
+                                        (2, 256, 14336, 8, 8)])
 def test_experts_gemv_bf16(T, H, I, E, K):
     x, w, ids, w13, w2 = _expert_case(T * 7 + H, T, H, I, E, K, torch.bfloat16)
     out = run_experts(x.to(DEV), torch.tensor(w, dtype=torch.float32, device=DEV),
