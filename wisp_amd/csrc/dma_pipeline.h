@@ -110,20 +110,28 @@ __device__ inline void chunk_copies(unsigned char* stage,
   }
 }
 
+struct NoSetup {
+  __device__ void operator()() const {}
+};
+
 // The S-stage pipeline over n chunks; chunk c starts off(c) bytes into every
-// row.  compute(ws, as, c) runs once chunk c has landed, with ws this wave's
-// weight slice and as the token tile of its stage.
-template <int NWR, int S, int TCW, typename Off, typename F>
+// row.  after_prologue() runs once the first S - 1 chunks' copies are issued
+// (setup whose loads should travel with them: what it writes to LDS is seen
+// by every wave from chunk 0's compute on, after the loop's barrier);
+// compute(ws, as, c) runs once chunk c has landed, with ws this wave's weight
+// slice and as the token tile of its stage.
+template <int NWR, int S, int TCW, typename Off, typename F, typename G = NoSetup>
 __device__ inline void pipeline(unsigned char* smem,
                                 const unsigned char* const (&wrow)[NWR / kRowsPerCopy],
                                 const unsigned char* const (&arow)[kMaxTokCopies], int n, Off off,
-                                F&& compute) {
+                                F&& compute, G&& after_prologue = G{}) {
   using Sm = Smem<NWR, S>;
   constexpr int PER = NWR / kRowsPerCopy + TCW;  // copies per wave and chunk
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
   for (int c = 0; c < S - 1; ++c)
     if (c < n) chunk_copies<NWR, TCW>(smem + c * Sm::kStage, wrow, arow, wave, lane, off(c));
+  after_prologue();
   for (int c = 0; c < n; ++c) {
     wait_chunk<PER, S - 2>(min(S - 2, n - 1 - c));
     lds_barrier();
@@ -136,13 +144,16 @@ __device__ inline void pipeline(unsigned char* smem,
 }
 
 // One pass for mrows tokens (NT = ceil(mrows / 16) tiles): the lane's token
-// source rows (row_of(r) for tile row r; rows past mrows repeat the last),
-// a drain of the previous pass (its copies and its readers of every stage),
-// then the pipeline with this wave's share of the tile's copies.
-template <int NWR, int S, int NT, typename RowOf, typename Off, typename F>
+// source rows (row_of(r) for tile row r, called by every lane; rows past
+// mrows repeat the last), a drain of the previous pass (its copies and its
+// readers of every stage and of anything after_prologue writes), then the
+// pipeline with this wave's share of the tile's copies.
+template <int NWR, int S, int NT, typename RowOf, typename Off, typename F,
+          typename G = NoSetup>
 __device__ inline void pass(unsigned char* smem,
                             const unsigned char* const (&wrow)[NWR / kRowsPerCopy], int mrows,
-                            RowOf row_of, int n, Off off, F&& compute) {
+                            RowOf row_of, int n, Off off, F&& compute,
+                            G&& after_prologue = G{}) {
   constexpr int copies = 16 * NT / kRowsPerCopy;  // token copies of the tile, all waves
   static_assert(copies <= 4 * kMaxTokCopies, "token copies per wave");
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -154,12 +165,22 @@ __device__ inline void pass(unsigned char* smem,
   lds_barrier();  // the previous pass's readers of every stage are done
   const int tcw = (copies - wave + 3) / 4;  // copies j = wave + 4i < copies: 0, 1 or 2
   if (tcw <= 0)
-    pipeline<NWR, S, 0>(smem, wrow, arow, n, off, compute);
+    pipeline<NWR, S, 0>(smem, wrow, arow, n, off, compute, after_prologue);
   else if (tcw == 1)
-    pipeline<NWR, S, 1>(smem, wrow, arow, n, off, compute);
+    pipeline<NWR, S, 1>(smem, wrow, arow, n, off, compute, after_prologue);
   else
-    pipeline<NWR, S, 2>(smem, wrow, arow, n, off, compute);
+    pipeline<NWR, S, 2>(smem, wrow, arow, n, off, compute, after_prologue);
 }
+
+// A pass's pair list held one entry per lane: lane r holds list[m0 + r]
+// (entries at or past the slot's count, read clamped to the list's length,
+// are never used), so a tile row's entry is a lane permute rather than a
+// dependent global load.  A kernel loads the first pass's entries together
+// with the slot's count.
+__device__ inline int list_entries(const int32_t* __restrict__ list, int m0, int len) {
+  return list[min(m0 + (int)(threadIdx.x & 63), len - 1)];
+}
+__device__ inline int list_entry(int held, int r) { return __shfl(held, r); }
 
 }  // namespace dma
 }  // namespace wisp

@@ -1248,12 +1248,12 @@ inline size_t fp8_dma_lds(int nkb) {
 }
 
 // Stages the pass's token scales: row r < 64 of the tile reads the scales of
-// tile row min(r, mrows - 1).  After a barrier, so the previous pass's
-// readers are done.
+// tile row min(r, mrows - 1).  Runs inside the pass, after its first copies
+// are issued (the pass's drain has seen the previous pass's readers out);
+// row_of is called by every lane.
 template <typename RowOf>
 __device__ inline void stage_token_scales(float* xsl, const float* __restrict__ scales, int nkb,
-                                          int mrows, bool first, RowOf row_of) {
-  if (!first) dma::lds_barrier();
+                                          int mrows, RowOf row_of) {
   for (int q = threadIdx.x; q < dma::kTokRows * nkb; q += 256) {
     const int r = q / nkb, kb = q - r * nkb;
     xsl[q] = scales[(size_t)row_of(min(r, mrows - 1)) * nkb + kb];
@@ -1268,22 +1268,23 @@ __global__ __launch_bounds__(256) void fp8_w13_dma_kernel(
     size_t s13_stride, int block_n, uint16_t* __restrict__ act) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int s = blockIdx.y;
-  const int M = counts[s];
-  if (M == 0) return;
   const int32_t* list = lists + (size_t)s * P;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int col = lane & 15, grp = lane >> 4;
   const int i0 = blockIdx.x * 64 + wave * 16;
   const int nkb = H / kKB;
+  const float* Sg = s13 + (size_t)s * s13_stride + (size_t)(i0 / block_n) * nkb;
+  const float* Su = s13 + (size_t)s * s13_stride + (size_t)((I + i0) / block_n) * nkb;
+  // loaded together: the slot's count, the first pass's pair list and the
+  // first 64 of this wave's gate and up scales (staged into LDS after the
+  // first copies are issued)
+  const int M = counts[s];
+  int held = dma::list_entries(list, 0, P);
+  const float sg0 = Sg[min(lane, nkb - 1)], su0 = Su[min(lane, nkb - 1)];
+  if (M == 0) return;
   float* xsl = reinterpret_cast<float*>(smem + dma::Smem<32, S>::kBytes);
   float* wsl = xsl + dma::kTokRows * nkb + wave * 2 * nkb;  // this wave's gate, up scales
   const uint8_t* W = w13 + (size_t)s * w13_stride;
-  const float* Sg = s13 + (size_t)s * s13_stride + (size_t)(i0 / block_n) * nkb;
-  const float* Su = s13 + (size_t)s * s13_stride + (size_t)((I + i0) / block_n) * nkb;
-  for (int q = lane; q < nkb; q += 64) {
-    wsl[q] = Sg[q];
-    wsl[nkb + q] = Su[q];
-  }
   // this lane's weight copy rows: slice rows 0-15 gate, 16-31 up
   const unsigned char* wrow[32 / dma::kRowsPerCopy];
 #pragma unroll
@@ -1294,14 +1295,24 @@ __global__ __launch_bounds__(256) void fp8_w13_dma_kernel(
   auto off = [](int c) { return (size_t)c * kKB; };
   for (int m0 = 0; m0 < M; m0 += dma::kTokRows) {
     const int mrows = min(M - m0, dma::kTokRows);
-    // the pairs of this lane's output rows (tile t, row col), loaded with
-    // the token-scale staging's own list loads rather than after the k loop
+    if (m0 > 0) held = dma::list_entries(list, m0, P);
+    // the pairs of this lane's output rows (tile t, row col)
     int pr[4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) pr[t] = list[m0 + min(t * 16 + col, mrows - 1)];
-    auto tok_of = [&](int r) { return list[m0 + r] / K; };
-    stage_token_scales(xsl, xs, nkb, mrows, m0 == 0, tok_of);
+    for (int t = 0; t < 4; ++t) pr[t] = dma::list_entry(held, min(t * 16 + col, mrows - 1));
+    auto tok_of = [&](int r) { return dma::list_entry(held, r) / K; };
     auto row_of = [&](int r) { return xq + (size_t)tok_of(r) * H; };
+    // once the pass's first copies are issued: the token scales and, in the
+    // first pass, this wave's weight scales
+    auto stage = [&]() {
+      stage_token_scales(xsl, xs, nkb, mrows, tok_of);
+      if (m0 == 0) {
+        for (int q = lane; q < nkb; q += 64) {
+          wsl[q] = q < 64 ? sg0 : Sg[q];
+          wsl[nkb + q] = q < 64 ? su0 : Su[q];
+        }
+      }
+    };
     f32x4 ag[4], au[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
@@ -1327,7 +1338,7 @@ __global__ __launch_bounds__(256) void fp8_w13_dma_kernel(
                                  au[t][j] = au[t][j] + (du[j] * sx) * su;
                                }
                              }
-                           });
+                           }, stage);
     };
     const int nt = (mrows + 15) >> 4;
     if (nt == 1)
@@ -1357,20 +1368,26 @@ __global__ __launch_bounds__(256) void fp8_w2_dma_kernel(
     const float* __restrict__ s2, size_t s2_stride, int block_n, uint16_t* __restrict__ y) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int s = blockIdx.y;
-  const int M = counts[s];
-  if (M == 0) return;
   const int32_t* list = lists + (size_t)s * P;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int col = lane & 15, grp = lane >> 4;
   const int h0 = blockIdx.x * 128 + wave * 32;
   const int nkb = I / kKB;
+  // this wave's weight scale q < 2 nkb: row group q / nkb, k-block q % nkb
+  auto wscale = [&](int q) {
+    const int g = q / nkb, kb = q - g * nkb;
+    return s2[(size_t)s * s2_stride + (size_t)((h0 + 16 * g) / block_n) * nkb + kb];
+  };
+  // loaded together: the slot's count, the first pass's pair list and the
+  // first 64 of this wave's weight scales (staged into LDS after the first
+  // copies are issued)
+  const int M = counts[s];
+  int held = dma::list_entries(list, 0, P);
+  const float ws0 = wscale(min(lane, 2 * nkb - 1));
+  if (M == 0) return;
   float* asl = reinterpret_cast<float*>(smem + dma::Smem<32, S>::kBytes);
   float* wsl = asl + dma::kTokRows * nkb + wave * 2 * nkb;  // scales of row groups 0, 1
   const uint8_t* W = w2 + (size_t)s * w2_stride;
-  for (int q = lane; q < 2 * nkb; q += 64) {
-    const int g = q / nkb, kb = q - g * nkb;
-    wsl[q] = s2[(size_t)s * s2_stride + (size_t)((h0 + 16 * g) / block_n) * nkb + kb];
-  }
   const unsigned char* wrow[32 / dma::kRowsPerCopy];
 #pragma unroll
   for (int i = 0; i < 32 / dma::kRowsPerCopy; ++i)
@@ -1378,18 +1395,25 @@ __global__ __launch_bounds__(256) void fp8_w2_dma_kernel(
   auto off = [](int c) { return (size_t)c * kKB; };
   for (int m0 = 0; m0 < M; m0 += dma::kTokRows) {
     const int mrows = min(M - m0, dma::kTokRows);
+    if (m0 > 0) held = dma::list_entries(list, m0, P);
     // the pairs and routing weights of this lane's output rows (tile t, row
-    // col): the pairs load with the token-scale staging's list loads, the
-    // weights with the pass's token-row loads, not after the k loop
+    // col); the weights load with the pass's first copies, not after the k
+    // loop
     int pr[4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) pr[t] = list[m0 + min(t * 16 + col, mrows - 1)];
-    auto pair_of = [&](int r) { return list[m0 + r]; };
-    stage_token_scales(asl, as_, nkb, mrows, m0 == 0, pair_of);
-    float pw[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) pw[t] = topk_w[pr[t]];
+    for (int t = 0; t < 4; ++t) pr[t] = dma::list_entry(held, min(t * 16 + col, mrows - 1));
+    auto pair_of = [&](int r) { return dma::list_entry(held, r); };
     auto row_of = [&](int r) { return aq + (size_t)pair_of(r) * I; };
+    float pw[4];
+    // once the pass's first copies are issued: the token scales, the routing
+    // weights and, in the first pass, this wave's weight scales
+    auto stage = [&]() {
+      stage_token_scales(asl, as_, nkb, mrows, pair_of);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) pw[t] = topk_w[pr[t]];
+      if (m0 == 0)
+        for (int q = lane; q < 2 * nkb; q += 64) wsl[q] = q < 64 ? ws0 : wscale(q);
+    };
     f32x4 acc[2][4];
 #pragma unroll
     for (int g = 0; g < 2; ++g)
@@ -1418,7 +1442,7 @@ __global__ __launch_bounds__(256) void fp8_w2_dma_kernel(
                                    acc[g][t][j] = acc[g][t][j] + (d[j] * sa) * sw[g];
                                }
                              }
-                           });
+                           }, stage);
     };
     const int nt = (mrows + 15) >> 4;
     if (nt == 1)

@@ -154,22 +154,22 @@ __device__ inline int k_col(int k, int rot, int Kdim) {
 // weights; the w2 tensor reads at 6.2 TB/s and w2 here at 4.5 TB/s.
 // ---------------------------------------------------------------------------
 
-// The pass's GEMM over Kdim columns for mrows tokens (list[m0 ..]):
-// acc[g][t] += W(row group g) . A(token tile t)^T for the NT = ceil(mrows /
-// 16) tiles the pass fills, NG row groups of 16 per wave, the k loop starting
-// rot columns in.  A is the token matrix (leading dimension ld); with
-// kTokenRows, pair p reads row p / K.  With the weights as the MFMA's first
+// The pass's GEMM over Kdim columns for mrows tokens (the pass's pair list
+// held one entry per lane in `held`, dma::list_entries): acc[g][t] +=
+// W(row group g) . A(token tile t)^T for the NT = ceil(mrows / 16) tiles the
+// pass fills, NG row groups of 16 per wave, the k loop starting rot columns
+// in.  A is the token matrix (leading dimension ld); with kTokenRows, pair p
+// reads row p / K.  With the weights as the MFMA's first
 // operand, lane l holds rows 4 (l / 16) + q, q < 4, of its group for token
 // column l % 16: four consecutive outputs of one token, stored at once.
 template <int NG, int S, bool kTokenRows>
 __device__ inline void dma_gemm(unsigned char* smem,
                                 const unsigned char* const (&wrow)[16 * NG / dma::kRowsPerCopy],
-                                const uint16_t* __restrict__ A, int ld, int K,
-                                const int32_t* __restrict__ list, int m0, int mrows, int Kdim,
-                                int rot, f32x4 (&acc)[NG][4]) {
+                                const uint16_t* __restrict__ A, int ld, int K, int held,
+                                int mrows, int Kdim, int rot, f32x4 (&acc)[NG][4]) {
   const int lane = threadIdx.x & 63;
   auto row_of = [&](int r) {
-    const int p = list[m0 + r];
+    const int p = dma::list_entry(held, r);
     return reinterpret_cast<const unsigned char*>(A + (size_t)(kTokenRows ? p / K : p) * ld);
   };
   auto off = [&](int c) { return (size_t)k_col(c * 64, rot, Kdim) * sizeof(uint16_t); };
@@ -209,14 +209,12 @@ __device__ inline void dma_gemm(unsigned char* smem,
 }
 
 // The pairs of the token columns this lane stores after the pass (tile t,
-// column lane % 16; columns past mrows repeat the last), loaded before the
-// pass so that they travel with its own token-row loads instead of adding a
-// memory round trip after the k loop.
-__device__ inline void epilogue_pairs(const int32_t* __restrict__ list, int m0, int mrows,
-                                      int (&pr)[4]) {
+// column lane % 16; columns past mrows repeat the last), from the pass's
+// lane-held pair list.
+__device__ inline void epilogue_pairs(int held, int mrows, int (&pr)[4]) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
-  for (int t = 0; t < 4; ++t) pr[t] = list[m0 + min(t * 16 + (lane & 15), mrows - 1)];
+  for (int t = 0; t < 4; ++t) pr[t] = dma::list_entry(held, min(t * 16 + (lane & 15), mrows - 1));
 }
 
 // bf16(silu(g) * u) of four consecutive columns, one 8-byte store at p.
@@ -234,9 +232,11 @@ __global__ __launch_bounds__(256) void mfma_w13_dma_kernel(
     uint16_t* __restrict__ act) {
   extern __shared__ __attribute__((aligned(16))) unsigned char dsm[];
   const int s = blockIdx.y;
-  const int M = counts[s];
-  if (M == 0) return;
   const int32_t* list = lists + (size_t)s * P;
+  // the slot's count and the first pass's pair list, loaded together
+  const int M = counts[s];
+  int held = dma::list_entries(list, 0, P);
+  if (M == 0) return;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int i0 = blockIdx.x * kPanel + wave * 16;
   const uint16_t* W = w13 + (size_t)s * w13_stride;
@@ -251,14 +251,15 @@ __global__ __launch_bounds__(256) void mfma_w13_dma_kernel(
   const int rot = k_rotation(H);
   for (int m0 = 0; m0 < M; m0 += dma::kTokRows) {
     const int mrows = min(M - m0, dma::kTokRows);
+    if (m0 > 0) held = dma::list_entries(list, m0, P);
     f32x4 acc[2][4];
 #pragma unroll
     for (int g = 0; g < 2; ++g)
 #pragma unroll
       for (int t = 0; t < 4; ++t) acc[g][t] = f32x4{0.f, 0.f, 0.f, 0.f};
     int pr[4];
-    epilogue_pairs(list, m0, mrows, pr);
-    dma_gemm<2, S, true>(dsm, wrow, x, H, K, list, m0, mrows, H, rot, acc);
+    epilogue_pairs(held, mrows, pr);
+    dma_gemm<2, S, true>(dsm, wrow, x, H, K, held, mrows, H, rot, acc);
 #pragma unroll
     for (int t = 0; t < 4; ++t)
       if (t * 16 + (lane & 15) < mrows)
@@ -273,9 +274,11 @@ __global__ __launch_bounds__(256) void mfma_w2_dma_kernel(
     float* __restrict__ y) {
   extern __shared__ __attribute__((aligned(16))) unsigned char dsm[];
   const int s = blockIdx.y;
-  const int M = counts[s];
-  if (M == 0) return;
   const int32_t* list = lists + (size_t)s * P;
+  // the slot's count and the first pass's pair list, loaded together
+  const int M = counts[s];
+  int held = dma::list_entries(list, 0, P);
+  if (M == 0) return;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   // NG row groups of 16 per wave
   const int h0 = blockIdx.x * kPanel * NG + wave * 16 * NG;
@@ -288,14 +291,15 @@ __global__ __launch_bounds__(256) void mfma_w2_dma_kernel(
   const int rot = k_rotation_w2<NG>(I);
   for (int m0 = 0; m0 < M; m0 += dma::kTokRows) {
     const int mrows = min(M - m0, dma::kTokRows);
+    if (m0 > 0) held = dma::list_entries(list, m0, P);
     f32x4 acc[NG][4];
 #pragma unroll
     for (int g = 0; g < NG; ++g)
 #pragma unroll
       for (int t = 0; t < 4; ++t) acc[g][t] = f32x4{0.f, 0.f, 0.f, 0.f};
     int pr[4];
-    epilogue_pairs(list, m0, mrows, pr);
-    dma_gemm<NG, S, false>(dsm, wrow, act, I, 1, list, m0, mrows, I, rot, acc);
+    epilogue_pairs(held, mrows, pr);
+    dma_gemm<NG, S, false>(dsm, wrow, act, I, 1, held, mrows, I, rot, acc);
 #pragma unroll
     for (int t = 0; t < 4; ++t)
       if (t * 16 + (lane & 15) < mrows) {
