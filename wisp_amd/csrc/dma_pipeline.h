@@ -148,12 +148,16 @@ __device__ inline void pipeline(unsigned char* smem,
 // mrows repeat the last), a drain of the previous pass (its copies and its
 // readers of every stage and of anything after_prologue writes), then the
 // pipeline with this wave's share of the tile's copies.
+// A block's first pass (`first`) has no earlier pass to drain.  (Issuing
+// its chunk 0 weight copies before the token rows are resolved measured
+// slower: the compiler's wait for the pair list, which row_of permutes, also
+// waits for those copies.)
 template <int NWR, int S, int NT, typename RowOf, typename Off, typename F,
           typename G = NoSetup>
 __device__ inline void pass(unsigned char* smem,
                             const unsigned char* const (&wrow)[NWR / kRowsPerCopy], int mrows,
                             RowOf row_of, int n, Off off, F&& compute,
-                            G&& after_prologue = G{}) {
+                            G&& after_prologue = G{}, bool first = false) {
   constexpr int copies = 16 * NT / kRowsPerCopy;  // token copies of the tile, all waves
   static_assert(copies <= 4 * kMaxTokCopies, "token copies per wave");
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -161,8 +165,10 @@ __device__ inline void pass(unsigned char* smem,
 #pragma unroll
   for (int i = 0; i < kMaxTokCopies; ++i)
     arow[i] = row_of(min((wave + 4 * i) * kRowsPerCopy + lane / kLanesPerRow, mrows - 1));
-  wait_vm<0>();   // nothing but this pass's copies is outstanding below
-  lds_barrier();  // the previous pass's readers of every stage are done
+  if (!first) {
+    wait_vm<0>();   // nothing but this pass's copies is outstanding below
+    lds_barrier();  // the previous pass's readers of every stage are done
+  }
   const int tcw = (copies - wave + 3) / 4;  // copies j = wave + 4i < copies: 0, 1 or 2
   if (tcw <= 0)
     pipeline<NWR, S, 0>(smem, wrow, arow, n, off, compute, after_prologue);
@@ -172,13 +178,24 @@ __device__ inline void pass(unsigned char* smem,
     pipeline<NWR, S, 2>(smem, wrow, arow, n, off, compute, after_prologue);
 }
 
+// A load issued where it is written: the compiler neither sinks a relaxed
+// atomic load below later control flow (a kernel's early exit on an empty
+// slot) nor moves it after later loads, where plain loads of restrict data
+// may go.
+__device__ inline int32_t load_early(const int32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ inline float load_early(const float* p) {
+  return __int_as_float(load_early(reinterpret_cast<const int32_t*>(p)));
+}
+
 // A pass's pair list held one entry per lane: lane r holds list[m0 + r]
 // (entries at or past the slot's count, read clamped to the list's length,
 // are never used), so a tile row's entry is a lane permute rather than a
 // dependent global load.  A kernel loads the first pass's entries together
 // with the slot's count.
 __device__ inline int list_entries(const int32_t* __restrict__ list, int m0, int len) {
-  return list[min(m0 + (int)(threadIdx.x & 63), len - 1)];
+  return load_early(list + min(m0 + (int)(threadIdx.x & 63), len - 1));
 }
 __device__ inline int list_entry(int held, int r) { return __shfl(held, r); }
 

@@ -1280,7 +1280,8 @@ __global__ __launch_bounds__(256) void fp8_w13_dma_kernel(
   // first copies are issued)
   const int M = counts[s];
   int held = dma::list_entries(list, 0, P);
-  const float sg0 = Sg[min(lane, nkb - 1)], su0 = Su[min(lane, nkb - 1)];
+  const float sg0 = dma::load_early(Sg + min(lane, nkb - 1));
+  const float su0 = dma::load_early(Su + min(lane, nkb - 1));
   if (M == 0) return;
   float* xsl = reinterpret_cast<float*>(smem + dma::Smem<32, S>::kBytes);
   float* wsl = xsl + dma::kTokRows * nkb + wave * 2 * nkb;  // this wave's gate, up scales
@@ -1338,7 +1339,7 @@ __global__ __launch_bounds__(256) void fp8_w13_dma_kernel(
                                  au[t][j] = au[t][j] + (du[j] * sx) * su;
                                }
                              }
-                           }, stage);
+                           }, stage, m0 == 0);
     };
     const int nt = (mrows + 15) >> 4;
     if (nt == 1)
@@ -1374,16 +1375,16 @@ __global__ __launch_bounds__(256) void fp8_w2_dma_kernel(
   const int h0 = blockIdx.x * 128 + wave * 32;
   const int nkb = I / kKB;
   // this wave's weight scale q < 2 nkb: row group q / nkb, k-block q % nkb
-  auto wscale = [&](int q) {
+  auto wscale_at = [&](int q) {
     const int g = q / nkb, kb = q - g * nkb;
-    return s2[(size_t)s * s2_stride + (size_t)((h0 + 16 * g) / block_n) * nkb + kb];
+    return s2 + (size_t)s * s2_stride + (size_t)((h0 + 16 * g) / block_n) * nkb + kb;
   };
   // loaded together: the slot's count, the first pass's pair list and the
   // first 64 of this wave's weight scales (staged into LDS after the first
   // copies are issued)
   const int M = counts[s];
   int held = dma::list_entries(list, 0, P);
-  const float ws0 = wscale(min(lane, 2 * nkb - 1));
+  const float ws0 = dma::load_early(wscale_at(min(lane, 2 * nkb - 1)));
   if (M == 0) return;
   float* asl = reinterpret_cast<float*>(smem + dma::Smem<32, S>::kBytes);
   float* wsl = asl + dma::kTokRows * nkb + wave * 2 * nkb;  // scales of row groups 0, 1
@@ -1412,7 +1413,7 @@ __global__ __launch_bounds__(256) void fp8_w2_dma_kernel(
 #pragma unroll
       for (int t = 0; t < 4; ++t) pw[t] = topk_w[pr[t]];
       if (m0 == 0)
-        for (int q = lane; q < 2 * nkb; q += 64) wsl[q] = q < 64 ? ws0 : wscale(q);
+        for (int q = lane; q < 2 * nkb; q += 64) wsl[q] = q < 64 ? ws0 : *wscale_at(q);
     };
     f32x4 acc[2][4];
 #pragma unroll
@@ -1442,7 +1443,7 @@ __global__ __launch_bounds__(256) void fp8_w2_dma_kernel(
                                    acc[g][t][j] = acc[g][t][j] + (d[j] * sa) * sw[g];
                                }
                              }
-                           }, stage);
+                           }, stage, m0 == 0);
     };
     const int nt = (mrows + 15) >> 4;
     if (nt == 1)

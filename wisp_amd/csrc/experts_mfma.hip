@@ -166,7 +166,8 @@ template <int NG, int S, bool kTokenRows>
 __device__ inline void dma_gemm(unsigned char* smem,
                                 const unsigned char* const (&wrow)[16 * NG / dma::kRowsPerCopy],
                                 const uint16_t* __restrict__ A, int ld, int K, int held,
-                                int mrows, int Kdim, int rot, f32x4 (&acc)[NG][4]) {
+                                int mrows, int Kdim, int rot, bool first,
+                                f32x4 (&acc)[NG][4]) {
   const int lane = threadIdx.x & 63;
   auto row_of = [&](int r) {
     const int p = dma::list_entry(held, r);
@@ -195,7 +196,8 @@ __device__ inline void dma_gemm(unsigned char* smem,
                 acc[g][t] =
                     __builtin_amdgcn_mfma_f32_16x16x32_bf16(b[g], a[t], acc[g][t], 0, 0, 0);
           }
-        });
+        },
+        dma::NoSetup{}, first);
   };
   const int nt = (mrows + 15) >> 4;
   if (nt == 1)
@@ -259,7 +261,7 @@ __global__ __launch_bounds__(256) void mfma_w13_dma_kernel(
       for (int t = 0; t < 4; ++t) acc[g][t] = f32x4{0.f, 0.f, 0.f, 0.f};
     int pr[4];
     epilogue_pairs(held, mrows, pr);
-    dma_gemm<2, S, true>(dsm, wrow, x, H, K, held, mrows, H, rot, acc);
+    dma_gemm<2, S, true>(dsm, wrow, x, H, K, held, mrows, H, rot, m0 == 0, acc);
 #pragma unroll
     for (int t = 0; t < 4; ++t)
       if (t * 16 + (lane & 15) < mrows)
@@ -299,7 +301,7 @@ __global__ __launch_bounds__(256) void mfma_w2_dma_kernel(
       for (int t = 0; t < 4; ++t) acc[g][t] = f32x4{0.f, 0.f, 0.f, 0.f};
     int pr[4];
     epilogue_pairs(held, mrows, pr);
-    dma_gemm<NG, S, false>(dsm, wrow, act, I, 1, held, mrows, I, rot, acc);
+    dma_gemm<NG, S, false>(dsm, wrow, act, I, 1, held, mrows, I, rot, m0 == 0, acc);
 #pragma unroll
     for (int t = 0; t < 4; ++t)
       if (t * 16 + (lane & 15) < mrows) {
