@@ -356,7 +356,22 @@ __global__ __launch_bounds__(64) void pager_kernel(
       id_out[p] = fr.ids[p];
     }
   } else if (STAGED) {
-    for (int p = lane; p < P; p += 64) fr.ids[p] = ids_in[p];
+    // 16 loads in flight per lane before their LDS stores: a 4096-pair call
+    // waits for 4 global round trips instead of 64.
+    constexpr int kBatch = 16;
+    for (int p0 = 0; p0 < P; p0 += 64 * kBatch) {
+      int v[kBatch];
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        const int p = p0 + i * 64 + lane;
+        v[i] = p < P ? ids_in[p] : 0;
+      }
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        const int p = p0 + i * 64 + lane;
+        if (p < P) fr.ids[p] = v[i];
+      }
+    }
     wave_lds_sync();
   }
   if (!logits && state_in_regs) mask_state();
@@ -419,7 +434,7 @@ __global__ __launch_bounds__(64) void pager_kernel(
   for (int w = 0; w < W; ++w) gu[w] = 0u;
   int sw = -1;  // the window the scan describes (-1: none)
   auto scan_window = [&](int b) {
-    load_window(b);
+    if (wb != b) load_window(b);
     const int lim = min(64, T - wb);  // tokens in the window
     const int closed = wb + lim == T ? lim : kOpenEnd;  // a group running to the window's end
 #pragma unroll
@@ -493,46 +508,72 @@ __global__ __launch_bounds__(64) void pager_kernel(
         for (int w = 0; w < W; ++w)
           u[w] = w < nwords ? (uint32_t)__builtin_amdgcn_readfirstlane((int)sm.need[w]) : 0u;
       } else {
-        // Greedy first-fit in token order: the group that starts at `start`
-        // from the window scan (scanning a window that starts there when the
-        // current one does not cover it).
-        int l = start - sw;
-        const bool covered = sw >= 0 && l >= 0 && l < 64;
-        int eo = covered ? __builtin_amdgcn_readlane(gend, l) : kOpenEnd;
-        if (eo == kOpenEnd && !(covered && l == 0)) {
-          scan_window(start);
-          l = 0;
-          eo = __builtin_amdgcn_readlane(gend, 0);
-        }
+        // The reference's working-set check (fused_moe.py:1102): a call
+        // whose distinct experts fit in cap is one group.  The union of all
+        // the tokens' masks decides it before any window scan (which would
+        // otherwise run every lane to the window's end).
+        bool whole = false;
+        if (start == 0) {
+          uint32_t all[W];
 #pragma unroll
-        for (int w = 0; w < W; ++w) u[w] = (uint32_t)__builtin_amdgcn_readlane((int)gu[w], l);
-        end = eo == kOpenEnd ? -1 : sw + eo;
-        // A group longer than the window (it starts the window): extend it
-        // window by window with a prefix OR across the lanes (tokens before
-        // `b` masked out), up to the first token whose union exceeds cap.
-        for (int b = sw + 64; b < T && end < 0;) {
-          if (b >= wb + 64) load_window(b);
-          sw = -1;  // wm no longer holds the scanned window
-          const int tl = wb + lane;
-          const bool live = tl >= b && tl < T;
-          uint32_t m[W];
+          for (int w = 0; w < W; ++w) all[w] = 0u;
+          for (int b = 0; b < T; b += 64) {
+            load_window(b);
+#pragma unroll
+            for (int w = 0; w < W; ++w) all[w] |= wave_or(wm[w]);
+          }
           int c = 0;
 #pragma unroll
-          for (int w = 0; w < W; ++w) {
-            m[w] = wave_prefix_or(live ? wm[w] : 0u, lane) | u[w];
-            c += __popc(m[w]);
-          }
-          const uint64_t over = ballot(live && c > cap);
-          const int last = over ? __builtin_ctzll(over) - 1 : min(63, T - 1 - wb);
-          if (last >= 0) {
+          for (int w = 0; w < W; ++w) c += __popc(all[w]);
+          if (c <= cap) {
+            whole = true;
+            end = T;
 #pragma unroll
-            for (int w = 0; w < W; ++w)
-              u[w] = (uint32_t)__builtin_amdgcn_readlane((int)m[w], last);
+            for (int w = 0; w < W; ++w) u[w] = all[w];
           }
-          if (over) end = wb + __builtin_ctzll(over);
-          b = wb + 64;
         }
-        if (end < 0) end = T;
+        if (!whole) {
+          // Greedy first-fit in token order: the group that starts at `start`
+          // from the window scan (scanning a window that starts there when the
+          // current one does not cover it).
+          int l = start - sw;
+          const bool covered = sw >= 0 && l >= 0 && l < 64;
+          int eo = covered ? __builtin_amdgcn_readlane(gend, l) : kOpenEnd;
+          if (eo == kOpenEnd && !(covered && l == 0)) {
+            scan_window(start);
+            l = 0;
+            eo = __builtin_amdgcn_readlane(gend, 0);
+          }
+#pragma unroll
+          for (int w = 0; w < W; ++w) u[w] = (uint32_t)__builtin_amdgcn_readlane((int)gu[w], l);
+          end = eo == kOpenEnd ? -1 : sw + eo;
+          // A group longer than the window (it starts the window): extend it
+          // window by window with a prefix OR across the lanes (tokens before
+          // `b` masked out), up to the first token whose union exceeds cap.
+          for (int b = sw + 64; b < T && end < 0;) {
+            if (b >= wb + 64) load_window(b);
+            sw = -1;  // wm no longer holds the scanned window
+            const int tl = wb + lane;
+            const bool live = tl >= b && tl < T;
+            uint32_t m[W];
+            int c = 0;
+#pragma unroll
+            for (int w = 0; w < W; ++w) {
+              m[w] = wave_prefix_or(live ? wm[w] : 0u, lane) | u[w];
+              c += __popc(m[w]);
+            }
+            const uint64_t over = ballot(live && c > cap);
+            const int last = over ? __builtin_ctzll(over) - 1 : min(63, T - 1 - wb);
+            if (last >= 0) {
+#pragma unroll
+              for (int w = 0; w < W; ++w)
+                u[w] = (uint32_t)__builtin_amdgcn_readlane((int)m[w], last);
+            }
+            if (over) end = wb + __builtin_ctzll(over);
+            b = wb + 64;
+          }
+          if (end < 0) end = T;
+        }
         // (the register path keeps the needed set in u and the loaded
         // experts in ballots)
         if (!regs) {
