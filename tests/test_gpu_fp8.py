@@ -201,11 +201,13 @@ def test_experts_fp8_batching_is_byte_invariant(algo):
     assert torch.equal(torch.cat(halves).view(torch.int32), full.view(torch.int32))
 
 
-GROUPED = [  # T, H, I, E, K, block: tile widths 1, 2 and 4 per pass, odd k-block counts
+GROUPED = [  # T, H, I, E, K, block: tile widths 1, 2 and 4 per pass, odd k-block counts;
+    # w2 blocks of 4 (H a multiple of 512), 2 (H = 768) and 1 (H = 384) panels
     (16, 2048, 768, 32, 8, (128, 128)),
     (70, 1024, 384, 16, 4, (64, 128)),
     (200, 512, 256, 24, 8, (128, 128)),
     (40, 384, 640, 12, 2, (128, 128)),
+    (33, 768, 256, 10, 4, (128, 128)),
 ]
 
 
@@ -221,12 +223,15 @@ def test_experts_fp8_grouped_match_oracle(T, H, I, E, K, block):
     assert _rel(out, want) < REL_TOL, _rel(out, want)
 
 
-def test_experts_fp8_grouped_bytes_equal_across_kernel_families():
+@pytest.mark.parametrize("H,I,block", [(1024, 384, (64, 128)), (768, 256, (128, 128)),
+                                         (384, 640, (128, 128))])
+def test_experts_fp8_grouped_bytes_equal_across_kernel_families(H, I, block):
     """Above 16 tokens the grouped path runs the LDS-staged kernels, up to 16
     the register-streaming ones; both take each output through the same
     k-block steps, so one call over 48 tokens, two of 24 and chunks of 8 or
-    16 give the same bytes for every token."""
-    T, H, I, E, K, block = 48, 1024, 384, 12, 4, (64, 128)
+    16 give the same bytes for every token (w2 blocks of 4, 2 and 1 panels
+    for H = 1024, 768 and 384)."""
+    T, E, K = 48, 12, 4
     _, w13, w2, s13, s2 = _experts(E, H, I, block, seed=21)
     ids, tw = _routing(T, E, K, seed=22)
     x = torch.randn((T, H), generator=torch.Generator().manual_seed(23)).to(torch.bfloat16)

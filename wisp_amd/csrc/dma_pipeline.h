@@ -86,27 +86,35 @@ struct Smem {
   static constexpr int kBytes = S * kStage;
 };
 
-// One stage's copies of the chunk that starts `off` bytes into every row:
-// this wave's NWR weight rows and its TCW token copies.  wrow[i] / arow[i]
-// are the lane's source rows (copy i covers rows [8i, 8i + 8) of the wave's
-// weights; token copy wave + 4i covers tile rows [8 (wave + 4i), +8)).
+// A chunk's byte offsets into the weight rows (w) and the token rows (t).
+// A chunk offset given as one number applies to both.
+struct Offs {
+  size_t w, t;
+};
+__device__ inline Offs offs_of(size_t o) { return Offs{o, o}; }
+__device__ inline Offs offs_of(Offs o) { return o; }
+
+// One stage's copies of the chunk at offsets o: this wave's NWR weight rows
+// and its TCW token copies.  wrow[i] / arow[i] are the lane's source rows
+// (copy i covers rows [8i, 8i + 8) of the wave's weights; token copy
+// wave + 4i covers tile rows [8 (wave + 4i), +8)).
 template <int NWR, int TCW>
 __device__ inline void chunk_copies(unsigned char* stage,
                                     const unsigned char* const (&wrow)[NWR / kRowsPerCopy],
                                     const unsigned char* const (&arow)[kMaxTokCopies], int wave,
-                                    int lane, size_t off) {
+                                    int lane, Offs o) {
   const int pos = lane % kLanesPerRow, sub = lane / kLanesPerRow;
 #pragma unroll
   for (int i = 0; i < NWR / kRowsPerCopy; ++i) {
     const int r = i * kRowsPerCopy + sub;
-    dma16(wrow[i] + off + ((pos ^ (r & 7)) << 4),
+    dma16(wrow[i] + o.w + ((pos ^ (r & 7)) << 4),
           stage + (wave * NWR + i * kRowsPerCopy) * kRowBytes);
   }
   unsigned char* at = stage + 4 * NWR * kRowBytes;
 #pragma unroll
   for (int i = 0; i < TCW; ++i) {
     const int r0 = (wave + 4 * i) * kRowsPerCopy;
-    dma16(arow[i] + off + ((pos ^ ((r0 + sub) & 7)) << 4), at + r0 * kRowBytes);
+    dma16(arow[i] + o.t + ((pos ^ ((r0 + sub) & 7)) << 4), at + r0 * kRowBytes);
   }
 }
 
@@ -114,8 +122,26 @@ struct NoSetup {
   __device__ void operator()() const {}
 };
 
+// One step of the pipeline: the copies of a later chunk into stage `wr`
+// (when `issue`), then the compute of chunk c from stage `rd`.  The two
+// stages never overlap, and the restrict parameters say so: the compiler's
+// memory-counter pass then sees that the compute's LDS reads do not depend
+// on the copies just issued.  Without that it waits for every copy in
+// flight before the first LDS read, so a block held one chunk in flight
+// whatever the stage count.
+template <int NWR, int TCW, typename F>
+__device__ __attribute__((always_inline)) inline void step(
+    unsigned char* __restrict__ wr, const unsigned char* __restrict__ rd, bool issue,
+    const unsigned char* const (&wrow)[NWR / kRowsPerCopy],
+    const unsigned char* const (&arow)[kMaxTokCopies], int wave, int lane, Offs o, F& compute,
+    int c) {
+  if (issue) chunk_copies<NWR, TCW>(wr, wrow, arow, wave, lane, o);
+  compute(rd + wave * NWR * kRowBytes, rd + 4 * NWR * kRowBytes, c);
+}
+
 // The S-stage pipeline over n chunks; chunk c starts off(c) bytes into every
-// row.  after_prologue() runs once the first S - 1 chunks' copies are issued
+// row (or off(c).w into the weight rows and off(c).t into the token rows).
+// after_prologue() runs once the first S - 1 chunks' copies are issued
 // (setup whose loads should travel with them: what it writes to LDS is seen
 // by every wave from chunk 0's compute on, after the loop's barrier);
 // compute(ws, as, c) runs once chunk c has landed, with ws this wave's weight
@@ -130,16 +156,15 @@ __device__ inline void pipeline(unsigned char* smem,
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
   for (int c = 0; c < S - 1; ++c)
-    if (c < n) chunk_copies<NWR, TCW>(smem + c * Sm::kStage, wrow, arow, wave, lane, off(c));
+    if (c < n)
+      chunk_copies<NWR, TCW>(smem + c * Sm::kStage, wrow, arow, wave, lane, offs_of(off(c)));
   after_prologue();
   for (int c = 0; c < n; ++c) {
     wait_chunk<PER, S - 2>(min(S - 2, n - 1 - c));
     lds_barrier();
-    if (c + S - 1 < n)
-      chunk_copies<NWR, TCW>(smem + ((c + S - 1) % S) * Sm::kStage, wrow, arow, wave, lane,
-                             off(c + S - 1));
-    const unsigned char* st = smem + (c % S) * Sm::kStage;
-    compute(st + wave * NWR * kRowBytes, st + Sm::kW, c);
+    const bool issue = c + S - 1 < n;
+    step<NWR, TCW>(smem + ((c + S - 1) % S) * Sm::kStage, smem + (c % S) * Sm::kStage, issue,
+                   wrow, arow, wave, lane, offs_of(off(issue ? c + S - 1 : c)), compute, c);
   }
 }
 

@@ -1229,7 +1229,12 @@ __global__ __launch_bounds__(256) void fp8_grouped_w2_kernel(
 // are staged once per block.
 //   fp8_w13_dma: grid (I / 64, nslots), wave w owns gate rows
 //     [64 bx + 16w, +16) and the matching up rows;
-//   fp8_w2_dma: grid (H / 128, nslots), wave w owns rows [128 bx + 32w, +32).
+//   fp8_w2_dma<S, NP>: grid (H / (128 NP), nslots); the block streams NP
+//     consecutive 128-row panels of its slot as one chunk sequence (the
+//     token tile is the same for all of them), wave w owning rows
+//     [128 (NP bx + p) + 32w, +32) of panel p, stored at the panel's last
+//     k-block.  A block's setup (count, pair list, scales) and its first
+//     chunk's latency are paid once per NP panels.
 // ---------------------------------------------------------------------------
 
 // A lane's fp8 MFMA operand from a swizzled LDS slice: row r, the 32 bytes
@@ -1240,11 +1245,11 @@ __device__ inline i32x8 lds_operand(const unsigned char* slice, int r, int grp) 
 }
 
 // Dynamic LDS of the LDS-staged kernels: the stages, the pass's token scales
-// [64][nkb], the four waves' weight scales [4][2][nkb].
-template <int S>
+// [64][nkb], the four waves' weight scales [4][NP][2][nkb].
+template <int S, int NP = 1>
 inline size_t fp8_dma_lds(int nkb) {
   return dma::Smem<32, S>::kBytes + (size_t)dma::kTokRows * nkb * sizeof(float) +
-         (size_t)4 * 2 * nkb * sizeof(float);
+         (size_t)4 * NP * 2 * nkb * sizeof(float);
 }
 
 // Stages the pass's token scales: row r < 64 of the tile reads the scales of
@@ -1361,7 +1366,25 @@ __global__ __launch_bounds__(256) void fp8_w13_dma_kernel(
   }
 }
 
-template <int S>
+// A wave's w2 outputs of one 32-row panel: D[row][col] is weight row
+// h0 + 16 g + 4 grp + j, token column col of tile t.
+__device__ inline void store_w2_tile(uint16_t* __restrict__ y, int H, int h0, const int (&pr)[4],
+                                     const float (&pw)[4], int mrows, int col, int grp,
+                                     const f32x4 (&acc)[2][4]) {
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int r = t * 16 + col;
+    if (r < mrows) {
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        store_bf16x4(y + (size_t)pr[t] * H + h0 + 16 * g + grp * 4, acc[g][t][0] * pw[t],
+                     acc[g][t][1] * pw[t], acc[g][t][2] * pw[t], acc[g][t][3] * pw[t]);
+      }
+    }
+  }
+}
+
+template <int S, int NP>
 __global__ __launch_bounds__(256) void fp8_w2_dma_kernel(
     const uint8_t* __restrict__ aq, const float* __restrict__ as_, int H, int I, int P,
     const int32_t* __restrict__ lists, const int32_t* __restrict__ counts,
@@ -1372,28 +1395,35 @@ __global__ __launch_bounds__(256) void fp8_w2_dma_kernel(
   const int32_t* list = lists + (size_t)s * P;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int col = lane & 15, grp = lane >> 4;
-  const int h0 = blockIdx.x * 128 + wave * 32;
+  const int hb = blockIdx.x * NP * 128 + wave * 32;  // this wave's rows in panel 0
   const int nkb = I / kKB;
-  // this wave's weight scale q < 2 nkb: row group q / nkb, k-block q % nkb
+  // this wave's weight scale q < 2 NP nkb: panel q / (2 nkb), row group
+  // (q / nkb) % 2, k-block q % nkb
   auto wscale_at = [&](int q) {
-    const int g = q / nkb, kb = q - g * nkb;
-    return s2 + (size_t)s * s2_stride + (size_t)((h0 + 16 * g) / block_n) * nkb + kb;
+    const int pg = q / nkb, kb = q - pg * nkb;
+    const int h = hb + (pg >> 1) * 128 + 16 * (pg & 1);
+    return s2 + (size_t)s * s2_stride + (size_t)(h / block_n) * nkb + kb;
   };
   // loaded together: the slot's count, the first pass's pair list and the
   // first 64 of this wave's weight scales (staged into LDS after the first
   // copies are issued)
   const int M = counts[s];
   int held = dma::list_entries(list, 0, P);
-  const float ws0 = dma::load_early(wscale_at(min(lane, 2 * nkb - 1)));
+  const float ws0 = dma::load_early(wscale_at(min(lane, 2 * NP * nkb - 1)));
   if (M == 0) return;
   float* asl = reinterpret_cast<float*>(smem + dma::Smem<32, S>::kBytes);
-  float* wsl = asl + dma::kTokRows * nkb + wave * 2 * nkb;  // scales of row groups 0, 1
+  float* wsl = asl + dma::kTokRows * nkb + wave * 2 * NP * nkb;  // [panel][row group][k-block]
   const uint8_t* W = w2 + (size_t)s * w2_stride;
   const unsigned char* wrow[32 / dma::kRowsPerCopy];
 #pragma unroll
   for (int i = 0; i < 32 / dma::kRowsPerCopy; ++i)
-    wrow[i] = W + (size_t)(h0 + i * dma::kRowsPerCopy + lane / dma::kLanesPerRow) * I;
-  auto off = [](int c) { return (size_t)c * kKB; };
+    wrow[i] = W + (size_t)(hb + i * dma::kRowsPerCopy + lane / dma::kLanesPerRow) * I;
+  // chunk q: panel q / nkb (128 rows further down per panel), k-block q % nkb
+  auto off = [&](int q) {
+    const int pn = q / nkb;
+    const size_t kb = (size_t)(q - pn * nkb) * kKB;
+    return dma::Offs{(size_t)pn * 128 * I + kb, kb};
+  };
   for (int m0 = 0; m0 < M; m0 += dma::kTokRows) {
     const int mrows = min(M - m0, dma::kTokRows);
     if (m0 > 0) held = dma::list_entries(list, m0, P);
@@ -1413,7 +1443,7 @@ __global__ __launch_bounds__(256) void fp8_w2_dma_kernel(
 #pragma unroll
       for (int t = 0; t < 4; ++t) pw[t] = topk_w[pr[t]];
       if (m0 == 0)
-        for (int q = lane; q < 2 * nkb; q += 64) wsl[q] = q < 64 ? ws0 : *wscale_at(q);
+        for (int q = lane; q < 2 * NP * nkb; q += 64) wsl[q] = q < 64 ? ws0 : *wscale_at(q);
     };
     f32x4 acc[2][4];
 #pragma unroll
@@ -1422,14 +1452,16 @@ __global__ __launch_bounds__(256) void fp8_w2_dma_kernel(
       for (int t = 0; t < 4; ++t) acc[g][t] = f32x4{0.f, 0.f, 0.f, 0.f};
     auto run = [&](auto nt) {
       constexpr int NT = decltype(nt)::value;
-      dma::pass<32, S, NT>(smem, wrow, mrows, row_of, nkb, off,
-                           [&](const unsigned char* ws, const unsigned char* ts, int c) {
+      dma::pass<32, S, NT>(smem, wrow, mrows, row_of, NP * nkb, off,
+                           [&](const unsigned char* ws, const unsigned char* ts, int q) {
+                             const int pn = NP > 1 ? q / nkb : 0;
+                             const int c = q - pn * nkb;
                              i32x8 a[2];
                              float sw[2];
 #pragma unroll
                              for (int g = 0; g < 2; ++g) {
                                a[g] = lds_operand(ws, g * 16 + col, grp);
-                               sw[g] = wsl[g * nkb + c];
+                               sw[g] = wsl[(2 * pn + g) * nkb + c];
                              }
 #pragma unroll
                              for (int t = 0; t < NT; ++t) {
@@ -1443,6 +1475,15 @@ __global__ __launch_bounds__(256) void fp8_w2_dma_kernel(
                                    acc[g][t][j] = acc[g][t][j] + (d[j] * sa) * sw[g];
                                }
                              }
+                             if (NP > 1 && c == nkb - 1) {
+                               // the panel's last k-block: its outputs, then
+                               // fresh sums for the next panel
+                               store_w2_tile(y, H, hb + pn * 128, pr, pw, mrows, col, grp, acc);
+#pragma unroll
+                               for (int g = 0; g < 2; ++g)
+#pragma unroll
+                                 for (int t = 0; t < 4; ++t) acc[g][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+                             }
                            }, stage, m0 == 0);
     };
     const int nt = (mrows + 15) >> 4;
@@ -1454,17 +1495,7 @@ __global__ __launch_bounds__(256) void fp8_w2_dma_kernel(
       run(std::integral_constant<int, 3>{});
     else
       run(std::integral_constant<int, 4>{});
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int r = t * 16 + col;
-      if (r < mrows) {
-#pragma unroll
-        for (int g = 0; g < 2; ++g) {
-          store_bf16x4(y + (size_t)pr[t] * H + h0 + 16 * g + grp * 4, acc[g][t][0] * pw[t],
-                       acc[g][t][1] * pw[t], acc[g][t][2] * pw[t], acc[g][t][3] * pw[t]);
-        }
-      }
-    }
+    if (NP == 1) store_w2_tile(y, H, hb, pr, pw, mrows, col, grp, acc);
   }
 }
 
@@ -1649,18 +1680,18 @@ const char* fp8_unsupported(int H, int I, int K, int block_n, int block_k) {
 }
 
 // The LDS-staged kernels with the activation quantisation between them.
-template <int S13, int S2>
+template <int S13, int S2, int NP2>
 bool launch_grouped_dma(const uint8_t* xq, const float* xs, uint8_t* aq, float* as, int T, int H,
                         int I, int K, int nslots, const int32_t* lists, const int32_t* counts,
                         const float* topk_w, const uint8_t* w13, size_t w13_stride,
                         const float* s13, size_t s13_stride, const uint8_t* w2, size_t w2_stride,
                         const float* s2, size_t s2_stride, int block_n, uint16_t* act,
                         uint16_t* y, hipStream_t st, const StageEvents* ev) {
-  const size_t l13 = fp8_dma_lds<S13>(H / kKB), l2 = fp8_dma_lds<S2>(I / kKB);
-  if (l13 > kMaxLds || l2 > kMaxLds || H % 128) return false;
+  const size_t l13 = fp8_dma_lds<S13>(H / kKB), l2 = fp8_dma_lds<S2, NP2>(I / kKB);
+  if (l13 > kMaxLds || l2 > kMaxLds || H % (128 * NP2)) return false;
   static std::atomic<uint64_t> big13{0}, big2{0};
   if (allow_lds(&fp8_w13_dma_kernel<S13>, l13, kMaxLds, &big13) != hipSuccess ||
-      allow_lds(&fp8_w2_dma_kernel<S2>, l2, kMaxLds, &big2) != hipSuccess) {
+      allow_lds(&fp8_w2_dma_kernel<S2, NP2>, l2, kMaxLds, &big2) != hipSuccess) {
     (void)hipGetLastError();
     return false;
   }
@@ -1673,7 +1704,8 @@ bool launch_grouped_dma(const uint8_t* xq, const float* xs, uint8_t* aq, float* 
   const long jobs = (long)P * (I / kKB);
   hipLaunchKernelGGL(quant_groups_kernel<uint16_t>, dim3((unsigned)((jobs + 15) / 16)),
                      dim3(256), 0, st, (const uint16_t*)act, P, I, aq, as);
-  launch_timed_lds(fp8_w2_dma_kernel<S2>, dim3(H / 128, nslots), dim3(256), (unsigned)l2, st, e2,
+  launch_timed_lds(fp8_w2_dma_kernel<S2, NP2>, dim3(H / (128 * NP2), nslots), dim3(256),
+                   (unsigned)l2, st, e2,
                    e3, aq, as, H, I, P, lists, counts, topk_w, w2, w2_stride, s2, s2_stride,
                    block_n, y);
   return true;
@@ -1734,15 +1766,24 @@ int experts_fp8_grouped(const void* x, int T, int H, int I, int K, const float* 
   // above 16 tokens the LDS-staged kernels (at 16 the register-streaming
   // ones are faster here: 97 against 102 us at the Qwen3-FP8 shape, resident);
   // they return false where their LDS would not fit
-  // Two stages: an fp8 row is half a bf16 row's bytes, so its k loop is
-  // short (16 and 6 chunks at the Qwen3 shape), and with 48 KiB of stages
-  // three blocks fit per CU and overlap each other's setup.  Measured on
-  // MI355X at the Qwen3-FP8 512-token chunk: 157 us, against 172 us with
-  // three stages.
-  if (T > 16 && launch_grouped_dma<2, 2>(xq, xs, aq, as, T, H, I, K, nslots, lists, counts,
-                                         topk_w, (const uint8_t*)w13, w13_stride, s13,
-                                         s13_stride, (const uint8_t*)w2, w2_stride, s2, s2_stride,
-                                         block_n, (uint16_t*)act, y, st, ev)) {
+  // w13 with two stages: an fp8 row is half a bf16 row's bytes, so its k
+  // loop is short (16 chunks at the Qwen3 shape), and with 48 KiB of stages
+  // three blocks fit per CU and overlap each other's setup (157 against
+  // 172 us for the Qwen3-FP8 512-token chunk with three stages, measured on
+  // MI355X).  w2 (6 chunks per 128-row panel) with four panels per block and
+  // three stages: two blocks per CU, each with two chunks in flight.
+  // Measured at the Qwen3-FP8 shape, two runs each: bs=32 step 35.0 / 34.9
+  // against 37.2 / 37.0 us with one panel and two stages, 512-token chunk
+  // 49.7 / 50.0 against 49.6 / 49.6 us; two panels per block with two stages
+  // leave a tail (1,024 blocks over 768 block slots): 41.1 and 52.8 us.
+  constexpr int kNP = 4;
+  const int np2 = H % (128 * kNP) == 0 ? kNP : H % 256 == 0 ? 2 : 1;
+  auto dma = np2 == kNP ? &launch_grouped_dma<2, 3, kNP>
+             : np2 == 2 ? &launch_grouped_dma<2, 3, 2>
+                        : &launch_grouped_dma<2, 3, 1>;
+  if (T > 16 && dma(xq, xs, aq, as, T, H, I, K, nslots, lists, counts, topk_w,
+                    (const uint8_t*)w13, w13_stride, s13, s13_stride, (const uint8_t*)w2,
+                    w2_stride, s2, s2_stride, block_n, (uint16_t*)act, y, st, ev)) {
     hipLaunchKernelGGL(fp8_combine_kernel, dim3((H + 255) / 256, T), dim3(256), 0, st, y, H, K,
                        nslots, slots, (uint16_t*)out);
     WISP_HIP_TRY(hipGetLastError());
