@@ -1772,10 +1772,11 @@ int experts_fp8_grouped(const void* x, int T, int H, int I, int K, const float* 
   // 172 us for the Qwen3-FP8 512-token chunk with three stages, measured on
   // MI355X).  w2 (6 chunks per 128-row panel) with four panels per block and
   // three stages: two blocks per CU, each with two chunks in flight.
-  // Measured at the Qwen3-FP8 shape, two runs each: bs=32 step 35.0 / 34.9
-  // against 37.2 / 37.0 us with one panel and two stages, 512-token chunk
-  // 49.7 / 50.0 against 49.6 / 49.6 us; two panels per block with two stages
-  // leave a tail (1,024 blocks over 768 block slots): 41.1 and 52.8 us.
+  // Measured at the Qwen3-FP8 shape, two runs each: bs=32 step 30.4 / 30.4
+  // against 33.7 / 33.7 us with one panel per block and 31.7 / 31.6 us with
+  // four panels and two stages; 512-token chunk 47.9 / 48.0 against
+  // 50.0 / 50.5 and 48.8 / 48.9 us.  Two panels per block with two stages
+  // leave a tail (1,024 blocks over 768 block slots).
   constexpr int kNP = 4;
   const int np2 = H % (128 * kNP) == 0 ? kNP : H % 256 == 0 ? 2 : 1;
   auto dma = np2 == kNP ? &launch_grouped_dma<2, 3, kNP>
