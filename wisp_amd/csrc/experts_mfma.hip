@@ -119,9 +119,9 @@ __global__ __launch_bounds__(64 * kGatherWaves) void gather_kernel(
 // Where the k loop of an output panel starts.  Every block streams its rows
 // chunk by chunk; when all blocks start at column 0, the reads in flight share
 // their low address bits and crowd a few memory channels (a pure read of the
-// Qwen3 w13 tensor in this order: 5.4 TB/s on MI355X).  Starting each panel
-// at its own multiple of 64 columns, evenly spread over the row, and wrapping
-// around gives 5.9 TB/s.  The start depends only on the panel (blockIdx.x),
+// Qwen3 w13 tensor in this order, non-temporal loads: 6.27 TB/s on MI355X).
+// Starting each panel at its own multiple of 64 columns, evenly spread over
+// the row, and wrapping around gives 6.99 TB/s.  The start depends only on the panel (blockIdx.x),
 // never on the slot, so an output's dot-product order is the same for any
 // slot placement or token grouping.
 __device__ inline int k_rotation(int Kdim) {
@@ -149,9 +149,10 @@ __device__ inline int k_col(int k, int rot, int Kdim) {
 // (128-byte) chunks, two 32-column k-steps of MFMA per chunk, the k rotation
 // of the output panel.  w13 blocks own a 64-row panel (each wave 16 gate and
 // 16 up rows); w2 blocks own 128 rows (32 per wave).
-// What bounds them: a pure read of the Qwen3 w13 tensor in this chunk order
-// and rotation runs at 5.9 TB/s on MI355X and w13 here at 5.3 TB/s of
-// weights; the w2 tensor reads at 6.2 TB/s and w2 here at 4.5 TB/s.
+// What bounds them: a pure read of the Qwen3 w13 tensor with these copies
+// (non-temporal), chunk order, rotation and occupancy runs at 6.95 TB/s on
+// MI355X and w13 here at 6.18 TB/s of weights; the w2 tensor reads at
+// 6.45 TB/s and w2 here at 4.90 TB/s.
 // ---------------------------------------------------------------------------
 
 // The pass's GEMM over Kdim columns for mrows tokens (the pass's pair list
