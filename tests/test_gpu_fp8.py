@@ -346,6 +346,50 @@ def test_fp8_state_subbatches_like_the_reference(small_fp8):
     assert st.slot_to_expert == ora.slot_to_expert and st.lru_tick == ora.lru_tick
 
 
+@pytest.fixture(scope="module")
+def full_fp8():
+    """The Qwen3-30B-A3B-FP8 layer at full size (128 experts), one 512-token
+    chunk with router logits ~N(0, 1), pinned masters."""
+    return W.fp8_layer(W.gaussian_logits("batch", seed=5, steps=1, tokens=512, weights=False),
+                       pin=True)
+
+
+def test_fp8_state_full_size_chunk_and_batches(full_fp8):
+    """At the full Qwen3-FP8 shape: the 512-token chunk through cap=32 (~4-token
+    groups on the register-streaming kernels) and through cap=E (one group on
+    the LDS-staged kernels, w2 blocks of four 128-row panels) give the same
+    bytes; decisions equal the reference pager's; sampled tokens match the
+    oracle.  Then two bs=32 steps, from the chunk's tokens, the same way."""
+    wl = full_fp8
+    E, K, cap = 128, wl.shape.top_k, 32
+    st = _fp8_state(wl, cap)
+    full = _fp8_state(wl, E)
+    ora = PagerOracle(E, cap)
+    w13, w2, s13, s2 = wl.views()
+    x, lg = wl.x[0].to(DEV), wl.logits[0].to(DEV)
+    out = st.forward(x, lg, K, True)
+    ref = full.forward(x, lg, K, True)
+    res = ora.forward(route(wl.logits[0], K)[1].tolist())
+    torch.cuda.synchronize()
+    assert len(res["groups"]) > 100
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    assert st.slot_to_expert == ora.slot_to_expert and st.lru_tick == ora.lru_tick
+    tw, ids = route(wl.logits[0], K)
+    pick = [0, 1, 77, 200, 311, 450, 510, 511]
+    want = F.moe_forward_fp8(wl.x[0][pick], tw[pick].astype(np.float32), ids[pick],
+                             w13, w2, s13, s2)
+    assert _rel(out[pick].float().cpu(), want) < REL_TOL
+    for a in (0, 32):
+        out = st.forward(x[a:a + 32], lg[a:a + 32], K, True)
+        ref = full.forward(x[a:a + 32], lg[a:a + 32], K, True)
+        ora.forward(route(wl.logits[0][a:a + 32], K)[1].tolist())
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), a
+        assert st.slot_to_expert == ora.slot_to_expert and st.lru_tick == ora.lru_tick, a
+        assert (st.stats_miss, st.stats_evict, st.stats_hits) == \
+            (ora.stats_miss, ora.stats_evict, ora.stats_hits), a
+
+
 def test_fp8_state_prefill_paged_equals_full(small_fp8):
     """A 64-token prefill chunk (grouped path) through cap=16: token groups,
     each group's experts paged in; bytes equal the cap=E run and decisions
