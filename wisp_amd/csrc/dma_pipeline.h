@@ -14,7 +14,11 @@
 // row; their results are never stored.  Each wave waits for its own copies
 // by vmcnt (a constant per chunk), then one barrier per chunk: after it,
 // every wave's copies of the chunk have landed and every wave is done with
-// the stage the next copy overwrites.
+// the stage the next copy overwrites.  The weight copies are non-temporal
+// (each weight byte is read once per launch); the token copies are not.
+// Each loop step names its copy stage and its compute stage as distinct
+// (restrict), so the compiler does not hold a chunk's LDS reads behind the
+// copies just issued for a later one.
 #pragma once
 
 #include "common.h"
