@@ -390,6 +390,53 @@ def test_fp8_state_full_size_chunk_and_batches(full_fp8):
             (ora.stats_miss, ora.stats_evict, ora.stats_hits), a
 
 
+def _max_rel(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+@pytest.mark.parametrize("tokens", [600, 1024])
+def test_fp8_state_chunk_above_the_staged_id_limit(tokens):
+    """Block-FP8 prefill chunks of more than 4096 (token, k) pairs at the full
+    Qwen3-FP8 shape: the pager reads the routed ids from global memory and
+    mirrors its device record to the host record.  Cap 32 (~tokens/4 token
+    groups) and cap = E (one group): each state's decisions, slot table and
+    ticks equal its own oracle pager's, the two give the same bytes, and
+    sampled rows are within 1e-2 of oracle/fp8.py in both the L2 and the max
+    norm.  A bs=32 call follows on both states."""
+    wl = W.fp8_layer(W.gaussian_logits("batch", seed=21 + tokens, steps=1, tokens=tokens,
+                                       weights=False), pin=True)
+    E, K = 128, wl.shape.top_k
+    assert tokens * K > 4096
+    sts = {cap: _fp8_state(wl, cap) for cap in (32, E)}
+    oras = {cap: PagerOracle(E, cap) for cap in (32, E)}
+    w13, w2, s13, s2 = wl.views()
+    x, lg = wl.x[0], wl.logits[0]
+    for i, (xc, lgc) in enumerate([(x, lg), (x[:32], lg[:32])]):
+        print(f"fp8 chunk {tokens} call {i}: {xc.shape[0]} tokens", flush=True)
+        outs = {cap: st.forward(xc.to(DEV), lgc.to(DEV), K, True) for cap, st in sts.items()}
+        torch.cuda.synchronize()
+        assert torch.equal(outs[32].view(torch.int16), outs[E].view(torch.int16)), i
+        if i == 0:
+            first = outs[32].float().cpu()
+        ids = route(lgc, K)[1].tolist()
+        for cap, st in sts.items():
+            res = oras[cap].forward(ids)
+            ora = oras[cap]
+            if i == 0:
+                assert (len(res["groups"]) > tokens // 8) == (cap < E)
+            assert st.slot_to_expert == ora.slot_to_expert and st.lru_tick == ora.lru_tick
+            assert (st.stats_miss, st.stats_evict, st.stats_hits) == \
+                (ora.stats_miss, ora.stats_evict, ora.stats_hits), (i, cap)
+    tw, ids = route(lg, K)
+    pick = [0, 1, 63, 64, 255, 256, 511, 512, tokens // 2 + 3, tokens - 1]
+    want = F.moe_forward_fp8(x[pick], tw[pick].astype(np.float32), ids[pick], w13, w2, s13, s2)
+    got = first[pick]
+    assert _rel(got, want) < REL_TOL
+    for r in range(len(pick)):
+        assert _max_rel(got[r], want[r]) < REL_TOL, pick[r]
+
+
 def test_fp8_state_prefill_paged_equals_full(small_fp8):
     """A 64-token prefill chunk (grouped path) through cap=16: token groups,
     each group's experts paged in; bytes equal the cap=E run and decisions

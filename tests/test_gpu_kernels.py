@@ -102,6 +102,36 @@ def test_gpu_pager_matches_oracle(E, K, cap, tmax):
                                        ora.stats_evict, ora.stats_hits]
 
 
+@pytest.mark.parametrize("E,K,cap,T", [(128, 8, 32, 520), (128, 8, 128, 1100),
+                                        (128, 8, 64, 700), (512, 8, 64, 600),
+                                        (200, 8, 100, 520), (256, 16, 300, 300)])
+def test_gpu_pager_above_the_staged_id_limit(E, K, cap, T):
+    """Calls of more than 4096 (token, k) pairs: the pager reads the routed
+    ids from global memory and mirrors its device record to the host record
+    at its end.  Register path (E <= 128, cap <= 64) and LDS path; greedy
+    token groups (cap < E) and one group (cap = E).  Each call is followed by
+    a small staged call on the same state; every decision, slot, tick and
+    counter is checked against the oracle."""
+    assert T * K > 4096
+    rng = np.random.default_rng(E * 13 + cap + T)
+    ora, dp = PagerOracle(E, cap), DevPager(E, cap)
+    for step in range(6):
+        n = T if step % 2 == 0 else int(rng.integers(1, 9))
+        # skewed routing, so groups see hits as well as misses
+        p = rng.dirichlet(np.full(E, 0.5))
+        ids = [rng.choice(E, K, replace=False, p=p).tolist() for _ in range(n)]
+        res = ora.forward(ids)
+        rec = dp.call(ids, K)
+        assert rec["status"] == 0, (step, rec["status"])
+        oracle_trace_matches(res, rec)
+        assert rec["slots"] == res["slots"], step
+        assert dp.s2e.tolist() == ora.slot_to_expert, step
+        assert dp.tick.tolist() == ora.lru_tick, step
+        assert dp.map.tolist() == ora.expert_map(), step
+        assert dp.ctr[:5].tolist() == [ora.lru_clock, ora.stats_forward, ora.stats_miss,
+                                       ora.stats_evict, ora.stats_hits], step
+
+
 def test_gpu_pager_overflow():
     dp = DevPager(8, 2)
     rec = dp.call([[0, 1, 1], [2, 3, 4]], 3)

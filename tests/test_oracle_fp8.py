@@ -187,3 +187,20 @@ def test_moe_fp8_routing_weight_and_linearity_in_w2_scales():
     # bf16 adds commute with a power of two)
     assert np.array_equal(F.moe_forward_fp8(x, tw, ids, w13c, w2c, s13, s2 * 2), base * 2)
     assert np.array_equal(F.moe_forward_fp8(x, tw * 2, ids, w13c, w2c, s13, s2), base * 2)
+
+
+def test_torch_cpu_baseline_close_to_oracle():
+    """The torch CPU block-FP8 fused-MoE that bench.py times as the FP8
+    line's CPU baseline computes the same function: within 1e-2 (relative
+    L2) of the oracle on a Qwen3-FP8-shaped layer with 16 experts."""
+    from oracle.moe import route
+    from wisp_amd import workloads as W
+    base = W.qwen3_decode(seed=2, steps=3, weights=False)
+    base.logits = base.logits[:, :, :16].contiguous()
+    wl = W.fp8_layer(base, experts=16)
+    w13, w2, s13, s2 = wl.views()
+    for t in range(3):
+        tw, ids = route(wl.logits[t], 8)
+        want = F.moe_forward_fp8(wl.x[t], tw.astype(np.float32), ids, w13, w2, s13, s2)
+        got = F.moe_forward_fp8_fast(wl.x[t], tw, ids, w13, w2, s13, s2).float().numpy()
+        assert np.linalg.norm(got - want) / np.linalg.norm(want) < 1e-2, t
