@@ -346,6 +346,14 @@ int wisp_layer_pagein_engine(void* handle);
 int wisp_layer_profile(void* handle, int enable, double* w13_ms, double* w2_ms,
                        int64_t* calls, int64_t* w13_calls);
 
+/* The w2 time (ms, dispatch timestamps) of the calls whose fused page-in +
+ * w13 launch copied nothing, and their number, since the last
+ * wisp_layer_profile: the same calls whose w13 time wisp_layer_profile
+ * reports in w13_ms on that path, so the two stages are averaged over one
+ * set of calls.  Read it before wisp_layer_profile, which resets it.
+ * No counterpart in the reference: measurement only. */
+int wisp_layer_profile_noload(void* handle, double* w2_ms, int64_t* calls);
+
 /* ---- group 4: cross-layer speculative prefetch ------------------------ */
 
 /* Dense expert co-activation table and the current step's observations, all

@@ -243,3 +243,53 @@ def quantize_weights(w, bn: int = 128, bk: int = 128) -> tuple[np.ndarray, np.nd
             codes[i * bn:(i + 1) * bn, j * bk:(j + 1) * bk] = fp8_encode(
                 np.clip(blk / s, -E4M3_MAX, E4M3_MAX))
     return codes, scales
+
+
+def _dequant_blocks(codes: torch.Tensor, scales: torch.Tensor, bn: int, bk: int) -> torch.Tensor:
+    """Block-FP8 weights ``[N, Kd]`` (e4m3fn) with block scales -> float32."""
+    w = codes.view(torch.float8_e4m3fn).to(torch.float32) if codes.dtype != torch.float8_e4m3fn \
+        else codes.to(torch.float32)
+    s = scales.to(torch.float32).repeat_interleave(bn, 0)[:w.shape[0]]
+    return w * s.repeat_interleave(bk, 1)[:, :w.shape[1]]
+
+
+def _quant_dequant_rows(x: torch.Tensor, bk: int) -> torch.Tensor:
+    """Per-row, per-group e4m3fn quantisation of ``x [R, C]`` (float32) and
+    back: the values a w8a8 GEMM sees for its activations."""
+    R, Cc = x.shape
+    g = x.view(R, Cc // bk, bk)
+    s = g.abs().amax(dim=2, keepdim=True).clamp_min(QUANT_EPS) / E4M3_MAX
+    q = (g / s).clamp(-E4M3_MAX, E4M3_MAX).to(torch.float8_e4m3fn).to(torch.float32)
+    return (q * s).view(R, Cc)
+
+
+def moe_forward_fp8_fast(x, topk_w, topk_ids, w13, w2, s13, s2, block=(128, 128)) -> torch.Tensor:
+    """The torch CPU block-FP8 fused-MoE timed as the CPU baseline of the
+    block-FP8 decode line (a plain torch implementation, not the oracle):
+    per routed expert, the weight blocks dequantised to float32, the
+    activations quantised per 128-group and back (w8a8), float32
+    ``linear``, SiLU*mul with vLLM's two bf16 roundings, the same for w2,
+    and the routing-order combine in float32.  Needs H and I to be multiples of the
+    block."""
+    bn, bk = block
+    x = torch.as_tensor(x).to(torch.float32)
+    ids = np.asarray(topk_ids, dtype=np.int64)
+    tw = torch.as_tensor(np.asarray(topk_w, dtype=np.float32))
+    T, K = ids.shape
+    I = w2.shape[2]
+    y = torch.zeros((T, K, x.shape[1]), dtype=torch.float32)
+    for e in np.unique(ids):
+        e = int(e)
+        rows = np.argwhere(ids == e)
+        xt = _quant_dequant_rows(x[torch.as_tensor(rows[:, 0])], bk)
+        h = torch.nn.functional.linear(xt, _dequant_blocks(w13[e], s13[e], bn, bk))
+        h = h.to(torch.bfloat16).to(torch.float32)
+        silu = torch.nn.functional.silu(h[:, :I]).to(torch.bfloat16).float()
+        act = (silu * h[:, I:]).to(torch.bfloat16).float()
+        yy = torch.nn.functional.linear(_quant_dequant_rows(act, bk),
+                                        _dequant_blocks(w2[e], s2[e], bn, bk))
+        y[torch.as_tensor(rows[:, 0]), torch.as_tensor(rows[:, 1])] = yy
+    out = torch.zeros((T, x.shape[1]), dtype=torch.float32)
+    for k in range(K):
+        out += tw[:, k:k + 1] * y[:, k]
+    return out.to(torch.bfloat16)

@@ -457,12 +457,19 @@ class WispMoEState:
         time is in ``w13``: a decode call that pages experts in runs its w13
         inside the page-in launch, which is timed as page-in); then switch
         timing on or off.  The switch covers ``pagein_stats`` too; timing is
-        off by default, since its events lengthen the stream."""
+        off by default, since its events lengthen the stream.
+        ``w2_noload`` / ``w2_noload_calls``: the w2 time of the calls whose
+        fused page-in + w13 launch copied nothing (the calls behind ``w13``
+        on that path), so both stages can be averaged over one set of calls."""
         a, b, n, n13 = C.c_double(), C.c_double(), C.c_int64(), C.c_int64()
+        b_nl, n_nl = C.c_double(), C.c_int64()
+        check(lib().wisp_layer_profile_noload(self._handle, C.byref(b_nl), C.byref(n_nl)),
+              "profile")
         check(lib().wisp_layer_profile(self._handle, int(enable), C.byref(a), C.byref(b),
                                        C.byref(n), C.byref(n13)), "profile")
         return {"w13": float(a.value), "w2": float(b.value), "calls": int(n.value),
-                "w13_calls": int(n13.value)}
+                "w13_calls": int(n13.value), "w2_noload": float(b_nl.value),
+                "w2_noload_calls": int(n_nl.value)}
 
     def resize_cap(self, new_cap: int) -> None:
         """Resize the scratch to ``new_cap`` slots at a drained barrier

@@ -108,6 +108,7 @@ SIGNATURES = {
     "wisp_layer_sync_record": (_i32, [_vp, C.POINTER(Workspace)]),
     "wisp_layer_profile": (_i32, [_vp, _i32, C.POINTER(C.c_double), C.POINTER(C.c_double),
                                   C.POINTER(C.c_int64), C.POINTER(C.c_int64)]),
+    "wisp_layer_profile_noload": (_i32, [_vp, C.POINTER(C.c_double), C.POINTER(C.c_int64)]),
     "wisp_cooccur_observe_layer": (_i32, [C.POINTER(Cooccur), _i32, _vp, _i32, _i32, _vp]),
     "wisp_cooccur_predict": (_i32, [C.POINTER(Cooccur), _i32, _i32, _vp, _i32, _i32, _vp, _vp,
                                     _vp]),

@@ -163,6 +163,7 @@ struct ProfLaunch {
   int kind = 0;          // 0: w13 kernel, 1: w2 kernel
   bool pending = false;
   bool counted = true;   // false for a speculative launch that found nothing to do
+  uint64_t gen = 0;      // the layer's launch number that last took this slot
 };
 
 // One copy-kernel launch: dispatch timestamps and the pinned word its first
@@ -172,6 +173,10 @@ struct PinLaunch {
   hipEvent_t start = nullptr, stop = nullptr;
   bool pending = false;
   bool fused = false;
+  // the w2 launch of the same call (fused launches), so that a call that
+  // copied nothing adds its w2 time to the no-load pair statistics
+  ProfLaunch* w2 = nullptr;
+  uint64_t w2_gen = 0;
 };
 
 struct Layer {
@@ -215,6 +220,11 @@ struct Layer {
   double prof_ms[2] = {0, 0};
   int64_t prof_calls = 0;
   int64_t prof_w13_calls = 0;  // calls whose w13 time is in prof_ms[0]
+  uint64_t prof_gen = 0;
+  // w2 time of the fused calls that copied nothing: the calls whose w13 time
+  // a fused launch adds to prof_ms[0]
+  double prof_w2_nl_ms = 0;
+  int64_t prof_w2_nl_calls = 0;
 };
 
 void prof_harvest(Layer& L, ProfLaunch& p) {
@@ -254,6 +264,7 @@ ProfLaunch* prof_begin(Layer& L, int kind) {
   }
   p.kind = kind;
   p.counted = true;
+  p.gen = ++L.prof_gen;
   return &p;
 }
 
@@ -348,9 +359,18 @@ void harvest_pin(Layer& L, int i) {
     } else if (p.fused) {
       L.prof_ms[0] += ms;
       L.prof_w13_calls += 1;
+      // the call's w2 launch, unless its timing slot was taken since
+      float m2 = 0.f;
+      if (p.w2 && p.w2->gen == p.w2_gen && p.w2->counted &&
+          hipEventSynchronize(p.w2->stop) == hipSuccess &&
+          hipEventElapsedTime(&m2, p.w2->start, p.w2->stop) == hipSuccess) {
+        L.prof_w2_nl_ms += m2;
+        L.prof_w2_nl_calls += 1;
+      }
     }
   }
   p.pending = false;
+  p.w2 = nullptr;
 }
 
 // Orders `st` after the layer's outstanding prefetch copies (before anything
@@ -382,6 +402,7 @@ int page_in_kernel(Layer& L, const int32_t* loads, const int32_t* count, int n, 
   harvest_pin(L, i);
   PinLaunch& p = L.pin[i];
   p.fused = fw != nullptr;
+  p.w2 = nullptr;
   PageInArgs a;
   a.loads = loads;
   a.count = count;
@@ -895,9 +916,16 @@ extern "C" int wisp_layer_forward(void* handle, const void* x, const void* logit
   if (T == 1 && one_group && L->kpin && a == WISP_ALGO_GEMV && L->fused_ok) {
     // [route+pager] [page-in + w13] [w2]
     const FusedW13 fw{x, T, K, ws->flags, ws->act, ws->slots};
+    const int pin_slot = L->pin_next;
     rc = page_in_kernel(*L, ws->loads, ws->flags, 0, st, &fw);
     if (rc != WISP_OK) return rc;
-    return w2(*L, ws->act, T, K, ws->topk_w, ws->slots, out, st, nullptr, nullptr);
+    ProfLaunch* p2 = nullptr;
+    rc = w2(*L, ws->act, T, K, ws->topk_w, ws->slots, out, st, nullptr, &p2);
+    if (rc == WISP_OK && p2) {
+      L->pin[pin_slot].w2 = p2;
+      L->pin[pin_slot].w2_gen = p2->gen;
+    }
+    return rc;
   }
   if (one_group && L->kpin) {
     rc = page_in_kernel(*L, ws->loads, ws->flags, 0, st);
@@ -1093,7 +1121,18 @@ extern "C" int wisp_layer_profile(void* handle, int enable, double* w13_ms, doub
   L->prof_ms[0] = L->prof_ms[1] = 0;
   L->prof_calls = 0;
   L->prof_w13_calls = 0;
+  L->prof_w2_nl_ms = 0;
+  L->prof_w2_nl_calls = 0;
   L->profile = enable != 0;
+  return WISP_OK;
+}
+
+extern "C" int wisp_layer_profile_noload(void* handle, double* w2_ms, int64_t* calls) {
+  Layer* L = (Layer*)handle;
+  if (!L) return WISP_ERR_INVALID;
+  for (int i = 0; i < wisp::kPinRing; ++i) wisp::harvest_pin(*L, i);
+  if (w2_ms) *w2_ms = L->prof_w2_nl_ms;
+  if (calls) *calls = L->prof_w2_nl_calls;
   return WISP_OK;
 }
 
