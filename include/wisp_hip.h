@@ -333,6 +333,18 @@ int wisp_layer_last_pagein(void* handle, float* ms, double* bytes);
 /* The page-in engine the layer uses (WISP_PAGEIN_*), or -1 for a bad handle. */
 int wisp_layer_pagein_engine(void* handle);
 
+/* Run the first half of a one-token paged call whose top-k equals cap
+ * (routing fused, copy-kernel engine, at most 128 experts, bf16 or fp32
+ * rows of 2 or 4 16-byte chunks per lane) as one launch: the pager in one
+ * wave, the page-in copies once it has decided, and w13 per slot from the
+ * slots' contents, which need no decision (enable != 0); or as the pager
+ * launch then the page-in + w13 launch (0, the default).  The outputs and
+ * decisions are the same; the fused launch shortens a call that loads
+ * nothing by ~2 us, but its pager runs behind the w13 stream's loads.
+ * No counterpart in the reference (the reference's forward is one vLLM
+ * call): a launch-structure choice of this implementation. */
+int wisp_layer_set_decode_fused(void* handle, int enable);
+
 /* Read and reset the accumulated execution time (dispatch timestamps) of the
  * w13+SiLU kernels and of the w2+combine kernels of all layer calls since the
  * last read, the number of layer calls, and the number of calls whose w13

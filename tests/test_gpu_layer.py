@@ -105,11 +105,31 @@ def test_toy_fp32_layer_all_steps():
     drive(wl, 4, wl.steps, tol=1e-5)
 
 
-def test_toy_fp32_layer_cap_equals_top_k():
+@pytest.mark.parametrize("fused", ["0", "1"])
+def test_toy_fp32_layer_cap_equals_top_k(monkeypatch, fused):
     # cap == top_k: every one-token call fills every slot, so the decode
-    # kernels lay their waves out by slot (a miss on most calls here)
+    # kernels lay their waves out by slot (a miss on most calls here); with
+    # WISP_DECODE_FUSED=1 the pager, page-in and w13 run as one launch
+    monkeypatch.setenv("WISP_DECODE_FUSED", fused)
     wl = W.toy(pin=True)
     drive(wl, wl.shape.top_k, wl.steps, tol=1e-5)
+
+
+@pytest.mark.parametrize("fused", ["0", "1"])
+def test_qwen3_decode_fused_launch_equals_two_launches(monkeypatch, fused):
+    """The Qwen3 decode sequence at cap 8 == top-k: with WISP_DECODE_FUSED=1
+    the pager wave, the page-in copies (started by the pager's epoch word)
+    and w13 per slot share one launch; the decisions, slot tables and ticks
+    equal the fixture's, outputs equal the resident layer's bytes and the
+    oracle's within 1e-2, and the timing counts the same calls and bytes."""
+    monkeypatch.setenv("WISP_DECODE_FUSED", fused)
+    wl = W.qwen3_decode(pin=True)  # the fixture's 256-step draw; 64 steps run
+    sts = drive(wl, 8, 64, tol=1e-2, timed=True, fixture=load_golden("qwen3.json.gz"))
+    st = sts["paged"]
+    ms, nbytes = st.pagein_stats()
+    assert ms > 0 and nbytes == st.stats_miss * wl.shape.expert_bytes
+    prof = st.profile(False)
+    assert prof["calls"] == 64 and prof["w2_noload_calls"] == prof["w13_calls"] > 0
 
 
 @pytest.mark.parametrize("engine,streams", [("kernel", "0"), ("memcpy", "0"), ("memcpy", "1"),
@@ -148,13 +168,15 @@ def test_batched_subbatching_matches_resident_bytes(monkeypatch, engine, streams
     assert sts["paged"].pagein_engine == engine
 
 
-@pytest.mark.parametrize("engine", ["kernel", "memcpy"])
+@pytest.mark.parametrize("engine", ["kernel", "memcpy", "fused"])
 def test_queued_decode_over_layers_matches_resident(monkeypatch, engine):
     # Four layers share the masters and are called round-robin with no host
     # synchronisation between calls, as a decode loop runs: every call's
     # output must still equal the resident layer's bytes, and each layer's
     # final pager state must equal its own oracle's.
-    monkeypatch.setenv("WISP_PAGEIN_ENGINE", engine)
+    # (fused: the copy-kernel engine with WISP_DECODE_FUSED=1)
+    monkeypatch.setenv("WISP_PAGEIN_ENGINE", "kernel" if engine == "fused" else engine)
+    monkeypatch.setenv("WISP_DECODE_FUSED", "1" if engine == "fused" else "0")
     wl = W.qwen3_decode(steps=40, pin=True)
     w13, w2 = wl.views()
     K, nl = wl.shape.top_k, 4
@@ -175,7 +197,7 @@ def test_queued_decode_over_layers_matches_resident(monkeypatch, engine):
         assert torch.equal(bits(outs[t]), bits(refs[t])), t
         oras[t % nl].forward(route(wl.logits[t], K)[1].tolist())
     for st, ora in zip(paged, oras):
-        assert st.pagein_engine == engine
+        assert st.pagein_engine == ("kernel" if engine == "fused" else engine)
         assert st.slot_to_expert == ora.slot_to_expert and st.lru_tick == ora.lru_tick
         assert (st.stats_forward, st.stats_miss, st.stats_evict, st.stats_hits) == \
             (ora.stats_forward, ora.stats_miss, ora.stats_evict, ora.stats_hits)

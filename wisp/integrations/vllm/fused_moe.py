@@ -119,6 +119,15 @@ def _resolve_pagein_engine() -> int:
     return _lib.WISP_PAGEIN_KERNEL if raw == "kernel" else _lib.WISP_PAGEIN_MEMCPY
 
 
+def _resolve_decode_fused() -> bool:
+    """``WISP_DECODE_FUSED=1``: a one-token call whose top-k equals cap runs
+    the pager, the page-in and w13 (per slot) as one launch instead of a
+    pager launch and a page-in + w13 launch (``wisp_layer_set_decode_fused``).
+    Off by default: the fused launch is ~2 us shorter per call that loads
+    nothing, but its pager runs behind the w13 stream's loads."""
+    return os.environ.get("WISP_DECODE_FUSED", "0").strip().lower() in ("1", "true", "yes", "on")
+
+
 _DTYPES = {torch.float32: _lib.WISP_F32, torch.bfloat16: _lib.WISP_BF16}
 
 
@@ -252,6 +261,8 @@ class WispMoEState:
         self._desc = self._make_desc()
         check(lib().wisp_layer_create(C.byref(self._desc), C.byref(self._handle)),
               "wisp_layer_create")
+        check(lib().wisp_layer_set_decode_fused(self._handle, int(_resolve_decode_fused())),
+              "wisp_layer_set_decode_fused")
 
     # -- construction helpers ---------------------------------------------
     def _alloc_scratch(self, cap: int) -> None:

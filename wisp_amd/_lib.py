@@ -105,6 +105,7 @@ SIGNATURES = {
     "wisp_layer_prime_identity": (_i32, [_vp, _vp]),
     "wisp_layer_last_pagein": (_i32, [_vp, _f32p, C.POINTER(C.c_double)]),
     "wisp_layer_pagein_engine": (_i32, [_vp]),
+    "wisp_layer_set_decode_fused": (_i32, [_vp, _i32]),
     "wisp_layer_sync_record": (_i32, [_vp, C.POINTER(Workspace)]),
     "wisp_layer_profile": (_i32, [_vp, _i32, C.POINTER(C.c_double), C.POINTER(C.c_double),
                                   C.POINTER(C.c_int64), C.POINTER(C.c_int64)]),

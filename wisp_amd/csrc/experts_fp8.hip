@@ -436,16 +436,23 @@ __device__ inline int32_t load_first(const int32_t* p) {
 // w13 + silu_and_mul for a one-token call.  A token's routed experts are
 // distinct, so every block computes its own pair (no search for other pairs
 // of its slot), and the token's activation loads go out first, with no wait
-// before them.  SLOTS (the call fills every slot: top-k == cap and the slots
-// come from the pager): blockIdx.y is a slot, whose weight and scale loads go
-// out before the slot table is read; the table then names the pair to store
-// (slot 0's blocks store zeros for pairs that name no slot of the scratch).
-// Per output the steps are fp8_w13_kernel's with one MFMA column, so act is
-// the same bit for bit.  Each of the NW waves takes KC k-blocks of H per
-// chunk.  Dynamic LDS: red [NW][2][64][4] f32, then per wave xs [KC] f32 and
-// xq [KC][kKB] codes.
+// before them.  A block owns 8 outputs i0 .. i0 + 7 (blockIdx.x = i0 / 8) and
+// puts their gate and up rows into one MFMA operand: operand rows 0-7 are
+// gate rows i0 .. i0 + 7, rows 8-15 the up rows I + i0 .. I + i0 + 7.  Each
+// output's steps are fp8_w13_kernel's (one MFMA column, the same k-block
+// ranges per wave, the waves' partial sums in wave order), with half the
+// weight registers of a 16-output block that holds gate and up in two
+// operands; so a Qwen3-shaped call (I 768, top-8) runs 768 blocks, three per
+// CU, where 16-output blocks ran 384, two or one per CU.  SLOTS (the call
+// fills every slot: top-k == cap and the slots come from the pager):
+// blockIdx.y is a slot, whose weight and scale loads go out before the slot
+// table is read; the table then names the pair to store (slot 0's blocks
+// store zeros for pairs that name no slot of the scratch).  Each of the NW
+// waves takes KC k-blocks of H per chunk.  Dynamic LDS: red [NW][2][64][4]
+// f32 (this block uses its first half), then per wave xs [KC] f32 and xq
+// [KC][kKB] codes.
 // ---------------------------------------------------------------------------
-// The block of 16-row tile `tile` and pair (or, with SLOTS, slot) `by`.
+// The block of 8-output tile `tile` and pair (or, with SLOTS, slot) `by`.
 // With `words` (the pager's per-pair words; a fused page-in launch), a pair
 // whose expert this call loaded is left to the copy blocks, which compute it
 // from the bytes they copy.
@@ -460,7 +467,7 @@ __device__ inline void w13_one_block(const uint16_t* __restrict__ x, int H, int 
   float* red = reinterpret_cast<float*>(smem);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int col = lane & 15, grp = lane >> 4;
-  const int i0 = tile * 16;
+  const int i0 = tile * 8;
   const int nkb = H / kKB;
   const int per = (nkb + NW - 1) / NW;
   const int kb0 = min(nkb, wave * per), kb1 = min(nkb, kb0 + per);
@@ -485,25 +492,24 @@ __device__ inline void w13_one_block(const uint16_t* __restrict__ x, int H, int 
     if (absent) s = 0;  // loads from slot 0, dropped (no branch around them)
   }
   const uint8_t* W = w13 + (size_t)s * w13_stride;
-  const float* Sg = s13 + (size_t)s * s13_stride + (size_t)(i0 / block_n) * nkb;
-  const float* Su = s13 + (size_t)s * s13_stride + (size_t)((I + i0) / block_n) * nkb;
-  const uint8_t* rowg = W + (size_t)(i0 + col) * H + grp * 32;
-  const uint8_t* rowu = W + (size_t)(I + i0 + col) * H + grp * 32;
+  // operand row `col`: gate row i0 + col, or up row I + i0 + col - 8; result
+  // rows 4 * grp .. 4 * grp + 3 are gate rows for grp < 2, up rows above
+  const uint8_t* row = W + (size_t)(col < 8 ? i0 + col : I + i0 + col - 8) * H + grp * 32;
+  const float* Sw = s13 + (size_t)s * s13_stride +
+                    (size_t)((grp < 2 ? i0 : I + i0) / block_n) * nkb;
 
-  f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   for (int kc = kb0; kc < kb1; kc += KC) {
     const int nk = min(KC, kb1 - kc);
     if (kc != kb0)
       xv = *reinterpret_cast<const u32x4*>(x + (size_t)(kc + min(grp, nk - 1)) * kKB + col * 8);
-    i32x8 wg[KC], wu[KC];
-    float sg[KC], su[KC];
+    i32x8 w[KC];
+    float sw[KC];
 #pragma unroll
     for (int kbi = 0; kbi < KC; ++kbi) {
       const int kb = kc + min(kbi, nk - 1);
-      wg[kbi] = ld32(rowg + (size_t)kb * kKB);
-      wu[kbi] = ld32(rowu + (size_t)kb * kKB);
-      sg[kbi] = Sg[kb];
-      su[kbi] = Su[kb];
+      w[kbi] = ld32(row + (size_t)kb * kKB);
+      sw[kbi] = Sw[kb];
     }
     {
       float v[8];
@@ -527,30 +533,19 @@ __device__ inline void w13_one_block(const uint16_t* __restrict__ x, int H, int 
       b[kbi] = lds32(xq + (size_t)min(kbi, nk - 1) * kKB + grp * 32);
       sa[kbi] = xs[min(kbi, nk - 1)];
     }
-    f32x4 dg[KC], du[KC];
+    f32x4 d[KC];
 #pragma unroll
-    for (int kbi = 0; kbi < KC; ++kbi) {
-      dg[kbi] = mfma_fp8(wg[kbi], b[kbi]);
-      du[kbi] = mfma_fp8(wu[kbi], b[kbi]);
-    }
+    for (int kbi = 0; kbi < KC; ++kbi) d[kbi] = mfma_fp8(w[kbi], b[kbi]);
 #pragma unroll
     for (int kbi = 0; kbi < KC; ++kbi) {
       if (kbi < nk) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          ag[j] = ag[j] + (dg[kbi][j] * sa[kbi]) * sg[kbi];
-          au[j] = au[j] + (du[kbi][j] * sa[kbi]) * su[kbi];
-        }
+        for (int j = 0; j < 4; ++j) acc[j] = acc[j] + (d[kbi][j] * sa[kbi]) * sw[kbi];
       }
     }
     wave_lds_sync();  // the slice is rewritten by the next chunk
   }
-  float* rw = red + ((size_t)wave * 2 * 64 + lane) * 4;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    rw[j] = ag[j];
-    rw[64 * 4 + j] = au[j];
-  }
+  *reinterpret_cast<f32x4*>(red + ((size_t)wave * 64 + lane) * 4) = acc;
   int p = by;
   uint64_t none = 0;  // SLOTS: pairs whose slot lies outside the scratch
   if (SLOTS) {
@@ -562,14 +557,32 @@ __device__ inline void w13_one_block(const uint16_t* __restrict__ x, int H, int 
   const int zp = absent ? p : -1;  // stored as zeros below
   if (absent) p = -1;
   block_lds_sync();
-  if (wave == 0 && col == 0 && p >= 0) {
-    f32x4 g, u;
-    sum_partials<NW>(red, lane, g, u);
+  if (wave == 0 && col == 0 && grp < 2 && p >= 0) {
+    // this lane's four gate outputs and, 32 lanes on, their up outputs,
+    // each summed over the waves in wave order from zero
+    f32x4 g = {0.f, 0.f, 0.f, 0.f}, u = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+    for (int w0 = 0; w0 < NW; w0 += 4) {
+      f32x4 pg[4], pu[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int w = min(w0 + i, NW - 1);
+        pg[i] = *reinterpret_cast<const f32x4*>(red + ((size_t)w * 64 + lane) * 4);
+        pu[i] = *reinterpret_cast<const f32x4*>(red + ((size_t)w * 64 + lane + 32) * 4);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (w0 + i < NW) {
+          g = g + pg[i];
+          u = u + pu[i];
+        }
+      }
+    }
     store_act4(act + (size_t)p * I + i0 + grp * 4, g, u);
   }
   for (; none; none &= none - 1)
-    if (threadIdx.x < 16) act[(size_t)__builtin_ctzll(none) * I + i0 + threadIdx.x] = 0;
-  if (zp >= 0 && threadIdx.x < 16) act[(size_t)zp * I + i0 + threadIdx.x] = 0;
+    if (threadIdx.x < 8) act[(size_t)__builtin_ctzll(none) * I + i0 + threadIdx.x] = 0;
+  if (zp >= 0 && threadIdx.x < 8) act[(size_t)zp * I + i0 + threadIdx.x] = 0;
 }
 
 template <int NW, int KC, bool SLOTS>
@@ -617,15 +630,23 @@ struct Fp8FusedArgs {
   int H, I, K, nslots, block_n;
 };
 
+// Byte offset of the copy blocks' per-wave staging in the fused launch's
+// LDS: after red [NW][2][64][4] f32 and the token's codes and scales.
+constexpr size_t fp8_copy_stage_off(int nw, int nkb) {
+  return ((size_t)nw * 2 * 64 * 4 * sizeof(float) + (size_t)nkb * (4 + kKB) + 15) / 16 * 16;
+}
+
 // Copy blocks of the fused launch, for NW * PER == H / kKB (every wave PER
 // k-blocks).  A tile's 32 rows (16 gate, 16 up) are read over the host link
 // as whole PER * 128-byte row segments, 16 bytes a lane (requests of 1 KiB
 // per instruction, where the MFMA layout, 16 rows x 32 bytes per
 // instruction, would cut them into 64-byte pieces and cost ~15 % of the
-// link); each wave stores its segments to the slot and, one k-block and one
-// of gate and up at a time, puts them in its own 2 KiB of LDS (its slot of
-// red, free until the tile's partial sums), whence it reads its MFMA
-// operands.
+// link); each wave stores its segments to the slot and, gate rows then up
+// rows, puts the PER k-blocks of 16 rows in its own PER * 2 KiB of LDS,
+// whence it reads its MFMA operands.  Staging a half's k-blocks at once lets
+// its load registers go before the MFMAs: one k-block at a time kept all
+// of them live through the tile (98 VGPRs, two blocks per CU for the whole
+// launch; 60 now, with the w13 blocks' 8-output tiles).
 template <int NW, int PER>
 __device__ inline void fp8_copy_w13_blocks(const Fp8FusedArgs& f, const PageInArgs& a,
                                            unsigned char* smem, int cb) {
@@ -645,7 +666,8 @@ __device__ inline void fp8_copy_w13_blocks(const Fp8FusedArgs& f, const PageInAr
   float* red = reinterpret_cast<float*>(smem);
   uint8_t* xq = reinterpret_cast<uint8_t*>(red + NW * 2 * 64 * 4);
   float* xs = reinterpret_cast<float*>(xq + (size_t)nkb * kKB);
-  uint8_t* ws = reinterpret_cast<uint8_t*>(red + (size_t)wave * 2 * 64 * 4);  // 16 rows x kKB
+  // this wave's staging: PER k-blocks of 16 rows x kKB
+  uint8_t* ws = smem + fp8_copy_stage_off(NW, nkb) + (size_t)wave * PER * 16 * kKB;
   // lane p < K holds the expert pair p's word says was loaded (or -1)
   const int mine = lane < f.K ? pair_word_loaded(f.words[lane]) : -1;
   // the token's k-blocks, one per 16-lane row
@@ -681,53 +703,54 @@ __device__ inline void fp8_copy_w13_blocks(const Fp8FusedArgs& f, const PageInAr
       sg[k] = S[(size_t)(i0 / f.block_n) * nkb + kb0 + k];
       su[k] = S[(size_t)((I + i0) / f.block_n) * nkb + kb0 + k];
     }
-    u32x4 v[NI];
-    size_t off[NI];
-#pragma unroll
-    for (int ii = 0; ii < NI; ++ii) {
+    // byte offset of load ii's 16 bytes in the slab (recomputed for the
+    // store rather than held: the registers bound the launch's occupancy)
+    auto off = [&](int ii) {
       const int rr = ii * RPI + seg_row;  // tile row: 0-15 gate, 16-31 up
-      off[ii] = (size_t)(rr < 16 ? i0 + rr : I + i0 + rr - 16) * H + (size_t)kb0 * kKB +
-                seg_cb * 16;
-      v[ii] = *reinterpret_cast<const u32x4*>(src + off[ii]);
-    }
+      return (uint32_t)((rr < 16 ? i0 + rr : I + i0 + rr - 16) * H + kb0 * kKB + seg_cb * 16);
+    };
+    u32x4 v[NI];
+#pragma unroll
+    for (int ii = 0; ii < NI; ++ii) v[ii] = *reinterpret_cast<const u32x4*>(src + off(ii));
 #pragma unroll
     for (int ii = 0; ii < NI; ++ii)
-      __builtin_nontemporal_store(v[ii], reinterpret_cast<u32x4*>(dst + off[ii]));
+      __builtin_nontemporal_store(v[ii], reinterpret_cast<u32x4*>(dst + off(ii)));
     f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
-    // LDS row r (0-15) of a staged k-block: its 8 16-byte blocks at
+    // LDS row r (0-15) of staged k-block k: its 8 16-byte blocks at
     // (block ^ (r & 7))
-    auto at = [&](int r, int cb) { return ws + r * kKB + ((cb ^ (r & 7)) << 4); };
-    // rows [16 h, 16 h + 16) of the tile (h 0: gate, 1: up), blocks
-    // 8k .. 8k + 7 of their segments; the wave's own LDS, so its reads of
-    // the previous staging come first in order
-    auto stage = [&](int h, int k) {
+    auto at = [&](int k, int r, int cb) {
+      return ws + (k * 16 + r) * kKB + ((cb ^ (r & 7)) << 4);
+    };
+    const int cb = grp * 2;  // the lane's 32 bytes of a k-block
+    // rows [16 h, 16 h + 16) of the tile (h 0: gate, 1: up), every k-block
+    // of their segments at once, then that half's MFMAs in k-block order;
+    // the wave's own LDS, so its reads of the gate half come first in order
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
 #pragma unroll
       for (int ii = 0; ii < NI; ++ii) {
         const int rr = ii * RPI + seg_row;
-        if ((rr >> 4) == h && (seg_cb >> 3) == k)
-          *reinterpret_cast<u32x4*>(at(rr & 15, seg_cb & 7)) = v[ii];
+        if ((rr >> 4) == h)
+          *reinterpret_cast<u32x4*>(at(seg_cb >> 3, rr & 15, seg_cb & 7)) = v[ii];
       }
       wave_lds_sync();
-    };
-    const int cb = grp * 2;  // the lane's 32 bytes of a k-block
 #pragma unroll
-    for (int k = 0; k < PER; ++k) {
-      stage(0, k);
-      const i32x8 wg = join(*reinterpret_cast<const u32x4*>(at(col, cb)),
-                            *reinterpret_cast<const u32x4*>(at(col, cb + 1)));
-      stage(1, k);
-      const i32x8 wu = join(*reinterpret_cast<const u32x4*>(at(col, cb)),
-                            *reinterpret_cast<const u32x4*>(at(col, cb + 1)));
-      const int kb = kb0 + k;
-      const i32x8 b = lds32(xq + (size_t)kb * kKB + grp * 32);
-      const float sa = xs[kb];
-      const f32x4 dg = mfma_fp8(wg, b);
-      const f32x4 du = mfma_fp8(wu, b);
+      for (int k = 0; k < PER; ++k) {
+        const i32x8 w = join(*reinterpret_cast<const u32x4*>(at(k, col, cb)),
+                             *reinterpret_cast<const u32x4*>(at(k, col, cb + 1)));
+        const int kb = kb0 + k;
+        const i32x8 b = lds32(xq + (size_t)kb * kKB + grp * 32);
+        const float sa = xs[kb];
+        const f32x4 d = mfma_fp8(w, b);
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        ag[jj] = ag[jj] + (dg[jj] * sa) * sg[k];
-        au[jj] = au[jj] + (du[jj] * sa) * su[k];
+        for (int jj = 0; jj < 4; ++jj) {
+          if (h == 0)
+            ag[jj] = ag[jj] + (d[jj] * sa) * sg[k];
+          else
+            au[jj] = au[jj] + (d[jj] * sa) * su[k];
+        }
       }
+      wave_lds_sync();  // the up half overwrites the staging
     }
     float* rw = red + ((size_t)wave * 2 * 64 + lane) * 4;
 #pragma unroll
@@ -760,12 +783,15 @@ __device__ inline void fp8_copy_w13_blocks(const Fp8FusedArgs& f, const PageInAr
 }
 
 // w13 blocks of KC k-blocks per wave chunk; copy blocks of PER k-blocks per
-// wave (NW * PER == H / kKB).
+// wave (NW * PER == H / kKB).  Six waves per SIMD (at most 80 VGPRs, which
+// the copy blocks reach without spilling): three 8-wave blocks per CU, so
+// the Qwen3-shaped launch's 768 w13 blocks run in one round.
 template <int NW, int KC, int PER, bool SLOTS>
-__global__ __launch_bounds__(NW * 64) void pagein_fp8_w13_kernel(Fp8FusedArgs f, PageInArgs a) {
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(6)))
+void pagein_fp8_w13_kernel(Fp8FusedArgs f, PageInArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   if (blockIdx.x >= kFp8CopyBlocks) {
-    const int ntile = f.I / 16;
+    const int ntile = f.I / 8;  // 8-output tiles
     const int local = blockIdx.x - kFp8CopyBlocks;
     const int by = local / ntile;
     w13_one_block<NW, KC, SLOTS>(f.x, f.H, f.I, f.K, f.slots, f.nslots, f.w13, f.w13_stride,
@@ -949,7 +975,10 @@ __global__ __launch_bounds__(NW * 64) void fp8_w2_kernel(
 // wave w quantises pair w's act into LDS and streams one expert's tile: pair
 // w's slot, or slot w with SLOTS (the call fills every slot: top-k == cap,
 // slots from the pager), whose loads then go out before the slot table
-// arrives.  Everything a wave needs after the LDS barrier is read at once
+// arrives.  (At the Qwen3 shape that is 128 blocks, half the CUs: 8-row
+// blocks, 256 of them, measured no faster, 6.0 against 5.6-6.0 us; the
+// kernel is bound by its chain of dependent steps, not by the CUs that
+// stream.)  Everything a wave needs after the LDS barrier is read at once
 // and its KB MFMAs are independent; only the scaled sums run in k-block
 // order.  Per output the steps are fp8_w2_kernel's with one job per pair, so
 // the bytes are the same.  Dynamic LDS: aq [K][I] codes, as [K][KB] f32,
@@ -1581,7 +1610,7 @@ hipError_t launch_w13(const W13Args& a, hipStream_t st, hipEvent_t e0, hipEvent_
   return hipGetLastError();
 }
 
-// The one-token w13 kernel: one block per (16-row tile, pair), or per
+// The one-token w13 kernel: one block per (8-output tile, pair), or per
 // (tile, slot) with SLOTS.
 template <int NW, int KC, bool SLOTS>
 hipError_t launch_w13_one(const W13Args& a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
@@ -1590,7 +1619,7 @@ hipError_t launch_w13_one(const W13Args& a, hipStream_t st, hipEvent_t e0, hipEv
   const size_t lds = (size_t)NW * 2 * 64 * 4 * sizeof(float) + (size_t)NW * KC * (4 + kKB);
   hipError_t e = allow_lds(kern, lds, kMaxLds, &big_lds);
   if (e != hipSuccess) return e;
-  const dim3 grid(a.I / 16, SLOTS ? a.nslots : a.P), block(NW * 64);
+  const dim3 grid(a.I / 8, SLOTS ? a.nslots : a.P), block(NW * 64);
   if (e0)
     hipExtLaunchKernelGGL(kern, grid, block, lds, st, e0, e1, 0, a.x, a.H, a.I, a.K, a.slots,
                           a.nslots, a.w13, a.w13_stride, a.s13, a.s13_stride, a.block_n, a.act);
@@ -1896,10 +1925,11 @@ hipError_t launch_pagein_fp8_w13(const Fp8FusedArgs& f, const PageInArgs& a, hip
   const auto kern = &pagein_fp8_w13_kernel<NW, KC, PER, SLOTS>;
   const int nkb = f.H / kKB;
   const size_t red = (size_t)NW * 2 * 64 * 4 * sizeof(float);
-  const size_t lds = red + std::max((size_t)NW * KC * (4 + kKB), (size_t)nkb * (4 + kKB));
+  const size_t lds = std::max(red + (size_t)NW * KC * (4 + kKB),
+                              fp8_copy_stage_off(NW, nkb) + (size_t)NW * PER * 16 * kKB);
   hipError_t e = allow_lds(kern, lds, kMaxLds, &big_lds);
   if (e != hipSuccess) return e;
-  const dim3 grid(kFp8CopyBlocks + f.I / 16 * (SLOTS ? f.nslots : f.K)), block(NW * 64);
+  const dim3 grid(kFp8CopyBlocks + f.I / 8 * (SLOTS ? f.nslots : f.K)), block(NW * 64);
   if (e0)
     hipExtLaunchKernelGGL(kern, grid, block, lds, st, e0, e1, 0, f, a);
   else

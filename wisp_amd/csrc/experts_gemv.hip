@@ -14,6 +14,7 @@
 #include "common.h"
 #include "pagein.h"
 #include "pager_core.h"
+#include "pager_wave.h"
 
 namespace wisp {
 namespace {
@@ -215,26 +216,14 @@ struct FusedW13Args {
   int H, I, K, cap;
 };
 
+// Copy block `cb` (of kPageInBlocks) of a fused page-in + w13 launch.
 template <typename T, int CH, bool FULL>
-__global__ __launch_bounds__(256) void pagein_w13_kernel(FusedW13Args f, PageInArgs a) {
+__device__ inline void pagein_w13_copy_block(const FusedW13Args& f, const PageInArgs& a, int cb) {
   constexpr int V = Vec<T>::N;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int H = f.H, I = f.I, nch = H / V;
-  if (blockIdx.x >= kPageInBlocks) {
-    const int nbx = (I + 3) / 4;
-    const int local = blockIdx.x - kPageInBlocks;
-    const int pair = local / nbx;
-    const int i = (local - pair * nbx) * 4 + wave;
-    if (i >= I) return;
-    const int32_t word = f.words[pair];
-    if (pair_word_loaded(word) >= 0) return;  // the copy blocks compute it
-    const int s = pair_word_slot(word);
-    w13_wave<T, CH, FULL>((const T*)f.x, H, I, f.K, pair, i, s < f.cap ? s : -1,
-                          (const T*)f.w13, f.w13_stride, (T*)f.act, lane);
-    return;
-  }
   const int n = *a.count;
-  if (a.hist && blockIdx.x == 0 && threadIdx.x == 0) {
+  if (a.hist && cb == 0 && threadIdx.x == 0) {
     *a.hist = n;
     __threadfence_system();
   }
@@ -246,7 +235,7 @@ __global__ __launch_bounds__(256) void pagein_w13_kernel(FusedW13Args f, PageInA
   uint4 xv[CH];
   load_row<T, CH, FULL, false>((const T*)f.x, nch, lane, xv);  // the call's one token
   int jcur = -1, e = -1, s = -1, pair = -1;
-  for (int q = blockIdx.x * 4 + wave; q < n * I; q += kPageInBlocks * 4) {
+  for (int q = cb * 4 + wave; q < n * I; q += kPageInBlocks * 4) {
     const int j = q / I, i = q - j * I;
     if (j != jcur) {
       jcur = j;
@@ -292,14 +281,100 @@ __global__ __launch_bounds__(256) void pagein_w13_kernel(FusedW13Args f, PageInA
     const int ej = a.loads[2 * j], sj = a.loads[2 * j + 1];
     if (ej < 0 || ej >= a.num_experts || sj < 0 || sj >= a.cap) continue;
     copy_range(p0.m + (size_t)ej * p0.m_stride + w13_bytes,
-               p0.d + (size_t)sj * p0.d_stride + w13_bytes, p0.bytes - w13_bytes, blockIdx.x,
+               p0.d + (size_t)sj * p0.d_stride + w13_bytes, p0.bytes - w13_bytes, cb,
                kPageInBlocks);
     for (int q = 1; q < a.nplanes; ++q) {
       const PageInPlane& pl = a.p[q];
       copy_range(pl.m + (size_t)ej * pl.m_stride, pl.d + (size_t)sj * pl.d_stride, pl.bytes,
-                 blockIdx.x, kPageInBlocks);
+                 cb, kPageInBlocks);
     }
   }
+}
+
+template <typename T, int CH, bool FULL>
+__global__ __launch_bounds__(256) void pagein_w13_kernel(FusedW13Args f, PageInArgs a) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (blockIdx.x >= kPageInBlocks) {
+    const int I = f.I, nbx = (I + 3) / 4;
+    const int local = blockIdx.x - kPageInBlocks;
+    const int pair = local / nbx;
+    const int i = (local - pair * nbx) * 4 + wave;
+    if (i >= I) return;
+    const int32_t word = f.words[pair];
+    if (pair_word_loaded(word) >= 0) return;  // the copy blocks compute it
+    const int s = pair_word_slot(word);
+    w13_wave<T, CH, FULL>((const T*)f.x, f.H, I, f.K, pair, i, s < f.cap ? s : -1,
+                          (const T*)f.w13, f.w13_stride, (T*)f.act, lane);
+    return;
+  }
+  pagein_w13_copy_block<T, CH, FULL>(f, a, blockIdx.x);
+}
+
+// ---------------------------------------------------------------------------
+// Kernel A'': the whole first half of a one-token call in one launch, for a
+// call that fills every slot (top-k == cap, one token: after the pager, the
+// slots hold exactly the token's experts) with routing fused:
+//   * block 0: the pager (pager_wave, wave 0): routing, the LRU decisions,
+//     the pair words and the load list; then it publishes the launch's
+//     epoch in `sync` (release at agent scope);
+//   * blocks 1 .. kPageInBlocks: Kernel A''s copy blocks, started when they
+//     see the epoch (acquire at agent scope): each loaded expert's act rows,
+//     per pair, from the bytes they copy;
+//   * the other blocks: Kernel A's blocks per (i-block, slot), writing
+//     act_spec[s][i] from whatever slot s holds at launch.  They need
+//     nothing from the pager, so the routing and the decisions run under
+//     their weight stream.  For a slot that this call loads, the value is
+//     computed from the old expert (or the bytes being copied) and is never
+//     read: the w2 kernel takes the copy blocks' act of that pair instead.
+// A call that loads nothing therefore costs the longer of the pager and the
+// w13 stream in one launch, where it cost a pager launch and then the w13
+// launch.
+// ---------------------------------------------------------------------------
+// Polls of the epoch word before a copy block gives up (about a second):
+// the pager wave never waits on anything, so the word arrives within
+// microseconds; the bound only keeps a broken launch from hanging the GPU.
+constexpr int kDecodeSpinLimit = 1 << 20;
+
+template <typename T, typename TL, int CH>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6))) void decode_w13_kernel(FusedW13Args f, PageInArgs a,
+                                                         DecodePagerArgs pa) {
+  // the pager wave's LDS for at most 128 experts and one token's pairs
+  __shared__ PagerSmemT<128> sm;
+  __shared__ FusedRouteSmemT<kMaxTopK> fr;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (blockIdx.x == 0) {
+    if (wave != 0) return;
+    pager_wave<TL, 2, true, 128, kMaxTopK>(
+        nullptr, (const TL*)pa.logits, pa.renorm, pa.topk_w, pa.topk_ids, 1, f.K, pa.E, f.cap, 0,
+        pa.map, pa.s2e, pa.tick, pa.ctr, pa.slots, const_cast<int32_t*>(f.words) - 1, pa.loads,
+        pa.rec, nullptr, sm, fr);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    if (lane == 0) __hip_atomic_store(pa.sync, pa.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+  if (blockIdx.x <= kPageInBlocks) {
+    __shared__ int seen;
+    if (threadIdx.x == 0) {
+      int it = 0;
+      while (__hip_atomic_load(pa.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != pa.epoch &&
+             ++it < kDecodeSpinLimit)
+        __builtin_amdgcn_s_sleep(2);
+      seen = it < kDecodeSpinLimit;
+    }
+    __syncthreads();
+    if (!seen) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    pagein_w13_copy_block<T, CH, true>(f, a, blockIdx.x - 1);
+    return;
+  }
+  const int I = f.I, nbx = (I + 3) / 4;
+  const int local = blockIdx.x - 1 - kPageInBlocks;
+  const int s = local / nbx;
+  const int i = (local - s * nbx) * 4 + wave;
+  if (i >= I) return;
+  // one token, K == cap: act_spec row s is "pair" s of a call of K pairs
+  w13_wave<T, CH, true>((const T*)f.x, f.H, I, f.K, s, i, s, (const T*)f.w13, f.w13_stride,
+                        (T*)pa.act_spec, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -371,14 +446,18 @@ __device__ inline void w2_dots(const uint4 (&wv)[RPH][CH], const T* __restrict__
 // slots and weights, without waiting for them, then finds the pair the slot
 // serves and dots its rows with that pair's act row.  Each row's arithmetic
 // is the same as with one wave per pair, so the output bytes are too.
-template <typename T, int LPR, int CH, int RPH, bool FULL, bool SLOTS>
+// SPEC (with SLOTS, after Kernel A''): `slots` holds the pager's pair words;
+// the act row of slot k is act_spec row k, or the pair's own act row when the
+// call loaded that pair's expert (the copy blocks computed it).
+template <typename T, int LPR, int CH, int RPH, bool FULL, bool SLOTS, bool SPEC = false>
 __global__ __launch_bounds__(1024) void w2_combine_kernel(const T* __restrict__ act, int H, int I,
                                                            int K, const float* __restrict__ topk_w,
                                                            const int32_t* __restrict__ slots,
                                                            const T* __restrict__ w2,
                                                            size_t w2_stride,
                                                            T* __restrict__ out,
-                                                           const int32_t* __restrict__ skip_if) {
+                                                           const int32_t* __restrict__ skip_if,
+                                                           const T* __restrict__ act_spec) {
   static_assert(LPR == 32 || LPR == 64, "a row spans half a wave or a whole wave");
   constexpr int V = Vec<T>::N;
   constexpr int RPB = 64 / LPR * RPH;  // rows per block
@@ -399,7 +478,8 @@ __global__ __launch_bounds__(1024) void w2_combine_kernel(const T* __restrict__ 
     // (both loaded ahead of the rows, so that waiting for them does not wait
     // for the rows: loads complete in order)
     const int jl = min(lane, K - 1);
-    const int sj = load_first(slots + t * K + jl);
+    const int32_t wd = load_first(slots + t * K + jl);
+    const int sj = SPEC ? pair_word_slot(wd) : wd;
     const float wj = __int_as_float(load_first((const int32_t*)topk_w + t * K + jl));
     uint4 wv[RPH][CHA];
     w2_load_rows<T, LPR, CHA, RPH, FULL>(w2 + (size_t)k * w2_stride, h0, H, I, l, wv);
@@ -411,7 +491,12 @@ __global__ __launch_bounds__(1024) void w2_combine_kernel(const T* __restrict__ 
     const float wsk = __shfl(wj, k);
     // unconditional (a wave whose slot serves no pair dots with pair 0's act
     // and drops the result): rows used under a branch would be loaded there
-    w2_dots<T, LPR, CHA, RPH, FULL>(wv, act + ((size_t)t * K + (p < 0 ? 0 : p)) * I, I, l, d);
+    const T* arow = act + ((size_t)t * K + (p < 0 ? 0 : p)) * I;
+    if (SPEC) {
+      const uint64_t loaded = __ballot(lane < K && pair_word_loaded(wd) >= 0);
+      if (!(p >= 0 && ((loaded >> p) & 1ull))) arow = act_spec + (size_t)k * I;
+    }
+    w2_dots<T, LPR, CHA, RPH, FULL>(wv, arow, I, l, d);
     if (lane == 0) wk[k] = sk >= 0 ? wsk : 0.f;
     if (sk < 0 && l == 0) {  // pair k reads no expert: its partials are 0
 #pragma unroll
@@ -481,6 +566,7 @@ struct LaunchCtl {
   int want = 0;
   const int32_t* skip_if = nullptr;
   bool slots = false;
+  const void* act_spec = nullptr;  // with slots: the w2 kernel's SPEC mode
 };
 
 template <typename T, int CH>
@@ -503,6 +589,13 @@ void launch_pagein_w13(const PageInArgs& a, const FusedW13Args& f, hipStream_t s
     launch_timed(pagein_w13_kernel<T, CH, true>, grid, dim3(256), st, ev_start, ev_stop, f, a);
   else
     launch_timed(pagein_w13_kernel<T, CH, false>, grid, dim3(256), st, ev_start, ev_stop, f, a);
+}
+
+template <typename T, typename TL, int CH>
+void launch_decode_w13(const PageInArgs& a, const FusedW13Args& f, const DecodePagerArgs& pa,
+                       hipStream_t st, hipEvent_t ev_start, hipEvent_t ev_stop) {
+  const dim3 grid(1 + kPageInBlocks + (f.I + 3) / 4 * f.cap);
+  launch_timed(decode_w13_kernel<T, TL, CH>, grid, dim3(256), st, ev_start, ev_stop, f, a, pa);
 }
 
 // The per-lane chunk count of the w13 kernels for a row of H elements (0 when
@@ -543,25 +636,49 @@ int dispatch_pagein_w13(const PageInArgs& a, const FusedW13Args& f, hipStream_t 
   return WISP_OK;
 }
 
+// Kernel A'' for whole rows of 2 or 4 chunks per lane (the other shapes keep
+// the separate pager launch: at 8 chunks the launch's 80 VGPRs spill).
+template <typename T, typename TL>
+int dispatch_decode_w13(const PageInArgs& a, const FusedW13Args& f, const DecodePagerArgs& pa,
+                        hipStream_t st, hipEvent_t ev_start, hipEvent_t ev_stop) {
+  const int ch = w13_chunks<T>(f.H);
+  if (f.H != ch * 64 * Vec<T>::N) return WISP_ERR_UNSUPPORTED;
+  switch (ch) {
+    case 2: launch_decode_w13<T, TL, 2>(a, f, pa, st, ev_start, ev_stop); break;
+    case 4: launch_decode_w13<T, TL, 4>(a, f, pa, st, ev_start, ev_stop); break;
+    default: return WISP_ERR_UNSUPPORTED;
+  }
+  return WISP_OK;
+}
+
 template <typename T, int LPR, int CH, int RPH = 1>
 void launch_w2(const T* act, int T_, int H, int I, int K, const float* w, const int32_t* slots,
                const T* w2, size_t w2_stride, T* out, hipStream_t st, const LaunchCtl& c) {
   constexpr int RPB = 64 / LPR * RPH;
   dim3 grid((H + RPB - 1) / RPB, T_);
   const bool full = CH > 0 && I == CH * LPR * Vec<T>::N;
-  if (CH > 0 && c.slots) {
+  const T* spec = (const T*)c.act_spec;
+  if (CH > 0 && c.slots && spec) {
+    if (full)
+      launch_timed(w2_combine_kernel<T, LPR, CH, RPH, true, true, true>, grid, dim3(64 * K), st,
+                   c.start, c.stop, act, H, I, K, w, slots, w2, w2_stride, out, c.skip_if, spec);
+    else
+      launch_timed(w2_combine_kernel<T, LPR, CH, RPH, false, true, true>, grid, dim3(64 * K),
+                   st, c.start, c.stop, act, H, I, K, w, slots, w2, w2_stride, out, c.skip_if,
+                   spec);
+  } else if (CH > 0 && c.slots) {
     if (full)
       launch_timed(w2_combine_kernel<T, LPR, CH, RPH, true, true>, grid, dim3(64 * K), st,
-                   c.start, c.stop, act, H, I, K, w, slots, w2, w2_stride, out, c.skip_if);
+                   c.start, c.stop, act, H, I, K, w, slots, w2, w2_stride, out, c.skip_if, spec);
     else
       launch_timed(w2_combine_kernel<T, LPR, CH, RPH, false, true>, grid, dim3(64 * K), st,
-                   c.start, c.stop, act, H, I, K, w, slots, w2, w2_stride, out, c.skip_if);
+                   c.start, c.stop, act, H, I, K, w, slots, w2, w2_stride, out, c.skip_if, spec);
   } else if (full) {
     launch_timed(w2_combine_kernel<T, LPR, CH, RPH, true, false>, grid, dim3(64 * K), st,
-                 c.start, c.stop, act, H, I, K, w, slots, w2, w2_stride, out, c.skip_if);
+                 c.start, c.stop, act, H, I, K, w, slots, w2, w2_stride, out, c.skip_if, spec);
   } else {
     launch_timed(w2_combine_kernel<T, LPR, CH, RPH, false, false>, grid, dim3(64 * K), st,
-                 c.start, c.stop, act, H, I, K, w, slots, w2, w2_stride, out, c.skip_if);
+                 c.start, c.stop, act, H, I, K, w, slots, w2, w2_stride, out, c.skip_if, spec);
   }
 }
 
@@ -616,6 +733,38 @@ int pagein_w13(const PageInArgs& a, const void* x, int dtype, int T_, int H, int
   return WISP_OK;
 }
 
+// Whether Kernel A'' serves a layer: a one-token call with top-k == cap <=
+// 64, at most 128 experts, rows of 2 or 4 chunks per lane.
+bool decode_w13_supported(int dtype, int H, int E, int K, int cap) {
+  const int V = dtype == WISP_F32 ? 4 : 8;
+  const int ch = H / V / 64;
+  return K == cap && cap <= 64 && E <= 128 && H % (64 * V) == 0 && (ch == 2 || ch == 4);
+}
+
+// Kernel A'': `a` as for pagein_w13 (a.count = flags), pager arguments in pa.
+int decode_w13(const PageInArgs& a, const void* x, int dtype, int logits_dtype, int H, int I,
+               int K, int32_t* flags, const void* w13, size_t w13_stride, void* act,
+               const DecodePagerArgs& pa, hipStream_t st, hipEvent_t ev_start,
+               hipEvent_t ev_stop) {
+  FusedW13Args f{x, flags + 1, w13, w13_stride, act, H, I, K, a.cap};
+  int rc;
+  if (dtype == WISP_F32)
+    rc = logits_dtype == WISP_BF16
+             ? dispatch_decode_w13<float, uint16_t>(a, f, pa, st, ev_start, ev_stop)
+             : dispatch_decode_w13<float, float>(a, f, pa, st, ev_start, ev_stop);
+  else
+    rc = logits_dtype == WISP_BF16
+             ? dispatch_decode_w13<uint16_t, uint16_t>(a, f, pa, st, ev_start, ev_stop)
+             : dispatch_decode_w13<uint16_t, float>(a, f, pa, st, ev_start, ev_stop);
+  if (rc != WISP_OK) {
+    wisp_set_last_error("hidden size outside the fused decode launch's coverage",
+                        "decode w13 kernel");
+    return rc;
+  }
+  WISP_HIP_TRY(hipGetLastError());
+  return WISP_OK;
+}
+
 int gemv_w13(const void* x, int dtype, int T_, int H, int I, int K, const int32_t* slots,
              const void* w13, size_t w13_stride, void* act, hipStream_t st,
              hipEvent_t ev_start, hipEvent_t ev_stop, const int32_t* pair_filter, int want) {
@@ -642,13 +791,15 @@ int gemv_w13(const void* x, int dtype, int T_, int H, int I, int K, const int32_
 // and runs the w2 kernel one wave per slot (cap 0: one wave per pair).
 int gemv_w2(const void* act, int dtype, int T_, int H, int I, int K, const float* topk_w,
             const int32_t* slots, const void* w2, size_t w2_stride, void* out, hipStream_t st,
-            hipEvent_t ev_start, hipEvent_t ev_stop, const int32_t* skip_if, int cap) {
+            hipEvent_t ev_start, hipEvent_t ev_stop, const int32_t* skip_if, int cap,
+            const void* act_spec) {
   if (T_ == 0) return WISP_OK;
   LaunchCtl c;
   c.start = ev_start;
   c.stop = ev_stop;
   c.skip_if = skip_if;
   c.slots = T_ == 1 && K == cap;
+  c.act_spec = c.slots ? act_spec : nullptr;
   const int rc = dtype == WISP_F32
       ? dispatch_w2<float>((const float*)act, T_, H, I, K, topk_w, slots, (const float*)w2,
                            w2_stride, (float*)out, st, c)
@@ -669,7 +820,7 @@ int experts_gemv(const void* x, int dtype, int T_, int H, int I, int K, const fl
                     ev ? ev->ev[0] : nullptr, ev ? ev->ev[1] : nullptr, nullptr, 0);
   if (rc != WISP_OK) return rc;
   return gemv_w2(act, dtype, T_, H, I, K, topk_w, slots, w2, w2_stride, out, st,
-                 ev ? ev->ev[2] : nullptr, ev ? ev->ev[3] : nullptr, nullptr, 0);
+                 ev ? ev->ev[2] : nullptr, ev ? ev->ev[3] : nullptr, nullptr, 0, nullptr);
 }
 
 }  // namespace wisp

@@ -71,7 +71,13 @@ int pagein_w13(const PageInArgs& a, const void* x, int dtype, int T, int H, int 
                hipStream_t st, hipEvent_t ev_start, hipEvent_t ev_stop);
 int gemv_w2(const void* act, int dtype, int T, int H, int I, int K, const float* topk_w,
             const int32_t* slots, const void* w2, size_t w2_stride, void* out, hipStream_t st,
-            hipEvent_t ev_start, hipEvent_t ev_stop, const int32_t* skip_if, int cap);
+            hipEvent_t ev_start, hipEvent_t ev_stop, const int32_t* skip_if, int cap,
+            const void* act_spec);
+bool decode_w13_supported(int dtype, int H, int E, int K, int cap);
+int decode_w13(const PageInArgs& a, const void* x, int dtype, int logits_dtype, int H, int I,
+               int K, int32_t* flags, const void* w13, size_t w13_stride, void* act,
+               const DecodePagerArgs& pa, hipStream_t st, hipEvent_t ev_start,
+               hipEvent_t ev_stop);
 int experts_gemv(const void* x, int dtype, int T, int H, int I, int K, const float* topk_w,
                  const int32_t* slots, const void* w13, size_t w13_stride, const void* w2,
                  size_t w2_stride, void* act, void* out, hipStream_t st, const StageEvents* ev);
@@ -225,6 +231,15 @@ struct Layer {
   // a fused launch adds to prof_ms[0]
   double prof_w2_nl_ms = 0;
   int64_t prof_w2_nl_calls = 0;
+  // The fused decode launch (pager, page-in and w13 in one grid, for
+  // one-token calls with top-k == cap): w13 per slot [spec_cap][inter] in
+  // the activation dtype, and the word its pager wave publishes the
+  // launch's epoch in (device memory, allocated with the layer).
+  void* act_spec = nullptr;
+  int spec_cap = 0;
+  uint32_t* decode_sync = nullptr;
+  uint32_t decode_epoch = 0;
+  bool decode_fused = false;  // wisp_layer_set_decode_fused
 };
 
 void prof_harvest(Layer& L, ProfLaunch& p) {
@@ -389,6 +404,9 @@ struct FusedW13 {
   const int32_t* flags;
   void* act;
   const int32_t* slots;
+  // with dec: the pager runs in the same launch (Kernel A'')
+  const DecodePagerArgs* dec = nullptr;
+  int logits_dtype = WISP_F32;
 };
 
 // Copy-kernel page-in on `st` of the (expert, slot) pairs at `loads` (device
@@ -422,7 +440,11 @@ int page_in_kernel(Layer& L, const int32_t* loads, const int32_t* count, int n, 
   a.hist = L.profile ? L.hist_dev + i : nullptr;
   hipEvent_t e0 = L.profile ? p.start : nullptr, e1 = L.profile ? p.stop : nullptr;
   int rc;
-  if (fw && L.fp8)
+  if (fw && fw->dec)
+    rc = decode_w13(a, fw->x, d.dtype, fw->logits_dtype, d.hidden, d.inter, fw->K,
+                    const_cast<int32_t*>(fw->flags), d.scratch_w13, d.scratch_w13_stride, fw->act,
+                    *fw->dec, st, e0, e1);
+  else if (fw && L.fp8)
     rc = pagein_fp8_w13(a, fw->x, d.hidden, d.inter, fw->K, fw->slots, fw->flags, d.cap,
                         d.scratch_w13, d.scratch_w13_stride, d.scratch_s13, d.scratch_s13_stride,
                         d.block_n, L.s13_off, fw->act, st, e0, e1, true);
@@ -554,7 +576,8 @@ int w13(Layer& L, const void* x, int T, int K, const int32_t* slots, void* act, 
 }
 
 int w2(Layer& L, const void* act, int T, int K, const float* w, const int32_t* slots, void* out,
-       hipStream_t st, const int32_t* skip_if, ProfLaunch** launched) {
+       hipStream_t st, const int32_t* skip_if, ProfLaunch** launched,
+       const void* act_spec = nullptr) {
   const wisp_layer_desc& d = L.d;
   if (L.fp8 && skip_if) return WISP_ERR_INVALID;  // no speculative block-FP8 launches
   ProfLaunch* p = prof_begin(L, 1);
@@ -566,7 +589,7 @@ int w2(Layer& L, const void* act, int T, int K, const float* w, const int32_t* s
                                   p ? p->stop : nullptr, true)
                  : gemv_w2(act, d.dtype, T, d.hidden, d.inter, K, w, slots, d.scratch_w2,
                            d.scratch_w2_stride, out, st, p ? p->start : nullptr,
-                           p ? p->stop : nullptr, skip_if, d.cap);
+                           p ? p->stop : nullptr, skip_if, d.cap, act_spec);
   if (p && rc == WISP_OK) p->pending = true;
   if (launched) *launched = p;
   return rc;
@@ -698,6 +721,26 @@ int check_ws(const wisp_workspace* ws, int T, int K) {
 using wisp::Layer;
 
 namespace wisp {
+// The fused decode launch's buffers for a scratch of `cap` slots: act_spec
+// [cap][inter] and the epoch word (zero, an epoch no launch uses).  Called at
+// creation and on a resize to more slots, both points where no kernel of the
+// layer is in flight.
+static int alloc_decode(Layer& L, int cap) {
+  const wisp_layer_desc& d = L.d;
+  if (L.fp8 || d.hidden < 1 || d.mode != WISP_MODE_PAGED || cap <= L.spec_cap) return WISP_OK;
+  if (L.act_spec) WISP_HIP_TRY(hipFree(L.act_spec));
+  L.act_spec = nullptr;
+  L.spec_cap = 0;
+  WISP_HIP_TRY(hipMalloc(&L.act_spec, (size_t)cap * d.inter * act_size(d.dtype)));
+  L.spec_cap = cap;
+  if (!L.decode_sync) {
+    WISP_HIP_TRY(hipMalloc((void**)&L.decode_sync, 256));
+    WISP_HIP_TRY(hipMemset(L.decode_sync, 0, 256));
+    L.decode_epoch = 0;
+  }
+  return WISP_OK;
+}
+
 // Block-FP8 fields of a descriptor: scale shapes consistent with the MLP
 // shape and the block, scale buffers present.
 static bool fp8_desc_ok(const wisp_layer_desc& d) {
@@ -758,6 +801,10 @@ extern "C" int wisp_layer_create(const wisp_layer_desc* desc, void** handle) {
     return WISP_ERR_HIP;
   }
   if (d.hidden > 0) setup_kernel_pagein(*L);
+  if (alloc_decode(*L, d.cap) != WISP_OK) {
+    wisp_layer_destroy(L);
+    return WISP_ERR_HIP;
+  }
   *handle = L;
   return WISP_OK;
 }
@@ -788,6 +835,8 @@ extern "C" int wisp_layer_destroy(void* handle) {
     if (L->pin[i].stop) (void)hipEventDestroy(L->pin[i].stop);
   }
   if (L->hist) (void)hipHostFree(L->hist);
+  if (L->act_spec) (void)hipFree(L->act_spec);
+  if (L->decode_sync) (void)hipFree(L->decode_sync);
   for (int c = 0; c < kCopyStreams; ++c)
     if (L->copy[c]) (void)hipStreamDestroy(L->copy[c]);
   delete L;
@@ -828,6 +877,7 @@ extern "C" int wisp_layer_set_scratch(void* handle, void* scratch_w13, void* scr
   L->d.slot_to_expert = slot_to_expert;
   L->d.lru_tick = lru_tick;
   set_fused_ok(*L);
+  if (alloc_decode(*L, cap) != WISP_OK) return WISP_ERR_HIP;
   return WISP_OK;
 }
 
@@ -905,6 +955,33 @@ extern "C" int wisp_layer_forward(void* handle, const void* x, const void* logit
   int32_t* rec_dev = ws->record_dev ? ws->record_dev : record_device_ptr(ws->record);
   int32_t* rec_host = ws->record_dev && !rec_dev_only ? record_device_ptr(ws->record) : nullptr;
   L->rec_on_device = rec_dev_only;
+  if (L->decode_fused && T == 1 && fuse_route && rec_dev_only && a == WISP_ALGO_GEMV &&
+      L->fused_ok && !L->fp8 && L->act_spec && L->spec_cap >= d.cap &&
+      (logits_dtype == WISP_F32 || logits_dtype == WISP_BF16) &&
+      decode_w13_supported(d.dtype, d.hidden, d.num_experts, K, d.cap)) {
+    // [route + pager + page-in + w13 per slot] [w2]: the launch's w13
+    // blocks need nothing from the pager (the call fills every slot), so the
+    // routing and the decisions run under their weight stream
+    rc = wait_prefetch(*L, st);
+    if (rc != WISP_OK) return rc;
+    if (++L->decode_epoch == 0) L->decode_epoch = 1;  // 0 is the word's initial value
+    const DecodePagerArgs pa{logits, renormalize, d.num_experts, ws->topk_w, ws->topk_ids,
+                             d.expert_map, d.slot_to_expert, d.lru_tick, d.counters, ws->slots,
+                             ws->loads, rec_dev, L->decode_sync, L->decode_epoch, L->act_spec};
+    FusedW13 fw{x, T, K, ws->flags, ws->act, ws->slots};
+    fw.dec = &pa;
+    fw.logits_dtype = logits_dtype;
+    const int pin_slot = L->pin_next;
+    rc = page_in_kernel(*L, ws->loads, ws->flags, 0, st, &fw);
+    if (rc != WISP_OK) return rc;
+    ProfLaunch* p2 = nullptr;
+    rc = w2(*L, ws->act, T, K, ws->topk_w, ws->flags + 1, out, st, nullptr, &p2, L->act_spec);
+    if (rc == WISP_OK && p2) {
+      L->pin[pin_slot].w2 = p2;
+      L->pin[pin_slot].w2_gen = p2->gen;
+    }
+    return rc;
+  }
   rc = launch_pager(ws->topk_ids, fuse_route ? logits : nullptr, logits_dtype, renormalize,
                     ws->topk_w, ws->topk_ids, T, K, d.num_experts, d.cap, 0, d.expert_map,
                     d.slot_to_expert, d.lru_tick, d.counters, ws->slots, ws->flags, ws->loads,
@@ -1099,6 +1176,13 @@ extern "C" int wisp_layer_sync_record(void* handle, const wisp_workspace* ws) {
     WISP_HIP_TRY(hipMemcpy(ws->record, ws->record_dev, (size_t)ws->record_words * sizeof(int32_t),
                            hipMemcpyDeviceToHost));
   }
+  return WISP_OK;
+}
+
+extern "C" int wisp_layer_set_decode_fused(void* handle, int enable) {
+  Layer* L = (Layer*)handle;
+  if (!L) return WISP_ERR_INVALID;
+  L->decode_fused = enable != 0;
   return WISP_OK;
 }
 

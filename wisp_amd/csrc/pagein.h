@@ -38,6 +38,25 @@ struct PageInArgs {
 
 int launch_pagein(const PageInArgs& a, hipStream_t st, hipEvent_t ev_start, hipEvent_t ev_stop);
 
+// The pager wave's arguments in a fused one-token decode launch (page-in,
+// w13 and the pager in one grid; the layer's call with top-k == cap).
+struct DecodePagerArgs {
+  const void* logits;  // [E] of the call's one token
+  int renorm, E;
+  float* topk_w;
+  int32_t* topk_ids;
+  int32_t* map;
+  int32_t* s2e;
+  int64_t* tick;
+  int64_t* ctr;
+  int32_t* slots;
+  int32_t* loads;
+  int32_t* rec;       // the device decision record
+  uint32_t* sync;     // the launch's epoch, published by the pager wave
+  uint32_t epoch;
+  void* act_spec;     // [cap][I]: w13 per slot
+};
+
 constexpr int kPageInUnroll = 4;
 
 // Copies `bytes` (a multiple of 16) from src to dst, spread over `nblocks`
