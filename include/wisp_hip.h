@@ -65,8 +65,10 @@ typedef struct ihipStream_t* wisp_stream_t; /* == hipStream_t */
 
 /* Message of the last failing call on this thread ("" if none). */
 const char* wisp_last_error(void);
-/* ABI version of this library: 2 (wisp_layer_desc carries the block-FP8
- * fields). */
+/* ABI version of this library: 3 (wisp_layer_desc carries the block-FP8
+ * fields; wisp_layer_desc and wisp_workspace end with struct_bytes, which
+ * the caller sets to the struct's sizeof and the library checks, so that a
+ * caller built against another layout is refused instead of misread). */
 int wisp_abi_version(void);
 /* int32 words a decision record needs for a call of T tokens x K experts. */
 int wisp_record_words(int T, int K);
@@ -193,15 +195,25 @@ size_t wisp_moe_fp8_work_bytes(int T, int K, int H, int I, int nslots);
 int wisp_quant_fp8_groups(const void* x, int dtype, int rows, int cols, int group, uint8_t* q,
                           float* scales, wisp_stream_t stream);
 
-/* Bytes of the device array wisp_moe_experts_noalloc works in, per GPU. */
+/* Bytes of the device array wisp_moe_experts_noalloc works in, per GPU, in
+ * a default build; building with WISP_NOALLOC_SCRATCH_MIB=n sets n MiB, and
+ * wisp_noalloc_scratch_bytes() returns the size the library was built with.
+ * Every process that loads the library holds this much HBM on each GPU it
+ * runs on, from the code object's load there until the process ends,
+ * whether or not it calls wisp_moe_experts_noalloc: count it in the HBM
+ * budget beside the layers' scratch (cap slots each). */
+#ifndef WISP_NOALLOC_SCRATCH_BYTES
 #define WISP_NOALLOC_SCRATCH_BYTES (64u << 20)
+#endif
+/* The size of that array in this build, in bytes. */
+size_t wisp_noalloc_scratch_bytes(void);
 
 /* wisp_moe_experts without act and work arguments, allocating nothing.
  * No counterpart in the reference: it is for callers that cannot allocate
  * device memory (work captured into a HIP graph, serving loops or harnesses
  * that forbid hipMalloc).  The act intermediate and the MFMA work buffer live
- * in a static device array of the library, WISP_NOALLOC_SCRATCH_BYTES per
- * GPU, held from the library's first use on that GPU until the process
+ * in a static device array of the library, wisp_noalloc_scratch_bytes()
+ * per GPU, held from the code object's load on that GPU until the process
  * ends.  A call needing more than that (T*K*I act elements, 256-byte
  * aligned, plus wisp_moe_work_bytes(T, K, H, nslots) on the MFMA path)
  * returns WISP_ERR_INVALID before any launch.  Every call on one GPU shares
@@ -263,6 +275,8 @@ typedef struct wisp_layer_desc {
   size_t master_s13_stride;      /* elements                             */
   const float* master_s2;
   size_t master_s2_stride;       /* elements                             */
+  size_t struct_bytes;           /* sizeof(wisp_layer_desc); another value
+                                    is refused (WISP_ERR_INVALID)         */
 } wisp_layer_desc;
 
 typedef struct wisp_workspace {
@@ -289,6 +303,8 @@ typedef struct wisp_workspace {
                                     work buffer (wisp_moe_work_bytes with
                                     nslots = cap)                         */
   size_t work_bytes;
+  size_t struct_bytes;           /* sizeof(wisp_workspace); another value
+                                    is refused (WISP_ERR_INVALID)         */
 } wisp_workspace;
 
 /* Create / destroy the per-layer context (copy stream, events). */

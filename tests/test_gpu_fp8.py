@@ -524,3 +524,40 @@ def test_install_wisp_fp8_standin_layer_matches_resident():
         elif hasattr(Fp8MoEMethod, f8m._PATCHED_FLAG):
             delattr(Fp8MoEMethod, f8m._PATCHED_FLAG)
         f8m._FP8_LAYER_STATES.clear()
+
+
+def test_fp8_state_from_weights_loaded_outside_the_slab():
+    """A block-FP8 layer whose parameters were created by the unpatched
+    create_weights (four separate tensors) gets its masters copied into one
+    pinned slab by the patched process_weights_after_loading; its outputs
+    equal the unpatched resident layer's bytes."""
+    from wisp.integrations.vllm.layer import Fp8FusedMoE, Fp8MoEMethod
+    E, H, I, K, block = 16, 512, 256, 4, (128, 128)
+    _, w13, w2, s13, s2 = _experts(E, H, I, block, seed=17)
+    g = torch.Generator().manual_seed(18)
+    x = torch.randn((3, H), generator=g).to(torch.bfloat16).to(DEV)
+    lg = torch.randn((3, E), generator=g).to(DEV)
+    names = ("create_weights", "process_weights_after_loading", "apply")
+    saved = {n: Fp8MoEMethod.__dict__[n] for n in names}
+    if getattr(Fp8MoEMethod, f8m._PATCHED_FLAG, False):  # build the layers unpatched
+        for n in names:
+            setattr(Fp8MoEMethod, n, getattr(Fp8MoEMethod, "_wisp_original_" + n))
+    try:
+        ref_layer = Fp8FusedMoE(E, K, H, I, block)  # every expert on the GPU
+        ref_layer.load_weights(w13, w2, s13, s2)
+        ref_layer.process_weights_after_loading()
+        ref = ref_layer(x, lg)
+        plain = Fp8FusedMoE(E, K, H, I, block)
+        plain.load_weights(w13, w2, s13, s2)
+        assert not hasattr(plain, "_wisp_fp8_slab")
+        f8m._patched_process_weights_after_loading(plain.quant_method, plain)
+        st = plain._wisp_fp8_state
+        assert plain._wisp_fp8_slab.is_pinned() and st.pagein_engine == "kernel"
+        assert plain.w13_weight.numel() == 0
+        out = f8m._patched_apply(plain.quant_method, plain, x, lg, K, True)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    finally:
+        for n, fn in saved.items():
+            setattr(Fp8MoEMethod, n, fn)
+        f8m._FP8_LAYER_STATES.clear()

@@ -84,6 +84,7 @@ def test_noalloc_equals_workspace_entry_point(dtype, algo, shape):
 def test_noalloc_refuses_calls_beyond_its_array():
     H, I, E, K = 2048, 768, 16, 8
     T = 4096  # act alone is 48 MiB, plus 268 MiB of MFMA work
+    assert _lib.lib().wisp_noalloc_scratch_bytes() < (48 + 268) << 20
     x = torch.zeros((T, H), dtype=torch.bfloat16, device=DEV)
     w13 = torch.zeros((E, 2 * I, H), dtype=torch.bfloat16, device=DEV)
     w2 = torch.zeros((E, H, I), dtype=torch.bfloat16, device=DEV)

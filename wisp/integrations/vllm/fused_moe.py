@@ -150,6 +150,7 @@ class _Workspace:
         self.work_bytes = 0
         self.work = None
         self.struct = _lib.Workspace()
+        self.struct.struct_bytes = C.sizeof(_lib.Workspace)
         self.topk_w = self.topk_ids = self.slots = self.flags = self.loads = None
         self.act = self.record = self.record_dev = None
 
@@ -277,6 +278,7 @@ class WispMoEState:
 
     def _make_desc(self) -> "_lib.LayerDesc":
         d = _lib.LayerDesc()
+        d.struct_bytes = C.sizeof(_lib.LayerDesc)
         d.num_experts, d.cap = self.num_experts, self.cap_experts
         d.hidden, d.inter = self.hidden, self.inter
         d.dtype = _DTYPES[self.dtype]

@@ -197,6 +197,7 @@ class WispMoEStateFP8(WispMoEState):
     def _make_desc(self) -> "_lib.LayerDesc":
         lay = self._layout
         d = _lib.LayerDesc()
+        d.struct_bytes = C.sizeof(_lib.LayerDesc)
         d.num_experts, d.cap = self.num_experts, self.cap_experts
         d.hidden, d.inter = self.hidden, self.inter
         d.dtype = _lib.WISP_FP8_E4M3
@@ -290,55 +291,57 @@ def _patched_create_weights(self, layer, num_experts, hidden_size,
     _set_attrs(params["w13_weight_scale_inv"], scale_attrs)
     _set_attrs(params["w2_weight_scale_inv"], scale_attrs)
     layer._wisp_fp8_slab = buf
-    layer._wisp_cpu_pin_w13, layer._wisp_cpu_pin_w2 = w13, w2
-    layer._wisp_cpu_pin_s13, layer._wisp_cpu_pin_s2 = s13, s2
     layer.w13_input_scale = None
     layer.w2_input_scale = None
     self.rocm_aiter_moe_enabled = False
 
 
-def _to_cpu(t: torch.Tensor) -> torch.Tensor:
-    return t if t.device.type == "cpu" else t.to("cpu")
+def _slab_masters_of(layer, block: tuple[int, int]):
+    """The layer's four block-FP8 tensors as views of one pinned ``[E, slab]``
+    host buffer, so that a miss moves an expert's weights and scales in one
+    copy.  After the patched create_weights the buffer already exists (the
+    layer's parameters are its views and the checkpoint loader filled them in
+    place); otherwise one is made and the loaded tensors are copied into it
+    from wherever they live."""
+    buf = getattr(layer, "_wisp_fp8_slab", None)
+    w13 = layer.w13_weight.data
+    E, two_i, H = w13.shape
+    if buf is not None:
+        return Fp8SlabLayout(H, two_i // 2, block).views(buf)
+    buf, *views = fp8_slab_masters(E, H, two_i // 2, block, pin=True)
+    loaded = (w13, layer.w2_weight.data, layer.w13_weight_scale_inv.data,
+              layer.w2_weight_scale_inv.data)
+    for dst, src in zip(views, loaded):
+        dst.copy_(src)
+    layer._wisp_fp8_slab = buf
+    return tuple(views)
 
 
 def _patched_process_weights_after_loading(self, layer) -> None:
-    """Build the layer's FP8 paging state (reference 206-269)."""
+    """Create the layer's block-FP8 paging state (the hook of reference
+    206-269): non-block FP8 keeps vLLM's own processing, a second call
+    changes nothing, and the layer's device parameters become 0-element
+    placeholders, since the expert kernels read the state's scratch."""
     if getattr(layer, "_wisp_fp8_state", None) is not None:
         return
     if not getattr(self, "block_quant", False):
         return type(self)._wisp_original_process_weights_after_loading(self, layer)
-    cpu_w13 = _to_cpu(getattr(layer, "_wisp_cpu_pin_w13", layer.w13_weight.data))
-    cpu_w2 = _to_cpu(getattr(layer, "_wisp_cpu_pin_w2", layer.w2_weight.data))
-    cpu_s13 = _to_cpu(getattr(layer, "_wisp_cpu_pin_s13", layer.w13_weight_scale_inv.data))
-    cpu_s2 = _to_cpu(getattr(layer, "_wisp_cpu_pin_s2", layer.w2_weight_scale_inv.data))
-
-    # Weight masters stay where they are (pinned when create_weights made the
-    # slab); only the small scale tensors are pinned here, as the reference
-    # does (215-230).
-    def _try_pin(t):
-        try:
-            return t if t.is_pinned() else t.pin_memory()
-        except RuntimeError:
-            return t
-    cpu_s13, cpu_s2 = _try_pin(cpu_s13), _try_pin(cpu_s2)
-
+    block = tuple(int(b) for b in self.weight_block_size)
+    masters = _slab_masters_of(layer, block)
     gpu = torch.device("cuda", torch.cuda.current_device())
-    E = int(cpu_w13.shape[0])
-    cap = _resolve_cap_experts(E)
-    st = WispMoEStateFP8(cpu_w13, cpu_w2, cpu_s13, cpu_s2, cap, gpu, len(_FP8_LAYER_STATES),
-                         block=tuple(self.weight_block_size))
+    E = int(masters[0].shape[0])
+    st = WispMoEStateFP8(*masters, _resolve_cap_experts(E), gpu, len(_FP8_LAYER_STATES),
+                         block=block)
     _FP8_LAYER_STATES.append(st)
     layer._wisp_fp8_state = st
-    # 0-element device placeholders: the apply path reads the scratch
-    # directly and the layer params are never consulted (reference 244-252)
-    layer.w13_weight.data = torch.empty(0, dtype=FP8, device=gpu)
-    layer.w2_weight.data = torch.empty(0, dtype=FP8, device=gpu)
-    layer.w13_weight_scale_inv.data = torch.empty(0, dtype=torch.float32, device=gpu)
-    layer.w2_weight_scale_inv.data = torch.empty(0, dtype=torch.float32, device=gpu)
+    for name, dtype in (("w13_weight", FP8), ("w2_weight", FP8),
+                        ("w13_weight_scale_inv", torch.float32),
+                        ("w2_weight_scale_inv", torch.float32)):
+        getattr(layer, name).data = torch.empty(0, dtype=dtype, device=gpu)
     self.moe_quant_config = st.quant_config
-    scratch_gib = st._scratch.numel() / 2 ** 30
     logger.info("wisp.fp8: layer %d init num_experts=%d cap=%d gpu_scratch=%.2f GiB engine=%s",
-                st.layer_idx, E, cap, scratch_gib, st.pagein_engine)
+                st.layer_idx, E, st.cap_experts, st._scratch.numel() / 2 ** 30,
+                st.pagein_engine)
 
 
 # Arguments of vLLM's apply this path supports only at these values (the

@@ -29,7 +29,7 @@ WISP_ALGO_GEMV = 1
 WISP_ALGO_MFMA = 2
 WISP_PAGEIN_MEMCPY = 0
 WISP_PAGEIN_KERNEL = 1
-WISP_NOALLOC_SCRATCH_BYTES = 64 << 20
+WISP_NOALLOC_SCRATCH_BYTES = 64 << 20  # a default build's; the library's: noalloc_scratch_bytes()
 
 # Decision-record header words (wisp_amd/csrc/pager_core.h).
 REC_STATUS, REC_GROUPS_DONE, REC_GROUPS_PLANNED, REC_FAIL_GROUP, REC_FAIL_UNIQUE, \
@@ -54,6 +54,7 @@ class LayerDesc(C.Structure):
         ("scratch_s2", _vp), ("scratch_s2_stride", _sz),
         ("master_s13", _vp), ("master_s13_stride", _sz),
         ("master_s2", _vp), ("master_s2_stride", _sz),
+        ("struct_bytes", _sz),
     ]
 
 
@@ -69,6 +70,7 @@ class Workspace(C.Structure):
         ("max_pairs", C.c_int), ("topk_w", _vp), ("topk_ids", _vp), ("slots", _vp),
         ("flags", _vp), ("loads", _vp), ("act", _vp), ("record", _vp),
         ("record_words", C.c_int), ("record_dev", _vp), ("work", _vp), ("work_bytes", _sz),
+        ("struct_bytes", _sz),
     ]
 
 
@@ -89,6 +91,7 @@ SIGNATURES = {
     "wisp_moe_experts": (_i32, [_vp, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _i32, _vp, _sz,
                                 _vp, _sz, _vp, _vp, _vp, _sz, _i32, _vp]),
     "wisp_moe_work_bytes": (_sz, [_i32, _i32, _i32, _i32]),
+    "wisp_noalloc_scratch_bytes": (_sz, []),
     "wisp_moe_experts_noalloc": (_i32, [_vp, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _i32, _vp,
                                         _sz, _vp, _sz, _vp, _i32, _vp]),
     "wisp_moe_experts_fp8": (_i32, [_vp, _i32, _i32, _i32, _i32, _vp, _vp, _i32, _vp, _sz, _vp,

@@ -54,7 +54,7 @@ def hipcc() -> str:
 
 
 def _compile(src: Path, obj: Path) -> None:
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *HIPCC_FLAGS, *_size_flags(), "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{res.stderr}")
@@ -63,6 +63,19 @@ def _compile(src: Path, obj: Path) -> None:
                     and "target-feature" not in l and l.strip())
     if err:
         print(f"[wisp build] {src.name}:\n{err}", file=sys.stderr)
+
+
+def _size_flags() -> list[str]:
+    """``WISP_NOALLOC_SCRATCH_MIB`` (default 64): MiB of the static device
+    array of wisp_moe_experts_noalloc, which every process that loads the
+    library holds on each GPU it runs on."""
+    mib = os.environ.get("WISP_NOALLOC_SCRATCH_MIB")
+    if mib is None:
+        return []
+    n = int(mib)
+    if not 1 <= n <= 4096:
+        raise ValueError(f"WISP_NOALLOC_SCRATCH_MIB={mib} outside 1..4096")
+    return [f"-DWISP_NOALLOC_SCRATCH_BYTES=({n}ull<<20)"]
 
 
 def build(verbose: bool = True) -> Path:

@@ -54,7 +54,7 @@ void wisp_set_last_error(const char* what, const char* where) {
 }
 
 extern "C" const char* wisp_last_error(void) { return g_last_error.c_str(); }
-extern "C" int wisp_abi_version(void) { return 2; }
+extern "C" int wisp_abi_version(void) { return 3; }
 
 namespace wisp {
 
@@ -705,7 +705,16 @@ int32_t* record_device_ptr(int32_t* rec) {
   return rec;
 }
 
+// A workspace laid out as this library's (its trailing struct_bytes).
+bool ws_layout_ok(const wisp_workspace* ws, const char* where) {
+  if (ws && ws->struct_bytes == sizeof(wisp_workspace)) return true;
+  wisp_set_last_error("wisp_workspace.struct_bytes is not sizeof(wisp_workspace) of this "
+                      "library's header", where);
+  return false;
+}
+
 int check_ws(const wisp_workspace* ws, int T, int K) {
+  if (!ws_layout_ok(ws, "wisp_layer_forward")) return WISP_ERR_INVALID;
   if (!ws || (int64_t)T * K > ws->max_pairs || !ws->topk_w || !ws->topk_ids || !ws->slots ||
       !ws->flags || !ws->loads || !ws->act || !ws->record ||
       ws->record_words < RecordLayout(T, K).words()) {
@@ -759,6 +768,11 @@ static bool fp8_desc_ok(const wisp_layer_desc& d) {
 extern "C" int wisp_layer_create(const wisp_layer_desc* desc, void** handle) {
   using namespace wisp;
   if (!desc || !handle) return WISP_ERR_INVALID;
+  if (desc->struct_bytes != sizeof(wisp_layer_desc)) {
+    wisp_set_last_error("wisp_layer_desc.struct_bytes is not sizeof(wisp_layer_desc) of this "
+                        "library's header", "wisp_layer_create");
+    return WISP_ERR_INVALID;
+  }
   const wisp_layer_desc& d = *desc;
   if (d.num_experts < 1 || d.num_experts > kMaxExperts || d.cap < 1 || d.cap > kMaxExperts ||
       d.hidden < 0 || d.inter < 0 || d.w13_elems < 1 || d.w2_elems < 1 ||
@@ -1055,6 +1069,7 @@ extern "C" int wisp_layer_ensure_resident(void* handle, const int32_t* ids, int 
                                           const wisp_workspace* ws, wisp_stream_t stream) {
   using namespace wisp;
   Layer* L = (Layer*)handle;
+  if (!ws_layout_ok(ws, "wisp_layer_ensure_resident")) return WISP_ERR_INVALID;
   if (!L || n < 0 || (n > 0 && !ids) || !ws || !ws->record ||
       ws->record_words < RecordLayout(n, 1).words())
     return WISP_ERR_INVALID;
@@ -1169,6 +1184,7 @@ extern "C" int wisp_layer_prefetch(void* handle, const int32_t* predicted,
 extern "C" int wisp_layer_sync_record(void* handle, const wisp_workspace* ws) {
   using namespace wisp;
   Layer* L = (Layer*)handle;
+  if (!ws_layout_ok(ws, "wisp_layer_sync_record")) return WISP_ERR_INVALID;
   if (!L || !ws || !ws->record || ws->record_words < 8) return WISP_ERR_INVALID;
   WISP_HIP_TRY(hipDeviceSynchronize());
   if (L->rec_on_device) {

@@ -122,3 +122,5 @@ extern "C" int wisp_moe_experts_noalloc(const void* x, int dtype, int T, int H, 
   return experts_gemv(x, dtype, T, H, I, K, topk_w, slots, w13, w13_stride, w2, w2_stride, act,
                       out, st, nullptr);
 }
+
+extern "C" size_t wisp_noalloc_scratch_bytes(void) { return (size_t)WISP_NOALLOC_SCRATCH_BYTES; }
