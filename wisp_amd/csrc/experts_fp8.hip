@@ -475,16 +475,19 @@ __device__ inline void w13_one_block(const uint16_t* __restrict__ x, int H, int 
                                        (size_t)wave * KC * (4 + kKB));
   uint8_t* xq = reinterpret_cast<uint8_t*>(xs + KC);
 
-  // the first chunk's activation loads, ahead of everything else (a wave
-  // without k-blocks loads the last one and drops it)
+  // The first chunk's activation loads go out first, then its weight and
+  // scale loads, then (SLOTS) the slot table, with nothing that waits in
+  // between: loads complete in order, so the quantisation waits for x only,
+  // and the weights stream while it runs.  (Left to itself the compiler
+  // waited for x and the table before issuing any weight load, which held
+  // every block's weights back by that round trip.)  A wave without k-blocks
+  // loads the last one and drops it.
   const int kbx = min(kb0 + min(grp, max(min(KC, kb1 - kb0), 1) - 1), nkb - 1);
   u32x4 xv = *reinterpret_cast<const u32x4*>(x + (size_t)kbx * kKB + col * 8);
   int s, sl = -1, wd = -1;
   bool absent = false;  // this block's pair reads no expert: it stores zeros
   if (SLOTS) {
     s = by;
-    sl = load_first(slots + min(lane, K - 1));  // lane j < K: pair j's slot
-    if (words) wd = load_first(words + min(lane, K - 1));
   } else {
     if (words && pair_word_loaded(words[by]) >= 0) return;
     s = slots[by];
@@ -497,19 +500,32 @@ __device__ inline void w13_one_block(const uint16_t* __restrict__ x, int H, int 
   const uint8_t* row = W + (size_t)(col < 8 ? i0 + col : I + i0 + col - 8) * H + grp * 32;
   const float* Sw = s13 + (size_t)s * s13_stride +
                     (size_t)((grp < 2 ? i0 : I + i0) / block_n) * nkb;
+  i32x8 w[KC];
+  float sw[KC];
+  auto load_chunk = [&](int kc) {
+    const int nk = min(KC, kb1 - kc);
+#pragma unroll
+    for (int kbi = 0; kbi < KC; ++kbi) {
+      const int kb = min(kc + min(kbi, nk - 1), nkb - 1);
+      w[kbi] = ld32(row + (size_t)kb * kKB);
+      sw[kbi] = Sw[kb];
+    }
+  };
+  load_chunk(kb0);
+  if (SLOTS) {
+    sl = load_first(slots + min(lane, K - 1));  // lane j < K: pair j's slot
+    // unconditional (read from the slots when there are no words): a load
+    // under a branch made the compiler wait for every load before it
+    wd = load_first((words ? words : slots) + min(lane, K - 1));
+  }
+  __builtin_amdgcn_sched_barrier(0);
 
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   for (int kc = kb0; kc < kb1; kc += KC) {
     const int nk = min(KC, kb1 - kc);
-    if (kc != kb0)
+    if (kc != kb0) {
       xv = *reinterpret_cast<const u32x4*>(x + (size_t)(kc + min(grp, nk - 1)) * kKB + col * 8);
-    i32x8 w[KC];
-    float sw[KC];
-#pragma unroll
-    for (int kbi = 0; kbi < KC; ++kbi) {
-      const int kb = kc + min(kbi, nk - 1);
-      w[kbi] = ld32(row + (size_t)kb * kKB);
-      sw[kbi] = Sw[kb];
+      load_chunk(kc);
     }
     {
       float v[8];
@@ -998,12 +1014,17 @@ __global__ __launch_bounds__(1024) void fp8_w2_one_kernel(
   float* as = reinterpret_cast<float*>(smem + (size_t)K * I);
   float* part = as + (size_t)K * KB;
 
+  // Load order: pair `wave`'s act (quarter-wave g quantises k-blocks g and
+  // g + 4), then the tile's weights and scales, then (SLOTS) the slot table
+  // and routing weights, with nothing that waits in between: loads complete
+  // in order, so the quantisation waits for act only while the weights
+  // stream.  (Left to itself the compiler put the quantisation, and its wait
+  // for act, between the weight loads.)  Without SLOTS the tile's slot comes
+  // from the table, which is then loaded first.
   // lane j < K: pair j's slot and routing weight (a slot outside the
   // scratch contributes zero)
   const int jl = min(lane, K - 1);
-  int sj = load_first(slots + jl);
-  const float wj = __int_as_float(load_first((const int32_t*)topk_w + jl));
-  // pair `wave`'s act: quarter-wave g quantises k-blocks g and g + 4
+  int sj = SLOTS ? -1 : load_first(slots + jl);
   u32x4 av[2];
 #pragma unroll
   for (int it = 0; it < 2; ++it) {
@@ -1011,7 +1032,7 @@ __global__ __launch_bounds__(1024) void fp8_w2_one_kernel(
     av[it] = *reinterpret_cast<const u32x4*>(act + (size_t)wave * I + (size_t)kb * kKB + col * 8);
   }
   // the tile this wave streams: slot `wave`, or pair `wave`'s slot
-  if (sj >= nslots) sj = -1;
+  if (!SLOTS && sj >= nslots) sj = -1;
   const int s = SLOTS ? wave : __builtin_amdgcn_readlane(sj, wave);
   const int sl = s >= 0 ? s : 0;  // an absent pair reads slot 0 and drops it
   const uint8_t* row = w2 + (size_t)sl * w2_stride + (size_t)(h0 + col) * I + grp * 32;
@@ -1023,6 +1044,9 @@ __global__ __launch_bounds__(1024) void fp8_w2_one_kernel(
     a[kb] = ld32(row + (size_t)kb * kKB);
     sw[kb] = S[kb];
   }
+  if (SLOTS) sj = load_first(slots + jl);
+  const float wj = __int_as_float(load_first((const int32_t*)topk_w + jl));
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int it = 0; it < 2; ++it) {
     float v[8];
@@ -1037,6 +1061,8 @@ __global__ __launch_bounds__(1024) void fp8_w2_one_kernel(
     }
   }
   block_lds_sync();  // the tile's loads stay in flight
+  __builtin_amdgcn_sched_barrier(0);  // nothing that reads sj above the barrier
+  if (SLOTS && sj >= nslots) sj = -1;
   // the pair this wave's tile serves (-1: none)
   int p = wave;
   if (SLOTS) {
