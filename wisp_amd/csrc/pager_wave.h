@@ -113,6 +113,14 @@ __device__ __attribute__((always_inline)) inline void pager_wave(
   // and reaches LDS after routing, so its loads travel while the router loads
   // and ranks the logits instead of before them.
   const bool state_in_regs = regs || (logits && cap <= VALS * 64);
+  // The state's pointers are read with the first kernel arguments (an empty
+  // asm statement that takes them), not in a second round trip after the
+  // first branch.  The first token's logits go out before the layer state's
+  // loads, so both arrive in one memory round trip (the routing loop below
+  // otherwise waited for the state before loading them).
+  asm volatile("" ::"s"(map_g), "s"(s2e_g), "s"(tick_g), "s"(ctr_g));
+  float raw0[VALS];
+  if (logits && T > 0) route_load_logits<TL, VALS>(logits, E, lane, raw0);
   int map_r[VALS], s2e_r[VALS];
   int64_t tick_r[VALS];
   // Register path: loads at clamped positions, with no branch around them,
@@ -157,7 +165,10 @@ __device__ __attribute__((always_inline)) inline void pager_wave(
     for (int t = 0; t < T; ++t) {
       float w;
       int id;
-      route_token_wave<TL, VALS>(logits + (size_t)t * E, E, K, renorm, lane, true, &w, &id);
+      if (t == 0)
+        route_token_loaded<VALS>(raw0, E, K, renorm, lane, true, &w, &id);
+      else
+        route_token_wave<TL, VALS>(logits + (size_t)t * E, E, K, renorm, lane, true, &w, &id);
       if (lane < K) {
         fr.w[t * K + lane] = w;
         fr.ids[t * K + lane] = id;

@@ -77,18 +77,22 @@ __device__ inline int wave_min_i32(int v) {
 // and the lowest position j holding it).  A round takes the wave max of the
 // lane bests; the winner is the lowest id e = 64 j + lane among the lanes
 // holding that value, and only the winning lane rescans its entries.
+// This lane's logits of one row, at clamped positions (the row is valid
+// even for an inactive token), with no branch around the loads: a load under
+// a branch waited for everything before it, one logit at a time.
 template <typename TL, int VALS>
-__device__ inline void route_token_wave(const TL* __restrict__ logits_row, int E, int K,
-                                        int renorm, int lane, bool active, float* w_out,
-                                        int* id_out) {
-  (void)RouteVals<VALS>();
-  const int per = min((E + 63) >> 6, VALS);
-  // every lane loads all its logits at clamped positions (the row is valid
-  // even for an inactive token), with no branch around the loads: a load
-  // under a branch waited for everything before it, one logit at a time
-  float raw[VALS];
+__device__ inline void route_load_logits(const TL* __restrict__ logits_row, int E, int lane,
+                                         float (&raw)[VALS]) {
 #pragma unroll
   for (int j = 0; j < VALS; ++j) raw[j] = load_logit(logits_row + min(j * 64 + lane, E - 1));
+}
+
+// route_token_wave on logits already loaded by route_load_logits.
+template <int VALS>
+__device__ inline void route_token_loaded(const float (&raw)[VALS], int E, int K, int renorm,
+                                          int lane, bool active, float* w_out, int* id_out) {
+  (void)RouteVals<VALS>();
+  const int per = min((E + 63) >> 6, VALS);
   float v[VALS];
   uint32_t taken = 0;  // bit j: entry j of this lane is not eligible
 #pragma unroll
@@ -152,6 +156,15 @@ __device__ inline void route_token_wave(const TL* __restrict__ logits_row, int E
     *w_out = p;
     *id_out = my_id;
   }
+}
+
+template <typename TL, int VALS>
+__device__ inline void route_token_wave(const TL* __restrict__ logits_row, int E, int K,
+                                        int renorm, int lane, bool active, float* w_out,
+                                        int* id_out) {
+  float raw[VALS];
+  route_load_logits<TL, VALS>(logits_row, E, lane, raw);
+  route_token_loaded<VALS>(raw, E, K, renorm, lane, active, w_out, id_out);
 }
 
 }  // namespace wisp
