@@ -464,6 +464,11 @@ __global__ __launch_bounds__(1024) void w2_combine_kernel(const T* __restrict__ 
   constexpr int CHA = CH > 0 ? CH : 1;
   __shared__ float part[kMaxKw2][RPB];
   __shared__ float wk[kMaxKw2];
+  // every pointer with the first kernel arguments (an empty asm statement
+  // that takes them): the skip test below otherwise made the rest a second
+  // round trip
+  asm volatile("" ::"s"(act), "s"(topk_w), "s"(slots), "s"(w2), "s"(out), "s"(skip_if), "s"(H),
+               "s"(I), "s"(K), "s"(w2_stride), "s"(act_spec));
   if (skip_if && *skip_if != 0) return;
   const int k = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int sub = lane / LPR, l = lane % LPR;
