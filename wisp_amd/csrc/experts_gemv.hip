@@ -344,7 +344,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6))) void d
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   if (blockIdx.x == 0) {
     if (wave != 0) return;
-    pager_wave<TL, 2, true, 128, kMaxTopK>(
+    pager_wave<TL, 2, true, 128, kMaxTopK, true>(
         nullptr, (const TL*)pa.logits, pa.renorm, pa.topk_w, pa.topk_ids, 1, f.K, pa.E, f.cap, 0,
         pa.map, pa.s2e, pa.tick, pa.ctr, pa.slots, const_cast<int32_t*>(f.words) - 1, pa.loads,
         pa.rec, nullptr, sm, fr);

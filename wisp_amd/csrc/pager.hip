@@ -188,7 +188,7 @@ int pager_decide_host(PagerView st, const int32_t* ids, int T, int K, int single
 
 namespace {
 
-template <typename TL, int VALS, bool STAGED>
+template <typename TL, int VALS, bool STAGED, bool ONE>
 __global__ __launch_bounds__(64) void pager_kernel(
     const int32_t* __restrict__ ids_in, const TL* __restrict__ logits, int renorm,
     float* __restrict__ w_out, int32_t* __restrict__ id_out, int T, int K, int E, int cap,
@@ -198,7 +198,7 @@ __global__ __launch_bounds__(64) void pager_kernel(
     int32_t* __restrict__ rec_host) {
   __shared__ PagerSmemT<kMaxExperts> sm;
   __shared__ FusedRouteSmemT<kStagedPairs> fr;
-  pager_wave<TL, VALS, STAGED, kMaxExperts, kStagedPairs>(
+  pager_wave<TL, VALS, STAGED, kMaxExperts, kStagedPairs, ONE>(
       ids_in, logits, renorm, w_out, id_out, T, K, E, cap, single_group, map_g, s2e_g, tick_g,
       ctr_g, slots_g, flags_g, loads_g, rec, rec_host, sm, fr);
 }
@@ -214,7 +214,7 @@ int launch_pager(const int32_t* ids, const void* logits, int logits_dtype, int r
   if (T < 0 || K < 1 || K > kMaxTopK || E < 1 || E > kMaxExperts || cap < 1 || cap > kMaxExperts ||
       rec_words < L.words() || !map || !s2e || !tick || !ctr || !rec ||
       (T > 0 && !ids && !logits) ||
-      (logits && (T > kFusedRouteTokens || !topk_w || !topk_ids ||
+      (logits && (T > kFusedRouteTokens || K > E || !topk_w || !topk_ids ||
                   (logits_dtype != WISP_F32 && logits_dtype != WISP_BF16)))) {
     wisp_set_last_error("invalid pager arguments", "wisp_pager_decide");
     return WISP_ERR_INVALID;
@@ -229,22 +229,41 @@ int launch_pager(const int32_t* ids, const void* logits, int logits_dtype, int r
     rec = rec_host;
     rec_host = nullptr;
   }
+  // A one-token call routed here on the register path (E <= 128, cap <= 64)
+  // runs the instance compiled for exactly that case.
+  const bool one = logits && T == 1 && E <= 128 && cap <= 64;
   with_route_vals(E, [&](auto vals) {
     constexpr int V = decltype(vals)::value;
+    if constexpr (V == 2) {
+      if (one && logits_dtype == WISP_BF16) {
+        hipLaunchKernelGGL((pager_kernel<uint16_t, 2, true, true>), dim3(1), dim3(64), 0, stream,
+                           ids, (const uint16_t*)logits, renorm, topk_w, topk_ids, T, K, E, cap,
+                           single_group, map, s2e, tick, ctr, slots, flags, loads, rec,
+                           rec_host);
+        return;
+      }
+      if (one) {
+        hipLaunchKernelGGL((pager_kernel<float, 2, true, true>), dim3(1), dim3(64), 0, stream,
+                           ids, (const float*)logits, renorm, topk_w, topk_ids, T, K, E, cap,
+                           single_group, map, s2e, tick, ctr, slots, flags, loads, rec,
+                           rec_host);
+        return;
+      }
+    }
     if (logits && logits_dtype == WISP_BF16)
-      hipLaunchKernelGGL((pager_kernel<uint16_t, V, true>), dim3(1), dim3(64), 0, stream, ids,
-                         (const uint16_t*)logits, renorm, topk_w, topk_ids, T, K, E, cap,
+      hipLaunchKernelGGL((pager_kernel<uint16_t, V, true, false>), dim3(1), dim3(64), 0, stream,
+                         ids, (const uint16_t*)logits, renorm, topk_w, topk_ids, T, K, E, cap,
                          single_group, map, s2e, tick, ctr, slots, flags, loads, rec,
                          rec_host);
     else if (staged)
-      hipLaunchKernelGGL((pager_kernel<float, V, true>), dim3(1), dim3(64), 0, stream, ids,
-                         (const float*)logits, renorm, topk_w, topk_ids, T, K, E, cap,
+      hipLaunchKernelGGL((pager_kernel<float, V, true, false>), dim3(1), dim3(64), 0, stream,
+                         ids, (const float*)logits, renorm, topk_w, topk_ids, T, K, E, cap,
                          single_group, map, s2e, tick, ctr, slots, flags, loads, rec,
                          rec_host);
     else
-      hipLaunchKernelGGL((pager_kernel<float, V, false>), dim3(1), dim3(64), 0, stream, ids,
-                         nullptr, renorm, topk_w, topk_ids, T, K, E, cap, single_group, map, s2e,
-                         tick, ctr, slots, flags, loads, rec, rec_host);
+      hipLaunchKernelGGL((pager_kernel<float, V, false, false>), dim3(1), dim3(64), 0, stream,
+                         ids, nullptr, renorm, topk_w, topk_ids, T, K, E, cap, single_group, map,
+                         s2e, tick, ctr, slots, flags, loads, rec, rec_host);
   });
   WISP_HIP_TRY(hipGetLastError());
   return WISP_OK;

@@ -87,7 +87,10 @@ __device__ inline int set_table_size(int n) {
 // pager_wave is the kernel's body: wave 0 of its block runs it (the pager
 // kernel, or the pager wave of a fused one-token decode launch), with its
 // LDS given by the caller for at most MAXE experts and, staged, MAXP pairs.
-template <typename TL, int VALS, bool STAGED, int MAXE, int MAXP>
+// ONE (decided at launch): a one-token call routed here, on the register
+// path (E <= 128, cap <= 64) - the decode step's case, compiled without the
+// other paths, whose set-up and register pressure it would otherwise carry.
+template <typename TL, int VALS, bool STAGED, int MAXE, int MAXP, bool ONE = false>
 __device__ __attribute__((always_inline)) inline void pager_wave(
     const int32_t* __restrict__ ids_in, const TL* __restrict__ logits, int renorm,
     float* __restrict__ w_out, int32_t* __restrict__ id_out, int T, int K, int E, int cap,
@@ -95,6 +98,9 @@ __device__ __attribute__((always_inline)) inline void pager_wave(
     int64_t* __restrict__ tick_g, int64_t* __restrict__ ctr_g, int32_t* __restrict__ slots_g,
     int32_t* __restrict__ flags_g, int32_t* __restrict__ loads_g, int32_t* __restrict__ rec,
     int32_t* __restrict__ rec_host, PagerSmemT<MAXE>& sm, FusedRouteSmemT<MAXP>& fr) {
+  static_assert(!ONE || (VALS == 2 && STAGED), "a routed one-token call on the register path");
+  if constexpr (ONE) T = 1;
+  const bool routed = ONE || logits != nullptr;
   constexpr int W = 2 * VALS;  // 32-bit mask words per token: E <= 32 * W
   const int lane = threadIdx.x & 63;
   const int nwords = (E + 31) >> 5;
@@ -107,22 +113,22 @@ __device__ __attribute__((always_inline)) inline void pager_wave(
   // scalar registers, so a group's decisions are lane arithmetic, ballots and
   // lane permutes instead of chains of LDS round trips.
   constexpr bool kRegsPath = VALS <= 2;
-  const bool regs = kRegsPath && cap <= 64;
+  const bool regs = ONE || (kRegsPath && cap <= 64);
   // Otherwise, with the router fused (the launcher picks VALS * 64 >= E) and
   // cap within the same bound, the layer state is read into registers first
   // and reaches LDS after routing, so its loads travel while the router loads
   // and ranks the logits instead of before them.
-  const bool state_in_regs = regs || (logits && cap <= VALS * 64);
+  const bool state_in_regs = regs || (routed && cap <= VALS * 64);
   // The state's pointers are read with the first kernel arguments (an empty
   // asm statement that takes them), not in a second round trip after the
   // first branch.  The first token's logits go out before the layer state's
   // loads, so both arrive in one memory round trip (the routing loop below
   // otherwise waited for the state before loading them).
   asm volatile("" ::"s"(map_g), "s"(s2e_g), "s"(tick_g), "s"(ctr_g));
-  float raw0[VALS];
-  if (logits && T > 0) route_load_logits<TL, VALS>(logits, E, lane, raw0);
-  int map_r[VALS], s2e_r[VALS];
-  int64_t tick_r[VALS];
+  float raw0[VALS] = {};
+  if (routed && T > 0) route_load_logits<TL, VALS>(logits, E, lane, raw0);
+  int map_r[VALS] = {}, s2e_r[VALS] = {};
+  int64_t tick_r[VALS] = {};
   // Register path: loads at clamped positions, with no branch around them,
   // masked (mask_state) only after the router has issued its logit loads, so
   // that both travel together.
@@ -155,26 +161,51 @@ __device__ __attribute__((always_inline)) inline void pager_wave(
   int64_t clock = ctr_g[kClock];
   int64_t n_forward = ctr_g[kForward], n_miss = ctr_g[kMiss], n_evict = ctr_g[kEvict],
           n_hits = ctr_g[kHits];
+  // Takes every value loaded above, on each path before the first global
+  // store.  The compiler tracks pending loads per path without knowing which
+  // paths run together, and one memory counter covers loads and stores: a
+  // load it still counts as pending at a later join (the logits of a call
+  // with no tokens, the state of a call that keeps it in LDS) would make it
+  // wait there for the whole counter, this call's output stores included.
+  auto take_loads = [&]() {
+#pragma unroll
+    for (int v = 0; v < VALS; ++v)
+      asm volatile("" ::"v"(raw0[v]), "v"(map_r[v]), "v"(s2e_r[v]), "v"(tick_r[v]));
+    asm volatile("" ::"v"(clock), "v"(n_forward), "v"(n_miss), "v"(n_evict), "v"(n_hits));
+  };
   // Routed ids: staged in LDS when the call has at most kStagedPairs pairs
   // or was routed here (STAGED), else read from global memory.
   auto id_at = [&](int p) -> int {
     if constexpr (STAGED) return fr.ids[p];
     else return ids_in[p];
   };
-  if (logits) {
+  // A routed call: the union of the chosen experts (bit v: expert
+  // 64 v + lane), and token 0's (weight, id) of routing position `lane`.
+  uint32_t picked_all = 0u;
+  float w0 = 0.f;
+  int id0 = -1;
+  if (routed) {
     for (int t = 0; t < T; ++t) {
       float w;
       int id;
+      uint32_t pk;
       if (t == 0)
-        route_token_loaded<VALS>(raw0, E, K, renorm, lane, true, &w, &id);
+        route_token_loaded<VALS>(raw0, E, K, renorm, lane, true, &w, &id, &pk);
       else
-        route_token_wave<TL, VALS>(logits + (size_t)t * E, E, K, renorm, lane, true, &w, &id);
+        route_token_wave<TL, VALS>(logits + (size_t)t * E, E, K, renorm, lane, true, &w, &id,
+                                   &pk);
+      picked_all |= pk;
+      if (t == 0) {
+        w0 = w;
+        id0 = id;
+      }
       if (lane < K) {
         fr.w[t * K + lane] = w;
         fr.ids[t * K + lane] = id;
       }
     }
     if (state_in_regs) mask_state();
+    take_loads();
     if (state_in_regs && !regs) {
 #pragma unroll
       for (int v = 0; v < VALS; ++v) {
@@ -186,10 +217,14 @@ __device__ __attribute__((always_inline)) inline void pager_wave(
         }
       }
     }
-    wave_lds_sync();
     // The first global stores come only now: a wait for the state's loads
-    // above would otherwise also wait for them.
-    for (int p = lane; p < P; p += 64) {
+    // above would otherwise also wait for them.  Token 0's from registers.
+    if (lane < K) {
+      w_out[lane] = w0;
+      id_out[lane] = id0;
+    }
+    wave_lds_sync();
+    for (int p = K + lane; p < P; p += 64) {
       w_out[p] = fr.w[p];
       id_out[p] = fr.ids[p];
     }
@@ -212,7 +247,10 @@ __device__ __attribute__((always_inline)) inline void pager_wave(
     }
     wave_lds_sync();
   }
-  if (!logits && state_in_regs) mask_state();
+  if (!routed) {
+    if (state_in_regs) mask_state();
+    take_loads();
+  }
   // Every pair starts as "not computed" (slot -1, not loaded); the same lane
   // owns pair p for all later writes.
   for (int p = lane; p < P; p += 64) {
@@ -220,9 +258,10 @@ __device__ __attribute__((always_inline)) inline void pager_wave(
     if (flags_g) flags_g[1 + p] = pair_word(-1, -1);
   }
 
-  // Validate ids.
+  // Validate ids (a routed call's ids are in range: K <= E).
   bool bad = false;
-  for (int p = lane; p < P; p += 64) bad |= (id_at(p) < 0 || id_at(p) >= E);
+  if (!routed)
+    for (int p = lane; p < P; p += 64) bad |= (id_at(p) < 0 || id_at(p) >= E);
   const bool any_bad = ballot(bad) != 0;
   // the planner's masks hold E <= 32 * W experts
   const bool masks_ok = E <= 32 * W;
@@ -323,7 +362,26 @@ __device__ __attribute__((always_inline)) inline void pager_wave(
       // ---- plan one group: tokens [start, end) -----------------------
       int end = start;
       uint32_t u[W];  // the group's needed experts (wave-uniform)
-      if (regs && (single_group || T == 1) && P <= 64) {
+      if (routed && (single_group || T == 1)) {
+        // a routed call's one group: the router's choices, by ballot
+#pragma unroll
+        for (int v = 0; v < VALS; ++v) {
+          const uint64_t b = ballot((picked_all >> v) & 1u);
+          u[2 * v] = (uint32_t)b;
+          u[2 * v + 1] = (uint32_t)(b >> 32);
+        }
+        end = T;
+        if (!regs && lane == 0) {
+          // (from one lane at constant places: a word picked by lane index
+          // made the words a private-memory array)
+#pragma unroll
+          for (int w = 0; w < W; ++w)
+            if (w < nwords) {
+              sm.need[w] = u[w];
+              sm.loaded[w] = 0u;
+            }
+        }
+      } else if (regs && (single_group || T == 1) && P <= 64) {
         // one pair per lane: the needed set by wave ORs of the pairs' bits
         const int e = lane < P ? id_at(lane) : -1;
 #pragma unroll
@@ -414,10 +472,10 @@ __device__ __attribute__((always_inline)) inline void pager_wave(
         }
         // (the register path keeps the needed set in u and the loaded
         // experts in ballots)
-        if (!regs) {
+        if (!regs && lane == 0) {
 #pragma unroll
           for (int w = 0; w < W; ++w)
-            if (lane == w && w < nwords) {
+            if (w < nwords) {
               sm.need[w] = u[w];
               sm.loaded[w] = 0u;
             }
@@ -430,11 +488,13 @@ __device__ __attribute__((always_inline)) inline void pager_wave(
 
       if (regs) {
         // need bit of expert e (0 <= e < E) from the scalar mask words
+        // (E <= 128 here, so the mask is words 0-3; two 64-bit halves and
+        // one select, where a select over the words by index became a
+        // private-memory array and a load)
         auto need_of = [&](int e) -> bool {
-          uint32_t w = u[0];
-#pragma unroll
-          for (int k = 1; k < W; ++k) w = (e >> 5) == k ? u[k] : w;
-          return (w >> (e & 31)) & 1u;
+          const uint64_t lo = ((uint64_t)u[1] << 32) | u[0];
+          const uint64_t hi = ((uint64_t)u[3] << 32) | u[2];
+          return (((e >> 6) ? hi : lo) >> (e & 63)) & 1ull;
         };
         // ---- needed and missing experts, ascending ----------------------
         uint64_t mb[VALS];
@@ -442,8 +502,8 @@ __device__ __attribute__((always_inline)) inline void pager_wave(
 #pragma unroll
         for (int v = 0; v < VALS; ++v) {
           const int e = v * 64 + lane;
-          const uint32_t needw = lane < 32 ? u[2 * v] : u[2 * v + 1];
-          const bool in = e < E && ((needw >> (lane & 31)) & 1u);
+          const uint64_t needw = ((uint64_t)u[2 * v + 1] << 32) | u[2 * v];
+          const bool in = e < E && ((needw >> lane) & 1ull);
           const bool miss = in && map_r[v] < 0;
           const uint64_t bb = ballot(in);
           mb[v] = ballot(miss);
@@ -612,7 +672,8 @@ __device__ __attribute__((always_inline)) inline void pager_wave(
         for (int base = t0 * K; base < t1 * K; base += 64) {
           const int p = base + lane;
           const bool valid = p < t1 * K;
-          const int e = valid ? id_at(p) : 0;
+          // (a routed one-token call's ids are token 0's, in registers)
+          const int e = !valid ? 0 : routed && T == 1 ? id0 : id_at(p);
           const int src = e & 63;
           int sl = __shfl(map_r[0], src);
           if (VALS > 1) {

@@ -5,12 +5,15 @@
 // logits j*64 + lane), top-k by logit (descending, ties to the lower id),
 // optional renormalisation over the k selected.  NaN logits rank as -inf.
 //
-// Reductions stay in registers: four DPP steps inside each 16-lane row
-// (xor 1, xor 2, half-mirror, mirror - after each step both partners hold
-// the same bits, since IEEE add and max are commutative), then the four row
-// results are combined with readlane in a fixed order.  The result is
-// deterministic and identical in every lane.  The softmax maximum is the
-// first top-k value, so the denominator pass follows the top-k rounds.
+// Top-k ranks 64-bit keys: an order-preserving image of the logit above the
+// complement of the expert id, so keys are distinct and the largest key is
+// the largest logit with the lowest id among equals.  A round takes the
+// wave maximum in two 32-bit passes (the high words, then the low words of
+// the lanes holding the maximal high word), each with the result in every
+// lane: DPP inside each 16-lane row, then the gfx950 row-pair and half-wave
+// swaps (v_permlane16_swap / v_permlane32_swap), so a round has no hand-off
+// through scalar registers and no branch.  The softmax sums combine row
+// totals with readlane in a fixed order, so the weights are deterministic.
 #pragma once
 
 #include <math.h>
@@ -49,34 +52,36 @@ __device__ inline float load_logit<uint16_t>(const uint16_t* p) {
   return __uint_as_float((uint32_t)(*p) << 16);
 }
 
-// Max over the 64 lanes, same bits in every lane.
-__device__ inline float wave_max_f32(float v) {
-  v = fmaxf(v, dpp_f32<0xB1>(v));
-  v = fmaxf(v, dpp_f32<0x4E>(v));
-  v = fmaxf(v, dpp_f32<0x141>(v));
-  v = fmaxf(v, dpp_f32<0x140>(v));
-  return fmaxf(fmaxf(readlane_f32(v, 0), readlane_f32(v, 16)),
-               fmaxf(readlane_f32(v, 32), readlane_f32(v, 48)));
+// Order-preserving image of a non-NaN float: unsigned comparison of images
+// is float comparison, with -0 ranked as +0.  Every image is above 0, which
+// marks an entry that cannot be chosen.
+__device__ inline uint32_t rank_bits(float x) {
+  const uint32_t u = __float_as_uint(x == 0.f ? 0.f : x);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// Minimum over the 64 lanes (same value in every lane).
-__device__ inline int wave_min_i32(int v) {
-  v = min(v, __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false));
-  v = min(v, __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false));
-  v = min(v, __builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, false));
-  v = min(v, __builtin_amdgcn_mov_dpp(v, 0x140, 0xF, 0xF, false));
-  return min(min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
-             min(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+// The float whose image rank_bits is r (r != 0).
+__device__ inline float unrank_bits(uint32_t r) {
+  return __uint_as_float((r & 0x80000000u) ? (r & 0x7fffffffu) : ~r);
 }
 
-// Routes one token.  Lanes < K return (weight, id) of routing position
-// `lane`; other lanes return (0, -1).  Needs no shared memory; all lanes of
-// the wave must call it.
-//
-// Top-k: each lane keeps the best of its own not-yet-taken entries (value
-// and the lowest position j holding it).  A round takes the wave max of the
-// lane bests; the winner is the lowest id e = 64 j + lane among the lanes
-// holding that value, and only the winning lane rescans its entries.
+// Unsigned max over the 64 lanes, in every lane: xor 1, xor 2, half-row
+// mirror and row mirror by DPP, then the row pairs and the two halves
+// exchanged by the gfx950 lane swaps.  All 64 lanes must be active.
+__device__ inline uint32_t wave_max_u32_all(uint32_t v) {
+  // (0 is max's identity, so each step folds into one v_max_u32 with DPP)
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));
+  // lane i of rows 0/1 (and 2/3) meet: row 2r of the first result and row
+  // 2r + 1 of the second hold this lane's partner, the others itself
+  const auto r16 = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  v = max((uint32_t)r16[0], (uint32_t)r16[1]);
+  const auto r32 = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return max((uint32_t)r32[0], (uint32_t)r32[1]);
+}
+
 // This lane's logits of one row, at clamped positions (the row is valid
 // even for an inactive token), with no branch around the loads: a load under
 // a branch waited for everything before it, one logit at a time.
@@ -87,64 +92,56 @@ __device__ inline void route_load_logits(const TL* __restrict__ logits_row, int 
   for (int j = 0; j < VALS; ++j) raw[j] = load_logit(logits_row + min(j * 64 + lane, E - 1));
 }
 
-// route_token_wave on logits already loaded by route_load_logits.
+// route_token_wave on logits already loaded by route_load_logits.  Lanes < K
+// return (weight, id) of routing position `lane`; other lanes return
+// (0, -1).  `picked` (optional): bit j is set in lane l when expert 64 j + l
+// was chosen.  Needs no shared memory; all lanes of the wave must call it,
+// with K <= E (every round then chooses an eligible entry).
 template <int VALS>
 __device__ inline void route_token_loaded(const float (&raw)[VALS], int E, int K, int renorm,
-                                          int lane, bool active, float* w_out, int* id_out) {
+                                          int lane, bool active, float* w_out, int* id_out,
+                                          uint32_t* picked = nullptr) {
   (void)RouteVals<VALS>();
   const int per = min((E + 63) >> 6, VALS);
   float v[VALS];
-  uint32_t taken = 0;  // bit j: entry j of this lane is not eligible
+  uint64_t key[VALS];  // 0: not eligible
 #pragma unroll
   for (int j = 0; j < VALS; ++j) {
     const bool ok = active && j < per && j * 64 + lane < E;
     const float x = raw[j];
     v[j] = ok && x == x ? x : -INFINITY;
-    if (!ok) taken |= 1u << j;
+    key[j] = ok ? ((uint64_t)rank_bits(v[j]) << 32) | (uint32_t)~(uint32_t)(j * 64 + lane) : 0ull;
   }
   *w_out = 0.f;
   *id_out = -1;
+  if (picked) *picked = 0u;
   if (!active) return;
 
-  // best eligible entry of this lane: value lb at position lbj (-1: none)
-  float lb = -INFINITY;
-  int lbj = -1;
-  auto rescan = [&]() {
-    lb = -INFINITY;
-    lbj = -1;
+  uint64_t lb = key[0];  // this lane's best remaining key
 #pragma unroll
-    for (int j = VALS - 1; j >= 0; --j)
-      if (!(taken & (1u << j)) && (lbj < 0 || v[j] >= lb)) {
-        lb = v[j];
-        lbj = j;
-      }
-  };
-  rescan();
-
-  float m = 0.f;
-  int my_id = -1;
-  float my_v = 0.f;
+  for (int j = 1; j < VALS; ++j) lb = key[j] > lb ? key[j] : lb;
+  uint32_t first = 0, my_hi = 0, my_lo = 0, sel = 0;
   for (int r = 0; r < K; ++r) {
-    const float bm = wave_max_f32(lbj >= 0 ? lb : -INFINITY);
-    if (r == 0) m = bm;
-    const bool cand = lbj >= 0 && lb == bm;
-    const uint64_t cb = __ballot(cand);
-    int e;
-    if (__popcll(cb) == 1) {
-      const int wl = __builtin_ctzll(cb);
-      e = __builtin_amdgcn_readlane(lbj, wl) * 64 + wl;
-    } else {
-      e = wave_min_i32(cand ? lbj * 64 + lane : 0x7fffffff);
-    }
-    if (lane == (e & 63)) {
-      taken |= 1u << (e >> 6);
-      rescan();
+    const uint32_t bh = (uint32_t)(lb >> 32);
+    const uint32_t mh = wave_max_u32_all(bh);
+    const uint32_t ml = wave_max_u32_all(bh == mh ? (uint32_t)lb : 0u);
+    if (r == 0) first = mh;
+    // the chosen entry leaves (its low word, an id's complement, is unique)
+    lb = 0ull;
+#pragma unroll
+    for (int j = 0; j < VALS; ++j) {
+      const bool hit = (uint32_t)key[j] == ml;
+      key[j] = hit ? 0ull : key[j];
+      sel |= hit ? 1u << j : 0u;
+      lb = key[j] > lb ? key[j] : lb;
     }
     if (lane == r) {
-      my_id = e;
-      my_v = bm;
+      my_hi = mh;
+      my_lo = ml;
     }
   }
+  const float m = unrank_bits(first);
+  const float my_v = lane < K ? unrank_bits(my_hi) : 0.f;
   float ls = 0.f;
 #pragma unroll
   for (int j = 0; j < VALS; ++j)
@@ -154,17 +151,18 @@ __device__ inline void route_token_loaded(const float (&raw)[VALS], int E, int K
   if (renorm) p = p / wave_sum_f32(p);
   if (lane < K) {
     *w_out = p;
-    *id_out = my_id;
+    *id_out = (int)~my_lo;
   }
+  if (picked) *picked = sel;
 }
 
 template <typename TL, int VALS>
 __device__ inline void route_token_wave(const TL* __restrict__ logits_row, int E, int K,
                                         int renorm, int lane, bool active, float* w_out,
-                                        int* id_out) {
+                                        int* id_out, uint32_t* picked = nullptr) {
   float raw[VALS];
   route_load_logits<TL, VALS>(logits_row, E, lane, raw);
-  route_token_loaded<VALS>(raw, E, K, renorm, lane, active, w_out, id_out);
+  route_token_loaded<VALS>(raw, E, K, renorm, lane, active, w_out, id_out, picked);
 }
 
 }  // namespace wisp
