@@ -43,6 +43,7 @@ template <int MAXP>
 struct FusedRouteSmemT {
   int32_t ids[MAXP];
   float w[kFusedRouteTokens * kMaxTopK];  // routing weights of a routed call
+  RoutePos pos;                           // the router's positions, per token
 };
 
 // Size of the table of a CPython set of n small ints built by insertion: 8
@@ -190,10 +191,10 @@ __device__ __attribute__((always_inline)) inline void pager_wave(
       int id;
       uint32_t pk;
       if (t == 0)
-        route_token_loaded<VALS>(raw0, E, K, renorm, lane, true, &w, &id, &pk);
+        route_token_loaded<VALS>(raw0, E, K, renorm, lane, true, &w, &id, fr.pos, &pk);
       else
         route_token_wave<TL, VALS>(logits + (size_t)t * E, E, K, renorm, lane, true, &w, &id,
-                                   &pk);
+                                   fr.pos, &pk);
       picked_all |= pk;
       if (t == 0) {
         w0 = w;

@@ -18,6 +18,7 @@ __global__ __launch_bounds__(256) void route_kernel(const TL* __restrict__ logit
                                                      int K, int renorm, float* __restrict__ w_out,
                                                      int32_t* __restrict__ id_out,
                                                      int64_t* __restrict__ forward_counter) {
+  __shared__ RoutePos pos[4];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   if (forward_counter && blockIdx.x == 0 && threadIdx.x == 0) forward_counter[0] += 1;
   const int t = blockIdx.x * 4 + wave;
@@ -25,7 +26,7 @@ __global__ __launch_bounds__(256) void route_kernel(const TL* __restrict__ logit
   float w;
   int id;
   route_token_wave<TL, VALS>(logits + (size_t)(active ? t : 0) * E, E, K, renorm, lane, active,
-                             &w, &id);
+                             &w, &id, pos[wave]);
   if (active && lane < K) {
     w_out[(size_t)t * K + lane] = w;
     id_out[(size_t)t * K + lane] = id;

@@ -7,13 +7,15 @@
 //
 // Top-k ranks 64-bit keys: an order-preserving image of the logit above the
 // complement of the expert id, so keys are distinct and the largest key is
-// the largest logit with the lowest id among equals.  A round takes the
-// wave maximum in two 32-bit passes (the high words, then the low words of
-// the lanes holding the maximal high word), each with the result in every
-// lane: DPP inside each 16-lane row, then the gfx950 row-pair and half-wave
-// swaps (v_permlane16_swap / v_permlane32_swap), so a round has no hand-off
-// through scalar registers and no branch.  The softmax sums combine row
-// totals with readlane in a fixed order, so the weights are deterministic.
+// the largest logit with the lowest id among equals.  A round takes the wave
+// maximum of the lanes' best images with the result in every lane (DPP
+// inside each 16-lane row, then the gfx950 row-pair and half-wave swaps,
+// v_permlane16_swap / v_permlane32_swap); the one lane holding it takes its
+// best entry.  Only when several lanes hold that image (equal logits) does a
+// second maximum, over their keys' low words, pick the lowest id.  Each lane
+// notes the round of the entries it gave, and writes them by routing
+// position to LDS once at the end.  The softmax sums combine row totals
+// with readlane in a fixed order, so the weights are deterministic.
 #pragma once
 
 #include <math.h>
@@ -65,6 +67,12 @@ __device__ inline float unrank_bits(uint32_t r) {
   return __uint_as_float((r & 0x80000000u) ? (r & 0x7fffffffu) : ~r);
 }
 
+// One wave's chosen entries by routing position.
+struct RoutePos {
+  int32_t id[kMaxTopK];
+  float v[kMaxTopK];
+};
+
 // Unsigned max over the 64 lanes, in every lane: xor 1, xor 2, half-row
 // mirror and row mirror by DPP, then the row pairs and the two halves
 // exchanged by the gfx950 lane swaps.  All 64 lanes must be active.
@@ -95,12 +103,12 @@ __device__ inline void route_load_logits(const TL* __restrict__ logits_row, int 
 // route_token_wave on logits already loaded by route_load_logits.  Lanes < K
 // return (weight, id) of routing position `lane`; other lanes return
 // (0, -1).  `picked` (optional): bit j is set in lane l when expert 64 j + l
-// was chosen.  Needs no shared memory; all lanes of the wave must call it,
+// was chosen.  `pos`: this wave's LDS.  All lanes of the wave must call it,
 // with K <= E (every round then chooses an eligible entry).
 template <int VALS>
 __device__ inline void route_token_loaded(const float (&raw)[VALS], int E, int K, int renorm,
                                           int lane, bool active, float* w_out, int* id_out,
-                                          uint32_t* picked = nullptr) {
+                                          RoutePos& pos, uint32_t* picked = nullptr) {
   (void)RouteVals<VALS>();
   const int per = min((E + 63) >> 6, VALS);
   float v[VALS];
@@ -120,28 +128,44 @@ __device__ inline void route_token_loaded(const float (&raw)[VALS], int E, int K
   uint64_t lb = key[0];  // this lane's best remaining key
 #pragma unroll
   for (int j = 1; j < VALS; ++j) lb = key[j] > lb ? key[j] : lb;
-  uint32_t first = 0, my_hi = 0, my_lo = 0, sel = 0;
+  uint32_t first = 0, sel = 0;
+  int rnd[VALS];  // the round entry j was chosen in (bit j of sel set)
+#pragma unroll
+  for (int j = 0; j < VALS; ++j) rnd[j] = 0;
   for (int r = 0; r < K; ++r) {
     const uint32_t bh = (uint32_t)(lb >> 32);
     const uint32_t mh = wave_max_u32_all(bh);
-    const uint32_t ml = wave_max_u32_all(bh == mh ? (uint32_t)lb : 0u);
     if (r == 0) first = mh;
-    // the chosen entry leaves (its low word, an id's complement, is unique)
+    bool mine = bh == mh;  // this lane's best entry is the round's choice
+    if (__popcll(__ballot(mine)) != 1) {
+      // equal logits in several lanes: the lowest id (largest low word)
+      const uint32_t ml = wave_max_u32_all(mine ? (uint32_t)lb : 0u);
+      mine = mine && (uint32_t)lb == ml;
+    }
+    // (in the choosing lane the low words tell its entries apart, and an
+    // entry leaves by losing its high word: it then ranks below every
+    // eligible key)
+    const uint32_t taken = (uint32_t)lb;
     lb = 0ull;
 #pragma unroll
     for (int j = 0; j < VALS; ++j) {
-      const bool hit = (uint32_t)key[j] == ml;
-      key[j] = hit ? 0ull : key[j];
+      const bool hit = mine && (uint32_t)key[j] == taken;
+      key[j] = hit ? (uint64_t)(uint32_t)key[j] : key[j];
       sel |= hit ? 1u << j : 0u;
+      rnd[j] = hit ? r : rnd[j];
       lb = key[j] > lb ? key[j] : lb;
     }
-    if (lane == r) {
-      my_hi = mh;
-      my_lo = ml;
-    }
   }
+#pragma unroll
+  for (int j = 0; j < VALS; ++j)
+    if ((sel >> j) & 1u) {
+      pos.id[rnd[j]] = j * 64 + lane;
+      pos.v[rnd[j]] = v[j];
+    }
+  wave_lds_sync();
   const float m = unrank_bits(first);
-  const float my_v = lane < K ? unrank_bits(my_hi) : 0.f;
+  const int my_id = lane < K ? pos.id[lane] : -1;
+  const float my_v = lane < K ? pos.v[lane] : 0.f;
   float ls = 0.f;
 #pragma unroll
   for (int j = 0; j < VALS; ++j)
@@ -151,7 +175,7 @@ __device__ inline void route_token_loaded(const float (&raw)[VALS], int E, int K
   if (renorm) p = p / wave_sum_f32(p);
   if (lane < K) {
     *w_out = p;
-    *id_out = (int)~my_lo;
+    *id_out = my_id;
   }
   if (picked) *picked = sel;
 }
@@ -159,10 +183,11 @@ __device__ inline void route_token_loaded(const float (&raw)[VALS], int E, int K
 template <typename TL, int VALS>
 __device__ inline void route_token_wave(const TL* __restrict__ logits_row, int E, int K,
                                         int renorm, int lane, bool active, float* w_out,
-                                        int* id_out, uint32_t* picked = nullptr) {
+                                        int* id_out, RoutePos& pos,
+                                        uint32_t* picked = nullptr) {
   float raw[VALS];
   route_load_logits<TL, VALS>(logits_row, E, lane, raw);
-  route_token_loaded<VALS>(raw, E, K, renorm, lane, active, w_out, id_out, picked);
+  route_token_loaded<VALS>(raw, E, K, renorm, lane, active, w_out, id_out, pos, picked);
 }
 
 }  // namespace wisp
