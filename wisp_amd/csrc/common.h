@@ -47,6 +47,17 @@ __device__ inline void wave_lds_sync() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
+// A wave-uniform word through the scalar data cache, for memory that no
+// kernel writes while this one runs.  Where the compiler cannot prove that
+// (a kernel that also stores through other pointers) it reads such a word
+// with a vector load and a readfirstlane, a vector memory round trip that a
+// weight stream then queues behind.
+__device__ inline int32_t scalar_word(const int32_t* p) {
+  int32_t v;
+  asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p) : "memory");
+  return v;
+}
+
 // v of the lane that DPP control kCtrl names (all rows and banks enabled).
 template <int kCtrl>
 __device__ inline float dpp_f32(float v) {

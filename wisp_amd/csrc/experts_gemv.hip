@@ -300,7 +300,7 @@ __global__ __launch_bounds__(256) void pagein_w13_kernel(FusedW13Args f, PageInA
     const int pair = local / nbx;
     const int i = (local - pair * nbx) * 4 + wave;
     if (i >= I) return;
-    const int32_t word = f.words[pair];
+    const int32_t word = scalar_word(f.words + pair);
     if (pair_word_loaded(word) >= 0) return;  // the copy blocks compute it
     const int s = pair_word_slot(word);
     w13_wave<T, CH, FULL>((const T*)f.x, f.H, I, f.K, pair, i, s < f.cap ? s : -1,
