@@ -50,6 +50,33 @@ def test_route_matches_oracle(E, K, dtype):
     assert np.allclose(w2.numpy(), w2_ref, rtol=2e-6, atol=1e-7)
 
 
+def tie_logits(rng, T, E, K):
+    """Router logits full of exact ties: values from a small set that holds
+    both zeros (-0.0 ranks as +0.0), with some -inf entries, at least K finite
+    per row (exact in float32 and bfloat16)."""
+    vals = np.array([-2.0, -1.0, -0.0, 0.0, 1.0, 2.0, 3.0], dtype=np.float32)
+    lg = rng.choice(vals, size=(T, E)).astype(np.float32)
+    for t in range(T):
+        n_inf = int(rng.integers(0, max(1, E - K)))
+        lg[t, rng.choice(E, n_inf, replace=False)] = -np.inf
+    return torch.from_numpy(lg)
+
+
+@pytest.mark.parametrize("E,K", [(8, 2), (60, 4), (128, 8), (256, 8), (512, 16)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_route_ties_match_oracle(E, K, dtype):
+    """Equal logits in several lanes (the router's second maximum over the
+    ids' complements) and in one lane (its best of two), -0.0 against +0.0
+    and -inf entries: ids exact (value descending, lower id first), weights
+    within float32 rounding of the float64 oracle."""
+    rng = np.random.default_rng(E * 13 + K)
+    logits = tie_logits(rng, 64, E, K).to(dtype)
+    w, ids = gpu_route(logits, K)
+    w_ref, ids_ref = route(logits.float(), K)
+    assert ids.numpy().tolist() == ids_ref.tolist()
+    assert np.allclose(w.numpy(), w_ref, rtol=2e-6, atol=1e-7)
+
+
 class DevPager:
     def __init__(self, E, cap):
         self.E, self.cap = E, cap

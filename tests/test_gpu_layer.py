@@ -306,6 +306,20 @@ def test_wide_expert_counts_with_fused_routing(monkeypatch, E, T):
     drive(wl, 48, wl.steps, tol=1e-2)
 
 
+@pytest.mark.parametrize("E,T", [(128, 1), (128, 8), (512, 1), (512, 4)])
+def test_fused_routing_with_tied_logits(monkeypatch, E, T):
+    """Routing fused into the pager (the one-token register-path instance at
+    E = 128, T = 1; the general instances otherwise) on logits full of exact
+    ties, -0.0 and -inf: ids and decisions bit-exact with the oracle, paged
+    bytes equal resident bytes."""
+    from tests.test_gpu_kernels import tie_logits
+    monkeypatch.setitem(W.SHAPES, "ties", W.LayerShape(256, 128, E, 8, 8 * T, torch.bfloat16))
+    wl = W.gaussian_logits("ties", seed=E + T, steps=12, tokens=T, pin=True)
+    rng = np.random.default_rng(E * 5 + T)
+    wl.logits = torch.stack([tie_logits(rng, T, E, 8) for _ in range(wl.steps)])
+    drive(wl, 8 * T, wl.steps, tol=1e-2)
+
+
 @pytest.mark.parametrize("T", [1, 3])
 def test_top_k_above_the_gemv_limit_takes_the_mfma_path(monkeypatch, T):
     """20 routed experts per token (the decode GEMV pair handles up to 16):

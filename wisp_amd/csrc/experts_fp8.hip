@@ -489,8 +489,8 @@ __device__ inline void w13_one_block(const uint16_t* __restrict__ x, int H, int 
   if (SLOTS) {
     s = by;
   } else {
-    if (words && pair_word_loaded(words[by]) >= 0) return;
-    s = slots[by];
+    if (words && pair_word_loaded(scalar_word(words + by)) >= 0) return;
+    s = scalar_word(slots + by);
     absent = s < 0 || s >= nslots;
     if (absent) s = 0;  // loads from slot 0, dropped (no branch around them)
   }
