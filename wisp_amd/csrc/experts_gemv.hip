@@ -415,19 +415,24 @@ __device__ inline void w2_load_rows(const T* __restrict__ wbase, int h0, int H, 
   }
 }
 
-// This lane's part of the RPH dot products of the rows in wv with one act
-// row: the FMA chain over its chunks in order.
-template <typename T, int LPR, int CH, int RPH, bool FULL>
-__device__ inline void w2_dots(const uint4 (&wv)[RPH][CH], const T* __restrict__ arow, int I,
-                               int l, float (&d)[RPH]) {
+// This lane's CH act chunks of one act row (chunks past the row read 0).
+template <typename T, int LPR, int CH, bool FULL>
+__device__ inline void w2_load_act(const T* __restrict__ arow, int I, int l, uint4 (&av)[CH]) {
   constexpr int V = Vec<T>::N;
   const int nch = I / V;
-  uint4 av[CH];
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     const int ch = c * LPR + l;
     av[c] = (FULL || ch < nch) ? ld16(arow + (size_t)ch * V) : make_uint4(0, 0, 0, 0);
   }
+}
+
+// This lane's part of the RPH dot products of the rows in wv with the act
+// chunks in av: the FMA chain over its chunks in order.
+template <typename T, int CH, int RPH>
+__device__ inline void w2_dots_av(const uint4 (&wv)[RPH][CH], const uint4 (&av)[CH],
+                                  float (&d)[RPH]) {
+  constexpr int V = Vec<T>::N;
 #pragma unroll
   for (int r = 0; r < RPH; ++r) {
 #pragma unroll
@@ -441,11 +446,24 @@ __device__ inline void w2_dots(const uint4 (&wv)[RPH][CH], const T* __restrict__
   }
 }
 
+// This lane's part of the RPH dot products of the rows in wv with one act
+// row: the FMA chain over its chunks in order.
+template <typename T, int LPR, int CH, int RPH, bool FULL>
+__device__ inline void w2_dots(const uint4 (&wv)[RPH][CH], const T* __restrict__ arow, int I,
+                               int l, float (&d)[RPH]) {
+  uint4 av[CH];
+  w2_load_act<T, LPR, CH, FULL>(arow, I, l, av);
+  w2_dots_av<T, CH, RPH>(wv, av, d);
+}
+
 // SLOTS (one token whose top-k equals cap, CH > 0): wave k streams slot k
 // instead of pair k's slot.  It issues its row loads right after the pairs'
 // slots and weights, without waiting for them, then finds the pair the slot
 // serves and dots its rows with that pair's act row.  Each row's arithmetic
 // is the same as with one wave per pair, so the output bytes are too.
+// Without SPEC the K act rows are staged in LDS first: wave k loads act row
+// k before anything else, so the act row a wave dots with comes from LDS
+// once the slot table names it, instead of a global load issued only then.
 // SPEC (with SLOTS, after Kernel A''): `slots` holds the pager's pair words;
 // the act row of slot k is act_spec row k, or the pair's own act row when the
 // call loaded that pair's expert (the copy blocks computed it).
@@ -464,6 +482,9 @@ __global__ __launch_bounds__(1024) void w2_combine_kernel(const T* __restrict__ 
   constexpr int CHA = CH > 0 ? CH : 1;
   __shared__ float part[kMaxKw2][RPB];
   __shared__ float wk[kMaxKw2];
+  // the staged act rows: [k][chunk][lane of a row group]
+  constexpr bool kStageAct = SLOTS && !SPEC && CH > 0 && kMaxKw2 * CHA * LPR * 16 <= 32768;
+  __shared__ uint4 act_s[kStageAct ? kMaxKw2 * CHA * LPR : 1];
   // every pointer with the first kernel arguments (an empty asm statement
   // that takes them): the skip test below otherwise made the rest a second
   // round trip
@@ -483,6 +504,12 @@ __global__ __launch_bounds__(1024) void w2_combine_kernel(const T* __restrict__ 
     // (both loaded ahead of the rows, so that waiting for them does not wait
     // for the rows: loads complete in order)
     const int jl = min(lane, K - 1);
+    uint4 av_k[CHA];  // act row k (staged)
+    if constexpr (kStageAct) {
+      w2_load_act<T, LPR, CHA, FULL>(act + ((size_t)t * K + k) * I, I, l, av_k);
+      // the act loads stay first: waiting for them waits for nothing after
+      __builtin_amdgcn_sched_barrier(0);
+    }
     const int32_t wd = load_first(slots + t * K + jl);
     const int sj = SPEC ? pair_word_slot(wd) : wd;
     const float wj = __int_as_float(load_first((const int32_t*)topk_w + t * K + jl));
@@ -490,18 +517,33 @@ __global__ __launch_bounds__(1024) void w2_combine_kernel(const T* __restrict__ 
     w2_load_rows<T, LPR, CHA, RPH, FULL>(w2 + (size_t)k * w2_stride, h0, H, I, l, wv);
     // nothing that waits for sj or wj may be scheduled above the row loads
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (kStageAct) {
+      if (sub == 0) {
+#pragma unroll
+        for (int c = 0; c < CHA; ++c) act_s[(k * CHA + c) * LPR + l] = av_k[c];
+      }
+      block_lds_sync();  // every wave's row; the weight rows stay in flight
+    }
     const uint64_t mine = __ballot(lane < K && sj == k);
     p = mine ? __builtin_ctzll(mine) : -1;
     const int sk = __shfl(sj, k);
     const float wsk = __shfl(wj, k);
     // unconditional (a wave whose slot serves no pair dots with pair 0's act
     // and drops the result): rows used under a branch would be loaded there
-    const T* arow = act + ((size_t)t * K + (p < 0 ? 0 : p)) * I;
-    if (SPEC) {
-      const uint64_t loaded = __ballot(lane < K && pair_word_loaded(wd) >= 0);
-      if (!(p >= 0 && ((loaded >> p) & 1ull))) arow = act_spec + (size_t)k * I;
+    if constexpr (kStageAct) {
+      const int pp = p < 0 ? 0 : p;
+      uint4 av[CHA];
+#pragma unroll
+      for (int c = 0; c < CHA; ++c) av[c] = act_s[(pp * CHA + c) * LPR + l];
+      w2_dots_av<T, CHA, RPH>(wv, av, d);
+    } else {
+      const T* arow = act + ((size_t)t * K + (p < 0 ? 0 : p)) * I;
+      if (SPEC) {
+        const uint64_t loaded = __ballot(lane < K && pair_word_loaded(wd) >= 0);
+        if (!(p >= 0 && ((loaded >> p) & 1ull))) arow = act_spec + (size_t)k * I;
+      }
+      w2_dots<T, LPR, CHA, RPH, FULL>(wv, arow, I, l, d);
     }
-    w2_dots<T, LPR, CHA, RPH, FULL>(wv, arow, I, l, d);
     if (lane == 0) wk[k] = sk >= 0 ? wsk : 0.f;
     if (sk < 0 && l == 0) {  // pair k reads no expert: its partials are 0
 #pragma unroll
