@@ -188,7 +188,7 @@ int pager_decide_host(PagerView st, const int32_t* ids, int T, int K, int single
 
 namespace {
 
-template <typename TL, int VALS, bool STAGED, bool ONE>
+template <typename TL, int VALS, bool STAGED, bool ONE, bool REGS = false>
 __global__ __launch_bounds__(64) void pager_kernel(
     const int32_t* __restrict__ ids_in, const TL* __restrict__ logits, int renorm,
     float* __restrict__ w_out, int32_t* __restrict__ id_out, int T, int K, int E, int cap,
@@ -198,7 +198,7 @@ __global__ __launch_bounds__(64) void pager_kernel(
     int32_t* __restrict__ rec_host) {
   __shared__ PagerSmemT<kMaxExperts> sm;
   __shared__ FusedRouteSmemT<kStagedPairs> fr;
-  pager_wave<TL, VALS, STAGED, kMaxExperts, kStagedPairs, ONE>(
+  pager_wave<TL, VALS, STAGED, kMaxExperts, kStagedPairs, ONE, REGS>(
       ids_in, logits, renorm, w_out, id_out, T, K, E, cap, single_group, map_g, s2e_g, tick_g,
       ctr_g, slots_g, flags_g, loads_g, rec, rec_host, sm, fr);
 }
@@ -230,8 +230,11 @@ int launch_pager(const int32_t* ids, const void* logits, int logits_dtype, int r
     rec_host = nullptr;
   }
   // A one-token call routed here on the register path (E <= 128, cap <= 64)
-  // runs the instance compiled for exactly that case.
+  // runs the instance compiled for exactly that case; a call with its ids
+  // given, on the register path and staged, runs the one compiled without
+  // routing and without the LDS path.
   const bool one = logits && T == 1 && E <= 128 && cap <= 64;
+  const bool regs_only = !logits && staged && E <= 128 && cap <= 64;
   with_route_vals(E, [&](auto vals) {
     constexpr int V = decltype(vals)::value;
     if constexpr (V == 2) {
@@ -245,6 +248,13 @@ int launch_pager(const int32_t* ids, const void* logits, int logits_dtype, int r
       if (one) {
         hipLaunchKernelGGL((pager_kernel<float, 2, true, true>), dim3(1), dim3(64), 0, stream,
                            ids, (const float*)logits, renorm, topk_w, topk_ids, T, K, E, cap,
+                           single_group, map, s2e, tick, ctr, slots, flags, loads, rec,
+                           rec_host);
+        return;
+      }
+      if (regs_only) {
+        hipLaunchKernelGGL((pager_kernel<float, 2, true, false, true>), dim3(1), dim3(64), 0,
+                           stream, ids, nullptr, renorm, topk_w, topk_ids, T, K, E, cap,
                            single_group, map, s2e, tick, ctr, slots, flags, loads, rec,
                            rec_host);
         return;

@@ -91,7 +91,11 @@ __device__ inline int set_table_size(int n) {
 // ONE (decided at launch): a one-token call routed here, on the register
 // path (E <= 128, cap <= 64) - the decode step's case, compiled without the
 // other paths, whose set-up and register pressure it would otherwise carry.
-template <typename TL, int VALS, bool STAGED, int MAXE, int MAXP, bool ONE = false>
+// REGS (decided at launch): a call whose ids were routed before the launch,
+// on the register path - batched decode and prefill chunks - compiled
+// without the routing and the LDS path.
+template <typename TL, int VALS, bool STAGED, int MAXE, int MAXP, bool ONE = false,
+          bool REGS = false>
 __device__ __attribute__((always_inline)) inline void pager_wave(
     const int32_t* __restrict__ ids_in, const TL* __restrict__ logits, int renorm,
     float* __restrict__ w_out, int32_t* __restrict__ id_out, int T, int K, int E, int cap,
@@ -100,8 +104,9 @@ __device__ __attribute__((always_inline)) inline void pager_wave(
     int32_t* __restrict__ flags_g, int32_t* __restrict__ loads_g, int32_t* __restrict__ rec,
     int32_t* __restrict__ rec_host, PagerSmemT<MAXE>& sm, FusedRouteSmemT<MAXP>& fr) {
   static_assert(!ONE || (VALS == 2 && STAGED), "a routed one-token call on the register path");
+  static_assert(!REGS || (VALS == 2 && !ONE), "ids given, on the register path");
   if constexpr (ONE) T = 1;
-  const bool routed = ONE || logits != nullptr;
+  const bool routed = ONE || (!REGS && logits != nullptr);
   constexpr int W = 2 * VALS;  // 32-bit mask words per token: E <= 32 * W
   const int lane = threadIdx.x & 63;
   const int nwords = (E + 31) >> 5;
@@ -114,7 +119,7 @@ __device__ __attribute__((always_inline)) inline void pager_wave(
   // scalar registers, so a group's decisions are lane arithmetic, ballots and
   // lane permutes instead of chains of LDS round trips.
   constexpr bool kRegsPath = VALS <= 2;
-  const bool regs = ONE || (kRegsPath && cap <= 64);
+  const bool regs = ONE || REGS || (kRegsPath && cap <= 64);
   // Otherwise, with the router fused (the launcher picks VALS * 64 >= E) and
   // cap within the same bound, the layer state is read into registers first
   // and reaches LDS after routing, so its loads travel while the router loads
