@@ -306,6 +306,19 @@ def test_wide_expert_counts_with_fused_routing(monkeypatch, E, T):
     drive(wl, 48, wl.steps, tol=1e-2)
 
 
+@pytest.mark.parametrize("E,K,cap", [(3, 1, 1), (17, 2, 5), (64, 8, 8), (64, 5, 64),
+                                     (100, 7, 30), (128, 1, 1), (128, 16, 16), (128, 8, 64)])
+def test_one_token_pager_instance(monkeypatch, E, K, cap):
+    """One-token calls routed in the pager on the register path (E <= 128,
+    cap <= 64) run the instance compiled for that case: E below a wave
+    (invalid lanes), K == cap (every call fills the scratch), cap = 1 and
+    cap = 64 (every lane a slot).  Ids, weights, decisions and state
+    bit-exact with the oracle over 40 calls, paged bytes equal to resident."""
+    monkeypatch.setitem(W.SHAPES, "one", W.LayerShape(256, 128, E, K, cap, torch.bfloat16))
+    wl = W.gaussian_logits("one", seed=E * 3 + K + cap, steps=40, tokens=1, pin=True)
+    drive(wl, cap, wl.steps, check_out_every=8, tol=1e-2)
+
+
 @pytest.mark.parametrize("E,T", [(128, 1), (128, 8), (512, 1), (512, 4)])
 def test_fused_routing_with_tied_logits(monkeypatch, E, T):
     """Routing fused into the pager (the one-token register-path instance at
