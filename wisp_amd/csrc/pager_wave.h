@@ -41,7 +41,7 @@ constexpr int kStagedPairs = 4096;
 // call routed in the wave.
 template <int MAXP>
 struct FusedRouteSmemT {
-  int32_t ids[MAXP];
+  alignas(16) int32_t ids[MAXP];
   float w[kFusedRouteTokens * kMaxTopK];  // routing weights of a routed call
   RoutePos pos;                           // the router's positions, per token
 };
@@ -234,6 +234,24 @@ __device__ __attribute__((always_inline)) inline void pager_wave(
       w_out[p] = fr.w[p];
       id_out[p] = fr.ids[p];
     }
+  } else if (STAGED && (reinterpret_cast<uintptr_t>(ids_in) & 15) == 0) {
+    // 16-byte loads, every one in flight before the LDS stores: a 4096-pair
+    // call waits for one global round trip (four ids a lane and load).
+    constexpr int kQ = (MAXP + 255) / 256;  // loads per lane for MAXP pairs
+    const int nq = P >> 2;                  // whole quads of ids
+    uint4 q[kQ];
+#pragma unroll
+    for (int i = 0; i < kQ; ++i) {
+      const int j = i * 64 + lane;
+      q[i] = j < nq ? reinterpret_cast<const uint4*>(ids_in)[j] : make_uint4(0u, 0u, 0u, 0u);
+    }
+    for (int p = 4 * nq + lane; p < P; p += 64) fr.ids[p] = ids_in[p];  // the last P % 4
+#pragma unroll
+    for (int i = 0; i < kQ; ++i) {
+      const int j = i * 64 + lane;
+      if (j < nq) reinterpret_cast<uint4*>(fr.ids)[j] = q[i];
+    }
+    wave_lds_sync();
   } else if (STAGED) {
     // 16 loads in flight per lane before their LDS stores: a 4096-pair call
     // waits for 4 global round trips instead of 64.
