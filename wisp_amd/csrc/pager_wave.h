@@ -190,6 +190,12 @@ __device__ __attribute__((always_inline)) inline void pager_wave(
   uint32_t picked_all = 0u;
   float w0 = 0.f;
   int id0 = -1;
+  // an id outside [0, E) (a routed call's ids are in range: K <= E); staged
+  // ids are checked in the registers they arrive in, except by REGS (whose
+  // main loop measured slower when it did: 18.1 -> 18.5 us a bs=32 call)
+  bool bad = false;
+  constexpr bool kCheckStaged = STAGED && !REGS;
+  auto out_of_range = [&](int e) { return (unsigned)e >= (unsigned)E; };
   if (routed) {
     for (int t = 0; t < T; ++t) {
       float w;
@@ -245,11 +251,20 @@ __device__ __attribute__((always_inline)) inline void pager_wave(
       const int j = i * 64 + lane;
       q[i] = j < nq ? reinterpret_cast<const uint4*>(ids_in)[j] : make_uint4(0u, 0u, 0u, 0u);
     }
-    for (int p = 4 * nq + lane; p < P; p += 64) fr.ids[p] = ids_in[p];  // the last P % 4
+    for (int p = 4 * nq + lane; p < P; p += 64) {  // the last P % 4
+      const int e = ids_in[p];
+      fr.ids[p] = e;
+      if constexpr (kCheckStaged) bad |= out_of_range(e);
+    }
 #pragma unroll
     for (int i = 0; i < kQ; ++i) {
       const int j = i * 64 + lane;
-      if (j < nq) reinterpret_cast<uint4*>(fr.ids)[j] = q[i];
+      if (j < nq) {
+        reinterpret_cast<uint4*>(fr.ids)[j] = q[i];
+        // as unsigned, a negative id is above every valid one
+        if constexpr (kCheckStaged)
+          bad |= out_of_range((int)max(max(q[i].x, q[i].y), max(q[i].z, q[i].w)));
+      }
     }
     wave_lds_sync();
   } else if (STAGED) {
@@ -266,7 +281,10 @@ __device__ __attribute__((always_inline)) inline void pager_wave(
 #pragma unroll
       for (int i = 0; i < kBatch; ++i) {
         const int p = p0 + i * 64 + lane;
-        if (p < P) fr.ids[p] = v[i];
+        if (p < P) {
+          fr.ids[p] = v[i];
+          if constexpr (kCheckStaged) bad |= out_of_range(v[i]);
+        }
       }
     }
     wave_lds_sync();
@@ -282,10 +300,18 @@ __device__ __attribute__((always_inline)) inline void pager_wave(
     if (flags_g) flags_g[1 + p] = pair_word(-1, -1);
   }
 
-  // Validate ids (a routed call's ids are in range: K <= E).
-  bool bad = false;
-  if (!routed)
-    for (int p = lane; p < P; p += 64) bad |= (id_at(p) < 0 || id_at(p) >= E);
+  // Validate the ids not checked above, four a lane at a time.
+  if (!routed && !kCheckStaged)
+    for (int p0 = 0; p0 < P; p0 += 256) {
+      int e[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int p = p0 + i * 64 + lane;
+        e[i] = p < P ? id_at(p) : 0;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) bad |= out_of_range(e[i]);
+    }
   const bool any_bad = ballot(bad) != 0;
   // the planner's masks hold E <= 32 * W experts
   const bool masks_ok = E <= 32 * W;
@@ -932,11 +958,30 @@ __device__ __attribute__((always_inline)) inline void pager_wave(
         nlru = n2;
         wave_lds_sync();
       }
-      for (int p = t0 * K + lane; p < t1 * K; p += 64) {
-        const int e = id_at(p);
-        if (slots_g) slots_g[p] = sm.map[e];
-        if (flags_g)
-          flags_g[1 + p] = pair_word(sm.map[e], (sm.loaded[e >> 5] >> (e & 31)) & 1u ? e : -1);
+      // four pairs a lane at a time: their id reads, then their state
+      // reads, then their stores, so the LDS round trips overlap
+      const int p1 = t1 * K;
+      for (int p0 = t0 * K; p0 < p1; p0 += 256) {
+        int e[4], m[4];
+        uint32_t ld[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int p = p0 + i * 64 + lane;
+          e[i] = p < p1 ? id_at(p) : 0;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          m[i] = sm.map[e[i]];
+          ld[i] = sm.loaded[e[i] >> 5];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int p = p0 + i * 64 + lane;
+          if (p < p1) {
+            if (slots_g) slots_g[p] = m[i];
+            if (flags_g) flags_g[1 + p] = pair_word(m[i], (ld[i] >> (e[i] & 31)) & 1u ? e[i] : -1);
+          }
+        }
       }
       groups_done = g + 1;
       wave_lds_sync();
