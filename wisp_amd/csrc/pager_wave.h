@@ -32,6 +32,12 @@ struct PagerSmemT {
   int32_t sorted[MAXE];
 };
 
+// Four 32-bit words stored by one 16-byte store at a dword-aligned address
+// (gfx950's global stores need only dword alignment).
+struct __attribute__((aligned(4))) Words4 {
+  int32_t w0, w1, w2, w3;
+};
+
 // Routed ids of calls up to this many (token, k) pairs are staged in LDS
 // once, so the serial parts of the kernel never wait on a global load (a
 // 512-token x top-8 chunk fits); larger calls read them from global memory.
@@ -293,12 +299,12 @@ __device__ __attribute__((always_inline)) inline void pager_wave(
     if (state_in_regs) mask_state();
     take_loads();
   }
-  // Every pair starts as "not computed" (slot -1, not loaded); the same lane
-  // owns pair p for all later writes.
-  for (int p = lane; p < P; p += 64) {
-    if (slots_g) slots_g[p] = -1;
-    if (flags_g) flags_g[1 + p] = pair_word(-1, -1);
-  }
+  // Each completed group writes its pairs' slot and flag words; the pairs
+  // from done_p on (groups not completed) are written "not computed" (slot
+  // -1, not loaded) at the end, so every word is stored once (a wave's
+  // stores are limited by its memory counter: a 4096-pair call spent ~3 us
+  // on stores it later overwrote).
+  int done_p = 0;
 
   // Validate the ids not checked above, four a lane at a time.
   if (!routed && !kCheckStaged)
@@ -338,8 +344,18 @@ __device__ __attribute__((always_inline)) inline void pager_wave(
     if (tw < T) {
       for (int j0 = 0; j0 < K; j0 += 8) {
         int e8[8];
+        if (STAGED && (K & 3) == 0) {
+          // the token's ids are 16-byte aligned in LDS: two reads, where
+          // eight 4-byte reads at a 4K-byte lane stride conflicted in banks
+          const uint4 a = *reinterpret_cast<const uint4*>(&fr.ids[tw * K + j0]);
+          const uint4 c = j0 + 4 < K ? *reinterpret_cast<const uint4*>(&fr.ids[tw * K + j0 + 4])
+                                     : make_uint4(~0u, ~0u, ~0u, ~0u);
+          e8[0] = (int)a.x; e8[1] = (int)a.y; e8[2] = (int)a.z; e8[3] = (int)a.w;
+          e8[4] = (int)c.x; e8[5] = (int)c.y; e8[6] = (int)c.z; e8[7] = (int)c.w;
+        } else {
 #pragma unroll
-        for (int jj = 0; jj < 8; ++jj) e8[jj] = j0 + jj < K ? id_at(tw * K + j0 + jj) : -1;
+          for (int jj = 0; jj < 8; ++jj) e8[jj] = j0 + jj < K ? id_at(tw * K + j0 + jj) : -1;
+        }
 #pragma unroll
         for (int jj = 0; jj < 8; ++jj) {
           const int e = e8[jj];
@@ -463,10 +479,49 @@ __device__ __attribute__((always_inline)) inline void pager_wave(
           uint32_t all[W];
 #pragma unroll
           for (int w = 0; w < W; ++w) all[w] = 0u;
-          for (int b = 0; b < T; b += 64) {
-            load_window(b);
+          if (STAGED && (P & 3) == 0) {
+            // a presence word per expert (sm.cand, free until the evictions
+            // fill it), set by every pair's id (validated above), four
+            // consecutive ids a lane by one 16-byte LDS read (a lane past
+            // the pairs re-reads the first four, whose experts are set
+            // anyway), then read back by ballot: straight-line code, where a
+            // token window's per-lane reads conflicted in banks and its mask
+            // set-up took ~18 instructions per id
+            int32_t* pres = sm.cand;
+            for (int e = lane; e < E; e += 64) pres[e] = 0;
+            wave_lds_sync();
+            for (int q0 = 0; q0 < P; q0 += 512) {
+              uint4 a[2];
 #pragma unroll
-            for (int w = 0; w < W; ++w) all[w] |= wave_or(wm[w]);
+              for (int h = 0; h < 2; ++h) {
+                const int p = q0 + 256 * h + 4 * lane;
+                a[h] = *reinterpret_cast<const uint4*>(&fr.ids[p < P ? p : 0]);
+              }
+#pragma unroll
+              for (int h = 0; h < 2; ++h) {
+                pres[a[h].x] = 1;
+                pres[a[h].y] = 1;
+                pres[a[h].z] = 1;
+                pres[a[h].w] = 1;
+              }
+            }
+            wave_lds_sync();
+#pragma unroll
+            for (int v = 0; v < VALS; ++v) {
+              const int e = v * 64 + lane;
+              const uint64_t b = ballot(e < E && pres[e] != 0);
+              all[2 * v] = (uint32_t)b;
+              all[2 * v + 1] = (uint32_t)(b >> 32);
+            }
+          } else {
+            for (int b = 0; b < T; b += 64) {
+              load_window(b);
+#pragma unroll
+              for (int w = 0; w < W; ++w) all[w] |= wm[w];
+            }
+            // the lanes' words to every lane
+#pragma unroll
+            for (int w = 0; w < W; ++w) all[w] = wave_or(all[w]);
           }
           int c = 0;
 #pragma unroll
@@ -736,6 +791,7 @@ __device__ __attribute__((always_inline)) inline void pager_wave(
           }
         }
         groups_done = g + 1;
+        done_p = t1 * K;
         wave_lds_sync();
         continue;
       }
@@ -958,36 +1014,67 @@ __device__ __attribute__((always_inline)) inline void pager_wave(
         nlru = n2;
         wave_lds_sync();
       }
-      // four pairs a lane at a time: their id reads, then their state
-      // reads, then their stores, so the LDS round trips overlap
+      // four consecutive pairs a lane, two quads at a time: their id
+      // reads, then their state reads, then one 16-byte store of each
+      // quad's slots and one of its flag words (dword-aligned), so the LDS
+      // round trips overlap and a 4096-pair group makes 32 + 32 stores where
+      // it made 128 + 128 (a wave's stores are limited by its memory
+      // counter)
       const int p1 = t1 * K;
-      for (int p0 = t0 * K; p0 < p1; p0 += 256) {
-        int e[4], m[4];
-        uint32_t ld[4];
+      // with K a multiple of 4 a quad never straddles the group's end; a
+      // lane past it re-reads the group's first quad and stores nothing
+      const bool quads = STAGED && (K & 3) == 0;
+      for (int p0 = t0 * K; p0 < p1; p0 += 512) {
+        int e[8], m[8], f[8];
+        uint32_t ld[8];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int p = p0 + i * 64 + lane;
-          e[i] = p < p1 ? id_at(p) : 0;
+        for (int h = 0; h < 2; ++h) {
+          const int p = p0 + 256 * h + 4 * lane;
+          if (quads) {
+            const uint4 a = *reinterpret_cast<const uint4*>(&fr.ids[p < p1 ? p : t0 * K]);
+            e[4 * h] = (int)a.x; e[4 * h + 1] = (int)a.y;
+            e[4 * h + 2] = (int)a.z; e[4 * h + 3] = (int)a.w;
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) e[4 * h + i] = p + i < p1 ? id_at(p + i) : 0;
+          }
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < 8; ++i) {
           m[i] = sm.map[e[i]];
           ld[i] = sm.loaded[e[i] >> 5];
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int p = p0 + i * 64 + lane;
-          if (p < p1) {
-            if (slots_g) slots_g[p] = m[i];
-            if (flags_g) flags_g[1 + p] = pair_word(m[i], (ld[i] >> (e[i] & 31)) & 1u ? e[i] : -1);
+        for (int i = 0; i < 8; ++i) f[i] = pair_word(m[i], (ld[i] >> (e[i] & 31)) & 1u ? e[i] : -1);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int p = p0 + 256 * h + 4 * lane;
+          const int* mh = m + 4 * h;
+          const int* fh = f + 4 * h;
+          if (p + 3 < p1) {
+            if (slots_g) *reinterpret_cast<Words4*>(slots_g + p) = Words4{mh[0], mh[1], mh[2], mh[3]};
+            if (flags_g)
+              *reinterpret_cast<Words4*>(flags_g + 1 + p) = Words4{fh[0], fh[1], fh[2], fh[3]};
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (p + i < p1) {
+                if (slots_g) slots_g[p + i] = mh[i];
+                if (flags_g) flags_g[1 + p + i] = fh[i];
+              }
           }
         }
       }
       groups_done = g + 1;
+      done_p = t1 * K;
       wave_lds_sync();
     }
   }
 
+  for (int p = done_p + lane; p < P; p += 64) {
+    if (slots_g) slots_g[p] = -1;
+    if (flags_g) flags_g[1 + p] = pair_word(-1, -1);
+  }
   if (regs) {
 #pragma unroll
     for (int v = 0; v < VALS; ++v)
