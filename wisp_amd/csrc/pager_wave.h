@@ -346,7 +346,8 @@ __device__ __attribute__((always_inline)) inline void pager_wave(
         int e8[8];
         if (STAGED && (K & 3) == 0) {
           // the token's ids are 16-byte aligned in LDS: two reads, where
-          // eight 4-byte reads at a 4K-byte lane stride conflicted in banks
+          // eight 4-byte reads with lanes 4 * K bytes apart conflicted in
+          // banks
           const uint4 a = *reinterpret_cast<const uint4*>(&fr.ids[tw * K + j0]);
           const uint4 c = j0 + 4 < K ? *reinterpret_cast<const uint4*>(&fr.ids[tw * K + j0 + 4])
                                      : make_uint4(~0u, ~0u, ~0u, ~0u);
