@@ -110,7 +110,10 @@ class DevPager:
                                            # the register path's edges: every lane a slot,
                                            # E <= 64 (one mask word pair), odd E and cap
                                            (128, 8, 64, 24), (64, 4, 64, 40), (100, 7, 63, 30),
-                                           (128, 8, 65, 24)])
+                                           (128, 8, 65, 24),
+                                           # the LDS path with top-k not a multiple of 4 (the
+                                           # ids' 16-byte reads and stores fall back to words)
+                                           (200, 3, 70, 30), (130, 5, 66, 40), (256, 6, 90, 50)])
 def test_gpu_pager_matches_oracle(E, K, cap, tmax):
     rng = np.random.default_rng(E * 7 + cap)
     ora, dp = PagerOracle(E, cap), DevPager(E, cap)
@@ -131,7 +134,8 @@ def test_gpu_pager_matches_oracle(E, K, cap, tmax):
 
 @pytest.mark.parametrize("E,K,cap,T", [(128, 8, 32, 520), (128, 8, 128, 1100),
                                         (128, 8, 64, 700), (512, 8, 64, 600),
-                                        (200, 8, 100, 520), (256, 16, 300, 300)])
+                                        (200, 8, 100, 520), (256, 16, 300, 300),
+                                        (300, 6, 150, 700)])
 def test_gpu_pager_above_the_staged_id_limit(E, K, cap, T):
     """Calls of more than 4096 (token, k) pairs: the pager reads the routed
     ids from global memory and mirrors its device record to the host record
