@@ -171,6 +171,26 @@ def test_gpu_pager_overflow():
     with pytest.raises(RuntimeError, match="sub-batch"):
         ora.forward([[0, 1, 1], [2, 3, 4]])
     assert dp.s2e.tolist() == ora.slot_to_expert and int(dp.ctr[4]) == ora.stats_hits
+    # the completed group's pairs hold their slots; the failed group's are
+    # written "not computed" (-1), not left at the buffer's initial -7
+    m = dp.map.tolist()
+    assert rec["slots"][0] == [m[0], m[1], m[1]] and min(rec["slots"][0]) >= 0
+    assert rec["slots"][1] == [-1, -1, -1]
+
+
+def test_gpu_pager_overflow_lds_path():
+    """The same on the LDS path (E > 128): a group of one token that needs more
+    experts than cap fails after the first group completed."""
+    dp, ora = DevPager(200, 4), PagerOracle(200, 4)
+    ids = [[0, 1, 2, 3, 0, 1, 2, 3], [10, 11, 12, 13, 14, 15, 16, 17]]
+    rec = dp.call(ids, 8)
+    assert rec["status"] == _lib.WISP_ERR_SUBBATCH and rec["fail_group"] == 1
+    with pytest.raises(RuntimeError, match="sub-batch"):
+        ora.forward(ids)
+    assert dp.s2e.tolist() == ora.slot_to_expert and dp.map.tolist() == ora.expert_map()
+    m = dp.map.tolist()
+    assert rec["slots"][0] == [m[e] for e in ids[0]] and min(rec["slots"][0]) >= 0
+    assert rec["slots"][1] == [-1] * 8
 
 
 def run_experts(x, w, slots, w13, w2, algo=_lib.WISP_ALGO_GEMV):
