@@ -269,7 +269,9 @@ def test_empty_calls_tick_the_clock_like_the_reference():
     """A zero-token call between decode steps returns an empty output and
     moves the pager as the reference's empty ensure_resident does (the
     clock and the call count tick); later calls keep matching the oracle and
-    the resident layer's bytes."""
+    the resident layer's bytes.  The resident layer takes the same empty
+    calls (a regression case: its routing launch read row 0 of the empty
+    logits buffer, a null pointer, and faulted)."""
     wl = W.toy(steps=8, pin=True)
     sh, K = wl.shape, wl.shape.top_k
     sts = states(wl, 4)
@@ -283,6 +285,12 @@ def test_empty_calls_tick_the_clock_like_the_reference():
             torch.cuda.synchronize()
             assert tuple(out0.shape) == (0, sh.hidden)
             ora.forward([])
+            # the resident layer too: its routing launch only ticks the
+            # call count and must not read the (empty) logits
+            n0 = res.stats_forward
+            assert tuple(res.forward(x0, lg0, K, True).shape) == (0, sh.hidden)
+            torch.cuda.synchronize()
+            assert res.stats_forward == n0 + 1
         x, lg = wl.x[t].to(DEV), wl.logits[t].to(DEV)
         out = paged.forward(x, lg, K, True)
         ref = res.forward(x, lg, K, True)
@@ -512,3 +520,50 @@ def test_overflow_token_raises_subbatch():
     x = wl.x[0].to(DEV)
     with pytest.raises(RuntimeError, match="sub-batch"):
         st.forward(x, wl.logits[0].to(DEV), 3, True)
+
+
+def test_calls_of_mixed_sizes_on_one_state():
+    """One paged state (E 128, top-8, cap 32) driven by calls of 0 to 70
+    tokens in a seeded order, so consecutive calls take different pager
+    instances on the same layer state: one token routed in the kernel, up to 8
+    tokens routed in the kernel, more tokens routed first (one group or
+    several).  Every call: routing and decisions bit-exact with the oracle,
+    the device state equal to the oracle's, paged bytes equal to a resident
+    state's; every output within 1e-2 of the float64 oracle."""
+    sh = W.LayerShape(256, 128, 128, 8, 32, torch.bfloat16)
+    g = torch.Generator().manual_seed(11)
+    slabs = W.alloc_slabs(sh, pin=True)
+    W.fill_expert_weights(slabs, sh, g)
+    w13, w2 = W.slab_views(slabs, sh)
+    sts = {m: WispMoEState(w13, w2, sh.experts if m == "resident" else sh.cap, m, DEV, 0)
+           for m in ("paged", "resident")}
+    sts["resident"].prime_identity()
+    ora = PagerOracle(sh.experts, sh.cap)
+    K = sh.top_k
+    rng = np.random.default_rng(5)
+    bias = torch.from_numpy(rng.normal(0.0, 1.5, sh.experts).astype(np.float32))
+    sizes = [1, 1, 8, 3, 70, 1, 0, 4, 40, 1, 12, 2, 1, 64, 5, 1, 9, 1, 33, 6]
+    xs, lgs, outs = [], [], []
+    for t, T in enumerate(sizes):
+        x = torch.randn((T, sh.hidden), generator=g).to(sh.dtype)
+        lg = torch.randn((T, sh.experts), generator=g) + bias
+        o = {m: st.forward(x.to(DEV), lg.to(DEV), K, True) for m, st in sts.items()}
+        torch.cuda.synchronize()
+        assert torch.equal(bits(o["paged"]), bits(o["resident"])), (t, T)
+        w_ref, ids_ref = route(lg, K)
+        res = ora.forward(ids_ref.tolist())
+        pst = sts["paged"]
+        if T:
+            w_gpu, ids_gpu = pst.last_topk
+            assert ids_gpu.cpu().numpy().tolist() == ids_ref.tolist(), (t, T)
+            assert np.allclose(w_gpu.cpu().numpy(), w_ref, rtol=2e-6, atol=1e-7), (t, T)
+            rec = parse_record(pst.last_record.numpy(), T, K)
+            oracle_trace_matches(res, rec)
+            assert pst.last_slots.cpu().tolist() == res["slots"], (t, T)
+            xs.append(x)
+            lgs.append(lg)
+            outs.append(o["paged"].cpu())
+        assert pst.slot_to_expert == ora.slot_to_expert and pst.lru_tick == ora.lru_tick, (t, T)
+    assert (pst.stats_forward, pst.stats_miss, pst.stats_evict, pst.stats_hits) == \
+        (ora.stats_forward, ora.stats_miss, ora.stats_evict, ora.stats_hits)
+    oracle_check(xs, lgs, outs, K, w13, w2, 1e-2, label="mixed sizes")

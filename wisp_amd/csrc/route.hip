@@ -21,6 +21,10 @@ __global__ __launch_bounds__(256) void route_kernel(const TL* __restrict__ logit
   __shared__ RoutePos pos[4];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   if (forward_counter && blockIdx.x == 0 && threadIdx.x == 0) forward_counter[0] += 1;
+  // a zero-token call launches this block for the counter only: its logits
+  // buffer may be empty (null), and the waves below load row 0 even for an
+  // inactive token
+  if (T <= 0) return;
   const int t = blockIdx.x * 4 + wave;
   const bool active = t < T;
   float w;
