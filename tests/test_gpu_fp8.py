@@ -561,3 +561,37 @@ def test_fp8_state_from_weights_loaded_outside_the_slab():
         for n, fn in saved.items():
             setattr(Fp8MoEMethod, n, fn)
         f8m._FP8_LAYER_STATES.clear()
+
+
+def test_fp8_state_calls_of_mixed_sizes(small_fp8):
+    """Calls of 0 to 64 tokens in a seeded order on one block-FP8 state (cap 8,
+    every one-token call fills the scratch) and on a cap=E state: the
+    one-token fused page-in launch, the decode kernels and the grouped
+    kernels follow each other on the same scratch and pager.  Every call:
+    bytes equal to the cap=E state's, decisions and state equal to the
+    oracle's; sampled outputs within the bf16 tolerance of the oracle."""
+    wl = small_fp8
+    E, K, cap, H = 32, wl.shape.top_k, 8, wl.shape.hidden
+    st, full = _fp8_state(wl, cap), _fp8_state(wl, E)
+    ora = PagerOracle(E, cap)
+    w13, w2, s13, s2 = wl.views()
+    g = torch.Generator().manual_seed(17)
+    bias = torch.randn((E,), generator=g) * 1.5
+    sizes = [1, 1, 8, 3, 40, 0, 1, 20, 5, 1, 64, 2, 1, 0, 13, 1]
+    for t, T in enumerate(sizes):
+        x = torch.randn((T, H), generator=g).to(torch.bfloat16)
+        lg = torch.randn((T, E), generator=g) + bias
+        out = st.forward(x.to(DEV), lg.to(DEV), K, True)
+        ref = full.forward(x.to(DEV), lg.to(DEV), K, True)
+        ids = route(lg, K)[1].tolist() if T else []
+        ora.forward(ids)
+        torch.cuda.synchronize()
+        assert tuple(out.shape) == (T, H), (t, T)
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), (t, T)
+        assert st.slot_to_expert == ora.slot_to_expert and st.lru_tick == ora.lru_tick, (t, T)
+        assert (st.stats_forward, st.stats_miss, st.stats_evict, st.stats_hits) == \
+            (ora.stats_forward, ora.stats_miss, ora.stats_evict, ora.stats_hits), (t, T)
+        if T and t % 3 == 0:
+            tw, rid = route(lg, K)
+            want = F.moe_forward_fp8(x, tw.astype(np.float32), rid, w13, w2, s13, s2)
+            assert _rel(out.float().cpu(), want) < REL_TOL, (t, T)
