@@ -567,3 +567,55 @@ def test_calls_of_mixed_sizes_on_one_state():
     assert (pst.stats_forward, pst.stats_miss, pst.stats_evict, pst.stats_hits) == \
         (ora.stats_forward, ora.stats_miss, ora.stats_evict, ora.stats_hits)
     oracle_check(xs, lgs, outs, K, w13, w2, 1e-2, label="mixed sizes")
+
+
+def test_mixed_sizes_with_resizes_and_prefetches():
+    """Calls of 0 to 70 tokens on one paged layer whose scratch is resized
+    between calls (32 -> 48 -> 70 -> 16 -> 64 -> 8 slots: the pager's register
+    path up to 64 slots, its LDS path above) and which takes speculative
+    prefetches between calls: after every call and prefetch the slot table,
+    ticks, clock and counters equal the oracle's, and every output's bytes
+    equal a resident layer's."""
+    sh = W.LayerShape(256, 128, 128, 8, 32, torch.bfloat16)
+    g = torch.Generator().manual_seed(23)
+    slabs = W.alloc_slabs(sh, pin=True)
+    W.fill_expert_weights(slabs, sh, g)
+    w13, w2 = W.slab_views(slabs, sh)
+    st = WispMoEState(w13, w2, sh.cap, "paged", DEV, 0)
+    res = WispMoEState(w13, w2, sh.experts, "resident", DEV, 1)
+    res.prime_identity()
+    ora = PagerOracle(sh.experts, sh.cap)
+    K = sh.top_k
+    rng = np.random.default_rng(29)
+    bias = torch.from_numpy(rng.normal(0.0, 1.5, sh.experts).astype(np.float32))
+    sizes = [1, 3, 8, 1, 40, 1, 0, 12, 1, 70, 2, 1, 33, 1, 5, 64, 1, 9, 1, 20, 1, 4]
+    resizes = {5: 48, 9: 70, 13: 16, 17: 64, 20: 8}
+    prefetches = {3, 8, 12, 16, 19, 21}
+
+    def check(label):
+        assert st.slot_to_expert == ora.slot_to_expert, label
+        assert st.lru_tick == ora.lru_tick and st.lru_clock == ora.lru_clock, label
+        assert (st.stats_forward, st.stats_miss, st.stats_evict, st.stats_hits) == \
+            (ora.stats_forward, ora.stats_miss, ora.stats_evict, ora.stats_hits), label
+
+    for t, T in enumerate(sizes):
+        if t in resizes:
+            torch.cuda.synchronize()
+            st.resize_cap(resizes[t])
+            ora.resize_cap(resizes[t])
+            assert st.cap_experts == ora.cap_experts
+            check(("resize", t))
+        if t in prefetches:
+            pred = set(int(e) for e in rng.choice(sh.experts, 6, replace=False))
+            st.prefetch_async(list(pred))
+            ora.prefetch_async(pred)
+            torch.cuda.synchronize()
+            check(("prefetch", t))
+        x = torch.randn((T, sh.hidden), generator=g).to(sh.dtype)
+        lg = torch.randn((T, sh.experts), generator=g) + bias
+        out = st.forward(x.to(DEV), lg.to(DEV), K, True)
+        ref = res.forward(x.to(DEV), lg.to(DEV), K, True)
+        ora.forward(route(lg, K)[1].tolist() if T else [])
+        torch.cuda.synchronize()
+        assert torch.equal(bits(out), bits(ref)), (t, T)
+        check((t, T))
