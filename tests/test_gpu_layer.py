@@ -619,3 +619,44 @@ def test_mixed_sizes_with_resizes_and_prefetches():
         torch.cuda.synchronize()
         assert torch.equal(bits(out), bits(ref)), (t, T)
         check((t, T))
+
+
+@pytest.mark.parametrize("fused", ["0", "1"])
+def test_bfloat16_router_logits(monkeypatch, fused):
+    """Router logits in bfloat16, as a bf16 model hands them over: the routing
+    fused into the pager (one-token instance, general instance, and with
+    WISP_DECODE_FUSED=1 the fused decode launch at cap == top-k) and the
+    routing kernel (more than 8 tokens) read them as their exact float32
+    values, so ids, weights and decisions equal the oracle's on those values
+    and paged bytes equal a resident layer's."""
+    monkeypatch.setenv("WISP_DECODE_FUSED", fused)
+    # H = 1024: rows of two 16-byte chunks per lane, a shape the fused decode
+    # launch serves
+    sh = W.LayerShape(1024, 128, 128, 8, 8, torch.bfloat16)
+    g = torch.Generator().manual_seed(31)
+    slabs = W.alloc_slabs(sh, pin=True)
+    W.fill_expert_weights(slabs, sh, g)
+    w13, w2 = W.slab_views(slabs, sh)
+    caps = {"decode": sh.cap, "batch": 32}
+    sts = {k: WispMoEState(w13, w2, c, "paged", DEV, 0) for k, c in caps.items()}
+    res = WispMoEState(w13, w2, sh.experts, "resident", DEV, 1)
+    res.prime_identity()
+    oras = {k: PagerOracle(sh.experts, c) for k, c in caps.items()}
+    K = sh.top_k
+    sizes = {"decode": [1] * 12, "batch": [1, 5, 1, 8, 20, 1, 3, 40]}
+    for key, seq in sizes.items():
+        st, ora = sts[key], oras[key]
+        for t, T in enumerate(seq):
+            x = torch.randn((T, sh.hidden), generator=g).to(sh.dtype)
+            lg = (torch.randn((T, sh.experts), generator=g) * 2.0).to(torch.bfloat16)
+            out = st.forward(x.to(DEV), lg.to(DEV), K, True)
+            ref = res.forward(x.to(DEV), lg.to(DEV), K, True)
+            w_ref, ids_ref = route(lg.float(), K)
+            ora_res = ora.forward(ids_ref.tolist())
+            torch.cuda.synchronize()
+            assert torch.equal(bits(out), bits(ref)), (key, t, T)
+            w_gpu, ids_gpu = st.last_topk
+            assert ids_gpu.cpu().numpy().tolist() == ids_ref.tolist(), (key, t, T)
+            assert np.allclose(w_gpu.cpu().numpy(), w_ref, rtol=2e-6, atol=1e-7), (key, t, T)
+            assert st.last_slots.cpu().tolist() == ora_res["slots"], (key, t, T)
+            assert st.slot_to_expert == ora.slot_to_expert and st.lru_tick == ora.lru_tick
