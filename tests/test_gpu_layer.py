@@ -522,14 +522,18 @@ def test_overflow_token_raises_subbatch():
         st.forward(x, wl.logits[0].to(DEV), 3, True)
 
 
-def test_calls_of_mixed_sizes_on_one_state():
+@pytest.mark.parametrize("engine,streams", [("kernel", "0"), ("memcpy", "0"), ("memcpy", "2")])
+def test_calls_of_mixed_sizes_on_one_state(monkeypatch, engine, streams):
     """One paged state (E 128, top-8, cap 32) driven by calls of 0 to 70
     tokens in a seeded order, so consecutive calls take different pager
     instances on the same layer state: one token routed in the kernel, up to 8
     tokens routed in the kernel, more tokens routed first (one group or
-    several).  Every call: routing and decisions bit-exact with the oracle,
-    the device state equal to the oracle's, paged bytes equal to a resident
-    state's; every output within 1e-2 of the float64 oracle."""
+    several); on both page-in engines.  Every call: routing and decisions
+    bit-exact with the oracle, the device state equal to the oracle's, paged
+    bytes equal to a resident state's; every output within 1e-2 of the
+    float64 oracle."""
+    monkeypatch.setenv("WISP_PAGEIN_ENGINE", engine)
+    monkeypatch.setenv("WISP_PAGEIN_STREAMS", streams)
     sh = W.LayerShape(256, 128, 128, 8, 32, torch.bfloat16)
     g = torch.Generator().manual_seed(11)
     slabs = W.alloc_slabs(sh, pin=True)
