@@ -563,13 +563,18 @@ def test_fp8_state_from_weights_loaded_outside_the_slab():
         f8m._FP8_LAYER_STATES.clear()
 
 
-def test_fp8_state_calls_of_mixed_sizes(small_fp8):
+@pytest.mark.parametrize("engine,logits_dtype", [("kernel", torch.float32),
+                                                  ("memcpy", torch.float32),
+                                                  ("kernel", torch.bfloat16)])
+def test_fp8_state_calls_of_mixed_sizes(monkeypatch, small_fp8, engine, logits_dtype):
     """Calls of 0 to 64 tokens in a seeded order on one block-FP8 state (cap 8,
     every one-token call fills the scratch) and on a cap=E state: the
     one-token fused page-in launch, the decode kernels and the grouped
-    kernels follow each other on the same scratch and pager.  Every call:
-    bytes equal to the cap=E state's, decisions and state equal to the
-    oracle's; sampled outputs within the bf16 tolerance of the oracle."""
+    kernels follow each other on the same scratch and pager (both page-in
+    engines; float32 and bfloat16 router logits).  Every call: bytes equal to
+    the cap=E state's, decisions and state equal to the oracle's; sampled
+    outputs within the bf16 tolerance of the oracle."""
+    monkeypatch.setenv("WISP_PAGEIN_ENGINE", engine)
     wl = small_fp8
     E, K, cap, H = 32, wl.shape.top_k, 8, wl.shape.hidden
     st, full = _fp8_state(wl, cap), _fp8_state(wl, E)
@@ -580,9 +585,10 @@ def test_fp8_state_calls_of_mixed_sizes(small_fp8):
     sizes = [1, 1, 8, 3, 40, 0, 1, 20, 5, 1, 64, 2, 1, 0, 13, 1]
     for t, T in enumerate(sizes):
         x = torch.randn((T, H), generator=g).to(torch.bfloat16)
-        lg = torch.randn((T, E), generator=g) + bias
+        lg = (torch.randn((T, E), generator=g) + bias).to(logits_dtype)
         out = st.forward(x.to(DEV), lg.to(DEV), K, True)
         ref = full.forward(x.to(DEV), lg.to(DEV), K, True)
+        lg = lg.float()
         ids = route(lg, K)[1].tolist() if T else []
         ora.forward(ids)
         torch.cuda.synchronize()
