@@ -352,6 +352,31 @@ def test_experts_mfma_absent_slot_contributes_zero():
     assert rel_err(out, moe_forward(x, wz.numpy(), ids, w13, w2, act_round="bf16")) < 4e-3
 
 
+# Slot ids outside [0, nslots) - at nslots, past it, far past it, below -1 -
+# read no expert and contribute zero on every expert path, as a slot of -1
+# does (the GEMV shapes take both w2 kernels: rows in registers and the
+# looping one).
+@pytest.mark.parametrize("algo,dtype,T,H,I,E,K", [
+    (_lib.WISP_ALGO_GEMV, torch.float32, 3, 512, 256, 8, 2),
+    (_lib.WISP_ALGO_GEMV, torch.bfloat16, 2, 1024, 384, 12, 4),
+    (_lib.WISP_ALGO_GEMV, torch.bfloat16, 2, 256, 8192, 4, 2),
+    (_lib.WISP_ALGO_MFMA, torch.bfloat16, 20, 512, 256, 8, 2)])
+def test_experts_out_of_range_slot_contributes_zero(algo, dtype, T, H, I, E, K):
+    x, w, ids, w13, w2 = _expert_case(T * 17 + I, T, H, I, E, K, dtype)
+    slots = torch.tensor(ids, dtype=torch.int32)
+    bad = [(0, 0, E), (0, K - 1, E + 5), (1, 1, 1 << 30), (T - 1, 0, -7)]
+    wt = torch.tensor(w, dtype=torch.float32)
+    wz = wt.clone()
+    for t, k, s in bad:
+        slots[t, k] = s
+        wz[t, k] = 0
+    out = run_experts(x.to(DEV), wt.to(DEV), slots.to(DEV), w13.to(DEV), w2.to(DEV), algo=algo)
+    if dtype == torch.float32:
+        assert rel_err(out, moe_forward(x, wz.numpy(), ids, w13, w2)) < 1e-5
+    else:
+        assert rel_err(out, moe_forward(x, wz.numpy(), ids, w13, w2, act_round="bf16")) < 4e-3
+
+
 def test_mfma_bytes_independent_of_slots_and_grouping():
     # A token's output must not depend on its slot numbers nor on which other
     # tokens share the call: this is what makes paged == resident bytes.

@@ -172,7 +172,7 @@ __global__ __launch_bounds__(256) void w13_silu_kernel(const T* __restrict__ x, 
                                                         const T* __restrict__ w13,
                                                         size_t w13_stride, T* __restrict__ act,
                                                         const int32_t* __restrict__ pair_filter,
-                                                        int want) {
+                                                        int want, int nslots) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int pair = blockIdx.y;
   // the pager's per-pair words: run only the pairs whose expert this call
@@ -180,7 +180,10 @@ __global__ __launch_bounds__(256) void w13_silu_kernel(const T* __restrict__ x, 
   if (pair_filter && (pair_word_loaded(pair_filter[pair]) >= 0) != (want != 0)) return;
   const int i = blockIdx.x * 4 + wave;
   if (i >= I) return;
-  w13_wave<T, CH, FULL>(x, H, I, K, pair, i, slots[pair], w13, w13_stride, act, lane);
+  // a slot outside [0, nslots) reads no expert, as a slot of -1
+  const int s = slots[pair];
+  w13_wave<T, CH, FULL>(x, H, I, K, pair, i, (unsigned)s < (unsigned)nslots ? s : -1, w13,
+                        w13_stride, act, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -475,7 +478,8 @@ __global__ __launch_bounds__(1024) void w2_combine_kernel(const T* __restrict__ 
                                                            size_t w2_stride,
                                                            T* __restrict__ out,
                                                            const int32_t* __restrict__ skip_if,
-                                                           const T* __restrict__ act_spec) {
+                                                           const T* __restrict__ act_spec,
+                                                           int nslots) {
   static_assert(LPR == 32 || LPR == 64, "a row spans half a wave or a whole wave");
   constexpr int V = Vec<T>::N;
   constexpr int RPB = 64 / LPR * RPH;  // rows per block
@@ -550,7 +554,9 @@ __global__ __launch_bounds__(1024) void w2_combine_kernel(const T* __restrict__ 
       for (int r = 0; r < RPH; ++r) part[k][sub * RPH + r] = 0.f;
     }
   } else {
-    const int s = slots[t * K + k];
+    // a slot outside [0, nslots) reads no expert, as a slot of -1
+    const int raw = slots[t * K + k];
+    const int s = (unsigned)raw < (unsigned)nslots ? raw : -1;
     if (lane == 0) wk[k] = s >= 0 ? topk_w[t * K + k] : 0.f;
     if (s >= 0 && h0 < H) {
       const T* wbase = w2 + (size_t)s * w2_stride;
@@ -614,6 +620,7 @@ struct LaunchCtl {
   const int32_t* skip_if = nullptr;
   bool slots = false;
   const void* act_spec = nullptr;  // with slots: the w2 kernel's SPEC mode
+  int nslots = 0;                  // slot ids at or above it read no expert
 };
 
 template <typename T, int CH>
@@ -622,10 +629,10 @@ void launch_w13(const T* x, int T_, int H, int I, int K, const int32_t* slots, c
   dim3 grid((I + 3) / 4, T_ * K);
   if (H == CH * 64 * Vec<T>::N)
     launch_timed(w13_silu_kernel<T, CH, true>, grid, dim3(256), st, c.start, c.stop, x, H, I, K,
-                 slots, w13, w13_stride, act, c.pair_filter, c.want);
+                 slots, w13, w13_stride, act, c.pair_filter, c.want, c.nslots);
   else
     launch_timed(w13_silu_kernel<T, CH, false>, grid, dim3(256), st, c.start, c.stop, x, H, I, K,
-                 slots, w13, w13_stride, act, c.pair_filter, c.want);
+                 slots, w13, w13_stride, act, c.pair_filter, c.want, c.nslots);
 }
 
 template <typename T, int CH>
@@ -708,24 +715,24 @@ void launch_w2(const T* act, int T_, int H, int I, int K, const float* w, const 
   if (CH > 0 && c.slots && spec) {
     if (full)
       launch_timed(w2_combine_kernel<T, LPR, CH, RPH, true, true, true>, grid, dim3(64 * K), st,
-                   c.start, c.stop, act, H, I, K, w, slots, w2, w2_stride, out, c.skip_if, spec);
+                   c.start, c.stop, act, H, I, K, w, slots, w2, w2_stride, out, c.skip_if, spec, c.nslots);
     else
       launch_timed(w2_combine_kernel<T, LPR, CH, RPH, false, true, true>, grid, dim3(64 * K),
                    st, c.start, c.stop, act, H, I, K, w, slots, w2, w2_stride, out, c.skip_if,
-                   spec);
+                   spec, c.nslots);
   } else if (CH > 0 && c.slots) {
     if (full)
       launch_timed(w2_combine_kernel<T, LPR, CH, RPH, true, true>, grid, dim3(64 * K), st,
-                   c.start, c.stop, act, H, I, K, w, slots, w2, w2_stride, out, c.skip_if, spec);
+                   c.start, c.stop, act, H, I, K, w, slots, w2, w2_stride, out, c.skip_if, spec, c.nslots);
     else
       launch_timed(w2_combine_kernel<T, LPR, CH, RPH, false, true>, grid, dim3(64 * K), st,
-                   c.start, c.stop, act, H, I, K, w, slots, w2, w2_stride, out, c.skip_if, spec);
+                   c.start, c.stop, act, H, I, K, w, slots, w2, w2_stride, out, c.skip_if, spec, c.nslots);
   } else if (full) {
     launch_timed(w2_combine_kernel<T, LPR, CH, RPH, true, false>, grid, dim3(64 * K), st,
-                 c.start, c.stop, act, H, I, K, w, slots, w2, w2_stride, out, c.skip_if, spec);
+                 c.start, c.stop, act, H, I, K, w, slots, w2, w2_stride, out, c.skip_if, spec, c.nslots);
   } else {
     launch_timed(w2_combine_kernel<T, LPR, CH, RPH, false, false>, grid, dim3(64 * K), st,
-                 c.start, c.stop, act, H, I, K, w, slots, w2, w2_stride, out, c.skip_if, spec);
+                 c.start, c.stop, act, H, I, K, w, slots, w2, w2_stride, out, c.skip_if, spec, c.nslots);
   }
 }
 
@@ -813,10 +820,11 @@ int decode_w13(const PageInArgs& a, const void* x, int dtype, int logits_dtype, 
 }
 
 int gemv_w13(const void* x, int dtype, int T_, int H, int I, int K, const int32_t* slots,
-             const void* w13, size_t w13_stride, void* act, hipStream_t st,
+             int nslots, const void* w13, size_t w13_stride, void* act, hipStream_t st,
              hipEvent_t ev_start, hipEvent_t ev_stop, const int32_t* pair_filter, int want) {
   if (T_ == 0) return WISP_OK;
   LaunchCtl c;
+  c.nslots = nslots;
   c.start = ev_start;
   c.stop = ev_stop;
   c.pair_filter = pair_filter;
@@ -837,11 +845,12 @@ int gemv_w13(const void* x, int dtype, int T_, int H, int I, int K, const int32_
 // With `cap` > 0, a one-token call whose top-k equals cap uses every slot
 // and runs the w2 kernel one wave per slot (cap 0: one wave per pair).
 int gemv_w2(const void* act, int dtype, int T_, int H, int I, int K, const float* topk_w,
-            const int32_t* slots, const void* w2, size_t w2_stride, void* out, hipStream_t st,
-            hipEvent_t ev_start, hipEvent_t ev_stop, const int32_t* skip_if, int cap,
-            const void* act_spec) {
+            const int32_t* slots, int nslots, const void* w2, size_t w2_stride, void* out,
+            hipStream_t st, hipEvent_t ev_start, hipEvent_t ev_stop, const int32_t* skip_if,
+            int cap, const void* act_spec) {
   if (T_ == 0) return WISP_OK;
   LaunchCtl c;
+  c.nslots = nslots;
   c.start = ev_start;
   c.stop = ev_stop;
   c.skip_if = skip_if;
@@ -861,12 +870,13 @@ int gemv_w2(const void* act, int dtype, int T_, int H, int I, int K, const float
 }
 
 int experts_gemv(const void* x, int dtype, int T_, int H, int I, int K, const float* topk_w,
-                 const int32_t* slots, const void* w13, size_t w13_stride, const void* w2,
-                 size_t w2_stride, void* act, void* out, hipStream_t st, const StageEvents* ev) {
-  int rc = gemv_w13(x, dtype, T_, H, I, K, slots, w13, w13_stride, act, st,
+                 const int32_t* slots, int nslots, const void* w13, size_t w13_stride,
+                 const void* w2, size_t w2_stride, void* act, void* out, hipStream_t st,
+                 const StageEvents* ev) {
+  int rc = gemv_w13(x, dtype, T_, H, I, K, slots, nslots, w13, w13_stride, act, st,
                     ev ? ev->ev[0] : nullptr, ev ? ev->ev[1] : nullptr, nullptr, 0);
   if (rc != WISP_OK) return rc;
-  return gemv_w2(act, dtype, T_, H, I, K, topk_w, slots, w2, w2_stride, out, st,
+  return gemv_w2(act, dtype, T_, H, I, K, topk_w, slots, nslots, w2, w2_stride, out, st,
                  ev ? ev->ev[2] : nullptr, ev ? ev->ev[3] : nullptr, nullptr, 0, nullptr);
 }
 

@@ -64,23 +64,24 @@ int launch_pager(const int32_t* ids, const void* logits, int logits_dtype, int r
                  int32_t* slots, int32_t* flags, int32_t* loads, int32_t* rec, int rec_words,
                  hipStream_t stream, int32_t* rec_host);
 int gemv_w13(const void* x, int dtype, int T, int H, int I, int K, const int32_t* slots,
-             const void* w13, size_t w13_stride, void* act, hipStream_t st,
+             int nslots, const void* w13, size_t w13_stride, void* act, hipStream_t st,
              hipEvent_t ev_start, hipEvent_t ev_stop, const int32_t* pair_filter, int want);
 int pagein_w13(const PageInArgs& a, const void* x, int dtype, int T, int H, int I, int K,
                const int32_t* flags, const void* w13, size_t w13_stride, void* act,
                hipStream_t st, hipEvent_t ev_start, hipEvent_t ev_stop);
 int gemv_w2(const void* act, int dtype, int T, int H, int I, int K, const float* topk_w,
-            const int32_t* slots, const void* w2, size_t w2_stride, void* out, hipStream_t st,
-            hipEvent_t ev_start, hipEvent_t ev_stop, const int32_t* skip_if, int cap,
-            const void* act_spec);
+            const int32_t* slots, int nslots, const void* w2, size_t w2_stride, void* out,
+            hipStream_t st, hipEvent_t ev_start, hipEvent_t ev_stop, const int32_t* skip_if,
+            int cap, const void* act_spec);
 bool decode_w13_supported(int dtype, int H, int E, int K, int cap);
 int decode_w13(const PageInArgs& a, const void* x, int dtype, int logits_dtype, int H, int I,
                int K, int32_t* flags, const void* w13, size_t w13_stride, void* act,
                const DecodePagerArgs& pa, hipStream_t st, hipEvent_t ev_start,
                hipEvent_t ev_stop);
 int experts_gemv(const void* x, int dtype, int T, int H, int I, int K, const float* topk_w,
-                 const int32_t* slots, const void* w13, size_t w13_stride, const void* w2,
-                 size_t w2_stride, void* act, void* out, hipStream_t st, const StageEvents* ev);
+                 const int32_t* slots, int nslots, const void* w13, size_t w13_stride,
+                 const void* w2, size_t w2_stride, void* act, void* out, hipStream_t st,
+                 const StageEvents* ev);
 int experts_mfma(const void* x, int T, int H, int I, int K, const float* topk_w,
                  const int32_t* slots, int nslots, const void* w13, size_t w13_stride,
                  const void* w2, size_t w2_stride, void* act, void* out, void* work,
@@ -568,7 +569,7 @@ int w13(Layer& L, const void* x, int T, int K, const int32_t* slots, void* act, 
   // a call's w13 may take two launches (pairs that hit, then loaded pairs);
   // the first of them counts the call
   if (p && !(filter && want == 1)) L.prof_w13_calls += 1;
-  int rc = gemv_w13(x, d.dtype, T, d.hidden, d.inter, K, slots, d.scratch_w13,
+  int rc = gemv_w13(x, d.dtype, T, d.hidden, d.inter, K, slots, d.cap, d.scratch_w13,
                     d.scratch_w13_stride, act, st, p ? p->start : nullptr,
                     p ? p->stop : nullptr, filter, want);
   if (p && rc == WISP_OK) p->pending = true;
@@ -587,7 +588,7 @@ int w2(Layer& L, const void* act, int T, int K, const float* w, const int32_t* s
                                   d.scratch_w2_stride, d.scratch_s2, d.scratch_s2_stride,
                                   d.block_n, out, st, p ? p->start : nullptr,
                                   p ? p->stop : nullptr, true)
-                 : gemv_w2(act, d.dtype, T, d.hidden, d.inter, K, w, slots, d.scratch_w2,
+                 : gemv_w2(act, d.dtype, T, d.hidden, d.inter, K, w, slots, d.cap, d.scratch_w2,
                            d.scratch_w2_stride, out, st, p ? p->start : nullptr,
                            p ? p->stop : nullptr, skip_if, d.cap, act_spec);
   if (p && rc == WISP_OK) p->pending = true;
@@ -1297,8 +1298,8 @@ extern "C" int wisp_moe_experts(const void* x, int dtype, int T, int H, int I, i
                         act, out, work, work_bytes, (hipStream_t)stream, nullptr);
   }
   if (a != WISP_ALGO_GEMV) return WISP_ERR_INVALID;
-  return experts_gemv(x, dtype, T, H, I, K, topk_w, slots, w13, w13_stride, w2, w2_stride, act,
-                      out, (hipStream_t)stream, nullptr);
+  return experts_gemv(x, dtype, T, H, I, K, topk_w, slots, nslots, w13, w13_stride, w2,
+                      w2_stride, act, out, (hipStream_t)stream, nullptr);
 }
 
 extern "C" size_t wisp_moe_work_bytes(int T, int K, int H, int nslots) {

@@ -28,8 +28,9 @@ static __device__ __align__(256) unsigned char scratch[WISP_NOALLOC_SCRATCH_BYTE
 namespace wisp {
 
 int experts_gemv(const void* x, int dtype, int T, int H, int I, int K, const float* topk_w,
-                 const int32_t* slots, const void* w13, size_t w13_stride, const void* w2,
-                 size_t w2_stride, void* act, void* out, hipStream_t st, const StageEvents* ev);
+                 const int32_t* slots, int nslots, const void* w13, size_t w13_stride,
+                 const void* w2, size_t w2_stride, void* act, void* out, hipStream_t st,
+                 const StageEvents* ev);
 int experts_mfma(const void* x, int T, int H, int I, int K, const float* topk_w,
                  const int32_t* slots, int nslots, const void* w13, size_t w13_stride,
                  const void* w2, size_t w2_stride, void* act, void* out, void* work,
@@ -119,8 +120,8 @@ extern "C" int wisp_moe_experts_noalloc(const void* x, int dtype, int T, int H, 
   if (a == WISP_ALGO_MFMA)
     return experts_mfma(x, T, H, I, K, topk_w, slots, nslots, w13, w13_stride, w2, w2_stride, act,
                         out, act + act_bytes, work_bytes, st, nullptr);
-  return experts_gemv(x, dtype, T, H, I, K, topk_w, slots, w13, w13_stride, w2, w2_stride, act,
-                      out, st, nullptr);
+  return experts_gemv(x, dtype, T, H, I, K, topk_w, slots, nslots, w13, w13_stride, w2,
+                      w2_stride, act, out, st, nullptr);
 }
 
 extern "C" size_t wisp_noalloc_scratch_bytes(void) { return (size_t)WISP_NOALLOC_SCRATCH_BYTES; }
