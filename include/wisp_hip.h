@@ -65,10 +65,11 @@ typedef struct ihipStream_t* wisp_stream_t; /* == hipStream_t */
 
 /* Message of the last failing call on this thread ("" if none). */
 const char* wisp_last_error(void);
-/* ABI version of this library: 3 (wisp_layer_desc carries the block-FP8
- * fields; wisp_layer_desc and wisp_workspace end with struct_bytes, which
- * the caller sets to the struct's sizeof and the library checks, so that a
- * caller built against another layout is refused instead of misread). */
+/* ABI version of this library: 4 (wisp_layer_desc carries the block-FP8
+ * fields and the packed masters; wisp_layer_desc and wisp_workspace end
+ * with struct_bytes, which the caller sets to the struct's sizeof and the
+ * library checks, so that a caller built against another layout is refused
+ * instead of misread). */
 int wisp_abi_version(void);
 /* int32 words a decision record needs for a call of T tokens x K experts. */
 int wisp_record_words(int T, int K);
@@ -275,6 +276,12 @@ typedef struct wisp_layer_desc {
   size_t master_s13_stride;      /* elements                             */
   const float* master_s2;
   size_t master_s2_stride;       /* elements                             */
+  /* bf16 layers: the masters' packed copy (wisp_pack_bf16), pinned host,
+     expert e at +e*packed_stride bytes, or NULL.  The copy-kernel engine
+     then pages in from it; the memcpy engine ignores it.  It must hold
+     exactly master_w13 / master_w2 as packed. */
+  const void* packed_master;
+  size_t packed_stride;          /* bytes                                */
   size_t struct_bytes;           /* sizeof(wisp_layer_desc); another value
                                     is refused (WISP_ERR_INVALID)         */
 } wisp_layer_desc;
@@ -306,6 +313,28 @@ typedef struct wisp_workspace {
   size_t struct_bytes;           /* sizeof(wisp_workspace); another value
                                     is refused (WISP_ERR_INVALID)         */
 } wisp_workspace;
+
+/* Packed bf16 masters.  No reference counterpart: the reference pages the
+ * bf16 masters as they are (fused_moe.py:338-354).  The packed copy holds
+ * the same values in ~0.77x the bytes (typical weights), so the copy-kernel
+ * engine's page-in moves fewer bytes over the host link and unpacks them
+ * into the slot; the slot's bytes are the master's exactly.  Per row of L
+ * values and block of 64 values: the sign and mantissa bytes, a 4-bit
+ * exponent code above the block's smallest nonzero exponent (code 15:
+ * exponent 0), the block's base exponent; a block whose exponents span more
+ * than 15 values keeps its 64 exponent bytes in the expert's exception
+ * area.  Experts are [E, 2I, H] (w13) and [E, H, I] (w2) bf16 at the given
+ * element strides; H and I must be multiples of 64.  Host-only calls (no
+ * device work), threaded over experts.
+ * wisp_pack_bf16_stride: bytes per packed expert (a multiple of 256) for
+ * these masters, 0 when the shape does not pack. */
+size_t wisp_pack_bf16_stride(int E, int H, int I, const void* master_w13,
+                             size_t master_w13_stride, const void* master_w2,
+                             size_t master_w2_stride);
+/* Packs the masters into out (E * stride bytes, host memory); stride at
+ * least wisp_pack_bf16_stride of the same masters. */
+int wisp_pack_bf16(int E, int H, int I, const void* master_w13, size_t master_w13_stride,
+                   const void* master_w2, size_t master_w2_stride, void* out, size_t stride);
 
 /* Create / destroy the per-layer context (copy stream, events). */
 int wisp_layer_create(const wisp_layer_desc* desc, void** handle);

@@ -29,7 +29,7 @@ def test_binding_covers_header():
 
 
 def test_host_only_entry_points(hiplib):
-    assert hiplib.wisp_abi_version() == 3
+    assert hiplib.wisp_abi_version() == 4
     # record: 8 header words + 8 per group + 4 per (token, k) pair
     assert hiplib.wisp_record_words(1, 8) == 8 + 8 + 4 * 8
     assert hiplib.wisp_record_words(0, 8) == 8 + 8 + 4

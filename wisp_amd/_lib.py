@@ -54,6 +54,7 @@ class LayerDesc(C.Structure):
         ("scratch_s2", _vp), ("scratch_s2_stride", _sz),
         ("master_s13", _vp), ("master_s13_stride", _sz),
         ("master_s2", _vp), ("master_s2_stride", _sz),
+        ("packed_master", _vp), ("packed_stride", _sz),
         ("struct_bytes", _sz),
     ]
 
@@ -78,6 +79,8 @@ class Workspace(C.Structure):
 SIGNATURES = {
     "wisp_last_error": (C.c_char_p, []),
     "wisp_abi_version": (_i32, []),
+    "wisp_pack_bf16_stride": (_sz, [_i32, _i32, _i32, _vp, _sz, _vp, _sz]),
+    "wisp_pack_bf16": (_i32, [_i32, _i32, _i32, _vp, _sz, _vp, _sz, _vp, _sz]),
     "wisp_record_words": (_i32, [_i32, _i32]),
     "wisp_route_topk_softmax": (_i32, [_vp, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp]),
     "wisp_pager_decide": (_i32, [_vp, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp,

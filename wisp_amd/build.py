@@ -26,6 +26,7 @@ SOURCES = [
     "experts_mfma.hip",
     "experts_fp8.hip",
     "pagein.hip",
+    "packed.hip",
     "prefetch.hip",
     "layer.hip",
     "probes.hip",

@@ -219,8 +219,95 @@ struct FusedW13Args {
   int H, I, K, cap;
 };
 
-// Copy block `cb` (of kPageInBlocks) of a fused page-in + w13 launch.
-template <typename T, int CH, bool FULL>
+// The copy blocks' work when the masters are packed (packed.h): each loaded
+// expert's w13 rows unpacked into its slot, one row pair per wave and
+// iteration; the expert's pair then reads the two rows back from the slot
+// with the resident blocks' own w13_wave, so its act bytes are theirs.
+// (Computing act from the unpacked registers instead held more registers
+// than the w13 blocks' budget, and all blocks of the launch get the most
+// any path needs.)  Then each loaded expert's w2 rows.
+template <int CH, bool FULL>
+__device__ inline void pagein_w13_packed(const FusedW13Args& f, const PageInArgs& a, int cb,
+                                         int mine) {
+  // wave-uniform (readfirstlane), so that the row bases sit in scalar
+  // registers
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int H = f.H, I = f.I, nch = H / 8;
+  const PackedSrc& pk = a.pk;
+  const packed::Layout Lp(H, I);
+  const int n = *a.count;
+  int jcur = -1, e = -1, s = -1, pair = -1;
+  for (int q = cb * 4 + wave; q < n * I; q += kPageInBlocks * 4) {
+    const int j = q / I, i = q - j * I;
+    if (j != jcur) {
+      jcur = j;
+      e = __builtin_amdgcn_readfirstlane(a.loads[2 * j]);
+      s = __builtin_amdgcn_readfirstlane(a.loads[2 * j + 1]);
+      const uint64_t m = __ballot(mine == e);
+      pair = m ? __builtin_ctzll(m) : -1;
+    }
+    if (e < 0 || e >= a.num_experts || s < 0 || s >= a.cap) continue;
+    const char* ex = pk.m + (size_t)e * pk.m_stride;
+    char* slot = pk.d13 + (size_t)s * pk.d13_stride;
+#pragma unroll 1
+    for (int r = 0; r < 2; ++r) {
+      const int row = r ? I + i : i;
+      const char* src = ex + (size_t)row * Lp.rs13;
+      u32x4* dst = reinterpret_cast<u32x4*>(slot + (size_t)row * H * sizeof(uint16_t));
+      const __amdgpu_buffer_rsrc_t rs = packed::row_rsrc(src, H);
+      packed::Chunk c[CH];
+      packed::for_each_chunk<CH>([&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        c[k] = packed::load_lane_chunk<k>(rs, H, lane);
+      });
+      // exception blocks are rare: a row without any takes the plain unpack
+      bool exc = false;
+#pragma unroll
+      for (int k = 0; k < CH; ++k)
+        exc |= (FULL || k * 64 + lane < nch) && packed::is_exception(c[k], k * 64 + lane);
+      const bool slow = __ballot(exc) != 0;
+#pragma unroll
+      for (int k = 0; k < CH; ++k) {
+        const int ch = k * 64 + lane;
+        if (FULL || ch < nch) {
+          const uint4 v = packed::unpack_plain(c[k]);
+          __builtin_nontemporal_store(u32x4{v.x, v.y, v.z, v.w}, dst + ch);
+        }
+      }
+      // a row with exception blocks rewrites their chunks afterwards (a
+      // separate pass: inline in the one above, it spilled registers of the
+      // w13 blocks that share this launch)
+      if (slow) {
+#pragma unroll
+        for (int k = 0; k < CH; ++k) {
+          const int ch = k * 64 + lane;
+          if ((FULL || ch < nch) && packed::is_exception(c[k], ch)) {
+            const uint4 v = packed::unpack_chunk(c[k], src, H, ch, ex + Lp.exc_off);
+            __builtin_nontemporal_store(u32x4{v.x, v.y, v.z, v.w}, dst + ch);
+          }
+        }
+      }
+    }
+    if (pair >= 0) {
+      // each lane reads back the chunks it stored: its own stores, in order
+      __threadfence_block();
+      w13_wave<uint16_t, CH, FULL>((const uint16_t*)f.x, H, I, f.K, pair, i, 0,
+                                   reinterpret_cast<const uint16_t*>(slot), 0,
+                                   (uint16_t*)f.act, lane);
+    }
+  }
+  for (int j = 0; j < n; ++j) {
+    const int ej = a.loads[2 * j], sj = a.loads[2 * j + 1];
+    if (ej < 0 || ej >= a.num_experts || sj < 0 || sj >= a.cap) continue;
+    const char* ex = pk.m + (size_t)ej * pk.m_stride;
+    unpack_rows<256, 2>(ex + Lp.w2_off, H, I, ex + Lp.exc_off,
+                        pk.d2 + (size_t)sj * pk.d2_stride, cb, kPageInBlocks);
+  }
+}
+
+// Copy block `cb` (of kPageInBlocks) of a fused page-in + w13 launch
+// (PACKED: from the packed masters).
+template <typename T, int CH, bool FULL, bool PACKED = false>
 __device__ inline void pagein_w13_copy_block(const FusedW13Args& f, const PageInArgs& a, int cb) {
   constexpr int V = Vec<T>::N;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -237,6 +324,10 @@ __device__ inline void pagein_w13_copy_block(const FusedW13Args& f, const PageIn
   const size_t row_bytes = (size_t)H * sizeof(T);
   uint4 xv[CH];
   load_row<T, CH, FULL, false>((const T*)f.x, nch, lane, xv);  // the call's one token
+  if constexpr (PACKED && sizeof(T) == 2) {
+    pagein_w13_packed<CH, FULL>(f, a, cb, mine);
+    return;
+  }
   int jcur = -1, e = -1, s = -1, pair = -1;
   for (int q = cb * 4 + wave; q < n * I; q += kPageInBlocks * 4) {
     const int j = q / I, i = q - j * I;
@@ -294,8 +385,8 @@ __device__ inline void pagein_w13_copy_block(const FusedW13Args& f, const PageIn
   }
 }
 
-template <typename T, int CH, bool FULL>
-__global__ __launch_bounds__(256) void pagein_w13_kernel(FusedW13Args f, PageInArgs a) {
+template <typename T, int CH, bool FULL, bool PACKED>
+__device__ inline void pagein_w13_body(const FusedW13Args& f, const PageInArgs& a) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   if (blockIdx.x >= kPageInBlocks) {
     const int I = f.I, nbx = (I + 3) / 4;
@@ -310,7 +401,24 @@ __global__ __launch_bounds__(256) void pagein_w13_kernel(FusedW13Args f, PageInA
                           (const T*)f.w13, f.w13_stride, (T*)f.act, lane);
     return;
   }
-  pagein_w13_copy_block<T, CH, FULL>(f, a, blockIdx.x);
+  pagein_w13_copy_block<T, CH, FULL, PACKED>(f, a, blockIdx.x);
+}
+
+template <typename T, int CH, bool FULL>
+__global__ __launch_bounds__(256) void pagein_w13_kernel(FusedW13Args f, PageInArgs a) {
+  pagein_w13_body<T, CH, FULL, false>(f, a);
+}
+
+// The same launch paging in from packed masters.  The unpack would take
+// more registers than the w13 blocks (which then hold fewer waves per SIMD
+// than they need to stream their weights in one round), so the launch is
+// held at the waves per SIMD the plain launch gets for the same row length.
+constexpr int packed_waves_per_eu(int ch) { return ch <= 3 ? 7 : ch == 4 ? 6 : ch <= 6 ? 4 : 3; }
+
+template <int CH, bool FULL>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(packed_waves_per_eu(CH))))
+void pagein_w13_packed_kernel(FusedW13Args f, PageInArgs a) {
+  pagein_w13_body<uint16_t, CH, FULL, true>(f, a);
 }
 
 // ---------------------------------------------------------------------------
@@ -338,7 +446,7 @@ __global__ __launch_bounds__(256) void pagein_w13_kernel(FusedW13Args f, PageInA
 // microseconds; the bound only keeps a broken launch from hanging the GPU.
 constexpr int kDecodeSpinLimit = 1 << 20;
 
-template <typename T, typename TL, int CH>
+template <typename T, typename TL, int CH, bool PACKED = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6))) void decode_w13_kernel(FusedW13Args f, PageInArgs a,
                                                          DecodePagerArgs pa) {
   // the pager wave's LDS for at most 128 experts and one token's pairs
@@ -367,7 +475,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6))) void d
     __syncthreads();
     if (!seen) return;
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    pagein_w13_copy_block<T, CH, true>(f, a, blockIdx.x - 1);
+    pagein_w13_copy_block<T, CH, true, PACKED>(f, a, blockIdx.x - 1);
     return;
   }
   const int I = f.I, nbx = (I + 3) / 4;
@@ -639,7 +747,19 @@ template <typename T, int CH>
 void launch_pagein_w13(const PageInArgs& a, const FusedW13Args& f, hipStream_t st,
                        hipEvent_t ev_start, hipEvent_t ev_stop) {
   const dim3 grid(kPageInBlocks + (f.I + 3) / 4 * f.K);
-  if (f.H == CH * 64 * Vec<T>::N)
+  const bool full = f.H == CH * 64 * Vec<T>::N;
+  if constexpr (sizeof(T) == 2) {
+    if (a.pk.m) {
+      if (full)
+        launch_timed(pagein_w13_packed_kernel<CH, true>, grid, dim3(256), st, ev_start, ev_stop,
+                     f, a);
+      else
+        launch_timed(pagein_w13_packed_kernel<CH, false>, grid, dim3(256), st, ev_start,
+                     ev_stop, f, a);
+      return;
+    }
+  }
+  if (full)
     launch_timed(pagein_w13_kernel<T, CH, true>, grid, dim3(256), st, ev_start, ev_stop, f, a);
   else
     launch_timed(pagein_w13_kernel<T, CH, false>, grid, dim3(256), st, ev_start, ev_stop, f, a);
@@ -649,7 +769,11 @@ template <typename T, typename TL, int CH>
 void launch_decode_w13(const PageInArgs& a, const FusedW13Args& f, const DecodePagerArgs& pa,
                        hipStream_t st, hipEvent_t ev_start, hipEvent_t ev_stop) {
   const dim3 grid(1 + kPageInBlocks + (f.I + 3) / 4 * f.cap);
-  launch_timed(decode_w13_kernel<T, TL, CH>, grid, dim3(256), st, ev_start, ev_stop, f, a, pa);
+  if (sizeof(T) == 2 && a.pk.m)
+    launch_timed(decode_w13_kernel<T, TL, CH, true>, grid, dim3(256), st, ev_start, ev_stop, f, a,
+                 pa);
+  else
+    launch_timed(decode_w13_kernel<T, TL, CH>, grid, dim3(256), st, ev_start, ev_stop, f, a, pa);
 }
 
 // The per-lane chunk count of the w13 kernels for a row of H elements (0 when

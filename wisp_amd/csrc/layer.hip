@@ -54,7 +54,7 @@ void wisp_set_last_error(const char* what, const char* where) {
 }
 
 extern "C" const char* wisp_last_error(void) { return g_last_error.c_str(); }
-extern "C" int wisp_abi_version(void) { return 3; }
+extern "C" int wisp_abi_version(void) { return 4; }
 
 namespace wisp {
 
@@ -195,6 +195,8 @@ struct Layer {
   size_t expert_bytes = 0;  // weight (and scale) bytes of one expert
   // kernel page-in (engine WISP_PAGEIN_KERNEL and eligible masters)
   bool kpin = false;
+  // with kpin: the device address of the packed masters, or null
+  const char* packed_dev = nullptr;
   // the fused page-in + w13 launch applies (plane 0 starts with the whole
   // w13 of an expert, in master and scratch alike; for block-FP8 experts
   // the plane is the whole [w13 | w2 | s13 | s2] slab, the w13 scales at
@@ -433,6 +435,8 @@ int page_in_kernel(Layer& L, const int32_t* loads, const int32_t* count, int n, 
     const Plane& pl = L.planes[q];
     a.p[q] = {pl.dev, pl.m_stride, pl.d, pl.d_stride, pl.bytes};
   }
+  a.pk = {L.packed_dev, d.packed_stride, d.hidden, d.inter, (char*)d.scratch_w13,
+          d.scratch_w13_stride * L.es, (char*)d.scratch_w2, d.scratch_w2_stride * L.es};
   // The pinned word that tells the timing how many experts a launch copied
   // is written (with a system-scope fence, a host-link round trip inside the
   // kernel) only while timing is on, like the dispatch-timestamp events: each
@@ -522,6 +526,9 @@ void setup_kernel_pagein(Layer& L) {
   L.hist_dev = (int32_t*)hd;
   for (int q = 0; q < L.nplanes; ++q) L.planes[q].dev = dev[q];
   L.kpin = true;
+  // a packed copy that is not pinned and mapped leaves the plain masters
+  if (d.packed_master)
+    L.packed_dev = mapped_host_range(d.packed_master, (size_t)d.num_experts * d.packed_stride);
   set_fused_ok(L);
 }
 
@@ -790,6 +797,15 @@ extern "C" int wisp_layer_create(const wisp_layer_desc* desc, void** handle) {
       d.pagein_streams > kCopyStreams ||
       (d.pagein_engine != WISP_PAGEIN_MEMCPY && d.pagein_engine != WISP_PAGEIN_KERNEL)) {
     wisp_set_last_error("invalid layer descriptor", "wisp_layer_create");
+    return WISP_ERR_INVALID;
+  }
+  if (d.packed_master &&
+      (d.dtype != WISP_BF16 || d.hidden < 64 || d.inter < 64 || d.hidden % 64 ||
+       d.inter % 64 || d.packed_stride % 256 ||
+       d.packed_stride < packed::Layout(d.hidden, d.inter).exc_off ||
+       ((uintptr_t)d.packed_master) % 16)) {
+    wisp_set_last_error("packed masters need a bf16 layer with hidden and inter multiples of 64 "
+                        "and the stride wisp_pack_bf16_stride gives", "wisp_layer_create");
     return WISP_ERR_INVALID;
   }
   Layer* L = new Layer();

@@ -2,6 +2,7 @@
 #pragma once
 
 #include "common.h"
+#include "packed.h"
 
 namespace wisp {
 
@@ -24,6 +25,20 @@ struct PageInPlane {
 // slab per expert (in master and scratch alike) copies them as one plane.
 constexpr int kMaxPlanes = 4;
 
+// A bf16 layer's packed masters (packed.h): expert e at m + e * m_stride
+// (the device address of their pinned, mapped host copy); its w13 rows
+// unpack to slot s at d13 + s * d13_stride, its w2 rows at d2 + s *
+// d2_stride (bytes).  m null: the planes are copied as they are.
+struct PackedSrc {
+  const char* m;
+  size_t m_stride;
+  int H, I;
+  char* d13;
+  size_t d13_stride;
+  char* d2;
+  size_t d2_stride;
+};
+
 // One page-in launch.  The load list holds (expert, slot) pairs; its length
 // is *count when count is non-null (written by the pager kernel), else n.
 struct PageInArgs {
@@ -34,6 +49,7 @@ struct PageInArgs {
   int nplanes;
   PageInPlane p[kMaxPlanes];
   int32_t* hist;  // device address of a pinned host word that receives n, or null
+  PackedSrc pk;
 };
 
 int launch_pagein(const PageInArgs& a, hipStream_t st, hipEvent_t ev_start, hipEvent_t ev_stop);
@@ -84,6 +100,70 @@ __device__ inline void copy_range(const char* __restrict__ src, char* __restrict
       if (i < n) __builtin_nontemporal_store(v[u], d + i);
     }
   }
+}
+
+// Unpacks `rows` packed rows of L values from src (row r at src + r *
+// row_bytes(L)) into bf16 rows at dst (row r at dst + r * 2L bytes), spread
+// over `nblocks` blocks of NT threads (`blk`: this block's index), one
+// 8-value chunk a thread and UNR chunks in flight; exc is the expert's
+// exception area.  Index math is 32-bit (an expert's rows hold fewer than
+// 2^32 chunks) and exception blocks are rewritten in a pass of their own:
+// both keep the scalar and vector registers low enough that the fused
+// page-in + w13 launch, whose w13 blocks get the registers its copy blocks
+// need, does not spill.
+template <int NT = 256, int UNR = kPageInUnroll>
+__device__ inline void unpack_rows(const char* __restrict__ src, int rows, int L,
+                                   const char* __restrict__ exc, char* __restrict__ dst, int blk,
+                                   int nblocks) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const unsigned nch = (unsigned)L / 8u, rb = (unsigned)packed::row_bytes(L);
+  const unsigned n = (unsigned)rows * nch, step = (unsigned)nblocks * NT * UNR;
+  for (unsigned base = (unsigned)blk * NT * UNR + threadIdx.x; base < n; base += step) {
+    packed::Chunk c[UNR];
+    unsigned off[UNR];
+    int q[UNR];
+    bool any = false;
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      const unsigned i = base + (unsigned)u * NT;
+      const unsigned r = i < n ? i / nch : 0u;
+      q[u] = (int)(i < n ? i - r * nch : 0u);
+      off[u] = r * rb;
+      if (i < n) c[u] = packed::load_chunk(src + off[u], L, q[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      const unsigned i = base + (unsigned)u * NT;
+      if (i < n) {
+        const uint4 v = packed::unpack_plain(c[u]);
+        __builtin_nontemporal_store(u32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4*>(dst) + i);
+        any |= packed::is_exception(c[u], q[u]);
+      }
+    }
+    if (any) {
+#pragma unroll
+      for (int u = 0; u < UNR; ++u) {
+        const unsigned i = base + (unsigned)u * NT;
+        if (i < n && packed::is_exception(c[u], q[u])) {
+          const uint4 v = packed::unpack_chunk(c[u], src + off[u], L, q[u], exc);
+          __builtin_nontemporal_store(u32x4{v.x, v.y, v.z, v.w},
+                                      reinterpret_cast<u32x4*>(dst) + i);
+        }
+      }
+    }
+  }
+}
+
+// One loaded expert's whole packed slab into its slot, over `nblocks`
+// blocks.
+template <int NT = 256>
+__device__ inline void unpack_expert(const PackedSrc& pk, int e, int s, int blk, int nblocks) {
+  const packed::Layout Lp(pk.H, pk.I);
+  const char* ex = pk.m + (size_t)e * pk.m_stride;
+  unpack_rows<NT>(ex, 2 * pk.I, pk.H, ex + Lp.exc_off, pk.d13 + (size_t)s * pk.d13_stride, blk,
+                  nblocks);
+  unpack_rows<NT>(ex + Lp.w2_off, pk.H, pk.I, ex + Lp.exc_off,
+                  pk.d2 + (size_t)s * pk.d2_stride, blk, nblocks);
 }
 
 // Device address of host memory [base, base + bytes) when that range lies

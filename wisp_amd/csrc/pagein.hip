@@ -26,6 +26,10 @@ __global__ __launch_bounds__(256) void pagein_kernel(PageInArgs a) {
   for (int j = 0; j < n; ++j) {
     const int e = a.loads[2 * j], s = a.loads[2 * j + 1];
     if (e < 0 || e >= a.num_experts || s < 0 || s >= a.cap) continue;
+    if (a.pk.m) {
+      unpack_expert(a.pk, e, s, blockIdx.x, gridDim.x);
+      continue;
+    }
     for (int q = 0; q < a.nplanes; ++q) {
       const PageInPlane& pl = a.p[q];
       copy_range(pl.m + (size_t)e * pl.m_stride, pl.d + (size_t)s * pl.d_stride, pl.bytes,
