@@ -30,6 +30,7 @@ from __future__ import annotations
 import ctypes as C
 import logging
 import os
+import weakref
 from typing import Any, Callable
 
 import torch
@@ -126,6 +127,23 @@ def _resolve_packed_masters() -> bool:
     from and unpacks into the slot.  ``0`` pages the masters as they are."""
     return os.environ.get("WISP_PACKED_MASTERS", "1").strip().lower() not in (
         "0", "false", "no", "off")
+
+
+class _PackedRef:
+    """A weak reference to a (packed tensor, stride) pair."""
+
+    def __init__(self, pair: tuple) -> None:
+        self._t = weakref.ref(pair[0])
+        self._stride = pair[1]
+
+    def __call__(self):
+        t = self._t()
+        return None if t is None else (t, self._stride)
+
+
+# packed master copies by (masters, their version counters): layers that
+# share masters share the copy while any of them holds it
+_PACKED_MASTERS: dict = {}
 
 
 def _resolve_decode_fused() -> bool:
@@ -292,16 +310,27 @@ class WispMoEState:
 
     def _pack_masters(self) -> None:
         """The masters' packed copy in pinned memory (no copy when the shape
-        does not pack: H and I must be multiples of 64)."""
+        does not pack: H and I must be multiples of 64).  States over the
+        same master tensors, unmodified since (torch's version counter),
+        share one packed copy."""
         w13, w2 = self.cpu_w13, self.cpu_w2
         args = (self.num_experts, self.hidden, self.inter, w13.data_ptr(), w13.stride(0),
                 w2.data_ptr(), w2.stride(0))
+        key = args + (w13._version, w2._version)
+        ref = _PACKED_MASTERS.get(key)
+        hit = ref() if ref is not None else None
+        if hit is not None:
+            self._packed, self._packed_stride = hit
+            return
         stride = lib().wisp_pack_bf16_stride(*args)
         if not stride:
             return
         packed = torch.empty(self.num_experts * stride, dtype=torch.uint8, pin_memory=True)
         check(lib().wisp_pack_bf16(*args, packed.data_ptr(), stride), "wisp_pack_bf16")
         self._packed, self._packed_stride = packed, int(stride)
+        for k in [k for k, r in _PACKED_MASTERS.items() if r() is None]:
+            del _PACKED_MASTERS[k]
+        _PACKED_MASTERS[key] = _PackedRef((packed, int(stride)))
 
     @property
     def packed_bytes_per_expert(self) -> int:
