@@ -753,8 +753,14 @@ def main() -> int:
         log(f"cpu baseline {time.perf_counter() - t_cpu:.1f}s")
     pmc_path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                             "qwen3_decode_pmc.json")
-    traffic = pmc_traffic(pmc_path, "pagein_w13_kernel")
+    # bf16 masters page in from their packed copy unless WISP_PACKED_MASTERS=0
+    packed = states[0]._packed is not None
+    w13_kernel = "pagein_w13_packed_kernel" if packed else "pagein_w13_kernel"
+    traffic = pmc_traffic(pmc_path, w13_kernel)
     link_best = max(link, link_big)  # the host link's best measured hipMemcpyAsync rate
+    # bytes the host link carried: the packed copy's stride per loaded expert
+    link_bytes = pin_bytes * states[0].packed_bytes_per_expert / sh.expert_bytes
+    link_gbps = link_bytes / (pin_ms * 1e-3) / 1e9 if pin_ms > 0 else 0.0
 
     value = args.steps / elapsed
     line = {
@@ -779,7 +785,7 @@ def main() -> int:
             "routing": "zipf(1.1) bias + 0.6 reuse of previous top-8",
         },
         "roofline": {
-            "kernel": "pagein_w13_kernel (gate/up GEMV + SiLU*mul; page-in blocks idle)",
+            "kernel": f"{w13_kernel} (gate/up GEMV + SiLU*mul; page-in blocks idle)",
             "bound": "hbm",
             "achieved": round(a13, 1),
             "peak": HBM_PEAK_GBPS,
@@ -792,10 +798,10 @@ def main() -> int:
                       f"({elapsed_ev / args.steps * 1e3:.4f} ms per step with the events); "
                       f"the fused page-in + w13 launch of the {prof['w13_calls']} calls that "
                       f"paged nothing in (on the others it is page-in time)",
-            "timing_off": timing_off(pmc_path, "pagein_w13_kernel", w13_bytes),
+            "timing_off": timing_off(pmc_path, w13_kernel, w13_bytes),
         },
         "expert_gemm": {
-            "kernels": "pagein_w13_kernel + w2_combine_kernel",
+            "kernels": f"{w13_kernel} + w2_combine_kernel",
             "bytes_per_token": w13_bytes + w2_bytes,
             "avg_us": round((t13 + t2) * 1e6, 3),
             "achieved_GBps": round(agemm, 1),
@@ -811,12 +817,19 @@ def main() -> int:
         "pagein": {
             "bytes": pin_bytes,
             "achieved_GBps": round(pin_gbps, 2),
+            "packed_masters": packed,
+            "link_bytes_per_expert": states[0].packed_bytes_per_expert,
+            "expert_bytes": sh.expert_bytes,
+            "link_bytes": link_bytes,
+            "link_achieved_GBps": round(link_gbps, 2),
             "link_GBps_9MiB_p50": round(link, 2),
             "link_GBps_256MiB_p50": round(link_big, 2),
-            "frac_of_link": round(pin_gbps / link_best, 4) if link_best else None,
+            "frac_of_link": round(link_gbps / link_best, 4) if link_best else None,
             "misses": miss, "hits": hits,
             "misses_per_call": round(miss / max(1, args.steps), 3),
-            "timing": "copy-kernel events over the second pass; misses and hits of the first",
+            "timing": "copy-kernel events over the second pass; misses and hits of the first; "
+                      "bytes and achieved_GBps count each loaded expert's bf16 bytes, link_* "
+                      "the bytes read over the host link",
         },
         "cpu_baseline": cpu,
     }
