@@ -226,7 +226,7 @@ struct FusedW13Args {
 // (Computing act from the unpacked registers instead held more registers
 // than the w13 blocks' budget, and all blocks of the launch get the most
 // any path needs.)  Then each loaded expert's w2 rows.
-template <int CH, bool FULL>
+template <int CH, bool FULL, int NCB>
 __device__ inline void pagein_w13_packed(const FusedW13Args& f, const PageInArgs& a, int cb,
                                          int mine) {
   // wave-uniform (readfirstlane), so that the row bases sit in scalar
@@ -237,7 +237,7 @@ __device__ inline void pagein_w13_packed(const FusedW13Args& f, const PageInArgs
   const packed::Layout Lp(H, I);
   const int n = *a.count;
   int jcur = -1, e = -1, s = -1, pair = -1;
-  for (int q = cb * 4 + wave; q < n * I; q += kPageInBlocks * 4) {
+  for (int q = cb * 4 + wave; q < n * I; q += NCB * 4) {
     const int j = q / I, i = q - j * I;
     if (j != jcur) {
       jcur = j;
@@ -301,13 +301,13 @@ __device__ inline void pagein_w13_packed(const FusedW13Args& f, const PageInArgs
     if (ej < 0 || ej >= a.num_experts || sj < 0 || sj >= a.cap) continue;
     const char* ex = pk.m + (size_t)ej * pk.m_stride;
     unpack_rows<256, 2>(ex + Lp.w2_off, H, I, ex + Lp.exc_off,
-                        pk.d2 + (size_t)sj * pk.d2_stride, cb, kPageInBlocks);
+                        pk.d2 + (size_t)sj * pk.d2_stride, cb, NCB);
   }
 }
 
-// Copy block `cb` (of kPageInBlocks) of a fused page-in + w13 launch
-// (PACKED: from the packed masters).
-template <typename T, int CH, bool FULL, bool PACKED = false>
+// Copy block `cb` (of kPageInBlocks, or NCB with PACKED) of a fused
+// page-in + w13 launch (PACKED: from the packed masters).
+template <typename T, int CH, bool FULL, bool PACKED = false, int NCB = kPageInBlocks>
 __device__ inline void pagein_w13_copy_block(const FusedW13Args& f, const PageInArgs& a, int cb) {
   constexpr int V = Vec<T>::N;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -325,7 +325,7 @@ __device__ inline void pagein_w13_copy_block(const FusedW13Args& f, const PageIn
   uint4 xv[CH];
   load_row<T, CH, FULL, false>((const T*)f.x, nch, lane, xv);  // the call's one token
   if constexpr (PACKED && sizeof(T) == 2) {
-    pagein_w13_packed<CH, FULL>(f, a, cb, mine);
+    pagein_w13_packed<CH, FULL, NCB>(f, a, cb, mine);
     return;
   }
   int jcur = -1, e = -1, s = -1, pair = -1;
@@ -385,12 +385,12 @@ __device__ inline void pagein_w13_copy_block(const FusedW13Args& f, const PageIn
   }
 }
 
-template <typename T, int CH, bool FULL, bool PACKED>
+template <typename T, int CH, bool FULL, bool PACKED, int NCB>
 __device__ inline void pagein_w13_body(const FusedW13Args& f, const PageInArgs& a) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  if (blockIdx.x >= kPageInBlocks) {
+  if (blockIdx.x >= NCB) {
     const int I = f.I, nbx = (I + 3) / 4;
-    const int local = blockIdx.x - kPageInBlocks;
+    const int local = blockIdx.x - NCB;
     const int pair = local / nbx;
     const int i = (local - pair * nbx) * 4 + wave;
     if (i >= I) return;
@@ -401,24 +401,31 @@ __device__ inline void pagein_w13_body(const FusedW13Args& f, const PageInArgs& 
                           (const T*)f.w13, f.w13_stride, (T*)f.act, lane);
     return;
   }
-  pagein_w13_copy_block<T, CH, FULL, PACKED>(f, a, blockIdx.x);
+  pagein_w13_copy_block<T, CH, FULL, PACKED, NCB>(f, a, blockIdx.x);
 }
 
 template <typename T, int CH, bool FULL>
 __global__ __launch_bounds__(256) void pagein_w13_kernel(FusedW13Args f, PageInArgs a) {
-  pagein_w13_body<T, CH, FULL, false>(f, a);
+  pagein_w13_body<T, CH, FULL, false, kPageInBlocks>(f, a);
 }
 
 // The same launch paging in from packed masters.  The unpack would take
 // more registers than the w13 blocks (which then hold fewer waves per SIMD
 // than they need to stream their weights in one round), so the launch is
 // held at the waves per SIMD the plain launch gets for the same row length.
+// Copy blocks of the packed launch: twice the plain launch's, since each
+// wave has less of the host link in flight (a packed row is ~3 KiB, and
+// the unpack and the read-back of the rows sit between its loads).
+// Measured at the Qwen3 decode shape: 51.8 GB/s of link with 64 blocks,
+// 54.0 with 128, the same with 192.
+constexpr int kPackedPageInBlocks = 128;
+
 constexpr int packed_waves_per_eu(int ch) { return ch <= 3 ? 7 : ch == 4 ? 6 : ch <= 6 ? 4 : 3; }
 
 template <int CH, bool FULL>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(packed_waves_per_eu(CH))))
 void pagein_w13_packed_kernel(FusedW13Args f, PageInArgs a) {
-  pagein_w13_body<uint16_t, CH, FULL, true>(f, a);
+  pagein_w13_body<uint16_t, CH, FULL, true, kPackedPageInBlocks>(f, a);
 }
 
 // ---------------------------------------------------------------------------
@@ -475,7 +482,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6))) void d
     __syncthreads();
     if (!seen) return;
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    pagein_w13_copy_block<T, CH, true, PACKED>(f, a, blockIdx.x - 1);
+    pagein_w13_copy_block<T, CH, true, PACKED, kPageInBlocks>(f, a, blockIdx.x - 1);
     return;
   }
   const int I = f.I, nbx = (I + 3) / 4;
@@ -750,6 +757,7 @@ void launch_pagein_w13(const PageInArgs& a, const FusedW13Args& f, hipStream_t s
   const bool full = f.H == CH * 64 * Vec<T>::N;
   if constexpr (sizeof(T) == 2) {
     if (a.pk.m) {
+      const dim3 grid(kPackedPageInBlocks + (f.I + 3) / 4 * f.K);
       if (full)
         launch_timed(pagein_w13_packed_kernel<CH, true>, grid, dim3(256), st, ev_start, ev_stop,
                      f, a);

@@ -41,7 +41,9 @@ __global__ __launch_bounds__(256) void pagein_kernel(PageInArgs a) {
 }  // namespace
 
 int launch_pagein(const PageInArgs& a, hipStream_t st, hipEvent_t ev_start, hipEvent_t ev_stop) {
-  launch_timed(pagein_kernel, dim3(kPageInBlocks), dim3(256), st, ev_start, ev_stop, a);
+  // packed masters: twice the blocks, since a chunk's loads move fewer bytes
+  launch_timed(pagein_kernel, dim3(a.pk.m ? 2 * kPageInBlocks : kPageInBlocks), dim3(256), st,
+               ev_start, ev_stop, a);
   WISP_HIP_TRY(hipGetLastError());
   return WISP_OK;
 }
