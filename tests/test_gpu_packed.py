@@ -95,3 +95,27 @@ def test_packed_resident_priming_and_resize(monkeypatch):
             torch.cuda.synchronize()
             assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
             _slots_hold_masters(paged, w13, w2)
+
+
+def test_packed_copy_shared_and_rebuilt_after_a_master_write(monkeypatch):
+    """States over the same masters share one packed copy; an in-place write
+    to the masters (torch's version counter) makes the next state pack anew,
+    and it pages the new values."""
+    monkeypatch.setenv("WISP_PAGEIN_ENGINE", "kernel")
+    monkeypatch.setenv("WISP_PACKED_MASTERS", "1")
+    E, H, I = 8, 128, 64
+    w13, w2 = _masters(E, H, I, 31)
+    a = WispMoEState(w13, w2, 4, "paged", DEV, 0)
+    b = WispMoEState(w13, w2, 4, "paged", DEV, 1)
+    assert a._packed is not None and a._packed is b._packed
+    w13[3].mul_(2.0)
+    w2[3].mul_(-1.0)
+    c = WispMoEState(w13, w2, 4, "paged", DEV, 2)
+    assert c._packed is not None and c._packed is not a._packed
+    lg = torch.zeros(1, E)
+    lg[0, 3], lg[0, 5] = 8.0, 4.0
+    x = torch.randn(1, H, generator=torch.Generator().manual_seed(32)).to(torch.bfloat16)
+    c.forward(x.to(DEV), lg.to(DEV), 2, True)
+    torch.cuda.synchronize()
+    assert sorted(e for e in c.slot_to_expert if e >= 0) == [3, 5]
+    assert _slots_hold_masters(c, w13, w2) == 2

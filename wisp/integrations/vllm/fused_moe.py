@@ -312,7 +312,9 @@ class WispMoEState:
         """The masters' packed copy in pinned memory (no copy when the shape
         does not pack: H and I must be multiples of 64).  States over the
         same master tensors, unmodified since (torch's version counter),
-        share one packed copy."""
+        share one packed copy.  The copy is taken here: a state pages the
+        masters as they were when it was built (the masters are written
+        once, at weight loading, before the states exist)."""
         w13, w2 = self.cpu_w13, self.cpu_w2
         args = (self.num_experts, self.hidden, self.inter, w13.data_ptr(), w13.stride(0),
                 w2.data_ptr(), w2.stride(0))
