@@ -98,16 +98,24 @@ void pack_expert(const Masters& m, int e, uint8_t* out) {
                      out + Lp.w2_off + r * Lp.rs2, exc + 64 * (size_t)nexc, nexc);
 }
 
-// Runs f(e) for every expert on up to 16 threads.
+// Runs f(e) for every expert on up to 16 threads (on the calling thread
+// alone when no thread can be started).
 template <typename F>
 void over_experts(int E, F f) {
   const int nt = std::max(1, std::min({E, 16, (int)std::thread::hardware_concurrency()}));
   std::vector<std::thread> th;
-  for (int t = 0; t < nt; ++t)
-    th.emplace_back([&, t] {
-      for (int e = t; e < E; e += nt) f(e);
-    });
+  int started = 0;
+  try {
+    for (; started < nt; ++started)
+      th.emplace_back([&, started] {
+        for (int e = started; e < E; e += nt) f(e);
+      });
+  } catch (...) {
+  }
   for (auto& x : th) x.join();
+  // experts of the threads that did not start
+  for (int t = started; t < nt; ++t)
+    for (int e = t; e < E; e += nt) f(e);
 }
 
 bool valid(int E, int H, int I, const void* w13, size_t s13, const void* w2, size_t s2) {
