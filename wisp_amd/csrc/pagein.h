@@ -154,16 +154,70 @@ __device__ inline void unpack_rows(const char* __restrict__ src, int rows, int L
   }
 }
 
+// The same unpack with 32 consecutive values (four chunks, half a block) a
+// thread and UNR such groups in flight: two 16-byte sign/mantissa loads and
+// one 16-byte code load per group.  For the page-in kernel, where no w13
+// blocks share the launch's registers.
+template <int NT = 256, int UNR = 2>
+__device__ inline void unpack_rows_wide(const char* __restrict__ src, int rows, int L,
+                                        const char* __restrict__ exc, char* __restrict__ dst,
+                                        int blk, int nblocks) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const unsigned ng = (unsigned)L / 32u, rb = (unsigned)packed::row_bytes(L);
+  const unsigned n = (unsigned)rows * ng, step = (unsigned)nblocks * NT * UNR;
+  const unsigned hdr = (unsigned)(L + L / 2), mo = hdr + (unsigned)packed::align_up(L / 64, 4);
+  for (unsigned base = (unsigned)blk * NT * UNR + threadIdx.x; base < n; base += step) {
+    u32x4 l0[UNR], l1[UNR], cd[UNR];
+    uint32_t bs[UNR], mk[UNR];
+    unsigned off[UNR], g[UNR];
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      const unsigned i = base + (unsigned)u * NT;
+      const unsigned r = i < n ? i / ng : 0u;
+      g[u] = i < n ? i - r * ng : 0u;
+      off[u] = r * rb;
+      if (i < n) {
+        const char* row = src + off[u];
+        l0[u] = *reinterpret_cast<const u32x4*>(row + 32u * g[u]);
+        l1[u] = *reinterpret_cast<const u32x4*>(row + 32u * g[u] + 16u);
+        cd[u] = *reinterpret_cast<const u32x4*>(row + (unsigned)L + 16u * g[u]);
+        bs[u] = *reinterpret_cast<const uint8_t*>(row + hdr + (g[u] >> 1));
+        mk[u] = *reinterpret_cast<const uint32_t*>(row + mo + 4u * (g[u] >> 6));
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      const unsigned i = base + (unsigned)u * NT;
+      if (i >= n) continue;
+      u32x4* d = reinterpret_cast<u32x4*>(dst) + 4u * i;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const u32x4& l = t < 2 ? l0[u] : l1[u];
+        packed::Chunk c;
+        c.lo = (uint64_t)l[2 * (t & 1)] | ((uint64_t)l[2 * (t & 1) + 1] << 32);
+        c.cd = cd[u][t];
+        c.base = bs[u];
+        c.mask = mk[u];
+        const int q = (int)(4u * g[u]) + t;
+        const uint4 v = packed::is_exception(c, q)
+                            ? packed::unpack_chunk(c, src + off[u], L, q, exc)
+                            : packed::unpack_plain(c);
+        __builtin_nontemporal_store(u32x4{v.x, v.y, v.z, v.w}, d + t);
+      }
+    }
+  }
+}
+
 // One loaded expert's whole packed slab into its slot, over `nblocks`
 // blocks.
 template <int NT = 256>
 __device__ inline void unpack_expert(const PackedSrc& pk, int e, int s, int blk, int nblocks) {
   const packed::Layout Lp(pk.H, pk.I);
   const char* ex = pk.m + (size_t)e * pk.m_stride;
-  unpack_rows<NT>(ex, 2 * pk.I, pk.H, ex + Lp.exc_off, pk.d13 + (size_t)s * pk.d13_stride, blk,
-                  nblocks);
-  unpack_rows<NT>(ex + Lp.w2_off, pk.H, pk.I, ex + Lp.exc_off,
-                  pk.d2 + (size_t)s * pk.d2_stride, blk, nblocks);
+  unpack_rows_wide<NT>(ex, 2 * pk.I, pk.H, ex + Lp.exc_off, pk.d13 + (size_t)s * pk.d13_stride,
+                       blk, nblocks);
+  unpack_rows_wide<NT>(ex + Lp.w2_off, pk.H, pk.I, ex + Lp.exc_off,
+                       pk.d2 + (size_t)s * pk.d2_stride, blk, nblocks);
 }
 
 // Device address of host memory [base, base + bytes) when that range lies
