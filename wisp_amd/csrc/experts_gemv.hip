@@ -300,8 +300,8 @@ __device__ inline void pagein_w13_packed(const FusedW13Args& f, const PageInArgs
     const int ej = a.loads[2 * j], sj = a.loads[2 * j + 1];
     if (ej < 0 || ej >= a.num_experts || sj < 0 || sj >= a.cap) continue;
     const char* ex = pk.m + (size_t)ej * pk.m_stride;
-    unpack_rows<256, 2>(ex + Lp.w2_off, H, I, ex + Lp.exc_off,
-                        pk.d2 + (size_t)sj * pk.d2_stride, cb, NCB);
+    unpack_rows_wide<256, 1>(ex + Lp.w2_off, H, I, ex + Lp.exc_off,
+                             pk.d2 + (size_t)sj * pk.d2_stride, cb, NCB);
   }
 }
 
