@@ -57,19 +57,6 @@ struct Chunk {
   uint32_t cd, base, mask;
 };
 
-// (32-bit offsets from the row: with a wave-uniform row the loads take the
-// scalar base and one offset register each)
-__device__ inline Chunk load_chunk(const char* __restrict__ row, int L, int q) {
-  const unsigned b = (unsigned)q >> 3, hdr = (unsigned)(L + L / 2);
-  Chunk c;
-  c.lo = *reinterpret_cast<const uint64_t*>(row + 8u * (unsigned)q);
-  c.cd = *reinterpret_cast<const uint32_t*>(row + ((unsigned)L + 4u * (unsigned)q));
-  c.base = *reinterpret_cast<const uint8_t*>(row + (hdr + b));
-  c.mask = *reinterpret_cast<const uint32_t*>(
-      row + (hdr + (unsigned)align_up(L / 64, 4) + 4u * (b >> 5)));
-  return c;
-}
-
 // Chunk k of a lane that owns chunks k * 64 + lane (the GEMV kernels' lane
 // layout) of a row of L values, as buffer loads from the row's resource:
 // the lane's offsets are one register per stream, the chunk's part an

@@ -104,60 +104,11 @@ __device__ inline void copy_range(const char* __restrict__ src, char* __restrict
 
 // Unpacks `rows` packed rows of L values from src (row r at src + r *
 // row_bytes(L)) into bf16 rows at dst (row r at dst + r * 2L bytes), spread
-// over `nblocks` blocks of NT threads (`blk`: this block's index), one
-// 8-value chunk a thread and UNR chunks in flight; exc is the expert's
-// exception area.  Index math is 32-bit (an expert's rows hold fewer than
-// 2^32 chunks) and exception blocks are rewritten in a pass of their own:
-// both keep the scalar and vector registers low enough that the fused
-// page-in + w13 launch, whose w13 blocks get the registers its copy blocks
-// need, does not spill.
-template <int NT = 256, int UNR = kPageInUnroll>
-__device__ inline void unpack_rows(const char* __restrict__ src, int rows, int L,
-                                   const char* __restrict__ exc, char* __restrict__ dst, int blk,
-                                   int nblocks) {
-  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-  const unsigned nch = (unsigned)L / 8u, rb = (unsigned)packed::row_bytes(L);
-  const unsigned n = (unsigned)rows * nch, step = (unsigned)nblocks * NT * UNR;
-  for (unsigned base = (unsigned)blk * NT * UNR + threadIdx.x; base < n; base += step) {
-    packed::Chunk c[UNR];
-    unsigned off[UNR];
-    int q[UNR];
-    bool any = false;
-#pragma unroll
-    for (int u = 0; u < UNR; ++u) {
-      const unsigned i = base + (unsigned)u * NT;
-      const unsigned r = i < n ? i / nch : 0u;
-      q[u] = (int)(i < n ? i - r * nch : 0u);
-      off[u] = r * rb;
-      if (i < n) c[u] = packed::load_chunk(src + off[u], L, q[u]);
-    }
-#pragma unroll
-    for (int u = 0; u < UNR; ++u) {
-      const unsigned i = base + (unsigned)u * NT;
-      if (i < n) {
-        const uint4 v = packed::unpack_plain(c[u]);
-        __builtin_nontemporal_store(u32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4*>(dst) + i);
-        any |= packed::is_exception(c[u], q[u]);
-      }
-    }
-    if (any) {
-#pragma unroll
-      for (int u = 0; u < UNR; ++u) {
-        const unsigned i = base + (unsigned)u * NT;
-        if (i < n && packed::is_exception(c[u], q[u])) {
-          const uint4 v = packed::unpack_chunk(c[u], src + off[u], L, q[u], exc);
-          __builtin_nontemporal_store(u32x4{v.x, v.y, v.z, v.w},
-                                      reinterpret_cast<u32x4*>(dst) + i);
-        }
-      }
-    }
-  }
-}
-
-// The same unpack with 32 consecutive values (four chunks, half a block) a
-// thread and UNR such groups in flight: two 16-byte sign/mantissa loads and
-// one 16-byte code load per group.  For the page-in kernel, where no w13
-// blocks share the launch's registers.
+// over `nblocks` blocks of NT threads (`blk`: this block's index), 32
+// consecutive values (four chunks, half a block) a thread and UNR such
+// groups in flight: two 16-byte sign/mantissa loads and one 16-byte code
+// load per group.  exc is the expert's exception area.  Index math is 32-bit
+// (an expert's rows hold fewer than 2^32 values).
 template <int NT = 256, int UNR = 2>
 __device__ inline void unpack_rows_wide(const char* __restrict__ src, int rows, int L,
                                         const char* __restrict__ exc, char* __restrict__ dst,
